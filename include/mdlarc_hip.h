@@ -1,0 +1,187 @@
+/*
+ * mdlarc_hip.h -- C ABI of libmdlarc_hip.so, the MI355X (gfx950) kernels of the TinyTransformer
+ * inference hot path of shyampathak22/mdlARC_scale.
+ *
+ * The reference has no FFI: its boundary is the PyTorch module / function API of
+ * src/transformer.py and src/inference.py.  Each entry point below replaces the reference ops
+ * named in its comment (file:line in the reference checkout).  The host side
+ * (mdlarc_scale_amd/, Python) binds these with ctypes; INTEGRATION.md shows the binding.
+ *
+ * Conventions
+ *   - bf16 tensors are passed as uint16_t* (raw bfloat16 bits), fp32 as float*.
+ *   - Every pointer is a DEVICE pointer unless stated otherwise; `stream` is a hipStream_t.
+ *   - Nothing allocates, frees or synchronises; all work is ordered on `stream`.
+ *   - Return 0 on success, a negative MDL_ERR_* for arguments rejected on the host before any
+ *     launch, or a positive hipError_t reported by the launch.
+ *   - Head dimension is 64 (all reference model sizes, src/transformer.py:728-745).
+ *   - KV cache layout is the reference StaticKVCache layout (src/inference.py:73-77):
+ *     one layer's K (or V) is [batch, n_heads, cache_slots, 64] bf16, slot-major rows of 128 B.
+ */
+#ifndef MDLARC_HIP_H
+#define MDLARC_HIP_H
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define MDL_OK 0
+#define MDL_ERR_NULL (-1)          /* a required pointer is NULL */
+#define MDL_ERR_ALIGN (-2)         /* a pointer or leading dimension breaks 16-byte alignment */
+#define MDL_ERR_SHAPE (-3)         /* a dimension is out of the supported range */
+#define MDL_ERR_HEAD_DIM (-4)      /* head_dim != 64 or d_model != n_heads * 64 */
+#define MDL_ERR_CACHE (-5)         /* slot range outside the cache */
+#define MDL_ERR_WORKSPACE (-6)     /* workspace too small */
+#define MDL_ERR_DTYPE (-7)         /* unsupported dtype code */
+
+#define MDL_DTYPE_F32 0
+#define MDL_DTYPE_BF16 1
+
+/* Library version (major*100 + minor) and a static string for an error code. */
+int mdl_version(void);
+const char* mdl_error_string(int code);
+
+/*
+ * K1 -- token + example embedding gather fused with the first RMSNorm.
+ * Replaces: TinyTransformer.forward token/example embedding (src/transformer.py:584-589),
+ *           _prefill / _decode_step embedding (src/inference.py:393-395, :433-435),
+ *           and the reduction of blocks[0].ln1 = RMSNorm.forward (src/transformer.py:45-48).
+ * For row m (batch row b = m / row_len):
+ *   x[m]     = tok_table[ids[m]] + (example_ids ? ex_table[example_ids[b]] : 0)     (fp32)
+ *   rstd[m]  = 1 / sqrt(mean(x[m]^2) + eps)
+ *   xg[m]    = bf16(x[m] * gamma)        (GEMM input; rstd is applied after the GEMM)
+ * Tables are fp32 or bf16 (table_dtype); ids are clamped into range (callers validate first).
+ */
+int mdl_embed_rmsnorm(const int64_t* ids, const int64_t* example_ids, const void* tok_table,
+                      const void* ex_table, int table_dtype, int vocab, int n_examples, int rows,
+                      int row_len, int d, const float* gamma, float eps, float* x_out,
+                      uint16_t* xg_out, float* rstd_out, void* stream);
+
+/*
+ * Residual add fused with the next RMSNorm's reduction.
+ * Replaces: the residual adds of TransformerBlock.forward (src/transformer.py:494-496),
+ *           _prefill / _decode_step (src/inference.py:412-413, :455-456), the fc_down bias
+ *           (src/transformer.py:443), and the reduction of the following ln2 / ln1 / ln_f.
+ *   x[m]    += delta[m] (+ bias)           delta bf16 [rows, d] (may be NULL), bias fp32 [d] or NULL
+ *   rstd[m]  = 1 / sqrt(mean(x[m]^2) + eps)
+ *   xg[m]    = bf16(x[m] * gamma)          (skipped when xg_out is NULL)
+ */
+int mdl_add_rmsnorm(float* x, const uint16_t* delta, const float* bias, int rows, int d,
+                    const float* gamma, float eps, uint16_t* xg_out, float* rstd_out,
+                    void* stream);
+
+/*
+ * K2 -- RMSNorm scale + Q/K/V split + 3D RoPE + static-cache write.
+ * Replaces: qkv reshape/unbind (src/inference.py:402-403, :439-440), the RMSNorm multiply of
+ *           ln1, RotaryEmbedding3D.apply_rotary (src/transformer.py:132-187, _rotate_half
+ *           :51-58), the transposes (src/inference.py:406) and StaticKVCache.update
+ *           (src/inference.py:84-92).
+ * qkv: bf16 [batch*seq, 3*d] (row stride qkv_ld elements) = (x*gamma) @ W_qkv^T, columns
+ *      [q heads | k heads | v heads] (src/transformer.py:317-318).  rstd: fp32 [batch*seq].
+ * pos: int64 [batch*seq, 3] (x, y, z); clamped to [0,max-1] per axis.
+ * rope_tab: fp32 [cos_x(max_x*px) | sin_x | cos_y(max_y*py) | sin_y | cos_z(max_z*pz) | sin_z],
+ *      the tables of RotaryEmbedding3D._build_cache (src/transformer.py:95-126).
+ * Outputs: q_out bf16 [batch*seq, d] = rope(q * rstd) * q_scale; k/v written to cache slot
+ *      (slot_dev ? *slot_dev : slot0) + s for token s of each batch row.
+ */
+int mdl_qkv_rope_cache(const uint16_t* qkv, int64_t qkv_ld, const float* rstd,
+                       const int64_t* pos, const float* rope_tab, int batch, int seq,
+                       int n_heads, int head_dim, int max_x, int max_y, int max_z, int px,
+                       int py, int pz, float q_scale, uint16_t* q_out, uint16_t* k_cache,
+                       uint16_t* v_cache, int cache_slots, int slot0, const int32_t* slot_dev,
+                       void* stream);
+
+/*
+ * K3 -- SwiGLU gate: silu(gate) * up, with the RMSNorm multiply of ln2 and the fc biases.
+ * Replaces: FeedForward.forward's silu(fc_gate(x)) * fc_up(x) (src/transformer.py:441-449).
+ * gate_up: bf16 [rows, 2*d_ff] (row stride ld) = (x*gamma2) @ [W_gate; W_up]^T.
+ *   h[m, j] = silu(rstd[m]*g[m,j] + bias_gate[j]) * (rstd[m]*u[m,j] + bias_up[j])   -> bf16
+ * rstd / biases may be NULL (treated as 1 / 0).  d_ff must be a multiple of 8.
+ */
+int mdl_swiglu(const uint16_t* gate_up, int64_t ld, const float* rstd, const float* bias_gate,
+               const float* bias_up, int rows, int d_ff, uint16_t* h_out, void* stream);
+
+/*
+ * K4a -- prefill / full-sequence attention on bf16 MFMA (flash style, online softmax).
+ * Replaces: F.scaled_dot_product_attention in _prefill (src/inference.py:409, mask from
+ *           _build_sdpa_mask :372-380, is_causal=True) and in MultiHeadSelfAttention.forward
+ *           (src/transformer.py:333-349, is_causal either way).
+ * q / out: bf16 [batch, seq, n_heads, 64]; q already multiplied by the softmax scale.
+ * keys:    k_cache / v_cache slots [0, seq) of [batch, n_heads, cache_slots, 64].
+ * Query i of row b sees key j iff j < seq, key_mask[b*seq + j] != 0 (key_mask may be NULL),
+ * j >= kv_start[b] (kv_start may be NULL; it must not exclude a visible key) and, if causal,
+ * j <= i.  A query with no visible key outputs 0 (torch CPU SDPA semantics).
+ */
+int mdl_attn_prefill(const uint16_t* q, const uint16_t* k_cache, const uint16_t* v_cache,
+                     int batch, int seq, int n_heads, int head_dim, int cache_slots,
+                     const uint8_t* key_mask, const int32_t* kv_start, int causal,
+                     uint16_t* out, void* stream);
+
+/*
+ * K4b -- decode attention over the static cache (split-K flash decoding).
+ * Replaces: F.scaled_dot_product_attention in _decode_step (src/inference.py:452) with the
+ *           mask rebuilt from full_attention_mask (src/inference.py:446-450, :557-558, :626).
+ * q / out: bf16 [batch, n_heads, 64] (q pre-scaled).  The query of row b sees slot j iff
+ *   kv_start[b] <= j <= t, t = (seq_dev ? *seq_dev : seq_pos), and
+ *   (j >= prompt_len || prompt_mask[b*prompt_len + j] != 0)   (prompt_mask may be NULL).
+ * workspace: fp32, at least mdl_attn_decode_workspace_bytes(...) bytes (may be NULL when
+ *   that is 0).  split_len: slots per work item (multiple of 128, >= 128).
+ */
+int64_t mdl_attn_decode_workspace_bytes(int batch, int n_heads, int cache_slots, int split_len);
+int mdl_attn_decode(const uint16_t* q, const uint16_t* k_cache, const uint16_t* v_cache,
+                    int batch, int n_heads, int head_dim, int cache_slots,
+                    const uint8_t* prompt_mask, int prompt_len, const int32_t* kv_start,
+                    int seq_pos, const int32_t* seq_dev, float* workspace,
+                    int64_t workspace_bytes, int split_len, uint16_t* out, void* stream);
+
+/*
+ * Final RMSNorm + LM head + greedy argmax.
+ * Replaces: model.lm_head(model.ln_f(x)) in _prefill / _decode_step (src/inference.py:417-424,
+ *           :459) including the x[b, lengths-1] row pick, and logits.argmax(-1)
+ *           (src/inference.py:573-574, :610-611; first index on ties).
+ * Row r uses x[row_index ? row_index[r] : r].  logits_out fp32 [rows, vocab] and token_out
+ * int64 [rows] may each be NULL.  w_head fp32 [vocab, d], gamma fp32 [d].  vocab <= 32.
+ */
+int mdl_lm_head(const float* x, const int32_t* row_index, int rows, int d, const float* gamma,
+                float eps, const float* w_head, int vocab, float* logits_out, int64_t* token_out,
+                void* stream);
+
+/*
+ * Grid-state initialisation from the prompt.
+ * Replaces: _derive_initial_state_from_prompt (src/inference.py:171-221) and the
+ *           lengths-1 index of _prefill (src/inference.py:420-424).
+ * ids int64 [batch, seq], pos int64 [batch, seq, 3], mask uint8 [batch, seq] or NULL (all valid).
+ * Outputs per row: gx, gy (int32), in_out (uint8), kv_start = first valid index (seq if none),
+ * last_row = b*seq + max(len-1, 0) (the row the reference's prefill reads its logits from).
+ */
+int mdl_grid_init(const int64_t* ids, const int64_t* pos, const uint8_t* mask, int batch,
+                  int seq, int max_x, int max_y, int32_t* gx, int32_t* gy, uint8_t* in_out,
+                  int32_t* kv_start, int32_t* last_row, void* stream);
+
+/*
+ * One grid-state step: position of the token each row just emitted, then advance the state.
+ * Replaces: GridStateUpdater.update (src/inference.py:127-168).
+ * token int64 [batch] -> pos_out int64 [batch, 3].  counters (int32[2], may be NULL) are
+ * incremented by one by this launch: {cache slot of the current token, output column}.
+ */
+int mdl_grid_step(const int64_t* token, int batch, int max_x, int max_y, int32_t* gx,
+                  int32_t* gy, uint8_t* in_out, int64_t* pos_out, int32_t* counters,
+                  void* stream);
+
+/*
+ * Commit one generated token per row.
+ * Replaces: generated.append / finished |= (next_token == END) (src/inference.py:589-590,
+ *           :622-626).
+ * out_ids[b*out_ld + c] = token[b], c = (counters ? counters[1] : col).  If token[b] == end_id
+ * and finish_step[b] < 0, finish_step[b] = c - gen_base (finish_step may be NULL).
+ */
+int mdl_decode_commit(const int64_t* token, int batch, int64_t* out_ids, int64_t out_ld,
+                      int col, const int32_t* counters, int32_t* finish_step, int gen_base,
+                      int end_id, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* MDLARC_HIP_H */

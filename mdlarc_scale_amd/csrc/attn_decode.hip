@@ -1,0 +1,224 @@
+// K4b -- decode attention: one query per (row, head) against the static KV cache.
+//
+// Split-K flash decoding.  Work item = (b*h, split): a 256-thread block streams `split_len`
+// cache slots of one head.  Inside a wavefront, lane = 8*grp + sub: the 8 lanes of a group own
+// one slot at a time and `sub` selects 8 of the 64 channels, so one 16-byte load per lane covers
+// 8 consecutive slots = 1 KiB of contiguous K (then V).  U slots per group are loaded before any
+// arithmetic, so each lane keeps 2*U 16-byte loads in flight.  Scores are reduced over the 8
+// lanes of a group with 3 xor-shuffles; every group keeps its own online-softmax state (max, sum,
+// 8 accumulators) in the log2 domain.  At the end the 8 groups, then the 4 waves (LDS), then the
+// splits (second kernel) are merged with the usual max-rescaled sums.
+//
+// Slot j of row b is visible iff kv_start[b] <= j <= t and (j >= prompt_len or
+// prompt_mask[b, j]), the decode mask of the reference (prompt mask, then every generated slot).
+#include "common.h"
+
+namespace mdl {
+
+constexpr float kLog2e = 1.4426950408889634f;
+constexpr int kPart = 2 + kHeadDim;   // m, l, acc[64] per split
+
+template <int U>
+__global__ __launch_bounds__(256) void attn_decode_kernel(
+    const uint16_t* __restrict__ q, const uint16_t* __restrict__ kc,
+    const uint16_t* __restrict__ vc, int n_heads, int slots, const uint8_t* __restrict__ pmask,
+    int plen, const int32_t* __restrict__ kv_start, int seq_pos,
+    const int32_t* __restrict__ seq_dev, int n_split, int split_len, float* __restrict__ ws,
+    uint16_t* __restrict__ out) {
+  const int bh = blockIdx.x;
+  const int split = blockIdx.y;
+  const int b = bh / n_heads;
+  const int wave = threadIdx.x >> 6;
+  const int lane = threadIdx.x & 63;
+  const int grp = lane >> 3;
+  const int sub = lane & 7;
+  const int t = seq_dev ? *seq_dev : seq_pos;
+  const int start = kv_start ? kv_start[b] : 0;
+  const int lo = start + split * split_len;
+  const int hi = min(lo + split_len, min(t + 1, slots));
+
+  __shared__ float red[4][kPart];
+
+  float m = -INFINITY, l = 0.f, acc[8];
+#pragma unroll
+  for (int i = 0; i < 8; ++i) acc[i] = 0.f;
+
+  if (lo < hi) {
+    float qf[8];
+    unpack8(*reinterpret_cast<const uint4*>(q + static_cast<int64_t>(bh) * kHeadDim + sub * 8),
+            qf);
+#pragma unroll
+    for (int i = 0; i < 8; ++i) qf[i] *= kLog2e;
+    const uint16_t* K = kc + static_cast<int64_t>(bh) * slots * kHeadDim + sub * 8;
+    const uint16_t* V = vc + static_cast<int64_t>(bh) * slots * kHeadDim + sub * 8;
+    const uint8_t* pm = pmask ? pmask + static_cast<int64_t>(b) * plen : nullptr;
+
+    for (int base = lo + wave * 8 * U; base < hi; base += 4 * 8 * U) {
+      uint4 kr[U], vr[U];
+      bool ok[U];
+#pragma unroll
+      for (int u = 0; u < U; ++u) {
+        const int j = base + u * 8 + grp;
+        ok[u] = j < hi;
+        if (ok[u]) {
+          kr[u] = *reinterpret_cast<const uint4*>(K + static_cast<int64_t>(j) * kHeadDim);
+          vr[u] = *reinterpret_cast<const uint4*>(V + static_cast<int64_t>(j) * kHeadDim);
+          if (pm && j < plen) ok[u] = pm[j] != 0;
+        } else {
+          kr[u] = make_uint4(0, 0, 0, 0);
+          vr[u] = make_uint4(0, 0, 0, 0);
+        }
+      }
+      float s[U];
+#pragma unroll
+      for (int u = 0; u < U; ++u) {
+        float kf[8];
+        unpack8(kr[u], kf);
+        float a = 0.f;
+#pragma unroll
+        for (int i = 0; i < 8; ++i) a += qf[i] * kf[i];
+        a += __shfl_xor(a, 1, kWave);
+        a += __shfl_xor(a, 2, kWave);
+        a += __shfl_xor(a, 4, kWave);
+        s[u] = ok[u] ? a : -INFINITY;
+      }
+      float mx = m;
+#pragma unroll
+      for (int u = 0; u < U; ++u) mx = fmaxf(mx, s[u]);
+      if (mx == -INFINITY) continue;
+      const float alpha = exp2f(m - mx);
+      l *= alpha;
+#pragma unroll
+      for (int i = 0; i < 8; ++i) acc[i] *= alpha;
+#pragma unroll
+      for (int u = 0; u < U; ++u) {
+        const float p = exp2f(s[u] - mx);
+        l += p;
+        float vf[8];
+        unpack8(vr[u], vf);
+#pragma unroll
+        for (int i = 0; i < 8; ++i) acc[i] += p * vf[i];
+      }
+      m = mx;
+    }
+  }
+
+  // merge the 8 slot groups of this wave
+#pragma unroll
+  for (int off = 8; off < 64; off <<= 1) {
+    const float mo = __shfl_xor(m, off, kWave);
+    const float lo2 = __shfl_xor(l, off, kWave);
+    const float mn = fmaxf(m, mo);
+    const float a = (m == -INFINITY) ? 0.f : exp2f(m - mn);
+    const float c = (mo == -INFINITY) ? 0.f : exp2f(mo - mn);
+    l = l * a + lo2 * c;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      const float ao = __shfl_xor(acc[i], off, kWave);
+      acc[i] = acc[i] * a + ao * c;
+    }
+    m = mn;
+  }
+  if (grp == 0) {
+#pragma unroll
+    for (int i = 0; i < 8; ++i) red[wave][2 + sub * 8 + i] = acc[i];
+    if (sub == 0) {
+      red[wave][0] = m;
+      red[wave][1] = l;
+    }
+  }
+  __syncthreads();
+  if (wave == 0) {
+    float M = red[0][0];
+#pragma unroll
+    for (int w = 1; w < 4; ++w) M = fmaxf(M, red[w][0]);
+    float L = 0.f, O = 0.f;
+#pragma unroll
+    for (int w = 0; w < 4; ++w) {
+      const float mw = red[w][0];
+      const float sc = (mw == -INFINITY) ? 0.f : exp2f(mw - M);
+      L += red[w][1] * sc;
+      O += red[w][2 + lane] * sc;
+    }
+    if (n_split == 1) {
+      const float o = L > 0.f ? O / L : 0.f;
+      out[static_cast<int64_t>(bh) * kHeadDim + lane] = static_cast<uint16_t>(f2bf(o));
+    } else {
+      float* p = ws + (static_cast<int64_t>(bh) * n_split + split) * kPart;
+      if (lane == 0) {
+        p[0] = M;
+        p[1] = L;
+      }
+      p[2 + lane] = O;
+    }
+  }
+}
+
+// Merge the per-split partial states of one (b, h): lane = channel.
+__global__ __launch_bounds__(256) void attn_decode_combine_kernel(const float* __restrict__ ws,
+                                                                  int n_bh, int n_split,
+                                                                  uint16_t* __restrict__ out) {
+  const int bh = blockIdx.x * 4 + (threadIdx.x >> 6);
+  const int lane = threadIdx.x & 63;
+  if (bh >= n_bh) return;
+  const float* p = ws + static_cast<int64_t>(bh) * n_split * kPart;
+  float M = -INFINITY;
+  for (int s = 0; s < n_split; ++s) M = fmaxf(M, p[s * kPart]);
+  float L = 0.f, O = 0.f;
+  for (int s = 0; s < n_split; ++s) {
+    const float ms = p[s * kPart];
+    const float sc = (ms == -INFINITY) ? 0.f : exp2f(ms - M);
+    L += p[s * kPart + 1] * sc;
+    O += p[s * kPart + 2 + lane] * sc;
+  }
+  const float o = L > 0.f ? O / L : 0.f;
+  out[static_cast<int64_t>(bh) * kHeadDim + lane] = static_cast<uint16_t>(f2bf(o));
+}
+
+constexpr int kUnroll = 4;
+constexpr int kSlotsPerIter = 4 * 8 * kUnroll;   // slots a block consumes per loop trip
+
+static int n_splits(int cache_slots, int split_len) {
+  return (cache_slots + split_len - 1) / split_len;
+}
+
+}  // namespace mdl
+
+using namespace mdl;
+
+extern "C" int64_t mdl_attn_decode_workspace_bytes(int batch, int n_heads, int cache_slots,
+                                                   int split_len) {
+  if (batch <= 0 || n_heads <= 0 || cache_slots <= 0 || split_len <= 0) return 0;
+  const int ns = n_splits(cache_slots, split_len);
+  if (ns <= 1) return 0;
+  return static_cast<int64_t>(batch) * n_heads * ns * kPart * static_cast<int64_t>(sizeof(float));
+}
+
+extern "C" int mdl_attn_decode(const uint16_t* q, const uint16_t* k_cache,
+                               const uint16_t* v_cache, int batch, int n_heads, int head_dim,
+                               int cache_slots, const uint8_t* prompt_mask, int prompt_len,
+                               const int32_t* kv_start, int seq_pos, const int32_t* seq_dev,
+                               float* workspace, int64_t workspace_bytes, int split_len,
+                               uint16_t* out, void* stream) {
+  if (!q || !k_cache || !v_cache || !out) return MDL_ERR_NULL;
+  if (head_dim != kHeadDim) return MDL_ERR_HEAD_DIM;
+  if (batch < 0 || n_heads <= 0 || cache_slots <= 0 || prompt_len < 0 ||
+      (prompt_mask && prompt_len == 0) || split_len < kSlotsPerIter ||
+      split_len % kSlotsPerIter != 0)
+    return MDL_ERR_SHAPE;
+  if (!seq_dev && (seq_pos < 0 || seq_pos >= cache_slots)) return MDL_ERR_CACHE;
+  if (!aligned16(q) || !aligned16(k_cache) || !aligned16(v_cache) || !aligned4(out))
+    return MDL_ERR_ALIGN;
+  if (batch == 0) return MDL_OK;
+  const int ns = n_splits(cache_slots, split_len);
+  const int64_t need = mdl_attn_decode_workspace_bytes(batch, n_heads, cache_slots, split_len);
+  if (need > 0 && (!workspace || workspace_bytes < need)) return MDL_ERR_WORKSPACE;
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  const int n_bh = batch * n_heads;
+  attn_decode_kernel<kUnroll><<<dim3(n_bh, ns), 256, 0, s>>>(
+      q, k_cache, v_cache, n_heads, cache_slots, prompt_mask, prompt_len, kv_start, seq_pos,
+      seq_dev, ns, split_len, workspace, out);
+  if (ns > 1)
+    attn_decode_combine_kernel<<<dim3((n_bh + 3) / 4), 256, 0, s>>>(workspace, n_bh, ns, out);
+  return launch_status();
+}

@@ -1,0 +1,67 @@
+// Shared device helpers for the mdlarc HIP kernels (gfx950 / CDNA4, wave64).
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include "../../include/mdlarc_hip.h"
+
+namespace mdl {
+
+constexpr int kWave = 64;
+constexpr int kHeadDim = 64;
+
+// ---- bf16 <-> f32 (bf16 stored as raw 16-bit words) ------------------------------------------
+__device__ __forceinline__ float bf2f(uint32_t h16) { return __uint_as_float(h16 << 16); }
+
+// Round-to-nearest-even, NaN kept quiet (same rounding torch uses for .to(bfloat16)).
+__device__ __forceinline__ uint32_t f2bf(float f) {
+  uint32_t u = __float_as_uint(f);
+  if ((u & 0x7fffffffu) > 0x7f800000u) return (u >> 16) | 0x40u;
+  u += 0x7fffu + ((u >> 16) & 1u);
+  return u >> 16;
+}
+
+__device__ __forceinline__ uint32_t pack_bf2(float lo, float hi) {
+  return f2bf(lo) | (f2bf(hi) << 16);
+}
+
+// 8 bf16 held in a uint4 -> 8 floats
+__device__ __forceinline__ void unpack8(const uint4 v, float* f) {
+  f[0] = bf2f(v.x & 0xffffu); f[1] = bf2f(v.x >> 16);
+  f[2] = bf2f(v.y & 0xffffu); f[3] = bf2f(v.y >> 16);
+  f[4] = bf2f(v.z & 0xffffu); f[5] = bf2f(v.z >> 16);
+  f[6] = bf2f(v.w & 0xffffu); f[7] = bf2f(v.w >> 16);
+}
+
+__device__ __forceinline__ uint4 pack8(const float* f) {
+  uint4 v;
+  v.x = pack_bf2(f[0], f[1]); v.y = pack_bf2(f[2], f[3]);
+  v.z = pack_bf2(f[4], f[5]); v.w = pack_bf2(f[6], f[7]);
+  return v;
+}
+
+// ---- wave64 reductions -----------------------------------------------------------------------
+__device__ __forceinline__ float wave_sum(float v) {
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, kWave);
+  return v;
+}
+
+__device__ __forceinline__ float wave_max(float v) {
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o, kWave));
+  return v;
+}
+
+// ---- host-side launch checking ---------------------------------------------------------------
+inline int launch_status() {
+  hipError_t e = hipGetLastError();
+  return e == hipSuccess ? MDL_OK : static_cast<int>(e);
+}
+
+inline bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
+inline bool aligned8(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 7u) == 0; }
+inline bool aligned4(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 3u) == 0; }
+
+}  // namespace mdl

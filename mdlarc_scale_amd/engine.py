@@ -1,0 +1,207 @@
+"""HIP execution engine of the TinyTransformer inference path.
+
+Dataflow per layer (M token rows, d channels, F ffn width; fp32 residual stream x):
+
+    xg = bf16(x * g1), rstd          <- K1 (layer 0) or add_rmsnorm (previous layer)
+    qkv = xg @ W_qkv^T               (hipBLASLt via torch.mm)                   [M, 3d] bf16
+    K2: q = rope(rstd*q)/8 -> [M, d]; k, v = rope(rstd*k), rstd*v -> cache slots
+    attn = K4(q, cache)              (prefill: MFMA flash; decode: split-K)      [M, d] bf16
+    delta = attn @ W_out^T                                                      [M, d] bf16
+    x += delta; xg = bf16(x * g2), rstd                            <- add_rmsnorm
+    gu = xg @ [W_gate; W_up]^T                                                  [M, 2F] bf16
+    h = silu(rstd*g + b_g) * (rstd*u + b_u)                         <- K3
+    delta = h @ W_down^T
+    x += delta + b_down; xg = bf16(x * g1_next), rstd               <- add_rmsnorm
+  final: logits = lm_head(ln_f(x)) and greedy argmax                <- lm_head kernel
+
+Weights are packed once per model version (bf16 GEMM operands, fp32 gains/biases/head); the
+embedding tables are read live from the module parameters, because test-time adaptation edits
+``example_embed.weight.data`` between calls.
+"""
+
+from __future__ import annotations
+
+from dataclasses import dataclass
+
+import torch
+
+from . import kernels as K
+from .transformer import TinyTransformer, softmax_scale
+
+START, NEWLINE, IO_SEP, END = 10, 11, 12, 13
+GRID_MAX_X, GRID_MAX_Y = 30, 29     # GridStateUpdater defaults (src/inference.py:107)
+
+
+class PackedWeights:
+    """Device copies of the weights in the layout the kernels and GEMMs consume."""
+
+    def __init__(self, model: TinyTransformer, device: torch.device):
+        cfg = model.config
+        bf = lambda t: t.detach().to(device=device, dtype=torch.bfloat16).contiguous()  # noqa: E731
+        f32 = lambda t: t.detach().to(device=device, dtype=torch.float32).contiguous()  # noqa: E731
+        self.qkv, self.out, self.gu, self.down = [], [], [], []
+        self.ln1, self.ln2, self.b_gate, self.b_up, self.b_down = [], [], [], [], []
+        for blk in model.blocks:
+            self.qkv.append(bf(blk.attn.qkv_proj.weight))
+            self.out.append(bf(blk.attn.out_proj.weight))
+            self.gu.append(torch.cat([bf(blk.ffn.fc_gate.weight), bf(blk.ffn.fc_up.weight)], 0))
+            self.down.append(bf(blk.ffn.fc_down.weight))
+            self.ln1.append(f32(blk.ln1.weight))
+            self.ln2.append(f32(blk.ln2.weight))
+            self.b_gate.append(f32(blk.ffn.fc_gate.bias))
+            self.b_up.append(f32(blk.ffn.fc_up.bias))
+            self.b_down.append(f32(blk.ffn.fc_down.bias))
+        self.ln_f = f32(model.ln_f.weight)
+        self.head = f32(model.lm_head.weight)
+        rope = model.blocks[0].attn.rope
+        self.rope_tab = rope.device_table(device)
+        self.rope_geom = (rope.max_x, rope.max_y, rope.max_z, rope.px, rope.py, rope.pz)
+        self.eps = cfg.norm_eps
+
+
+@dataclass
+class Scratch:
+    """Activation buffers for M rows (reused across layers)."""
+
+    x: torch.Tensor
+    xg: torch.Tensor
+    rstd: torch.Tensor
+    qkv: torch.Tensor
+    q: torch.Tensor
+    attn: torch.Tensor
+    delta: torch.Tensor
+    gu: torch.Tensor
+    h: torch.Tensor
+
+    @staticmethod
+    def alloc(rows: int, d: int, d_ff: int, device: torch.device) -> "Scratch":
+        e = lambda *s, dt=torch.bfloat16: torch.empty(*s, dtype=dt, device=device)  # noqa: E731
+        return Scratch(x=e(rows, d, dt=torch.float32), xg=e(rows, d),
+                       rstd=e(rows, dt=torch.float32), qkv=e(rows, 3 * d), q=e(rows, d),
+                       attn=e(rows, d), delta=e(rows, d), gu=e(rows, 2 * d_ff), h=e(rows, d_ff))
+
+
+def choose_split_len(n_bh: int, slots: int) -> int:
+    """Slots per decode-attention work item: aim for >= 8192 items, multiples of 128."""
+    n_split = max(1, -(-8192 // max(n_bh, 1)))
+    per = -(-slots // n_split)
+    return max(256, -(-per // 128) * 128)
+
+
+class HipEngine:
+    def __init__(self, model: TinyTransformer):
+        self.model = model
+        self._packed: PackedWeights | None = None
+        self._sig: tuple | None = None
+
+    def invalidate(self) -> None:
+        self._packed, self._sig = None, None
+
+    def _signature(self) -> tuple:
+        return tuple((p.data_ptr(), p._version, p.dtype, p.device)
+                     for n, p in self.model.named_parameters()
+                     if not n.startswith(("token_embed", "example_embed")))
+
+    def packed(self, device: torch.device) -> PackedWeights:
+        sig = self._signature()
+        if self._packed is None or sig != self._sig:
+            with torch.no_grad():
+                self._packed = PackedWeights(self.model, device)
+            self._sig = sig
+        return self._packed
+
+    # -- helpers -------------------------------------------------------------------------------
+    @property
+    def cfg(self):
+        return self.model.config
+
+    def _tables(self):
+        m = self.model
+        return m.token_embed.weight.detach(), m.example_embed.weight.detach()
+
+    @staticmethod
+    def _check_device(t: torch.Tensor) -> torch.device:
+        if not t.is_cuda:
+            raise RuntimeError("mdlarc_scale_amd runs the inference path on a ROCm GPU; move the "
+                               f"model and inputs to a GPU device (got {t.device})")
+        return t.device
+
+    def _validate_ids(self, ids: torch.Tensor, ex: torch.Tensor | None) -> None:
+        if ids.numel() and (int(ids.min()) < 0 or int(ids.max()) >= self.cfg.vocab_size):
+            raise IndexError("input_ids out of range of the token embedding")
+        if ex is not None and ex.numel() and (int(ex.min()) < 0 or
+                                              int(ex.max()) >= self.cfg.num_examples):
+            raise IndexError("example_ids out of range of the example embedding")
+
+    # -- full-sequence layers (prefill / forward) ------------------------------------------------
+    def run_prompt(self, W: PackedWeights, ids: torch.Tensor, pos: torch.Tensor,
+                   ex_ids: torch.Tensor | None, key_mask: torch.Tensor | None,
+                   kv_start: torch.Tensor | None, causal: bool, kv_layers,
+                   sc: Scratch) -> None:
+        """Run every layer over [B, S] tokens; leaves the final residual in ``sc.x``.
+        ``kv_layers(li)`` returns the (k, v) [B, H, slots, 64] views to write slots [0, S)."""
+        cfg = self.cfg
+        B, S = ids.shape
+        H, d = cfg.n_heads, cfg.d_model
+        tok, ex = self._tables()
+        use_ex = ex_ids if (ex_ids is not None and cfg.use_example_embedding) else None
+        K.embed_rmsnorm(ids.reshape(-1), use_ex, tok, ex if use_ex is not None else None, S,
+                        W.ln1[0], W.eps, sc.x, sc.xg, sc.rstd)
+        qs = softmax_scale(d // H)
+        for li in range(cfg.n_layers):
+            kc, vc = kv_layers(li)
+            torch.mm(sc.xg, W.qkv[li].t(), out=sc.qkv)
+            K.qkv_rope_cache(sc.qkv, sc.rstd, pos, W.rope_tab, W.rope_geom, B, S, H, qs, sc.q,
+                             kc, vc, slot0=0)
+            K.attn_prefill(sc.q, kc, vc, B, S, H, key_mask, kv_start, causal, sc.attn)
+            self._mlp(W, li, sc)
+
+    def _mlp(self, W: PackedWeights, li: int, sc: Scratch) -> None:
+        """out_proj + residual, ln2, SwiGLU MLP + residual, next norm (shared by both phases)."""
+        cfg = self.cfg
+        torch.mm(sc.attn, W.out[li].t(), out=sc.delta)
+        K.add_rmsnorm(sc.x, sc.delta, None, W.ln2[li], W.eps, sc.xg, sc.rstd)
+        torch.mm(sc.xg, W.gu[li].t(), out=sc.gu)
+        K.swiglu(sc.gu, sc.rstd, W.b_gate[li], W.b_up[li], sc.h)
+        torch.mm(sc.h, W.down[li].t(), out=sc.delta)
+        last = li + 1 == cfg.n_layers
+        K.add_rmsnorm(sc.x, sc.delta, W.b_down[li], W.ln_f if last else W.ln1[li + 1], W.eps,
+                      None if last else sc.xg, sc.rstd)
+
+    @torch.no_grad()
+    def forward(self, ids: torch.Tensor, pos: torch.Tensor, ex_ids: torch.Tensor | None,
+                attention_mask: torch.Tensor | None, is_causal: bool) -> torch.Tensor:
+        """``TinyTransformer.forward`` on the HIP path: logits [B, S, V] in the model dtype."""
+        return self.forward_f32(ids, pos, ex_ids, attention_mask, is_causal).to(
+            self.model.lm_head.weight.dtype)
+
+    @torch.no_grad()
+    def forward_f32(self, ids, pos, ex_ids=None, attention_mask=None, is_causal=True):
+        dev = self._check_device(ids)
+        cfg = self.cfg
+        B, S = ids.shape
+        ids = ids.to(torch.int64).contiguous()
+        pos = pos.to(device=dev, dtype=torch.int64).contiguous()
+        if ex_ids is not None:
+            ex_ids = ex_ids.to(device=dev, dtype=torch.int64).contiguous()
+        self._validate_ids(ids, ex_ids)
+        W = self.packed(dev)
+        mask = None
+        if attention_mask is not None:
+            mask = attention_mask.to(device=dev, dtype=torch.bool).to(torch.uint8).contiguous()
+        H = cfg.n_heads
+        kbuf = torch.empty(B, H, S, 64, dtype=torch.bfloat16, device=dev)
+        vbuf = torch.empty_like(kbuf)
+        sc = Scratch.alloc(B * S, cfg.d_model, cfg.d_ff, dev)
+        self.run_prompt(W, ids, pos, ex_ids, mask, None, is_causal, lambda li: (kbuf, vbuf), sc)
+        logits = torch.empty(B * S, cfg.vocab_size, dtype=torch.float32, device=dev)
+        K.lm_head(sc.x, None, B * S, W.ln_f, W.eps, W.head, logits, None)
+        return logits.view(B, S, cfg.vocab_size)
+
+
+def engine_for(model: TinyTransformer) -> HipEngine:
+    eng = getattr(model, "_hip_engine", None)
+    if eng is None or eng.model is not model:
+        eng = HipEngine(model)
+        object.__setattr__(model, "_hip_engine", eng)
+    return eng

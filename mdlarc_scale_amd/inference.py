@@ -1,0 +1,561 @@
+"""Batched static-KV-cache generation -- drop-in for src/inference.py of
+shyampathak22/mdlARC_scale.
+
+``generate_output`` keeps the reference's signature and token-for-token semantics
+(src/inference.py:487-628), including its quirks:
+  * the first token and the initial grid state come from index ``lengths-1`` of each row even
+    when the batch is left-padded (src/inference.py:185-191, :420-424);
+  * rows that emitted END keep generating; the loop stops before a step once every row has
+    emitted END (:589-595, :622-623);
+  * the total length is capped at ``max_seq_len`` and an over-long prompt comes back unchanged.
+
+The greedy loop keeps all state on the GPU: each decode step is a fixed launch sequence (grid
+step -> embedding -> layers -> head/argmax -> commit) with the cache slot and output column in a
+device counter, and the host reads the per-row END step only every ``SYNC_EVERY`` steps, then
+trims the output to where the reference would have stopped.
+"""
+
+from __future__ import annotations
+
+from dataclasses import dataclass
+
+import numpy as np
+import torch
+import torch.nn.functional as F
+
+from . import kernels as K
+from .data import (
+    DIHEDRAL_TRANSFORMS,
+    END_TOKEN_ID,
+    IO_SEP_TOKEN_ID,
+    NEWLINE_TOKEN_ID,
+    START_TOKEN_ID,
+    apply_color_perm_grid,
+    compute_positions_3d,
+    decode_output_grid,
+    encode_example,
+    generate_color_permutations,
+)
+from .engine import GRID_MAX_X, GRID_MAX_Y, HipEngine, PackedWeights, Scratch, choose_split_len
+from .engine import engine_for
+from .transformer import TinyTransformer, softmax_scale
+
+SYNC_EVERY = 8
+
+
+# =============================================================================================
+# decoding constraints (src/inference.py:36-43, :285-364)
+# =============================================================================================
+
+@dataclass(frozen=True)
+class DecodingConstraints:
+    palette_mask: torch.Tensor | None = None
+    target_shape: torch.Tensor | None = None
+    palette_penalty: float = 2.0
+    shape_penalty: float = 2.0
+    disallow_tokens: tuple[int, ...] = (START_TOKEN_ID, IO_SEP_TOKEN_ID)
+
+
+def _per_row(t: torch.Tensor | None, batch: int, width: int, device) -> torch.Tensor | None:
+    """[batch, width] view of a constraint tensor, broadcasting a single row; None if the
+    batch sizes are incompatible (the reference then ignores the constraint)."""
+    if t is None:
+        return None
+    t = t.to(device).reshape(-1, width)
+    if t.shape[0] == batch:
+        return t
+    return t.expand(batch, width) if t.shape[0] == 1 else None
+
+
+def apply_logit_constraints(logits: torch.Tensor, gx: torch.Tensor, gy: torch.Tensor,
+                            constraints: DecodingConstraints | None) -> torch.Tensor:
+    """Soft palette / shape penalties on logits [B, V] (src/inference.py:285-364), in place.
+    ``gx``/``gy`` are the grid state after consuming the current input token."""
+    if constraints is None:
+        return logits
+    B = logits.shape[0]
+    for tok in constraints.disallow_tokens:
+        logits[:, tok] = float("-inf")
+    pal = _per_row(constraints.palette_mask, B, 10, logits.device)
+    if pal is not None:
+        logits[:, :10] -= (~pal.bool()).to(logits.dtype) * constraints.palette_penalty
+    shape = _per_row(constraints.target_shape, B, 2, logits.device)
+    if shape is not None:
+        th, tw = shape[:, 0], shape[:, 1]
+        has = (th >= 0) & (tw >= 0)
+        x, y = gx.long(), gy.long()
+        pen = constraints.shape_penalty
+        row_full = (has & (x >= tw)).to(logits.dtype) * pen
+        row_open = (has & (x < tw)).to(logits.dtype) * pen
+        past_end = (has & (y >= th)).to(logits.dtype) * pen
+        logits[:, :10] -= (row_full + past_end)[:, None]
+        logits[:, NEWLINE_TOKEN_ID] -= row_open + past_end
+    return logits
+
+
+def _pick(logits: torch.Tensor, temperature: float, top_k: int | None) -> torch.Tensor:
+    """Greedy argmax or (top-k) multinomial sampling (src/inference.py:573-583)."""
+    if temperature <= 0:
+        return logits.argmax(-1)
+    lt = logits / max(temperature, 1e-6)
+    if top_k is not None and top_k > 0:
+        vals, idx = torch.topk(lt, min(top_k, lt.shape[-1]), dim=-1)
+        probs = torch.zeros_like(lt).scatter_(1, idx, F.softmax(vals, dim=-1))
+    else:
+        probs = F.softmax(lt, dim=-1)
+    return torch.multinomial(probs, 1).squeeze(-1)
+
+
+# =============================================================================================
+# cache and grid state (API of src/inference.py:51-221)
+# =============================================================================================
+
+class StaticKVCache:
+    """Preallocated [n_layers, 2, B, H, max_seq_len, head_dim] cache (src/inference.py:51-96).
+    The HIP path keeps it in bf16 (the attention kernels' operand type)."""
+
+    def __init__(self, batch_size: int, max_seq_len: int, n_layers: int, n_heads: int,
+                 head_dim: int, device: torch.device, dtype: torch.dtype = torch.bfloat16):
+        self.batch_size, self.max_seq_len, self.n_layers = batch_size, max_seq_len, n_layers
+        self.seq_len = 0
+        self.cache = torch.zeros(n_layers, 2, batch_size, n_heads, max_seq_len, head_dim,
+                                 device=device, dtype=dtype)
+
+    def reset(self) -> None:
+        self.cache.zero_()
+        self.seq_len = 0
+
+    def layer(self, layer_idx: int) -> tuple[torch.Tensor, torch.Tensor]:
+        return self.cache[layer_idx, 0], self.cache[layer_idx, 1]
+
+    def update(self, layer_idx: int, k: torch.Tensor, v: torch.Tensor):
+        n = k.size(2)
+        end = self.seq_len + n
+        self.cache[layer_idx, 0, :, :, self.seq_len:end] = k
+        self.cache[layer_idx, 1, :, :, self.seq_len:end] = v
+        return self.cache[layer_idx, 0, :, :, :end], self.cache[layer_idx, 1, :, :, :end]
+
+    def advance(self, n: int = 1) -> None:
+        self.seq_len += n
+
+
+class GridStateUpdater:
+    """Per-row (x, y, in_output) decode-position tracker (src/inference.py:104-168), stepped by
+    the ``mdl_grid_step`` kernel on the GPU."""
+
+    def __init__(self, batch_size: int, device: torch.device, max_x: int = GRID_MAX_X,
+                 max_y: int = GRID_MAX_Y):
+        self.device, self.max_x, self.max_y = torch.device(device), max_x, max_y
+        HipEngine._check_device(torch.empty(0, device=self.device))
+        self.gx = torch.zeros(batch_size, dtype=torch.int32, device=self.device)
+        self.gy = torch.zeros(batch_size, dtype=torch.int32, device=self.device)
+        self.gio = torch.ones(batch_size, dtype=torch.uint8, device=self.device)
+        self._pos = torch.empty(batch_size, 3, dtype=torch.int64, device=self.device)
+
+    @property
+    def x(self) -> torch.Tensor:
+        return self.gx.long()
+
+    @property
+    def y(self) -> torch.Tensor:
+        return self.gy.long()
+
+    @property
+    def in_output(self) -> torch.Tensor:
+        return self.gio.bool()
+
+    def reset(self) -> None:
+        self.gx.zero_()
+        self.gy.zero_()
+        self.gio.fill_(1)
+
+    def set_state(self, x: torch.Tensor, y: torch.Tensor, in_output: torch.Tensor) -> None:
+        self.gx.copy_(x.to(self.device).clamp(-2**31, 2**31 - 1).to(torch.int32))
+        self.gy.copy_(y.to(self.device).clamp(-2**31, 2**31 - 1).to(torch.int32))
+        self.gio.copy_(in_output.to(self.device).to(torch.uint8))
+
+    def update(self, tokens: torch.Tensor) -> torch.Tensor:
+        tok = tokens.to(self.device, torch.int64).reshape(-1).contiguous()
+        K.grid_step(tok, self.gx, self.gy, self.gio, self._pos, None, self.max_x, self.max_y)
+        return self._pos.clone()
+
+
+def _derive_initial_state_from_prompt(input_ids: torch.Tensor, positions_3d: torch.Tensor,
+                                      attention_mask: torch.Tensor | None, max_x: int,
+                                      max_y: int):
+    """Grid state after the prompt, read at index lengths-1 (src/inference.py:171-221)."""
+    B, S = input_ids.shape
+    dev = input_ids.device
+    mask = None if attention_mask is None else attention_mask.to(dev).bool().to(
+        torch.uint8).contiguous()
+    gx = torch.empty(B, dtype=torch.int32, device=dev)
+    gy = torch.empty_like(gx)
+    io = torch.empty(B, dtype=torch.uint8, device=dev)
+    K.grid_init(input_ids.to(torch.int64).contiguous(),
+                positions_3d.to(dev, torch.int64).contiguous(), mask, gx, gy, io, None, None,
+                max_x, max_y)
+    return gx.long(), gy.long(), io.bool()
+
+
+# =============================================================================================
+# generation
+# =============================================================================================
+
+@dataclass
+class DecodeState:
+    """Device-resident state of one batched generation."""
+
+    B: int
+    S: int
+    total: int
+    ex: torch.Tensor            # [B] int64 example ids
+    pmask: torch.Tensor         # [B, S] uint8 prompt mask
+    kv_start: torch.Tensor      # [B] int32 first valid prompt slot
+    last_row: torch.Tensor      # [B] int32 prefill row the first token is read from
+    gx: torch.Tensor
+    gy: torch.Tensor
+    gio: torch.Tensor
+    pos: torch.Tensor           # [B, 3] int64 position of the current input token
+    tok: torch.Tensor           # [B] int64 current token
+    counters: torch.Tensor      # int32 [2]: cache slot of the current token, output column
+    out_ids: torch.Tensor       # [B, total] int64
+    finish: torch.Tensor        # [B] int32 first generated index of END, -1 if none
+    logits: torch.Tensor        # [B, V] fp32
+    cache: StaticKVCache
+    sc: Scratch
+    ws: torch.Tensor | None
+    split_len: int
+
+
+class Generator:
+    """Prefill + decode loop of ``generate_output`` on the HIP kernels."""
+
+    def __init__(self, model: TinyTransformer):
+        self.model = model
+        self.eng = engine_for(model)
+
+    def prepare(self, input_ids, positions_3d, example_ids, prompt_mask, total) -> DecodeState:
+        cfg = self.model.config
+        dev = input_ids.device
+        B, S = input_ids.shape
+        H, hd = cfg.n_heads, cfg.d_model // cfg.n_heads
+        cache = StaticKVCache(B, total, cfg.n_layers, H, hd, dev)
+        pmask = prompt_mask.to(torch.uint8).contiguous()
+        i32 = lambda: torch.empty(B, dtype=torch.int32, device=dev)  # noqa: E731
+        gx, gy, kv_start, last_row = i32(), i32(), i32(), i32()
+        gio = torch.empty(B, dtype=torch.uint8, device=dev)
+        K.grid_init(input_ids, positions_3d, pmask, gx, gy, gio, kv_start, last_row)
+        split = choose_split_len(B * H, total)
+        nbytes = K.attn_decode_workspace_bytes(B, H, total, split)
+        ws = torch.empty(max(nbytes // 4, 1), dtype=torch.float32, device=dev) if nbytes else None
+        out_ids = torch.empty(B, total, dtype=torch.int64, device=dev)
+        out_ids[:, :S] = input_ids
+        return DecodeState(
+            B=B, S=S, total=total, ex=example_ids, pmask=pmask, kv_start=kv_start,
+            last_row=last_row, gx=gx, gy=gy, gio=gio,
+            pos=torch.empty(B, 3, dtype=torch.int64, device=dev),
+            tok=torch.empty(B, dtype=torch.int64, device=dev),
+            counters=torch.tensor([S - 1, S], dtype=torch.int32, device=dev),
+            out_ids=out_ids, finish=torch.full((B,), -1, dtype=torch.int32, device=dev),
+            logits=torch.empty(B, cfg.vocab_size, dtype=torch.float32, device=dev),
+            cache=cache, sc=Scratch.alloc(B, cfg.d_model, cfg.d_ff, dev), ws=ws,
+            split_len=split)
+
+    def prefill(self, st: DecodeState, W: PackedWeights, input_ids, positions_3d) -> None:
+        """``_prefill`` (src/inference.py:383-424): all layers over the prompt, K/V into slots
+        [0, S), logits of row lengths-1 into ``st.logits`` and its argmax into ``st.tok``."""
+        cfg = self.model.config
+        sc = Scratch.alloc(st.B * st.S, cfg.d_model, cfg.d_ff, input_ids.device)
+        self.eng.run_prompt(W, input_ids, positions_3d, st.ex, st.pmask, st.kv_start, True,
+                            st.cache.layer, sc)
+        K.lm_head(sc.x, st.last_row, st.B, W.ln_f, W.eps, W.head, st.logits, st.tok)
+        st.cache.advance(st.S)
+
+    def decode_layers(self, st: DecodeState, W: PackedWeights, want_logits: bool) -> None:
+        """``_decode_step`` (src/inference.py:427-459) for the token in ``st.tok`` at the
+        position in ``st.pos``; K/V go to slot counters[0]; greedy token back into ``st.tok``."""
+        cfg = self.model.config
+        sc, B = st.sc, st.B
+        H = cfg.n_heads
+        tok_tab, ex_tab = self.eng._tables()
+        use_ex = st.ex if cfg.use_example_embedding else None
+        K.embed_rmsnorm(st.tok, use_ex, tok_tab, ex_tab if use_ex is not None else None, 1,
+                        W.ln1[0], W.eps, sc.x, sc.xg, sc.rstd)
+        qs = softmax_scale(cfg.d_model // H)
+        slot = st.counters[0:1]
+        for li in range(cfg.n_layers):
+            kc, vc = st.cache.layer(li)
+            torch.mm(sc.xg, W.qkv[li].t(), out=sc.qkv)
+            K.qkv_rope_cache(sc.qkv, sc.rstd, st.pos, W.rope_tab, W.rope_geom, B, 1, H, qs,
+                             sc.q, kc, vc, slot_dev=slot)
+            K.attn_decode(sc.q, kc, vc, B, H, st.pmask, st.S, st.kv_start, 0, slot, st.ws,
+                          st.split_len, sc.attn)
+            self.eng._mlp(W, li, sc)
+        K.lm_head(sc.x, None, B, W.ln_f, W.eps, W.head, st.logits if want_logits else None,
+                  st.tok)
+
+    def greedy_step(self, st: DecodeState, W: PackedWeights, stop_on_end: bool) -> None:
+        """One full device-side decode step of greedy generation."""
+        K.grid_step(st.tok, st.gx, st.gy, st.gio, st.pos, st.counters)
+        self.decode_layers(st, W, want_logits=False)
+        K.decode_commit(st.tok, st.out_ids, 0, st.counters, st.finish if stop_on_end else None,
+                        st.S, END_TOKEN_ID)
+
+
+def generate_output(model: TinyTransformer, input_ids: torch.Tensor, positions_3d: torch.Tensor,
+                    example_ids: torch.Tensor | None = None,
+                    attention_mask: torch.Tensor | None = None, max_new_tokens: int = 900,
+                    temperature: float = 0.0, top_k: int | None = None, stop_on_end: bool = True,
+                    use_compile: bool = False,
+                    constraints: DecodingConstraints | None = None) -> torch.Tensor:
+    """Autoregressive generation with a static KV cache; returns [B, S + generated] int64
+    (src/inference.py:487-628).  ``use_compile`` is accepted for API compatibility; the HIP
+    path needs no compiler."""
+    del use_compile
+    model.eval()
+    eng = engine_for(model)
+    dev = eng._check_device(input_ids)
+    cfg = model.config
+    B, S = input_ids.shape
+    ids = input_ids.to(torch.int64).contiguous()
+    pos = positions_3d.to(device=dev, dtype=torch.int64).contiguous()
+    ex = (torch.zeros(B, dtype=torch.int64, device=dev) if example_ids is None
+          else example_ids.to(device=dev, dtype=torch.int64).contiguous())
+    if attention_mask is None:
+        prompt_mask = torch.ones(B, S, dtype=torch.bool, device=dev)
+    else:
+        if tuple(attention_mask.shape) != (B, S):
+            raise ValueError("attention_mask must have shape [batch, seq_len]")
+        prompt_mask = attention_mask.to(device=dev, dtype=torch.bool)
+    total = min(S + max_new_tokens, cfg.max_seq_len)
+    max_new = total - S
+    if max_new <= 0:
+        return input_ids
+    eng._validate_ids(ids, ex)
+    gen = Generator(model)
+    with torch.no_grad():
+        W = eng.packed(dev)
+        st = gen.prepare(ids, pos, ex, prompt_mask, total)
+        gen.prefill(st, W, ids, pos)
+        eager = temperature > 0 or constraints is not None
+        if eager:
+            apply_logit_constraints(st.logits, st.gx, st.gy, constraints)
+            st.tok.copy_(_pick(st.logits, temperature, top_k))
+        K.decode_commit(st.tok, st.out_ids, S, None, st.finish if stop_on_end else None, S,
+                        END_TOKEN_ID)
+        produced = 1
+        for step in range(1, max_new):
+            if stop_on_end and (eager or step % SYNC_EVERY == 0) and bool((st.finish >= 0).all()):
+                break
+            if eager:
+                K.grid_step(st.tok, st.gx, st.gy, st.gio, st.pos, st.counters)
+                gen.decode_layers(st, W, want_logits=True)
+                apply_logit_constraints(st.logits, st.gx, st.gy, constraints)
+                st.tok.copy_(_pick(st.logits, temperature, top_k))
+                K.decode_commit(st.tok, st.out_ids, 0, st.counters,
+                                st.finish if stop_on_end else None, S, END_TOKEN_ID)
+            else:
+                gen.greedy_step(st, W, stop_on_end)
+            produced += 1
+        g = produced
+        if stop_on_end:
+            fin = st.finish.cpu()
+            if bool((fin >= 0).all()):
+                g = min(g, int(fin.max()) + 1)
+    return st.out_ids[:, :S + g]
+
+
+# =============================================================================================
+# task-level helpers (src/inference.py:631-1008)
+# =============================================================================================
+
+def predict_grid(model: TinyTransformer, input_grids, output_grids, test_input, device,
+                 example_id: int = 0, max_output_tokens: int = 900, temperature: float = 0.0,
+                 top_k: int | None = None, use_compile: bool = False,
+                 constraints: DecodingConstraints | None = None):
+    """One prompt -> predicted output grid or None (src/inference.py:631-694)."""
+    model.eval()
+    toks: list[int] = []
+    for inp, out in zip(input_grids, output_grids, strict=True):
+        toks += encode_example(inp, out)
+    toks += encode_example(test_input, None)
+    ids = torch.tensor([toks], dtype=torch.long, device=device)
+    pos = torch.from_numpy(compute_positions_3d(toks))[None].to(device)
+    ex = torch.tensor([example_id], dtype=torch.long, device=device)
+    with torch.no_grad():
+        out_ids = generate_output(model, ids, pos, ex, max_new_tokens=max_output_tokens,
+                                  temperature=temperature, top_k=top_k, stop_on_end=True,
+                                  constraints=constraints)
+    seq = out_ids[0].cpu().tolist()
+    seps = [i for i, t in enumerate(seq) if t == IO_SEP_TOKEN_ID]
+    return decode_output_grid(seq[seps[-1]:]) if seps else None
+
+
+def _grid_shape(grid) -> tuple[int, int] | None:
+    if not grid or not grid[0]:
+        return None
+    w = len(grid[0])
+    return (len(grid), w) if all(len(r) == w for r in grid) else None
+
+
+def _infer_output_shape(task: dict) -> tuple[int, int] | None:
+    shapes = [_grid_shape(p.get("output")) for p in task.get("train", [])]
+    if not shapes or any(s is None for s in shapes) or len(set(shapes)) != 1:
+        return None
+    return shapes[0]
+
+
+def _collect_palette(task: dict, test_idx: int, include_test_input: bool = False) -> set[int]:
+    cols: set[int] = set()
+    grids = [p.get(k) for p in task.get("train", []) for k in ("input", "output")]
+    if include_test_input and task.get("test"):
+        grids.append(task["test"][test_idx]["input"])
+    for g in grids:
+        for row in g or []:
+            cols.update(int(v) for v in row)
+    return cols
+
+
+def _transform_shape(shape, dihedral_idx: int):
+    if shape is None:
+        return None
+    return (shape[1], shape[0]) if dihedral_idx in (1, 3, 6, 7) else shape
+
+
+@dataclass
+class _Variant:
+    tokens: list[int]
+    dihedral: int
+    perm: tuple[int, ...] | None
+    palette: set[int] | None
+    shape: tuple[int, int] | None
+
+
+def _build_variants(task, test_idx, use_train_examples, num_color_perms, num_samples,
+                    constrain, base_palette, base_shape) -> list[_Variant]:
+    """Every dihedral x colour-permutation prompt, in the reference's order
+    (src/inference.py:794-827)."""
+    pairs = task["train"] if use_train_examples else []
+    test_in = task["test"][test_idx]["input"]
+    perms = generate_color_permutations(num_color_perms, seed=42)
+    out: list[_Variant] = []
+    for di, fn in enumerate(DIHEDRAL_TRANSFORMS):
+        ins = [fn(p["input"]) for p in pairs]
+        outs = [fn(p["output"]) for p in pairs]
+        tin = fn(test_in)
+        shape = _transform_shape(base_shape, di) if constrain else None
+        for pi in range(num_color_perms):
+            perm = perms[pi]
+            palette = None
+            if base_palette is not None:
+                palette = {int(perm[c]) for c in base_palette} if pi > 0 else base_palette
+            if pi > 0:
+                ins_p = [apply_color_perm_grid(g, perm) for g in ins]
+                outs_p = [apply_color_perm_grid(g, perm) for g in outs]
+                tin_p = apply_color_perm_grid(tin, perm)
+            else:
+                ins_p, outs_p, tin_p = ins, outs, tin
+            toks: list[int] = []
+            for a, b in zip(ins_p, outs_p, strict=True):
+                toks += encode_example(a, b)
+            toks += encode_example(tin_p, None)
+            ptuple = tuple(int(v) for v in perm) if pi > 0 else None
+            out += [_Variant(toks, di, ptuple, palette, shape) for _ in range(num_samples)]
+    return out
+
+
+def left_pad_batch(prompts: list[list[int]], device) -> tuple[torch.Tensor, ...]:
+    """Left-pad with END / position (0,0,0) and build the bool mask (src/inference.py:877-890)."""
+    n = max(len(p) for p in prompts)
+    B = len(prompts)
+    ids = np.full((B, n), END_TOKEN_ID, dtype=np.int64)
+    pos = np.zeros((B, n, 3), dtype=np.int64)
+    mask = np.zeros((B, n), dtype=bool)
+    for i, p in enumerate(prompts):
+        k = len(p)
+        ids[i, n - k:] = p
+        pos[i, n - k:] = compute_positions_3d(p)
+        mask[i, n - k:] = True
+    to = lambda a: torch.from_numpy(a).to(device)  # noqa: E731
+    return to(ids), to(pos), to(mask)
+
+
+def predict_with_augmentations(model: TinyTransformer, task: dict, test_idx: int, device,
+                               example_id: int = 0, use_train_examples: bool = True,
+                               num_color_perms: int = 8, max_output_tokens: int = 900,
+                               num_samples: int = 1, sample_temperature: float = 0.0,
+                               sample_top_k: int | None = None, constrain_decoding: bool = False,
+                               palette_penalty: float = 2.0, shape_penalty: float = 2.0,
+                               batched: bool = True, use_compile: bool = False,
+                               max_batch_size: int = 16):
+    """All dihedral x colour-permutation predictions for AAIVR voting
+    (src/inference.py:697-920): list of (grid | None, dihedral_idx, perm_tuple | None).
+
+    ``batched`` runs the prompts in left-padded chunks of ``max_batch_size`` (the reference's
+    16, which also fixes each chunk's padding and hence its ``lengths-1`` rows); otherwise one
+    prompt at a time."""
+    del use_compile
+    model.eval()
+    num_samples = max(1, num_samples)
+    base_palette = _collect_palette(task, test_idx) if constrain_decoding else None
+    base_shape = _infer_output_shape(task) if constrain_decoding else None
+    variants = _build_variants(task, test_idx, use_train_examples, num_color_perms, num_samples,
+                               constrain_decoding, base_palette, base_shape)
+    chunk = max_batch_size if batched else 1
+    preds = []
+    for c0 in range(0, len(variants), chunk):
+        part = variants[c0:c0 + chunk]
+        constraints = None
+        if constrain_decoding:
+            constraints = _chunk_constraints(part, device, palette_penalty, shape_penalty,
+                                             batched)
+        if batched:
+            ids, pos, mask = left_pad_batch([v.tokens for v in part], device)
+        else:
+            ids, pos, mask = left_pad_batch([part[0].tokens], device)
+            mask = None
+        ex = torch.full((len(part),), example_id, dtype=torch.long, device=device)
+        with torch.no_grad():
+            out_ids = generate_output(model, ids, pos, ex, attention_mask=mask,
+                                      max_new_tokens=max_output_tokens,
+                                      temperature=sample_temperature, top_k=sample_top_k,
+                                      stop_on_end=True, constraints=constraints)
+        rows = out_ids.cpu().tolist()
+        for v, seq in zip(part, rows):
+            seps = [j for j, t in enumerate(seq) if t == IO_SEP_TOKEN_ID]
+            grid = decode_output_grid(seq[seps[-1]:]) if seps else None
+            preds.append((grid, v.dihedral, v.perm))
+    return preds
+
+
+def _chunk_constraints(part: list[_Variant], device, palette_penalty, shape_penalty,
+                       batched: bool) -> DecodingConstraints:
+    """Per-row palette / target-shape tensors of one chunk (src/inference.py:842-875 batched,
+    :973-992 sequential)."""
+    n = len(part)
+    pal = None
+    if batched:
+        m = torch.ones(n, 10, dtype=torch.bool)
+        any_pal = False
+        for i, v in enumerate(part):
+            if v.palette:
+                any_pal = True
+                m[i] = False
+                for c in v.palette:
+                    if 0 <= c < 10:
+                        m[i, c] = True
+        pal = m.to(device) if any_pal else None
+    elif part[0].palette:
+        m = torch.zeros(1, 10, dtype=torch.bool)
+        for c in part[0].palette:
+            if 0 <= c < 10:
+                m[0, c] = True
+        pal = m.to(device)
+    shp = torch.full((n, 2), -1, dtype=torch.long)
+    any_shape = False
+    for i, v in enumerate(part):
+        if v.shape is not None:
+            any_shape = True
+            shp[i] = torch.tensor(v.shape)
+    return DecodingConstraints(palette_mask=pal, target_shape=shp.to(device) if any_shape else None,
+                               palette_penalty=palette_penalty, shape_penalty=shape_penalty)

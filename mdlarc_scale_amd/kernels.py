@@ -1,0 +1,242 @@
+"""Tensor-level wrappers of the C-ABI entry points.
+
+Each wrapper checks device, dtype, shape and contiguity of its torch tensors, then passes raw
+device pointers and the current HIP stream to the library.  Checks that need no device data run
+here, in Python, before any launch (the C side repeats the ones it can see); a failed check or a
+non-zero library status raises ``RuntimeError`` / ``ValueError``.
+"""
+
+from __future__ import annotations
+
+import ctypes
+
+import torch
+
+from . import _lib
+
+BF16, F32, I64, I32, U8 = torch.bfloat16, torch.float32, torch.int64, torch.int32, torch.uint8
+HEAD_DIM = 64
+
+
+def _p(t: torch.Tensor | None) -> ctypes.c_void_p | None:
+    return None if t is None else ctypes.c_void_p(t.data_ptr())
+
+
+def _stream() -> ctypes.c_void_p:
+    return ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
+
+
+def _need(t: torch.Tensor | None, name: str, dtype: torch.dtype, numel: int | None = None,
+          optional: bool = False) -> None:
+    if t is None:
+        if optional:
+            return
+        raise ValueError(f"{name} is required")
+    if not t.is_cuda:
+        raise ValueError(f"{name} must be a GPU tensor (got {t.device})")
+    if t.dtype != dtype:
+        raise ValueError(f"{name} must be {dtype} (got {t.dtype})")
+    if not t.is_contiguous():
+        raise ValueError(f"{name} must be contiguous")
+    if numel is not None and t.numel() < numel:
+        raise ValueError(f"{name} has {t.numel()} elements, needs {numel}")
+
+
+def table_dtype_code(t: torch.Tensor) -> int:
+    if t.dtype == F32:
+        return 0
+    if t.dtype == BF16:
+        return 1
+    raise ValueError(f"embedding tables must be float32 or bfloat16 (got {t.dtype})")
+
+
+def embed_rmsnorm(ids: torch.Tensor, example_ids: torch.Tensor | None, tok_table: torch.Tensor,
+                  ex_table: torch.Tensor | None, row_len: int, gamma: torch.Tensor, eps: float,
+                  x_out: torch.Tensor, xg_out: torch.Tensor | None,
+                  rstd_out: torch.Tensor) -> None:
+    rows = ids.numel()
+    vocab, d = tok_table.shape
+    _need(ids, "ids", I64)
+    _need(example_ids, "example_ids", I64, optional=True)
+    _need(tok_table, "tok_table", tok_table.dtype)
+    if example_ids is not None:
+        _need(ex_table, "ex_table", tok_table.dtype)
+        if ex_table.shape[1] != d:
+            raise ValueError("example table width differs from token table width")
+        if example_ids.numel() * row_len < rows:
+            raise ValueError("example_ids shorter than the number of batch rows")
+    _need(gamma, "gamma", F32, d)
+    _need(x_out, "x_out", F32, rows * d)
+    _need(xg_out, "xg_out", BF16, rows * d, optional=True)
+    _need(rstd_out, "rstd_out", F32, rows)
+    n_ex = ex_table.shape[0] if ex_table is not None else 0
+    _lib.check(_lib.lib().mdl_embed_rmsnorm(
+        _p(ids), _p(example_ids), _p(tok_table), _p(ex_table), table_dtype_code(tok_table),
+        vocab, n_ex, rows, row_len, d, _p(gamma), eps, _p(x_out), _p(xg_out), _p(rstd_out),
+        _stream()), "mdl_embed_rmsnorm")
+
+
+def add_rmsnorm(x: torch.Tensor, delta: torch.Tensor | None, bias: torch.Tensor | None,
+                gamma: torch.Tensor, eps: float, xg_out: torch.Tensor | None,
+                rstd_out: torch.Tensor) -> None:
+    rows, d = x.shape
+    _need(x, "x", F32)
+    _need(delta, "delta", BF16, rows * d, optional=True)
+    _need(bias, "bias", F32, d, optional=True)
+    _need(gamma, "gamma", F32, d)
+    _need(xg_out, "xg_out", BF16, rows * d, optional=True)
+    _need(rstd_out, "rstd_out", F32, rows)
+    _lib.check(_lib.lib().mdl_add_rmsnorm(
+        _p(x), _p(delta), _p(bias), rows, d, _p(gamma), eps, _p(xg_out), _p(rstd_out),
+        _stream()), "mdl_add_rmsnorm")
+
+
+def qkv_rope_cache(qkv: torch.Tensor, rstd: torch.Tensor | None, pos: torch.Tensor,
+                   rope_tab: torch.Tensor, rope_geom: tuple[int, int, int, int, int, int],
+                   batch: int, seq: int, n_heads: int, q_scale: float, q_out: torch.Tensor,
+                   k_cache: torch.Tensor, v_cache: torch.Tensor, slot0: int = 0,
+                   slot_dev: torch.Tensor | None = None) -> None:
+    """rope_geom = (max_x, max_y, max_z, px, py, pz); k/v_cache are one layer's
+    [batch, n_heads, slots, 64] bf16 (contiguous views of the static cache)."""
+    rows, d = batch * seq, n_heads * HEAD_DIM
+    _need(qkv, "qkv", BF16, rows * 3 * d)
+    if qkv.dim() != 2 or qkv.shape[1] != 3 * d:
+        raise ValueError(f"qkv must be [rows, {3 * d}]")
+    _need(rstd, "rstd", F32, rows, optional=True)
+    _need(pos, "pos", I64, rows * 3)
+    _need(rope_tab, "rope_tab", F32)
+    _need(q_out, "q_out", BF16, rows * d)
+    for name, c in (("k_cache", k_cache), ("v_cache", v_cache)):
+        _need(c, name, BF16)
+        if c.dim() != 4 or c.shape[0] != batch or c.shape[1] != n_heads or c.shape[3] != 64:
+            raise ValueError(f"{name} must be [batch, n_heads, slots, 64]")
+    _need(slot_dev, "slot_dev", I32, 1, optional=True)
+    slots = k_cache.shape[2]
+    mx, my, mz, px, py, pz = rope_geom
+    _lib.check(_lib.lib().mdl_qkv_rope_cache(
+        _p(qkv), qkv.shape[1], _p(rstd), _p(pos), _p(rope_tab), batch, seq, n_heads, HEAD_DIM,
+        mx, my, mz, px, py, pz, q_scale, _p(q_out), _p(k_cache), _p(v_cache), slots, slot0,
+        _p(slot_dev), _stream()), "mdl_qkv_rope_cache")
+
+
+def swiglu(gate_up: torch.Tensor, rstd: torch.Tensor | None, bias_gate: torch.Tensor | None,
+           bias_up: torch.Tensor | None, h_out: torch.Tensor) -> None:
+    rows, two_f = gate_up.shape
+    f = two_f // 2
+    _need(gate_up, "gate_up", BF16)
+    _need(rstd, "rstd", F32, rows, optional=True)
+    _need(bias_gate, "bias_gate", F32, f, optional=True)
+    _need(bias_up, "bias_up", F32, f, optional=True)
+    _need(h_out, "h_out", BF16, rows * f)
+    _lib.check(_lib.lib().mdl_swiglu(
+        _p(gate_up), two_f, _p(rstd), _p(bias_gate), _p(bias_up), rows, f, _p(h_out),
+        _stream()), "mdl_swiglu")
+
+
+def attn_prefill(q: torch.Tensor, k_cache: torch.Tensor, v_cache: torch.Tensor, batch: int,
+                 seq: int, n_heads: int, key_mask: torch.Tensor | None,
+                 kv_start: torch.Tensor | None, causal: bool, out: torch.Tensor) -> None:
+    n = batch * seq * n_heads * HEAD_DIM
+    _need(q, "q", BF16, n)
+    _need(out, "out", BF16, n)
+    for name, c in (("k_cache", k_cache), ("v_cache", v_cache)):
+        _need(c, name, BF16)
+        if c.dim() != 4 or c.shape[0] != batch or c.shape[1] != n_heads or c.shape[3] != 64:
+            raise ValueError(f"{name} must be [batch, n_heads, slots, 64]")
+    _need(key_mask, "key_mask", U8, batch * seq, optional=True)
+    _need(kv_start, "kv_start", I32, batch, optional=True)
+    _lib.check(_lib.lib().mdl_attn_prefill(
+        _p(q), _p(k_cache), _p(v_cache), batch, seq, n_heads, HEAD_DIM, k_cache.shape[2],
+        _p(key_mask), _p(kv_start), 1 if causal else 0, _p(out), _stream()),
+        "mdl_attn_prefill")
+
+
+def attn_decode_workspace_bytes(batch: int, n_heads: int, slots: int, split_len: int) -> int:
+    return int(_lib.lib().mdl_attn_decode_workspace_bytes(batch, n_heads, slots, split_len))
+
+
+def attn_decode(q: torch.Tensor, k_cache: torch.Tensor, v_cache: torch.Tensor, batch: int,
+                n_heads: int, prompt_mask: torch.Tensor | None, prompt_len: int,
+                kv_start: torch.Tensor | None, seq_pos: int, seq_dev: torch.Tensor | None,
+                workspace: torch.Tensor | None, split_len: int, out: torch.Tensor) -> None:
+    n = batch * n_heads * HEAD_DIM
+    _need(q, "q", BF16, n)
+    _need(out, "out", BF16, n)
+    for name, c in (("k_cache", k_cache), ("v_cache", v_cache)):
+        _need(c, name, BF16)
+        if c.dim() != 4 or c.shape[0] != batch or c.shape[1] != n_heads or c.shape[3] != 64:
+            raise ValueError(f"{name} must be [batch, n_heads, slots, 64]")
+    _need(prompt_mask, "prompt_mask", U8, batch * prompt_len, optional=True)
+    _need(kv_start, "kv_start", I32, batch, optional=True)
+    _need(seq_dev, "seq_dev", I32, 1, optional=True)
+    _need(workspace, "workspace", F32, optional=True)
+    ws_bytes = 0 if workspace is None else workspace.numel() * 4
+    _lib.check(_lib.lib().mdl_attn_decode(
+        _p(q), _p(k_cache), _p(v_cache), batch, n_heads, HEAD_DIM, k_cache.shape[2],
+        _p(prompt_mask), prompt_len, _p(kv_start), seq_pos, _p(seq_dev), _p(workspace),
+        ws_bytes, split_len, _p(out), _stream()), "mdl_attn_decode")
+
+
+def lm_head(x: torch.Tensor, row_index: torch.Tensor | None, rows: int, gamma: torch.Tensor,
+            eps: float, w_head: torch.Tensor, logits_out: torch.Tensor | None,
+            token_out: torch.Tensor | None) -> None:
+    d = x.shape[-1]
+    vocab = w_head.shape[0]
+    _need(x, "x", F32)
+    _need(row_index, "row_index", I32, rows, optional=True)
+    if row_index is None and x.numel() < rows * d:
+        raise ValueError("x has fewer rows than requested")
+    _need(gamma, "gamma", F32, d)
+    _need(w_head, "w_head", F32, vocab * d)
+    _need(logits_out, "logits_out", F32, rows * vocab, optional=True)
+    _need(token_out, "token_out", I64, rows, optional=True)
+    _lib.check(_lib.lib().mdl_lm_head(
+        _p(x), _p(row_index), rows, d, _p(gamma), eps, _p(w_head), vocab, _p(logits_out),
+        _p(token_out), _stream()), "mdl_lm_head")
+
+
+def grid_init(ids: torch.Tensor, pos: torch.Tensor, mask: torch.Tensor | None, gx: torch.Tensor,
+              gy: torch.Tensor, in_out: torch.Tensor, kv_start: torch.Tensor | None,
+              last_row: torch.Tensor | None, max_x: int = 30, max_y: int = 29) -> None:
+    batch, seq = ids.shape
+    _need(ids, "ids", I64)
+    _need(pos, "pos", I64, batch * seq * 3)
+    _need(mask, "mask", U8, batch * seq, optional=True)
+    _need(gx, "gx", I32, batch)
+    _need(gy, "gy", I32, batch)
+    _need(in_out, "in_out", U8, batch)
+    _need(kv_start, "kv_start", I32, batch, optional=True)
+    _need(last_row, "last_row", I32, batch, optional=True)
+    _lib.check(_lib.lib().mdl_grid_init(
+        _p(ids), _p(pos), _p(mask), batch, seq, max_x, max_y, _p(gx), _p(gy), _p(in_out),
+        _p(kv_start), _p(last_row), _stream()), "mdl_grid_init")
+
+
+def grid_step(token: torch.Tensor, gx: torch.Tensor, gy: torch.Tensor, in_out: torch.Tensor,
+              pos_out: torch.Tensor, counters: torch.Tensor | None, max_x: int = 30,
+              max_y: int = 29) -> None:
+    batch = token.numel()
+    _need(token, "token", I64)
+    _need(gx, "gx", I32, batch)
+    _need(gy, "gy", I32, batch)
+    _need(in_out, "in_out", U8, batch)
+    _need(pos_out, "pos_out", I64, batch * 3)
+    _need(counters, "counters", I32, 2, optional=True)
+    _lib.check(_lib.lib().mdl_grid_step(
+        _p(token), batch, max_x, max_y, _p(gx), _p(gy), _p(in_out), _p(pos_out), _p(counters),
+        _stream()), "mdl_grid_step")
+
+
+def decode_commit(token: torch.Tensor, out_ids: torch.Tensor, col: int,
+                  counters: torch.Tensor | None, finish_step: torch.Tensor | None,
+                  gen_base: int, end_id: int) -> None:
+    batch = token.numel()
+    _need(token, "token", I64)
+    _need(out_ids, "out_ids", I64)
+    if out_ids.dim() != 2 or out_ids.shape[0] != batch:
+        raise ValueError("out_ids must be [batch, columns]")
+    _need(counters, "counters", I32, 2, optional=True)
+    _need(finish_step, "finish_step", I32, batch, optional=True)
+    _lib.check(_lib.lib().mdl_decode_commit(
+        _p(token), batch, _p(out_ids), out_ids.shape[1], col, _p(counters), _p(finish_step),
+        gen_base, end_id, _stream()), "mdl_decode_commit")

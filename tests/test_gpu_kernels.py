@@ -1,0 +1,346 @@
+"""Kernel-level parity on the GPU: every entry point of libmdlarc_hip.so, called through the C ABI
+(mdlarc_scale_amd.kernels), against the CPU oracle on identical seeded inputs.
+
+Tolerances: values the kernel rounds to bf16 are compared at bf16 resolution
+(|a-b| <= 1e-2*|b| + atol); fp32 outputs at fp32 resolution; integer outputs exactly.
+"""
+
+import math
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import reference_path as rp
+
+pytestmark = pytest.mark.gpu
+
+DEV = "cuda"
+
+
+def K():
+    from mdlarc_scale_amd import kernels
+
+    return kernels
+
+
+def bf(t):
+    return t.to(torch.bfloat16)
+
+
+def close_bf16(got, ref, atol=1e-3, rtol=1e-2):
+    got, ref = got.float().cpu(), ref.float().cpu()
+    err = (got - ref).abs()
+    bound = atol + rtol * ref.abs()
+    assert bool((err <= bound).all()), f"max err {err.max().item():.3e}, worst ratio " \
+        f"{(err / bound).max().item():.2f}"
+
+
+def _cfg(d, H):
+    return rp.OracleConfig(d_model=d, n_heads=H, n_layers=1, d_ff=64)
+
+
+# ---------------------------------------------------------------------------- K1 / add_rmsnorm
+
+@pytest.mark.parametrize("d", [128, 256, 768, 1280])
+@pytest.mark.parametrize("table_dtype", [torch.float32, torch.bfloat16])
+@pytest.mark.parametrize("with_ex", [True, False])
+def test_embed_rmsnorm(d, table_dtype, with_ex):
+    g = torch.Generator().manual_seed(d)
+    B, S, V, NE = 3, 37, 14, 5
+    tok = torch.randn(V, d, generator=g).to(table_dtype)
+    ex = torch.randn(NE, d, generator=g).to(table_dtype)
+    ids = torch.randint(0, V, (B, S), generator=g)
+    ex_ids = torch.randint(0, NE, (B,), generator=g)
+    gamma = 1 + 0.1 * torch.randn(d, generator=g)
+    x_ref = tok.float()[ids] + (ex.float()[ex_ids][:, None] if with_ex else 0)
+    x_ref = x_ref.reshape(B * S, d)
+    r_ref = torch.rsqrt((x_ref.double() ** 2).mean(-1) + 1e-5).float()
+    x = torch.empty(B * S, d, device=DEV)
+    xg = torch.empty(B * S, d, device=DEV, dtype=torch.bfloat16)
+    r = torch.empty(B * S, device=DEV)
+    K().embed_rmsnorm(ids.to(DEV).reshape(-1), ex_ids.to(DEV) if with_ex else None, tok.to(DEV),
+                      ex.to(DEV) if with_ex else None, S, gamma.to(DEV), 1e-5, x, xg, r)
+    torch.cuda.synchronize()
+    assert torch.allclose(x.cpu(), x_ref, atol=1e-6, rtol=1e-6)
+    assert torch.allclose(r.cpu(), r_ref, rtol=2e-6)
+    close_bf16(xg, x_ref * gamma, atol=1e-6, rtol=4e-3)
+
+
+@pytest.mark.parametrize("d", [256, 768, 1024])
+def test_add_rmsnorm(d):
+    g = torch.Generator().manual_seed(7)
+    M = 129
+    x0 = torch.randn(M, d, generator=g)
+    delta = bf(torch.randn(M, d, generator=g))
+    bias = 0.1 * torch.randn(d, generator=g)
+    gamma = 1 + 0.1 * torch.randn(d, generator=g)
+    for use_delta, use_bias, use_xg in ((True, True, True), (True, False, True),
+                                        (False, False, False)):
+        x = x0.to(DEV).clone()
+        xg = torch.empty(M, d, device=DEV, dtype=torch.bfloat16) if use_xg else None
+        r = torch.empty(M, device=DEV)
+        K().add_rmsnorm(x, delta.to(DEV) if use_delta else None, bias.to(DEV) if use_bias else None,
+                        gamma.to(DEV), 1e-5, xg, r)
+        torch.cuda.synchronize()
+        ref = x0 + (delta.float() if use_delta else 0) + (bias if use_bias else 0)
+        assert torch.allclose(x.cpu(), ref, atol=1e-6)
+        assert torch.allclose(r.cpu(), torch.rsqrt(ref.pow(2).mean(-1) + 1e-5), rtol=2e-6)
+        if use_xg:
+            close_bf16(xg, ref * gamma, atol=1e-6, rtol=4e-3)
+
+
+# ---------------------------------------------------------------------------- K2
+
+@pytest.mark.parametrize("H,S,slot0", [(2, 1, 5), (4, 33, 0), (12, 64, 10), (20, 7, 100)])
+def test_qkv_rope_cache(H, S, slot0):
+    d = 64 * H
+    B, slots = 3, 200
+    cfg = _cfg(d, H)
+    g = torch.Generator().manual_seed(H * 100 + S)
+    qkv = bf(torch.randn(B * S, 3 * d, generator=g))
+    rstd = 0.5 + torch.rand(B * S, generator=g)
+    pos = torch.randint(-3, 40, (B * S, 3), generator=g)
+    from mdlarc_scale_amd.transformer import RotaryEmbedding3D
+
+    rope = RotaryEmbedding3D(64, cfg.max_x, cfg.max_y, cfg.max_z)
+    tab = rope.device_table(DEV)
+    geom = (rope.max_x, rope.max_y, rope.max_z, rope.px, rope.py, rope.pz)
+    q = torch.empty(B * S, d, device=DEV, dtype=torch.bfloat16)
+    kc = torch.full((B, H, slots, 64), 7.0, device=DEV, dtype=torch.bfloat16)
+    vc = torch.full_like(kc, 7.0)
+    K().qkv_rope_cache(qkv.to(DEV), rstd.to(DEV), pos.to(DEV), tab, geom, B, S, H, 0.125, q, kc,
+                       vc, slot0=slot0)
+    torch.cuda.synchronize()
+    y = (qkv.float() * rstd[:, None]).view(B, S, 3, H, 64)
+    tabs = rp.rope3d_tables(cfg)
+    p3 = pos.view(B, S, 3)
+    q_ref = rp.apply_rope3d(y[:, :, 0], p3, tabs, cfg) * 0.125
+    k_ref = rp.apply_rope3d(y[:, :, 1], p3, tabs, cfg)
+    close_bf16(q.view(B, S, H, 64), q_ref)
+    close_bf16(kc[:, :, slot0:slot0 + S].permute(0, 2, 1, 3), k_ref)
+    close_bf16(vc[:, :, slot0:slot0 + S].permute(0, 2, 1, 3), y[:, :, 2])
+    untouched = torch.ones(slots, dtype=torch.bool)
+    untouched[slot0:slot0 + S] = False
+    assert bool((kc[:, :, untouched.to(DEV)] == 7).all())
+    assert bool((vc[:, :, untouched.to(DEV)] == 7).all())
+
+
+def test_qkv_rope_cache_device_slot():
+    H, B, slots = 2, 4, 50
+    d = 128
+    qkv = bf(torch.randn(B, 3 * d)).to(DEV)
+    from mdlarc_scale_amd.transformer import RotaryEmbedding3D
+
+    rope = RotaryEmbedding3D(64, 32, 32, 8)
+    geom = (32, 32, 8, rope.px, rope.py, rope.pz)
+    pos = torch.randint(0, 30, (B, 3)).to(DEV)
+    slot = torch.tensor([17], dtype=torch.int32, device=DEV)
+    outs = []
+    for mode in ("host", "dev"):
+        q = torch.empty(B, d, device=DEV, dtype=torch.bfloat16)
+        kc = torch.zeros(B, H, slots, 64, device=DEV, dtype=torch.bfloat16)
+        vc = torch.zeros_like(kc)
+        if mode == "host":
+            K().qkv_rope_cache(qkv, None, pos, rope.device_table(DEV), geom, B, 1, H, 0.125, q, kc,
+                               vc, slot0=17)
+        else:
+            K().qkv_rope_cache(qkv, None, pos, rope.device_table(DEV), geom, B, 1, H, 0.125, q, kc,
+                               vc, slot0=0, slot_dev=slot)
+        outs.append((q, kc, vc))
+    torch.cuda.synchronize()
+    for a, b in zip(*outs):
+        assert torch.equal(a, b)
+    assert bool(outs[1][1][:, :, 17].abs().sum() > 0)
+
+
+# ---------------------------------------------------------------------------- K3
+
+@pytest.mark.parametrize("F", [192, 704, 2048, 3392])
+def test_swiglu(F):
+    g = torch.Generator().manual_seed(F)
+    M = 77
+    gu = bf(3 * torch.randn(M, 2 * F, generator=g))
+    r = 0.5 + torch.rand(M, generator=g)
+    bg = 0.1 * torch.randn(F, generator=g)
+    bu = 0.1 * torch.randn(F, generator=g)
+    h = torch.empty(M, F, device=DEV, dtype=torch.bfloat16)
+    K().swiglu(gu.to(DEV), r.to(DEV), bg.to(DEV), bu.to(DEV), h)
+    torch.cuda.synchronize()
+    a = gu[:, :F].float() * r[:, None] + bg
+    b = gu[:, F:].float() * r[:, None] + bu
+    close_bf16(h, rp.silu(a) * b, atol=1e-4)
+    h2 = torch.empty_like(h)
+    K().swiglu(gu.to(DEV), None, None, None, h2)
+    torch.cuda.synchronize()
+    close_bf16(h2, rp.silu(gu[:, :F].float()) * gu[:, F:].float(), atol=1e-4)
+
+
+# ---------------------------------------------------------------------------- K4a prefill
+
+def _masks(B, S, kind, g):
+    m = torch.ones(B, S, dtype=torch.bool)
+    if kind == "left":
+        for b in range(B):
+            n = int(torch.randint(0, S + 1, (1,), generator=g)) if b else S
+            m[b, :S - n] = False
+    elif kind == "holes":
+        m = torch.rand(B, S, generator=g) < 0.7
+    return m
+
+
+@pytest.mark.parametrize("S", [1, 37, 64, 130, 257])
+@pytest.mark.parametrize("kind", ["none", "left", "holes"])
+@pytest.mark.parametrize("causal", [True, False])
+def test_attn_prefill(S, kind, causal):
+    g = torch.Generator().manual_seed(S * 7 + len(kind) + causal)
+    B, H, slots = 3, 2, S + 9
+    q = bf(torch.randn(B, S, H, 64, generator=g) * 0.125)            # pre-scaled by 1/8
+    kc = bf(torch.randn(B, H, slots, 64, generator=g))
+    vc = bf(torch.randn(B, H, slots, 64, generator=g))
+    mask = _masks(B, S, kind, g) if kind != "none" else None
+    kv_start = None
+    if mask is not None:
+        first = torch.where(mask.any(1), mask.float().argmax(1), torch.full((B,), S))
+        kv_start = first.to(torch.int32).to(DEV)
+    out = torch.empty(B, S, H, 64, device=DEV, dtype=torch.bfloat16)
+    K().attn_prefill(q.to(DEV), kc.to(DEV), vc.to(DEV), B, S, H,
+                     None if mask is None else mask.to(torch.uint8).to(DEV), kv_start, causal, out)
+    torch.cuda.synchronize()
+    ref = rp.attention((q.float() * 8).transpose(1, 2), kc[:, :, :S].float(), vc[:, :, :S].float(),
+                       mask, causal)
+    close_bf16(out.transpose(1, 2), ref, atol=8e-3, rtol=2e-2)
+
+
+# ---------------------------------------------------------------------------- K4b decode
+
+@pytest.mark.parametrize("split_len", [128, 256, 4096])
+@pytest.mark.parametrize("with_mask", [True, False])
+def test_attn_decode(split_len, with_mask):
+    g = torch.Generator().manual_seed(split_len + with_mask)
+    B, H, slots, S = 5, 3, 700, 300
+    t = 611
+    q = bf(torch.randn(B, H, 64, generator=g) * 0.125)
+    kc = bf(torch.randn(B, H, slots, 64, generator=g))
+    vc = bf(torch.randn(B, H, slots, 64, generator=g))
+    pm = _masks(B, S, "left", g) if with_mask else None
+    if with_mask:
+        pm[2, 250:260] = False                       # a hole inside the prompt
+    kv_start = None
+    if pm is not None:
+        kv_start = torch.where(pm.any(1), pm.float().argmax(1), torch.full((B,), S))
+        kv_start = kv_start.to(torch.int32).to(DEV)
+    ws_n = K().attn_decode_workspace_bytes(B, H, slots, split_len) // 4
+    ws = torch.empty(max(ws_n, 1), device=DEV) if ws_n else None
+    out = torch.empty(B, H, 64, device=DEV, dtype=torch.bfloat16)
+    for dev_seq in (False, True):
+        seq_dev = torch.tensor([t], dtype=torch.int32, device=DEV) if dev_seq else None
+        K().attn_decode(q.to(DEV), kc.to(DEV), vc.to(DEV), B, H,
+                        None if pm is None else pm.to(torch.uint8).to(DEV), S if pm is not None
+                        else 0, kv_start, t, seq_dev, ws, split_len, out)
+        torch.cuda.synchronize()
+        keymask = torch.ones(B, t + 1, dtype=torch.bool)
+        if pm is not None:
+            keymask[:, :S] = pm
+        ref = rp.attention((q.float() * 8)[:, :, None], kc[:, :, :t + 1].float(),
+                           vc[:, :, :t + 1].float(), keymask, causal=False)[:, :, 0]
+        close_bf16(out, ref, atol=5e-3, rtol=2e-2)
+
+
+# ---------------------------------------------------------------------------- head + state
+
+@pytest.mark.parametrize("d", [128, 768, 1280])
+def test_lm_head_and_argmax(d):
+    g = torch.Generator().manual_seed(d)
+    M, V = 50, 14
+    x = torch.randn(M, d, generator=g) * 3
+    gamma = 1 + 0.1 * torch.randn(d, generator=g)
+    w = torch.randn(V, d, generator=g) / math.sqrt(d)
+    w[9] = w[4]                                        # exact tie between tokens 4 and 9
+    rows = torch.randperm(M, generator=g)[:20].to(torch.int32)
+    logits = torch.empty(20, V, device=DEV)
+    tok = torch.empty(20, dtype=torch.int64, device=DEV)
+    K().lm_head(x.to(DEV), rows.to(DEV), 20, gamma.to(DEV), 1e-5, w.to(DEV), logits, tok)
+    torch.cuda.synchronize()
+    ref = rp.rmsnorm(x[rows.long()].double(), gamma.double(), 1e-5) @ w.double().T
+    assert torch.allclose(logits.cpu().double(), ref, atol=2e-5, rtol=1e-5)
+    lg = logits.cpu()
+    assert torch.equal(tok.cpu(), lg.argmax(-1))
+    # forcing the tie to be the max: first index must win
+    w2 = torch.zeros(V, d)
+    w2[4] = w2[9] = 1.0
+    t2 = torch.empty(20, dtype=torch.int64, device=DEV)
+    K().lm_head(x.abs().to(DEV), rows.to(DEV), 20, torch.ones(d, device=DEV), 1e-5, w2.to(DEV),
+                None, t2)
+    torch.cuda.synchronize()
+    assert bool((t2.cpu() == 4).all())
+
+
+def test_grid_kernels_match_reference_golden():
+    gs = np.load("tests/golden/grid_state.npz")
+    toks = torch.from_numpy(gs["tokens"])
+    n, steps = toks.shape
+    gx = torch.from_numpy(gs["x0"]).to(torch.int32).to(DEV)
+    gy = torch.from_numpy(gs["y0"]).to(torch.int32).to(DEV)
+    io = torch.from_numpy(gs["io0"]).to(torch.uint8).to(DEV)
+    pos = torch.empty(n, 3, dtype=torch.int64, device=DEV)
+    counters = torch.tensor([5, 9], dtype=torch.int32, device=DEV)
+    trace = []
+    for s in range(steps):
+        K().grid_step(toks[:, s].contiguous().to(DEV), gx, gy, io, pos, counters)
+        trace.append(pos.cpu().numpy().copy())
+    assert np.array_equal(np.stack(trace, 1), gs["positions"])
+    fin = np.stack([gx.cpu().numpy(), gy.cpu().numpy(), io.cpu().numpy()], 1).astype(np.int64)
+    assert np.array_equal(fin, gs["final"])
+    assert counters.cpu().tolist() == [5 + steps, 9 + steps]
+    B = gs["p_ids"].shape[0]
+    ox, oy = torch.empty(B, dtype=torch.int32, device=DEV), torch.empty(B, dtype=torch.int32,
+                                                                        device=DEV)
+    oio = torch.empty(B, dtype=torch.uint8, device=DEV)
+    kvs = torch.empty(B, dtype=torch.int32, device=DEV)
+    last = torch.empty(B, dtype=torch.int32, device=DEV)
+    mask = torch.from_numpy(gs["p_mask"])
+    K().grid_init(torch.from_numpy(gs["p_ids"]).to(DEV), torch.from_numpy(gs["p_pos"]).to(DEV),
+                  mask.to(torch.uint8).to(DEV), ox, oy, oio, kvs, last)
+    init = np.stack([ox.cpu().numpy(), oy.cpu().numpy(), oio.cpu().numpy()], 1).astype(np.int64)
+    assert np.array_equal(init, gs["init"])
+    L = mask.shape[1]
+    n_valid = mask.sum(1)
+    first = torch.where(n_valid > 0, mask.float().argmax(1), torch.full((B,), L))
+    assert torch.equal(kvs.cpu().long(), first)
+    assert torch.equal(last.cpu().long(), torch.arange(B) * L + (n_valid - 1).clamp(min=0))
+
+
+def test_decode_commit():
+    B, cols = 6, 10
+    out = torch.full((B, cols), -7, dtype=torch.int64, device=DEV)
+    fin = torch.tensor([-1, -1, 3, -1, -1, -1], dtype=torch.int32, device=DEV)
+    tok = torch.tensor([13, 2, 13, 11, 13, 0], dtype=torch.int64, device=DEV)
+    K().decode_commit(tok, out, 6, None, fin, 4, 13)
+    counters = torch.tensor([0, 8], dtype=torch.int32, device=DEV)
+    K().decode_commit(tok.flip(0).contiguous(), out, 0, counters, fin, 4, 13)
+    torch.cuda.synchronize()
+    assert out[:, 6].cpu().tolist() == [13, 2, 13, 11, 13, 0]
+    assert out[:, 8].cpu().tolist() == [0, 13, 11, 13, 2, 13]
+    assert fin.cpu().tolist() == [2, 4, 3, 4, 2, 4]
+
+
+def test_capi_rejects_bad_arguments_before_launch():
+    from mdlarc_scale_amd import _lib
+
+    L = _lib.lib()
+    x = torch.zeros(16, 64, device=DEV)
+    # head_dim must be 64
+    assert L.mdl_attn_prefill(x.data_ptr(), x.data_ptr(), x.data_ptr(), 1, 4, 1, 32, 4, None,
+                              None, 1, x.data_ptr(), None) == -4
+    # cache overflow: slot0 + seq > slots
+    assert L.mdl_qkv_rope_cache(x.data_ptr(), 192, None, x.data_ptr(), x.data_ptr(), 1, 4, 1, 64,
+                                32, 32, 8, 10, 10, 12, 0.125, x.data_ptr(), x.data_ptr(),
+                                x.data_ptr(), 4, 1, None, None) == -5
+    # misaligned pointer
+    assert L.mdl_swiglu(x.data_ptr() + 2, 16, None, None, None, 1, 8, x.data_ptr(), None) == -2
+    # workspace too small for a multi-split decode
+    assert L.mdl_attn_decode(x.data_ptr(), x.data_ptr(), x.data_ptr(), 1, 1, 64, 1024, None, 0,
+                             None, 5, None, None, 0, 128, x.data_ptr(), None) == -6
+    with pytest.raises(RuntimeError, match="head_dim"):
+        _lib.check(-4, "probe")
