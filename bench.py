@@ -1,0 +1,365 @@
+#!/usr/bin/env python3
+"""Benchmark of the TinyTransformer inference hot path on one MI355X.
+
+Headline (BASELINE.json ``metric``): greedy decode tokens/s of the small model (d=768, 12 heads,
+4 layers, d_ff=2048, bf16) at B=256: 32 synthetic tasks x 8 dihedral /
+colour variants, prompts of 300-1800 tokens left-padded into one batch, a 2,048-slot static KV
+cache, greedy decode up to 930 tokens (capped by the cache at 2048 - S_pad, as the reference's
+``max_total_len`` does).
+
+    python bench.py [--gpus 1] [--steps K] [--warmup W]
+
+A *step* is one greedy decode step of the whole B=256 batch (grid state -> embedding -> 4 layers
+-> LM head / argmax -> commit), replayed from the captured HIP graph the product path uses.  The
+prompt prefill runs once before the timed region (reported separately).  ``value`` =
+B * K / (timed seconds).
+
+Also reported on the same JSON line:
+* ``roofline``: decode attention (the dominant kernel, HBM-bound).  Its timed-region launches
+  are re-issued one by one with HIP events on the launching stream (same layers, same cache
+  fills t, same buffers) to get the average launch duration; achieved GB/s = algorithmic bytes
+  per launch (K/V slots each row attends, q, output, prompt mask) / that duration.
+* ``cpu_baseline``: the fp32 CPU oracle (oracle/reference_path.py) decoding the same B=256 batch
+  from the same cache contents for a bounded number of steps on the host cores.
+* ``microbench``: BASELINE config 1 -- the fused norm / RoPE / SwiGLU kernels at N=65,536
+  tokens, d=768, F=2048, GB/s against the 8 TB/s HBM peak (buffer sets rotated so the 256 MB
+  MALL cannot hold the working set).
+"""
+
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import platform
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+if ROOT not in sys.path:
+    sys.path.insert(0, ROOT)
+
+HBM_PEAK_GBS = 8000.0          # MI355X HBM3E
+BF16_PEAK_TFLOPS = 2500.0      # MI355X dense bf16 MFMA
+METRIC = "greedy decode tokens/s at small, B=256; fused-kernel HBM GB/s as % of peak"
+
+
+def _args():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=128)
+    ap.add_argument("--warmup", type=int, default=8)
+    ap.add_argument("--cpu-seconds", type=float, default=15.0,
+                    help="time bound of the CPU-baseline sample (0 disables it)")
+    ap.add_argument("--no-micro", action="store_true", help="skip the config-1 microbench")
+    ap.add_argument("--eager", action="store_true",
+                    help="launch every kernel from the host instead of replaying a HIP graph")
+    return ap.parse_args()
+
+
+class Timer:
+    """HIP events on the current stream."""
+
+    def __init__(self):
+        import torch
+
+        self.a = torch.cuda.Event(enable_timing=True)
+        self.b = torch.cuda.Event(enable_timing=True)
+
+    def start(self):
+        self.a.record()
+
+    def stop(self):
+        self.b.record()
+
+    def ms(self) -> float:
+        self.b.synchronize()
+        return self.a.elapsed_time(self.b)
+
+
+def decode_attention_bytes(B, H, t, kv_start, S):
+    """Algorithmic bytes of one decode-attention launch at cache position t: every row reads the
+    K and V rows of the slots it attends (kv_start[b]..t, 2 x 64 bf16 per head each), its q
+    (64 bf16 per head), writes the split output (2 x 64 bf16 per head) and reads its prompt mask
+    bytes once."""
+    import torch
+
+    n = (t + 1 - kv_start.to(torch.int64)).clamp(min=0)
+    kv = int(n.sum()) * H * 64 * 2 * 2
+    q = B * H * 64 * 2
+    out = B * H * 64 * 2 * 2
+    mask = int((S - kv_start.to(torch.int64)).clamp(min=0).sum())
+    return kv + q + out + mask
+
+
+def microbench(dev):
+    """K1 / K2 / K3 at N = 64 x 1024 tokens, d = 768, 12 heads, F = 2048."""
+    import torch
+
+    from mdlarc_scale_amd import kernels as K
+    from mdlarc_scale_amd.transformer import RotaryEmbedding3D
+    from mdlarc_scale_amd.workload import SPECS, build_prompts, left_pad
+
+    Bm, T, d, H, F = 64, 1024, 768, 12, 2048
+    N = Bm * T
+    g = torch.Generator(device="cpu").manual_seed(1)
+    sets = 3
+    # positions from synthetic grids (config 0 generator), tiled to T tokens per row
+    prompts = build_prompts(SPECS["tiny_cpu"])
+    _, pos_p, _ = left_pad(prompts)
+    flat = pos_p.reshape(-1, 3)
+    reps = (N + flat.shape[0] - 1) // flat.shape[0]
+    pos = flat.repeat(reps, 1)[:N].contiguous().to(dev)
+    rope = RotaryEmbedding3D(64, 32, 32, 8)
+    tab = rope.device_table(dev)
+    geom = (32, 32, 8, rope.px, rope.py, rope.pz)
+    res = {}
+
+    def timeit(fn, n_iter=20):
+        for i in range(3):
+            fn(i % sets)
+        t = Timer()
+        t.start()
+        for i in range(n_iter):
+            fn(i % sets)
+        t.stop()
+        return t.ms() / n_iter
+
+    # K1: embedding gather + example add + RMSNorm -> x fp32, split x*gamma, rstd
+    tok = torch.randn(14, d, generator=g).to(dev, torch.bfloat16)
+    ex = torch.randn(1280, d, generator=g).to(dev, torch.bfloat16)
+    gamma = (1 + 0.1 * torch.randn(d, generator=g)).to(dev)
+    ids = [torch.randint(0, 14, (N,), generator=g).to(dev) for _ in range(sets)]
+    exi = [torch.randint(0, 1280, (Bm,), generator=g).to(dev) for _ in range(sets)]
+    xo = [torch.empty(N, d, device=dev) for _ in range(sets)]
+    xs = [torch.empty(N, 2 * d, device=dev, dtype=torch.bfloat16) for _ in range(sets)]
+    rs = [torch.empty(N, device=dev) for _ in range(sets)]
+    ms = timeit(lambda i: K.embed_rmsnorm(ids[i], exi[i], tok, ex, T, gamma, 1e-5, xo[i], xs[i],
+                                          rs[i]))
+    nbytes = N * 8 + N * d * 4 + N * 2 * d * 2 + N * 4
+    res["k1_embed_rmsnorm"] = dict(ms=ms, bytes=nbytes, gbs=nbytes / ms / 1e6)
+    del xo, xs, rs
+
+    # K2: qkv (fp32 GEMM output) -> rstd scale + split + 3D RoPE + q out + K/V cache write
+    qkv = [torch.randn(N, 3 * d, generator=g).to(dev) for _ in range(sets)]
+    rstd = [(0.5 + torch.rand(N, generator=g)).to(dev) for _ in range(sets)]
+    q = [torch.empty(N, d, device=dev, dtype=torch.bfloat16) for _ in range(sets)]
+    kc = [torch.empty(Bm, H, T, 64, device=dev, dtype=torch.bfloat16) for _ in range(sets)]
+    vc = [torch.empty_like(kc[0]) for _ in range(sets)]
+    ms = timeit(lambda i: K.qkv_rope_cache(qkv[i], rstd[i], pos, tab, geom, Bm, T, H, 0.125, q[i],
+                                           kc[i], vc[i], slot0=0))
+    nbytes = N * (3 * d * 4 + 4 + 24 + d * 2 + 2 * d * 2)
+    res["k2_qkv_rope_cache"] = dict(ms=ms, bytes=nbytes, gbs=nbytes / ms / 1e6)
+    del qkv, rstd, q, kc, vc
+
+    # K3: SwiGLU [N, 2F] fp32 -> split h [N, 2F] bf16
+    gu = [torch.randn(N, 2 * F, generator=g).to(dev) for _ in range(sets)]
+    rstd = [(0.5 + torch.rand(N, generator=g)).to(dev) for _ in range(sets)]
+    bg = (0.1 * torch.randn(F, generator=g)).to(dev)
+    bu = (0.1 * torch.randn(F, generator=g)).to(dev)
+    h = [torch.empty(N, 2 * F, device=dev, dtype=torch.bfloat16) for _ in range(sets)]
+    ms = timeit(lambda i: K.swiglu(gu[i], rstd[i], bg, bu, h[i]))
+    nbytes = N * (2 * F * 4 + 4 + 2 * F * 2)
+    res["k3_swiglu"] = dict(ms=ms, bytes=nbytes, gbs=nbytes / ms / 1e6)
+    del gu, h
+    for v in res.values():
+        v["frac_of_peak"] = round(v["gbs"] / HBM_PEAK_GBS, 4)
+        v["ms"] = round(v["ms"], 5)
+        v["gbs"] = round(v["gbs"], 1)
+    return res
+
+
+def cpu_baseline(model_state, cfg, st, ex, t0, seconds):
+    """fp32 CPU oracle decoding the same B rows from the GPU's cache contents (upcast to fp32)
+    for as many steps as fit in ``seconds`` (at least 2)."""
+    import torch
+
+    from oracle import reference_path as rp
+
+    ocfg = rp.OracleConfig(cfg.d_model, cfg.n_heads, cfg.n_layers, cfg.d_ff, cfg.num_examples,
+                           cfg.max_seq_len)
+    om = rp.OracleModel(ocfg, model_state, dtype=torch.float32)
+    B, S, total = st.B, st.S, st.total
+    cache = st.cache.cache.cpu().float()
+    tok = st.tok.cpu()
+    grid = rp.GridState(st.gx.cpu(), st.gy.cpu(), st.gio.cpu())
+    key_mask = torch.ones(B, total, dtype=torch.bool)
+    key_mask[:, :S] = st.pmask.cpu().bool()
+    exc = ex.cpu()
+    steps, t = 0, t0
+    start = time.perf_counter()
+    while t + 1 < total:
+        pos = grid.update(tok)
+        logits = om.decode_step(tok, pos, exc, cache, t, key_mask[:, :t + 1])
+        tok = logits.argmax(-1)
+        steps += 1
+        t += 1
+        if time.perf_counter() - start >= seconds and steps >= 2:
+            break
+    el = time.perf_counter() - start
+    return dict(value=round(B * steps / el, 2), unit="tokens/s", cores=torch.get_num_threads(),
+                kind="port",
+                sample=f"B={B} rows x {steps} greedy decode steps of the fp32 oracle "
+                       f"(oracle/reference_path.py OracleModel.decode_step) from cache fill "
+                       f"t={t0}, cache filled from the GPU prefill/decode K/V upcast to fp32; "
+                       f"{el:.1f} s on {torch.get_num_threads()} threads "
+                       f"({platform.processor() or platform.machine()}, "
+                       f"os.cpu_count()={os.cpu_count()})")
+
+
+def main() -> int:
+    args = _args()
+    if args.gpus != 1:
+        print("bench.py runs on exactly one GPU: this build measures the single-GPU hot path "
+              "(decode rows shard by batch with no exchange; see DESIGN.md). Use --gpus 1.",
+              file=sys.stderr)
+        return 2
+    import torch
+
+    from mdlarc_scale_amd import _lib, create_small_model
+    from mdlarc_scale_amd import kernels as K
+    from mdlarc_scale_amd import inference as I
+    from mdlarc_scale_amd.data import END_TOKEN_ID
+    from mdlarc_scale_amd.engine import engine_for
+    from mdlarc_scale_amd.workload import SPECS, build_prompts, left_pad
+
+    if not torch.cuda.is_available():
+        print("bench.py needs a ROCm GPU", file=sys.stderr)
+        return 1
+    _lib.lib()
+    dev = torch.device("cuda:0")
+    spec = SPECS["small_b256"]
+    t_build = time.perf_counter()
+    prompts = build_prompts(spec)
+    ids, pos, mask = left_pad(prompts)
+    B, S = ids.shape
+    per_task = spec.batch // spec.n_tasks
+    ex = torch.arange(spec.n_tasks).repeat_interleave(per_task)
+    host_build_s = time.perf_counter() - t_build
+
+    torch.manual_seed(0)
+    model = create_small_model(dropout=0.0, max_seq_len=spec.cache_slots)
+    model = model.to(torch.bfloat16)                 # bf16 model
+    model_state = {k: v.float().clone() for k, v in model.state_dict().items()}
+    model = model.to(dev).eval()
+    cfg = model.config
+    total = min(S + spec.max_new, cfg.max_seq_len)
+    max_new = total - S
+    need = args.warmup + args.steps
+    if need + 1 > max_new:
+        print(f"--warmup + --steps = {need} exceeds the {max_new - 1} decode steps the "
+              f"{cfg.max_seq_len}-slot cache leaves after the {S}-token prompts", file=sys.stderr)
+        return 2
+
+    eng = engine_for(model)
+    gen = I.Generator(model)
+    ids_d, pos_d, mask_d, ex_d = ids.to(dev), pos.to(dev), mask.to(dev), ex.to(dev)
+    with torch.no_grad():
+        W = eng.packed(dev)
+        st = gen.prepare(ids_d, pos_d, ex_d, mask_d, total)
+        torch.cuda.synchronize()
+        tp = Timer()
+        tp.start()
+        gen.prefill(st, W, ids_d, pos_d)
+        tp.stop()
+        prefill_ms = tp.ms()
+        K.decode_commit(st.tok, st.out_ids, S, None, st.finish, S, END_TOKEN_ID)
+        # warmup: one eager step, capture, replays
+        gen.greedy_step(st, W, True)
+        graph = None if args.eager else gen.capture_greedy(st, W, True)
+        for _ in range(args.warmup - 1):
+            graph.replay() if graph is not None else gen.greedy_step(st, W, True)
+        torch.cuda.synchronize()
+        t_first = S + args.warmup              # cache slot of the first timed step's token
+        tm = Timer()
+        wall0 = time.perf_counter()
+        tm.start()
+        for _ in range(args.steps):
+            graph.replay() if graph is not None else gen.greedy_step(st, W, True)
+        tm.stop()
+        torch.cuda.synchronize()
+        wall_s = time.perf_counter() - wall0
+        timed_ms = tm.ms()
+
+        # decode attention: re-issue the timed region's launches one by one with HIP events
+        H = cfg.n_heads
+        kv_start_h = st.kv_start.cpu()
+        ev = []
+        for i in range(args.steps):
+            t = t_first + i
+            for li in range(cfg.n_layers):
+                kc, vc = st.cache.layer(li)
+                a = torch.cuda.Event(enable_timing=True)
+                b = torch.cuda.Event(enable_timing=True)
+                a.record()
+                K.attn_decode(st.sc.q, kc, vc, B, H, st.pmask, S, st.kv_start, t, None, st.ws,
+                              st.split_len, st.sc.attn)
+                b.record()
+                ev.append((a, b, t))
+        torch.cuda.synchronize()
+        durs = [a.elapsed_time(b) for a, b, _ in ev]
+        bytes_l = [decode_attention_bytes(B, H, t, kv_start_h, S) for _, _, t in ev]
+        attn_ms = sum(durs) / len(durs)
+        attn_bytes = sum(bytes_l) / len(bytes_l)
+        achieved = attn_bytes / attn_ms / 1e6
+
+        micro = None if args.no_micro else microbench(dev)
+
+        cpu = None
+        if args.cpu_seconds > 0:
+            cpu = cpu_baseline(model_state, cfg, st, ex, S + args.warmup + args.steps,
+                               args.cpu_seconds)
+
+    n_valid = mask.sum(1)
+    prefill_flops = cfg.n_layers * 4 * 64 * H * int((n_valid * (n_valid + 1) // 2).sum())
+    value = B * args.steps / (timed_ms / 1e3)
+    out = {
+        "metric": METRIC,
+        "value": round(value, 1),
+        "unit": "tokens/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(timed_ms / args.steps, 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16",
+        "data": "synthetic",
+        "config": {
+            "workload": "BASELINE config 2: small TinyTransformer (d=768, 12 heads, 4 layers, "
+                        "d_ff=2048) bf16, random init seed 0, B=256 greedy decode "
+                        "(32 tasks x 8 dihedral+colour variants, left-padded)",
+            "model": "small", "global_batch": B, "seq_len": S, "cache_slots": total,
+            "decode_steps_available": max_new - 1, "timed_cache_fill": [t_first,
+                                                                        t_first + args.steps],
+            "prompt_len_min": int(n_valid.min()), "prompt_len_mean": round(float(
+                n_valid.float().mean()), 1), "prompt_len_max": int(n_valid.max()),
+            "parallelism": "single GPU (rows shard by batch across GPUs, no exchange)",
+            "graph": not args.eager, "workload_seed": spec.seed,
+        },
+        "roofline": {
+            "kernel": "attn_decode_kernel (+ attn_decode_combine_kernel)",
+            "bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS,
+            "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None,
+            "avg_launch_ms": round(attn_ms, 5), "bytes_per_launch": int(attn_bytes),
+            "launches_timed": len(durs),
+        },
+        "cpu_baseline": cpu,
+        "prefill": {
+            "ms": round(prefill_ms, 3), "tokens": int(n_valid.sum()), "padded_tokens": B * S,
+            "tokens_per_s": round(int(n_valid.sum()) / (prefill_ms / 1e3), 1),
+            "attention_causal_tflop": round(prefill_flops / 1e12, 3),
+        },
+        "microbench": micro,
+        "wall_s_timed": round(wall_s, 4),
+        "host_prompt_build_s": round(host_build_s, 3),
+    }
+    if cpu:
+        out["vs_cpu"] = round(value / cpu["value"], 1)
+    print(json.dumps(out), flush=True)
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())

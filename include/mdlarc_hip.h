@@ -14,6 +14,11 @@
  *   - Return 0 on success, a negative MDL_ERR_* for arguments rejected on the host before any
  *     launch, or a positive hipError_t reported by the launch.
  *   - Head dimension is 64 (all reference model sizes, src/transformer.py:728-745).
+ *   - GEMM inputs ("split activations") are written as hi|lo bf16 pairs: a row of K values is 2K
+ *     bf16, hi = bf16(v) in columns [0, K), lo = bf16(v - hi) in [K, 2K).  Multiplied with a
+ *     weight packed as [W | W] ([N, 2K] bf16) a bf16 GEMM with fp32 accumulation returns
+ *     (hi + lo) . w, i.e. the fp32 activation against the bf16 weight.  GEMM outputs are
+ *     consumed in fp32.
  *   - KV cache layout is the reference StaticKVCache layout (src/inference.py:73-77):
  *     one layer's K (or V) is [batch, n_heads, cache_slots, 64] bf16, slot-major rows of 128 B.
  */
@@ -50,25 +55,26 @@ const char* mdl_error_string(int code);
  * For row m (batch row b = m / row_len):
  *   x[m]     = tok_table[ids[m]] + (example_ids ? ex_table[example_ids[b]] : 0)     (fp32)
  *   rstd[m]  = 1 / sqrt(mean(x[m]^2) + eps)
- *   xg[m]    = bf16(x[m] * gamma)        (GEMM input; rstd is applied after the GEMM)
+ *   xs[m]    = split(x[m] * gamma)       bf16 [rows, 2d] (GEMM input; rstd is applied after
+ *                                        the GEMM).  xs_out may be NULL.
  * Tables are fp32 or bf16 (table_dtype); ids are clamped into range (callers validate first).
  */
 int mdl_embed_rmsnorm(const int64_t* ids, const int64_t* example_ids, const void* tok_table,
                       const void* ex_table, int table_dtype, int vocab, int n_examples, int rows,
                       int row_len, int d, const float* gamma, float eps, float* x_out,
-                      uint16_t* xg_out, float* rstd_out, void* stream);
+                      uint16_t* xs_out, float* rstd_out, void* stream);
 
 /*
  * Residual add fused with the next RMSNorm's reduction.
  * Replaces: the residual adds of TransformerBlock.forward (src/transformer.py:494-496),
  *           _prefill / _decode_step (src/inference.py:412-413, :455-456), the fc_down bias
  *           (src/transformer.py:443), and the reduction of the following ln2 / ln1 / ln_f.
- *   x[m]    += delta[m] (+ bias)           delta bf16 [rows, d] (may be NULL), bias fp32 [d] or NULL
+ *   x[m]    += delta[m] (+ bias)           delta fp32 [rows, d] (may be NULL), bias fp32 [d] or NULL
  *   rstd[m]  = 1 / sqrt(mean(x[m]^2) + eps)
- *   xg[m]    = bf16(x[m] * gamma)          (skipped when xg_out is NULL)
+ *   xs[m]    = split(x[m] * gamma)         bf16 [rows, 2d] (skipped when xs_out is NULL)
  */
-int mdl_add_rmsnorm(float* x, const uint16_t* delta, const float* bias, int rows, int d,
-                    const float* gamma, float eps, uint16_t* xg_out, float* rstd_out,
+int mdl_add_rmsnorm(float* x, const float* delta, const float* bias, int rows, int d,
+                    const float* gamma, float eps, uint16_t* xs_out, float* rstd_out,
                     void* stream);
 
 /*
@@ -77,7 +83,7 @@ int mdl_add_rmsnorm(float* x, const uint16_t* delta, const float* bias, int rows
  *           ln1, RotaryEmbedding3D.apply_rotary (src/transformer.py:132-187, _rotate_half
  *           :51-58), the transposes (src/inference.py:406) and StaticKVCache.update
  *           (src/inference.py:84-92).
- * qkv: bf16 [batch*seq, 3*d] (row stride qkv_ld elements) = (x*gamma) @ W_qkv^T, columns
+ * qkv: fp32 [batch*seq, 3*d] (row stride qkv_ld elements) = (x*gamma) @ W_qkv^T, columns
  *      [q heads | k heads | v heads] (src/transformer.py:317-318).  rstd: fp32 [batch*seq].
  * pos: int64 [batch*seq, 3] (x, y, z); clamped to [0,max-1] per axis.
  * rope_tab: fp32 [cos_x(max_x*px) | sin_x | cos_y(max_y*py) | sin_y | cos_z(max_z*pz) | sin_z],
@@ -85,7 +91,7 @@ int mdl_add_rmsnorm(float* x, const uint16_t* delta, const float* bias, int rows
  * Outputs: q_out bf16 [batch*seq, d] = rope(q * rstd) * q_scale; k/v written to cache slot
  *      (slot_dev ? *slot_dev : slot0) + s for token s of each batch row.
  */
-int mdl_qkv_rope_cache(const uint16_t* qkv, int64_t qkv_ld, const float* rstd,
+int mdl_qkv_rope_cache(const float* qkv, int64_t qkv_ld, const float* rstd,
                        const int64_t* pos, const float* rope_tab, int batch, int seq,
                        int n_heads, int head_dim, int max_x, int max_y, int max_z, int px,
                        int py, int pz, float q_scale, uint16_t* q_out, uint16_t* k_cache,
@@ -95,11 +101,12 @@ int mdl_qkv_rope_cache(const uint16_t* qkv, int64_t qkv_ld, const float* rstd,
 /*
  * K3 -- SwiGLU gate: silu(gate) * up, with the RMSNorm multiply of ln2 and the fc biases.
  * Replaces: FeedForward.forward's silu(fc_gate(x)) * fc_up(x) (src/transformer.py:441-449).
- * gate_up: bf16 [rows, 2*d_ff] (row stride ld) = (x*gamma2) @ [W_gate; W_up]^T.
- *   h[m, j] = silu(rstd[m]*g[m,j] + bias_gate[j]) * (rstd[m]*u[m,j] + bias_up[j])   -> bf16
- * rstd / biases may be NULL (treated as 1 / 0).  d_ff must be a multiple of 8.
+ * gate_up: fp32 [rows, 2*d_ff] (row stride ld) = (x*gamma2) @ [W_gate; W_up]^T.
+ *   h[m, j] = silu(rstd[m]*g[m,j] + bias_gate[j]) * (rstd[m]*u[m,j] + bias_up[j])
+ * h_out: split bf16 [rows, 2*d_ff].  rstd / biases may be NULL (treated as 1 / 0).  d_ff must
+ * be a multiple of 8.
  */
-int mdl_swiglu(const uint16_t* gate_up, int64_t ld, const float* rstd, const float* bias_gate,
+int mdl_swiglu(const float* gate_up, int64_t ld, const float* rstd, const float* bias_gate,
                const float* bias_up, int rows, int d_ff, uint16_t* h_out, void* stream);
 
 /*
@@ -107,7 +114,8 @@ int mdl_swiglu(const uint16_t* gate_up, int64_t ld, const float* rstd, const flo
  * Replaces: F.scaled_dot_product_attention in _prefill (src/inference.py:409, mask from
  *           _build_sdpa_mask :372-380, is_causal=True) and in MultiHeadSelfAttention.forward
  *           (src/transformer.py:333-349, is_causal either way).
- * q / out: bf16 [batch, seq, n_heads, 64]; q already multiplied by the softmax scale.
+ * q: bf16 [batch, seq, n_heads, 64], already multiplied by the softmax scale.
+ * out: split bf16 [batch*seq, 2*n_heads*64] (the out-projection GEMM input).
  * keys:    k_cache / v_cache slots [0, seq) of [batch, n_heads, cache_slots, 64].
  * Query i of row b sees key j iff j < seq, key_mask[b*seq + j] != 0 (key_mask may be NULL),
  * j >= kv_start[b] (kv_start may be NULL; it must not exclude a visible key) and, if causal,
@@ -122,7 +130,8 @@ int mdl_attn_prefill(const uint16_t* q, const uint16_t* k_cache, const uint16_t*
  * K4b -- decode attention over the static cache (split-K flash decoding).
  * Replaces: F.scaled_dot_product_attention in _decode_step (src/inference.py:452) with the
  *           mask rebuilt from full_attention_mask (src/inference.py:446-450, :557-558, :626).
- * q / out: bf16 [batch, n_heads, 64] (q pre-scaled).  The query of row b sees slot j iff
+ * q: bf16 [batch, n_heads, 64] (pre-scaled); out: split bf16 [batch, 2*n_heads*64].
+ * The query of row b sees slot j iff
  *   kv_start[b] <= j <= t, t = (seq_dev ? *seq_dev : seq_pos), and
  *   (j >= prompt_len || prompt_mask[b*prompt_len + j] != 0)   (prompt_mask may be NULL).
  * workspace: fp32, at least mdl_attn_decode_workspace_bytes(...) bytes (may be NULL when

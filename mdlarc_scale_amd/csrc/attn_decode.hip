@@ -18,6 +18,18 @@ namespace mdl {
 constexpr float kLog2e = 1.4426950408889634f;
 constexpr int kPart = 2 + kHeadDim;   // m, l, acc[64] per split
 
+// Channel `lane` of head h = bh % n_heads of batch row b = bh / n_heads into the out-projection
+// GEMM input: row b holds 2*n_heads*64 bf16, hi of every head then lo of every head.
+__device__ __forceinline__ void store_split(uint16_t* out, int bh, int n_heads, int lane,
+                                            float o) {
+  const int b = bh / n_heads, h = bh - b * n_heads;
+  const int64_t d = static_cast<int64_t>(n_heads) * kHeadDim;
+  uint16_t* p = out + static_cast<int64_t>(b) * 2 * d + h * kHeadDim + lane;
+  const uint32_t hi = f2bf(o);
+  p[0] = static_cast<uint16_t>(hi);
+  p[d] = static_cast<uint16_t>(f2bf(o - bf2f(hi)));
+}
+
 template <int U>
 __global__ __launch_bounds__(256) void attn_decode_kernel(
     const uint16_t* __restrict__ q, const uint16_t* __restrict__ kc,
@@ -141,8 +153,7 @@ __global__ __launch_bounds__(256) void attn_decode_kernel(
       O += red[w][2 + lane] * sc;
     }
     if (n_split == 1) {
-      const float o = L > 0.f ? O / L : 0.f;
-      out[static_cast<int64_t>(bh) * kHeadDim + lane] = static_cast<uint16_t>(f2bf(o));
+      store_split(out, bh, n_heads, lane, L > 0.f ? O / L : 0.f);
     } else {
       float* p = ws + (static_cast<int64_t>(bh) * n_split + split) * kPart;
       if (lane == 0) {
@@ -156,7 +167,8 @@ __global__ __launch_bounds__(256) void attn_decode_kernel(
 
 // Merge the per-split partial states of one (b, h): lane = channel.
 __global__ __launch_bounds__(256) void attn_decode_combine_kernel(const float* __restrict__ ws,
-                                                                  int n_bh, int n_split,
+                                                                  int n_bh, int n_heads,
+                                                                  int n_split,
                                                                   uint16_t* __restrict__ out) {
   const int bh = blockIdx.x * 4 + (threadIdx.x >> 6);
   const int lane = threadIdx.x & 63;
@@ -171,8 +183,7 @@ __global__ __launch_bounds__(256) void attn_decode_combine_kernel(const float* _
     L += p[s * kPart + 1] * sc;
     O += p[s * kPart + 2 + lane] * sc;
   }
-  const float o = L > 0.f ? O / L : 0.f;
-  out[static_cast<int64_t>(bh) * kHeadDim + lane] = static_cast<uint16_t>(f2bf(o));
+  store_split(out, bh, n_heads, lane, L > 0.f ? O / L : 0.f);
 }
 
 constexpr int kUnroll = 4;
@@ -219,6 +230,7 @@ extern "C" int mdl_attn_decode(const uint16_t* q, const uint16_t* k_cache,
       q, k_cache, v_cache, n_heads, cache_slots, prompt_mask, prompt_len, kv_start, seq_pos,
       seq_dev, ns, split_len, workspace, out);
   if (ns > 1)
-    attn_decode_combine_kernel<<<dim3((n_bh + 3) / 4), 256, 0, s>>>(workspace, n_bh, ns, out);
+    attn_decode_combine_kernel<<<dim3((n_bh + 3) / 4), 256, 0, s>>>(workspace, n_bh, n_heads,
+                                                                     ns, out);
   return launch_status();
 }

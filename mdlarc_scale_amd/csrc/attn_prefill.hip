@@ -13,7 +13,8 @@
 // is inside the instruction, so any common key order of the two operands is exact.
 //
 // Online softmax in the log2 domain, fp32 throughout; the per-lane partial row sums are merged
-// across the 4 lane groups once at the end.  Queries with no visible key produce 0.
+// across the 4 lane groups once at the end.  Queries with no visible key produce 0.  The output
+// (the out-projection GEMM input) is written as a hi|lo bf16 pair per row, see common.h.
 #include "common.h"
 
 namespace mdl {
@@ -163,14 +164,17 @@ __global__ __launch_bounds__(256) void attn_prefill_kernel(
   float l = l_run + __shfl_xor(l_run, 16, kWave);
   l += __shfl_xor(l, 32, kWave);
   if (qi < S) {
+    // output row (b, qi) holds 2*H*64 bf16: hi of every head, then lo of every head
     const float inv = l > 0.f ? 1.f / l : 0.f;
-    uint16_t* op = out + ((static_cast<int64_t>(b) * S + qi) * H + h) * kHeadDim;
+    const int64_t d = static_cast<int64_t>(H) * kHeadDim;
+    uint16_t* op = out + (static_cast<int64_t>(b) * S + qi) * 2 * d + h * kHeadDim;
 #pragma unroll
     for (int db = 0; db < 4; ++db) {
-      uint2 w;
-      w.x = pack_bf2(o[db][0] * inv, o[db][1] * inv);
-      w.y = pack_bf2(o[db][2] * inv, o[db][3] * inv);
-      *reinterpret_cast<uint2*>(op + 16 * db + 4 * g) = w;
+      const float t[4] = {o[db][0] * inv, o[db][1] * inv, o[db][2] * inv, o[db][3] * inv};
+      uint2 hi, lo;
+      split4(t, hi, lo);
+      *reinterpret_cast<uint2*>(op + 16 * db + 4 * g) = hi;
+      *reinterpret_cast<uint2*>(op + d + 16 * db + 4 * g) = lo;
     }
   }
 }

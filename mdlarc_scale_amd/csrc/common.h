@@ -41,6 +41,38 @@ __device__ __forceinline__ uint4 pack8(const float* f) {
   return v;
 }
 
+// ---- split activations -----------------------------------------------------------------------
+// A GEMM input row of width K is stored as 2K bf16: hi = bf16(v) in columns [0, K) and
+// lo = bf16(v - hi) in [K, 2K) (v - hi is exact in fp32).  Against a weight packed as [W | W]
+// the bf16 GEMM then returns (hi + lo) . w, i.e. v to about 2^-17 relative instead of the 2^-9
+// of a single bf16 rounding; the same buffer read as [2M, K] gives hi.w and lo.w as row pairs.
+__device__ __forceinline__ void split_bf2(float a, float b, uint32_t& hi, uint32_t& lo) {
+  const uint32_t ha = f2bf(a), hb = f2bf(b);
+  hi = ha | (hb << 16);
+  lo = f2bf(a - bf2f(ha)) | (f2bf(b - bf2f(hb)) << 16);
+}
+
+// 4 floats -> hi (uint2) and lo (uint2)
+__device__ __forceinline__ void split4(const float* f, uint2& hi, uint2& lo) {
+  split_bf2(f[0], f[1], hi.x, lo.x);
+  split_bf2(f[2], f[3], hi.y, lo.y);
+}
+
+// 8 floats -> hi (uint4) and lo (uint4)
+__device__ __forceinline__ void split8(const float* f, uint4& hi, uint4& lo) {
+  split_bf2(f[0], f[1], hi.x, lo.x);
+  split_bf2(f[2], f[3], hi.y, lo.y);
+  split_bf2(f[4], f[5], hi.z, lo.z);
+  split_bf2(f[6], f[7], hi.w, lo.w);
+}
+
+__device__ __forceinline__ void load8f(const float* p, float* f) {
+  const float4 a = *reinterpret_cast<const float4*>(p);
+  const float4 b = *reinterpret_cast<const float4*>(p + 4);
+  f[0] = a.x; f[1] = a.y; f[2] = a.z; f[3] = a.w;
+  f[4] = b.x; f[5] = b.y; f[6] = b.z; f[7] = b.w;
+}
+
 // ---- wave64 reductions -----------------------------------------------------------------------
 __device__ __forceinline__ float wave_sum(float v) {
 #pragma unroll

@@ -1,9 +1,11 @@
 // K2 -- RMSNorm scale + Q/K/V split + 3D RoPE + static-cache write, one pass over the qkv GEMM
 // output.
 //
-// Work item = 8 consecutive bf16 of one token's qkv row (one 16-byte load).  Items are numbered
-// token-major, so a wavefront reads 1 KiB of contiguous qkv and writes q (contiguous) or a
-// 128-byte head row of the K/V cache per 8 lanes.  The 8 values are 4 interleaved RoPE pairs of
+// qkv is the fp32 output of the projection GEMM (the GEMM accumulates in fp32 and returns it
+// unrounded).  Work item = 8 consecutive values of one token's qkv row (two 16-byte loads).
+// Items are numbered token-major, so a wavefront reads 2 KiB of contiguous qkv and writes q
+// (contiguous) or a 128-byte head row of the K/V cache per 8 lanes.  The 8 values are 4
+// interleaved RoPE pairs of
 // one head, rotated in fp32 with the per-axis cos/sin tables of the reference
 // (RotaryEmbedding3D._build_cache); pair j of a head uses axis x for j < px, y for
 // px <= j < px+py and z otherwise, exactly the split of RotaryEmbedding3D.apply_rotary.
@@ -16,7 +18,7 @@ struct RopeArgs {
 };
 
 __global__ __launch_bounds__(256) void qkv_rope_cache_kernel(
-    const uint16_t* __restrict__ qkv, int64_t ld, const float* __restrict__ rstd,
+    const float* __restrict__ qkv, int64_t ld, const float* __restrict__ rstd,
     const int64_t* __restrict__ pos, const float* __restrict__ tab, RopeArgs ra, int64_t rows,
     int seq, int n_heads, float q_scale, uint16_t* __restrict__ q_out,
     uint16_t* __restrict__ kc, uint16_t* __restrict__ vc, int slots, int slot0,
@@ -34,7 +36,7 @@ __global__ __launch_bounds__(256) void qkv_rope_cache_kernel(
   const int dim0 = (cc & 7) * 8;
 
   float f[8];
-  unpack8(*reinterpret_cast<const uint4*>(qkv + m * ld + c * 8), f);
+  load8f(qkv + m * ld + c * 8, f);
   const float r = rstd ? rstd[m] : 1.f;
 #pragma unroll
   for (int i = 0; i < 8; ++i) f[i] *= r;
@@ -85,7 +87,7 @@ __global__ __launch_bounds__(256) void qkv_rope_cache_kernel(
 
 using namespace mdl;
 
-extern "C" int mdl_qkv_rope_cache(const uint16_t* qkv, int64_t qkv_ld, const float* rstd,
+extern "C" int mdl_qkv_rope_cache(const float* qkv, int64_t qkv_ld, const float* rstd,
                                   const int64_t* pos, const float* rope_tab, int batch, int seq,
                                   int n_heads, int head_dim, int max_x, int max_y, int max_z,
                                   int px, int py, int pz, float q_scale, uint16_t* q_out,
@@ -98,7 +100,7 @@ extern "C" int mdl_qkv_rope_cache(const uint16_t* qkv, int64_t qkv_ld, const flo
     return MDL_ERR_SHAPE;
   if (cache_slots <= 0 || (!slot_dev && (slot0 < 0 || slot0 + seq > cache_slots)))
     return MDL_ERR_CACHE;
-  if (!aligned16(qkv) || qkv_ld % 8 != 0 || !aligned16(q_out) || !aligned16(k_cache) ||
+  if (!aligned16(qkv) || qkv_ld % 4 != 0 || !aligned16(q_out) || !aligned16(k_cache) ||
       !aligned16(v_cache) || !aligned4(rope_tab))
     return MDL_ERR_ALIGN;
   const int64_t rows = static_cast<int64_t>(batch) * seq;

@@ -1,14 +1,16 @@
 // K3 -- SwiGLU gate: h = silu(rstd*g + b_g) * (rstd*u + b_u), the down-projection input.
 //
-// gate|up come from ONE concatenated GEMM, [rows, 2*d_ff] bf16.  A work item is 8 channels:
-// one 16-byte load from the gate half, one from the up half, 2x32 bytes of fp32 bias (L2
-// resident) and one 16-byte store, so each wavefront streams 1 KiB per operand with no reuse --
-// a pure HBM-bound pass.  rstd applies ln2's RMSNorm multiply deferred past the GEMM.
+// gate|up come from ONE concatenated GEMM, [rows, 2*d_ff] fp32 (the GEMM's unrounded fp32
+// accumulators).  A work item is 8 channels: two 16-byte loads from the gate half, two from the
+// up half, 2x32 bytes of fp32 bias (L2 resident) and two 16-byte stores of h as a hi|lo bf16
+// pair ([rows, 2*d_ff], hi in [0, d_ff), lo in [d_ff, 2*d_ff)), so each wavefront streams 2 KiB
+// per input operand with no reuse -- a pure HBM-bound pass.  rstd applies ln2's RMSNorm
+// multiply deferred past the GEMM.
 #include "common.h"
 
 namespace mdl {
 
-__global__ __launch_bounds__(256) void swiglu_kernel(const uint16_t* __restrict__ gu, int64_t ld,
+__global__ __launch_bounds__(256) void swiglu_kernel(const float* __restrict__ gu, int64_t ld,
                                                      const float* __restrict__ rstd,
                                                      const float* __restrict__ bg,
                                                      const float* __restrict__ bu, int64_t rows,
@@ -18,10 +20,10 @@ __global__ __launch_bounds__(256) void swiglu_kernel(const uint16_t* __restrict_
   if (idx >= rows * per_row) return;
   const int64_t m = idx / per_row;
   const int c = static_cast<int>(idx - m * per_row) * 8;
-  const uint16_t* row = gu + m * ld;
+  const float* row = gu + m * ld;
   float g[8], u[8];
-  unpack8(*reinterpret_cast<const uint4*>(row + c), g);
-  unpack8(*reinterpret_cast<const uint4*>(row + d_ff + c), u);
+  load8f(row + c, g);
+  load8f(row + d_ff + c, u);
   const float r = rstd ? rstd[m] : 1.f;
   float o[8];
 #pragma unroll
@@ -30,20 +32,24 @@ __global__ __launch_bounds__(256) void swiglu_kernel(const uint16_t* __restrict_
     const float b = r * u[i] + (bu ? bu[c + i] : 0.f);
     o[i] = a / (1.f + __expf(-a)) * b;
   }
-  *reinterpret_cast<uint4*>(h + m * d_ff + c) = pack8(o);
+  uint4 hi, lo;
+  split8(o, hi, lo);
+  uint16_t* hr = h + m * 2 * d_ff + c;
+  *reinterpret_cast<uint4*>(hr) = hi;
+  *reinterpret_cast<uint4*>(hr + d_ff) = lo;
 }
 
 }  // namespace mdl
 
 using namespace mdl;
 
-extern "C" int mdl_swiglu(const uint16_t* gate_up, int64_t ld, const float* rstd,
+extern "C" int mdl_swiglu(const float* gate_up, int64_t ld, const float* rstd,
                           const float* bias_gate, const float* bias_up, int rows, int d_ff,
                           uint16_t* h_out, void* stream) {
   if (!gate_up || !h_out) return MDL_ERR_NULL;
   if (rows < 0 || d_ff <= 0 || d_ff % 8 != 0 || ld < 2 * static_cast<int64_t>(d_ff))
     return MDL_ERR_SHAPE;
-  if (!aligned16(gate_up) || ld % 8 != 0 || !aligned16(h_out)) return MDL_ERR_ALIGN;
+  if (!aligned16(gate_up) || ld % 4 != 0 || !aligned16(h_out)) return MDL_ERR_ALIGN;
   if (rows == 0) return MDL_OK;
   const int64_t items = static_cast<int64_t>(rows) * (d_ff / 8);
   swiglu_kernel<<<dim3(static_cast<unsigned>((items + 255) / 256)), 256, 0,

@@ -37,10 +37,13 @@ from .data import (
     generate_color_permutations,
 )
 from .engine import GRID_MAX_X, GRID_MAX_Y, HipEngine, PackedWeights, Scratch, choose_split_len
-from .engine import engine_for
+from .engine import engine_for, gemm_f32
 from .transformer import TinyTransformer, softmax_scale
 
 SYNC_EVERY = 8
+# Replay greedy decode steps from one captured HIP graph (False: launch every kernel from the host
+# each step; same kernels, same results).
+USE_GRAPHS = True
 
 
 # =============================================================================================
@@ -280,12 +283,12 @@ class Generator:
         tok_tab, ex_tab = self.eng._tables()
         use_ex = st.ex if cfg.use_example_embedding else None
         K.embed_rmsnorm(st.tok, use_ex, tok_tab, ex_tab if use_ex is not None else None, 1,
-                        W.ln1[0], W.eps, sc.x, sc.xg, sc.rstd)
+                        W.ln1[0], W.eps, sc.x, sc.xs, sc.rstd)
         qs = softmax_scale(cfg.d_model // H)
         slot = st.counters[0:1]
         for li in range(cfg.n_layers):
             kc, vc = st.cache.layer(li)
-            torch.mm(sc.xg, W.qkv[li].t(), out=sc.qkv)
+            gemm_f32(sc.xs, W.qkv[li], sc.qkv)
             K.qkv_rope_cache(sc.qkv, sc.rstd, st.pos, W.rope_tab, W.rope_geom, B, 1, H, qs,
                              sc.q, kc, vc, slot_dev=slot)
             K.attn_decode(sc.q, kc, vc, B, H, st.pmask, st.S, st.kv_start, 0, slot, st.ws,
@@ -300,6 +303,18 @@ class Generator:
         self.decode_layers(st, W, want_logits=False)
         K.decode_commit(st.tok, st.out_ids, 0, st.counters, st.finish if stop_on_end else None,
                         st.S, END_TOKEN_ID)
+
+    def capture_greedy(self, st: DecodeState, W: PackedWeights,
+                       stop_on_end: bool) -> torch.cuda.CUDAGraph:
+        """Record ``greedy_step`` into a HIP graph.  Every buffer it touches is preallocated in
+        ``st`` and the cache slot / output column advance through ``st.counters`` on the device,
+        so one recording replays as every later step.  Capturing launches nothing; the caller
+        must have run the step eagerly once (library handles and GEMM workspaces initialised).
+        The step records no memset nodes."""
+        g = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(g):
+            self.greedy_step(st, W, stop_on_end)
+        return g
 
 
 def generate_output(model: TinyTransformer, input_ids: torch.Tensor, positions_3d: torch.Tensor,
@@ -344,6 +359,7 @@ def generate_output(model: TinyTransformer, input_ids: torch.Tensor, positions_3
         K.decode_commit(st.tok, st.out_ids, S, None, st.finish if stop_on_end else None, S,
                         END_TOKEN_ID)
         produced = 1
+        graph = None
         for step in range(1, max_new):
             if stop_on_end and (eager or step % SYNC_EVERY == 0) and bool((st.finish >= 0).all()):
                 break
@@ -354,8 +370,12 @@ def generate_output(model: TinyTransformer, input_ids: torch.Tensor, positions_3
                 st.tok.copy_(_pick(st.logits, temperature, top_k))
                 K.decode_commit(st.tok, st.out_ids, 0, st.counters,
                                 st.finish if stop_on_end else None, S, END_TOKEN_ID)
+            elif graph is not None:
+                graph.replay()
             else:
                 gen.greedy_step(st, W, stop_on_end)
+                if USE_GRAPHS and step + 1 < max_new:
+                    graph = gen.capture_greedy(st, W, stop_on_end)
             produced += 1
         g = produced
         if stop_on_end:

@@ -52,8 +52,9 @@ def table_dtype_code(t: torch.Tensor) -> int:
 
 def embed_rmsnorm(ids: torch.Tensor, example_ids: torch.Tensor | None, tok_table: torch.Tensor,
                   ex_table: torch.Tensor | None, row_len: int, gamma: torch.Tensor, eps: float,
-                  x_out: torch.Tensor, xg_out: torch.Tensor | None,
+                  x_out: torch.Tensor, xs_out: torch.Tensor | None,
                   rstd_out: torch.Tensor) -> None:
+    """x = tok[ids] + ex[example_ids], rstd, xs = split(x * gamma) as [rows, 2d] bf16."""
     rows = ids.numel()
     vocab, d = tok_table.shape
     _need(ids, "ids", I64)
@@ -67,27 +68,28 @@ def embed_rmsnorm(ids: torch.Tensor, example_ids: torch.Tensor | None, tok_table
             raise ValueError("example_ids shorter than the number of batch rows")
     _need(gamma, "gamma", F32, d)
     _need(x_out, "x_out", F32, rows * d)
-    _need(xg_out, "xg_out", BF16, rows * d, optional=True)
+    _need(xs_out, "xs_out", BF16, rows * 2 * d, optional=True)
     _need(rstd_out, "rstd_out", F32, rows)
     n_ex = ex_table.shape[0] if ex_table is not None else 0
     _lib.check(_lib.lib().mdl_embed_rmsnorm(
         _p(ids), _p(example_ids), _p(tok_table), _p(ex_table), table_dtype_code(tok_table),
-        vocab, n_ex, rows, row_len, d, _p(gamma), eps, _p(x_out), _p(xg_out), _p(rstd_out),
+        vocab, n_ex, rows, row_len, d, _p(gamma), eps, _p(x_out), _p(xs_out), _p(rstd_out),
         _stream()), "mdl_embed_rmsnorm")
 
 
 def add_rmsnorm(x: torch.Tensor, delta: torch.Tensor | None, bias: torch.Tensor | None,
-                gamma: torch.Tensor, eps: float, xg_out: torch.Tensor | None,
+                gamma: torch.Tensor, eps: float, xs_out: torch.Tensor | None,
                 rstd_out: torch.Tensor) -> None:
+    """x += delta (+ bias) in place (fp32), rstd, xs = split(x * gamma) as [rows, 2d] bf16."""
     rows, d = x.shape
     _need(x, "x", F32)
-    _need(delta, "delta", BF16, rows * d, optional=True)
+    _need(delta, "delta", F32, rows * d, optional=True)
     _need(bias, "bias", F32, d, optional=True)
     _need(gamma, "gamma", F32, d)
-    _need(xg_out, "xg_out", BF16, rows * d, optional=True)
+    _need(xs_out, "xs_out", BF16, rows * 2 * d, optional=True)
     _need(rstd_out, "rstd_out", F32, rows)
     _lib.check(_lib.lib().mdl_add_rmsnorm(
-        _p(x), _p(delta), _p(bias), rows, d, _p(gamma), eps, _p(xg_out), _p(rstd_out),
+        _p(x), _p(delta), _p(bias), rows, d, _p(gamma), eps, _p(xs_out), _p(rstd_out),
         _stream()), "mdl_add_rmsnorm")
 
 
@@ -99,7 +101,7 @@ def qkv_rope_cache(qkv: torch.Tensor, rstd: torch.Tensor | None, pos: torch.Tens
     """rope_geom = (max_x, max_y, max_z, px, py, pz); k/v_cache are one layer's
     [batch, n_heads, slots, 64] bf16 (contiguous views of the static cache)."""
     rows, d = batch * seq, n_heads * HEAD_DIM
-    _need(qkv, "qkv", BF16, rows * 3 * d)
+    _need(qkv, "qkv", F32, rows * 3 * d)
     if qkv.dim() != 2 or qkv.shape[1] != 3 * d:
         raise ValueError(f"qkv must be [rows, {3 * d}]")
     _need(rstd, "rstd", F32, rows, optional=True)
@@ -121,13 +123,14 @@ def qkv_rope_cache(qkv: torch.Tensor, rstd: torch.Tensor | None, pos: torch.Tens
 
 def swiglu(gate_up: torch.Tensor, rstd: torch.Tensor | None, bias_gate: torch.Tensor | None,
            bias_up: torch.Tensor | None, h_out: torch.Tensor) -> None:
+    """h = silu(rstd*g + b_g) * (rstd*u + b_u) from fp32 gate|up, written as split [rows, 2F]."""
     rows, two_f = gate_up.shape
     f = two_f // 2
-    _need(gate_up, "gate_up", BF16)
+    _need(gate_up, "gate_up", F32)
     _need(rstd, "rstd", F32, rows, optional=True)
     _need(bias_gate, "bias_gate", F32, f, optional=True)
     _need(bias_up, "bias_up", F32, f, optional=True)
-    _need(h_out, "h_out", BF16, rows * f)
+    _need(h_out, "h_out", BF16, rows * 2 * f)
     _lib.check(_lib.lib().mdl_swiglu(
         _p(gate_up), two_f, _p(rstd), _p(bias_gate), _p(bias_up), rows, f, _p(h_out),
         _stream()), "mdl_swiglu")
@@ -136,9 +139,10 @@ def swiglu(gate_up: torch.Tensor, rstd: torch.Tensor | None, bias_gate: torch.Te
 def attn_prefill(q: torch.Tensor, k_cache: torch.Tensor, v_cache: torch.Tensor, batch: int,
                  seq: int, n_heads: int, key_mask: torch.Tensor | None,
                  kv_start: torch.Tensor | None, causal: bool, out: torch.Tensor) -> None:
+    """out: split [batch*seq, 2*n_heads*64] bf16."""
     n = batch * seq * n_heads * HEAD_DIM
     _need(q, "q", BF16, n)
-    _need(out, "out", BF16, n)
+    _need(out, "out", BF16, 2 * n)
     for name, c in (("k_cache", k_cache), ("v_cache", v_cache)):
         _need(c, name, BF16)
         if c.dim() != 4 or c.shape[0] != batch or c.shape[1] != n_heads or c.shape[3] != 64:
@@ -159,9 +163,10 @@ def attn_decode(q: torch.Tensor, k_cache: torch.Tensor, v_cache: torch.Tensor, b
                 n_heads: int, prompt_mask: torch.Tensor | None, prompt_len: int,
                 kv_start: torch.Tensor | None, seq_pos: int, seq_dev: torch.Tensor | None,
                 workspace: torch.Tensor | None, split_len: int, out: torch.Tensor) -> None:
+    """out: split [batch, 2*n_heads*64] bf16."""
     n = batch * n_heads * HEAD_DIM
     _need(q, "q", BF16, n)
-    _need(out, "out", BF16, n)
+    _need(out, "out", BF16, 2 * n)
     for name, c in (("k_cache", k_cache), ("v_cache", v_cache)):
         _need(c, name, BF16)
         if c.dim() != 4 or c.shape[0] != batch or c.shape[1] != n_heads or c.shape[3] != 64:

@@ -1,0 +1,134 @@
+"""Seeded synthetic ARC grid-token workloads for the benchmark configurations.
+
+A prompt is ``n_pairs`` demo (input, output) pairs plus one test input, tokenised as the
+reference does (START grid IO_SEP grid END per pair, the test input closed by IO_SEP; src/data.py
+:75-93) with 3D positions from ``compute_positions_3d`` (src/data.py:124-175).  Grid sides are
+uniform in ``[lo, hi]``; a cell is colour 0 with probability 1/2, otherwise uniform over 1..9.
+Task-level variants apply one of the 8 dihedral transforms (src/data.py:224-233) to every grid and
+a random permutation of colours 1..9 with 0 fixed (src/data.py:257-278), as the augmentation
+batching of src/inference.py:794-827 does.  Draws whose prompt length falls outside the stated
+range are rejected and redrawn.
+"""
+
+from __future__ import annotations
+
+from dataclasses import dataclass
+
+import numpy as np
+import torch
+
+from .data import DIHEDRAL_TRANSFORMS, END_TOKEN_ID, compute_positions_3d, encode_example
+
+
+@dataclass(frozen=True)
+class WorkloadSpec:
+    name: str
+    preset: str            # model size (transformer.MODEL_SIZES key)
+    batch: int
+    n_tasks: int           # distinct tasks; batch / n_tasks variants each
+    pairs: tuple[int, int]
+    side: tuple[int, int]
+    prompt_len: tuple[int, int]
+    cache_slots: int
+    max_new: int
+    seed: int
+
+
+# BASELINE.json configs 0 and 2-4 (config 1 is the fused-kernel microbench, no prompts).
+# The stated token ranges and cache sizes are authoritative; where the stated grid sizes cannot
+# meet them, the side range is narrowed so they can:
+#   config 3: 4-5 pairs of 20-30-sided grids give 5,000-10,000 tokens, not 1,500-3,500 -> sides
+#             8-26 (mean ~300 tokens per grid);
+#   config 4: 5 pairs + test of 30x30 grids is 11 x 930 = 10,230 tokens, not ~5,600, and would
+#             not leave 930 decode slots in a 6,656-slot cache -> sides 18-24, prompts
+#             5,000-5,726 tokens (6,656 - 930).
+SPECS = {
+    "tiny_cpu": WorkloadSpec("tiny_cpu", "tiny", 8, 8, (3, 3), (1, 30), (1, 10_000), 0, 64,
+                             20261201),
+    "small_b256": WorkloadSpec("small_b256", "small", 256, 32, (2, 3), (1, 30), (300, 1800),
+                               2048, 930, 20261203),
+    "medium_b128": WorkloadSpec("medium_b128", "medium", 128, 16, (4, 5), (8, 26),
+                                (1500, 3500), 4096, 930, 20261204),
+    "large_b64": WorkloadSpec("large_b64", "large", 64, 8, (5, 5), (18, 24), (5000, 6656 - 930),
+                              6656, 930, 20261205),
+}
+
+MAX_DRAWS = 20_000     # rejection-sampling attempts per task before giving up
+
+
+def random_grid(rng: np.random.Generator, h: int, w: int) -> np.ndarray:
+    g = rng.integers(1, 10, size=(h, w))
+    g[rng.random((h, w)) < 0.5] = 0
+    return g
+
+
+def _draw_task(rng: np.random.Generator, spec: WorkloadSpec) -> list[np.ndarray]:
+    """[in0, out0, in1, out1, ..., test_in] as numpy grids."""
+    n_pairs = int(rng.integers(spec.pairs[0], spec.pairs[1] + 1))
+    lo, hi = spec.side
+    grids = []
+    for _ in range(2 * n_pairs + 1):
+        h, w = rng.integers(lo, hi + 1, size=2)
+        grids.append(random_grid(rng, int(h), int(w)))
+    return grids
+
+
+def _tokens(grids: list[np.ndarray]) -> list[int]:
+    toks: list[int] = []
+    for i in range(0, len(grids) - 1, 2):
+        toks += encode_example(grids[i].tolist(), grids[i + 1].tolist())
+    toks += encode_example(grids[-1].tolist(), None)
+    return toks
+
+
+def _variant(grids: list[np.ndarray], dihedral: int, perm: np.ndarray) -> list[int]:
+    f = DIHEDRAL_TRANSFORMS[dihedral]
+    return _tokens([np.asarray(f(perm[g].tolist()), dtype=np.int64) for g in grids])
+
+
+def build_prompts(spec: WorkloadSpec) -> list[list[int]]:
+    """``spec.batch`` prompts: n_tasks tasks x (batch / n_tasks) dihedral + colour variants."""
+    rng = np.random.default_rng(spec.seed)
+    per_task = spec.batch // spec.n_tasks
+    lo, hi = spec.prompt_len
+    prompts: list[list[int]] = []
+    for _ in range(spec.n_tasks):
+        for _attempt in range(MAX_DRAWS):
+            grids = _draw_task(rng, spec)
+            # cheap pre-check: an h x w grid is h*(w+1) tokens, its transpose w*(h+1); the
+            # variants' lengths lie between the two totals (START/IO_SEP/END added)
+            n_tok = sum(g.shape[0] * (g.shape[1] + 1) for g in grids)
+            n_tok_t = sum(g.shape[1] * (g.shape[0] + 1) for g in grids)
+            n_special = 3 * (len(grids) // 2) + 2
+            if not (lo <= min(n_tok, n_tok_t) + n_special and
+                    max(n_tok, n_tok_t) + n_special <= hi):
+                continue
+            variants = []
+            for v in range(per_task):
+                perm = np.arange(10, dtype=np.int64)
+                if v > 0:
+                    perm[1:] = rng.permutation(np.arange(1, 10))
+                variants.append(_variant(grids, v % 8, perm))
+            if all(lo <= len(t) <= hi for t in variants):
+                break
+        else:
+            raise RuntimeError(f"{spec.name}: no task within {spec.prompt_len} tokens after "
+                               f"{MAX_DRAWS} draws; widen the grid-side range")
+        prompts += variants
+    return prompts
+
+
+def left_pad(prompts: list[list[int]]) -> tuple[torch.Tensor, torch.Tensor, torch.Tensor]:
+    """Left-pad with END and position (0,0,0); bool mask of real tokens (src/inference.py:
+    877-890).  Returns CPU tensors ids [B,S], pos [B,S,3], mask [B,S]."""
+    S = max(len(p) for p in prompts)
+    B = len(prompts)
+    ids = np.full((B, S), END_TOKEN_ID, dtype=np.int64)
+    pos = np.zeros((B, S, 3), dtype=np.int64)
+    mask = np.zeros((B, S), dtype=bool)
+    for b, p in enumerate(prompts):
+        n = len(p)
+        ids[b, S - n:] = p
+        pos[b, S - n:] = compute_positions_3d(p)
+        mask[b, S - n:] = True
+    return torch.from_numpy(ids), torch.from_numpy(pos), torch.from_numpy(mask)

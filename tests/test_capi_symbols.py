@@ -1,0 +1,55 @@
+"""The C-ABI library loads on a machine without a GPU and exports exactly what
+include/mdlarc_hip.h declares (no compute calls: those need a GPU)."""
+
+import ctypes
+
+import pytest
+
+from mdlarc_scale_amd import _lib
+
+
+def _require_lib():
+    if not _lib.available():
+        pytest.skip("libmdlarc_hip.so not built (python -m mdlarc_scale_amd.build)")
+
+
+def test_header_declares_every_bound_symbol():
+    declared = _lib.header_symbols()
+    assert len(declared) == len(set(declared))
+    assert sorted(declared) == sorted(_lib.SIGNATURES)
+
+
+def test_library_exports_every_declared_symbol():
+    _require_lib()
+    handle = ctypes.CDLL(str(_lib.LIB_PATH))
+    for name in _lib.header_symbols():
+        assert hasattr(handle, name), f"{name} declared in the header but not exported"
+
+
+def test_host_only_entry_points():
+    """Entry points that do no device work answer without a GPU."""
+    _require_lib()
+    L = _lib.lib()
+    assert L.mdl_version() >= 100
+    assert L.mdl_error_string(0) == b"ok"
+    assert b"head_dim" in L.mdl_error_string(-4)
+    # workspace sizing is host arithmetic: one split needs none, several need B*H*splits*66 fp32
+    assert L.mdl_attn_decode_workspace_bytes(4, 2, 256, 256) == 0
+    assert L.mdl_attn_decode_workspace_bytes(4, 2, 1024, 256) == 4 * 2 * 4 * 66 * 4
+
+
+def test_argument_errors_are_reported_before_any_launch():
+    """Shape / pointer checks return negative codes on the host, without touching a device."""
+    _require_lib()
+    L = _lib.lib()
+    fake = 1 << 20                                  # never dereferenced: rejected first
+    assert L.mdl_attn_prefill(fake, fake, fake, 1, 4, 1, 32, 4, None, None, 1, fake, None) == -4
+    assert L.mdl_swiglu(None, 16, None, None, None, 1, 8, fake, None) == -1
+    assert L.mdl_swiglu(fake, 16, None, None, None, 1, 12, fake, None) == -3
+    assert L.mdl_swiglu(fake + 2, 16, None, None, None, 1, 8, fake, None) == -2
+    assert L.mdl_qkv_rope_cache(fake, 192, None, fake, fake, 1, 4, 1, 64, 32, 32, 8, 10, 10, 12,
+                                0.125, fake, fake, fake, 4, 1, None, None) == -5
+    assert L.mdl_attn_decode(fake, fake, fake, 1, 1, 64, 1024, None, 0, None, 5, None, None, 0,
+                             128, fake, None) == -6
+    with pytest.raises(RuntimeError, match="head_dim"):
+        _lib.check(-4, "probe")
