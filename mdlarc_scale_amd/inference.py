@@ -118,11 +118,15 @@ class StaticKVCache:
     The HIP path keeps it in bf16 (the attention kernels' operand type)."""
 
     def __init__(self, batch_size: int, max_seq_len: int, n_layers: int, n_heads: int,
-                 head_dim: int, device: torch.device, dtype: torch.dtype = torch.bfloat16):
+                 head_dim: int, device: torch.device, dtype: torch.dtype = torch.bfloat16, *,
+                 zero: bool = True):
+        """``zero=False`` skips the initial fill: the generation path writes every slot before
+        any kernel reads it (prefill writes [0, S), each decode step writes its slot first)."""
         self.batch_size, self.max_seq_len, self.n_layers = batch_size, max_seq_len, n_layers
         self.seq_len = 0
-        self.cache = torch.zeros(n_layers, 2, batch_size, n_heads, max_seq_len, head_dim,
-                                 device=device, dtype=dtype)
+        alloc = torch.zeros if zero else torch.empty
+        self.cache = alloc(n_layers, 2, batch_size, n_heads, max_seq_len, head_dim,
+                           device=device, dtype=dtype)
 
     def reset(self) -> None:
         self.cache.zero_()
@@ -242,7 +246,7 @@ class Generator:
         dev = input_ids.device
         B, S = input_ids.shape
         H, hd = cfg.n_heads, cfg.d_model // cfg.n_heads
-        cache = StaticKVCache(B, total, cfg.n_layers, H, hd, dev)
+        cache = StaticKVCache(B, total, cfg.n_layers, H, hd, dev, zero=False)
         pmask = prompt_mask.to(torch.uint8).contiguous()
         i32 = lambda: torch.empty(B, dtype=torch.int32, device=dev)  # noqa: E731
         gx, gy, kv_start, last_row = i32(), i32(), i32(), i32()
@@ -272,7 +276,7 @@ class Generator:
         self.eng.run_prompt(W, input_ids, positions_3d, st.ex, st.pmask, st.kv_start, True,
                             st.cache.layer, sc)
         K.lm_head(sc.x, st.last_row, st.B, W.ln_f, W.eps, W.head, st.logits, st.tok)
-        st.cache.advance(st.S)
+        st.cache.seq_len = st.S
 
     def decode_layers(self, st: DecodeState, W: PackedWeights, want_logits: bool) -> None:
         """``_decode_step`` (src/inference.py:427-459) for the token in ``st.tok`` at the
@@ -328,10 +332,17 @@ def generate_output(model: TinyTransformer, input_ids: torch.Tensor, positions_3
     path needs no compiler."""
     del use_compile
     model.eval()
-    eng = engine_for(model)
-    dev = eng._check_device(input_ids)
     cfg = model.config
     B, S = input_ids.shape
+    # argument checks and the early return in the reference's order (src/inference.py:527-537)
+    if attention_mask is not None and tuple(attention_mask.shape) != (B, S):
+        raise ValueError("attention_mask must have shape [batch, seq_len]")
+    total = min(S + max_new_tokens, cfg.max_seq_len)
+    max_new = total - S
+    if max_new <= 0:
+        return input_ids
+    eng = engine_for(model)
+    dev = eng._check_device(input_ids)
     ids = input_ids.to(torch.int64).contiguous()
     pos = positions_3d.to(device=dev, dtype=torch.int64).contiguous()
     ex = (torch.zeros(B, dtype=torch.int64, device=dev) if example_ids is None
@@ -339,13 +350,7 @@ def generate_output(model: TinyTransformer, input_ids: torch.Tensor, positions_3
     if attention_mask is None:
         prompt_mask = torch.ones(B, S, dtype=torch.bool, device=dev)
     else:
-        if tuple(attention_mask.shape) != (B, S):
-            raise ValueError("attention_mask must have shape [batch, seq_len]")
         prompt_mask = attention_mask.to(device=dev, dtype=torch.bool)
-    total = min(S + max_new_tokens, cfg.max_seq_len)
-    max_new = total - S
-    if max_new <= 0:
-        return input_ids
     eng._validate_ids(ids, ex)
     gen = Generator(model)
     with torch.no_grad():
