@@ -297,27 +297,24 @@ def main() -> int:
         wall_s = time.perf_counter() - wall0
         timed_ms = tm.ms()
 
-        # decode attention: re-issue the timed region's launches one by one with HIP events
+        # decode attention: re-issue the timed region's launches (every layer at every cache
+        # position t of the timed steps) back to back on the launching stream, between one pair
+        # of HIP events; the queue never drains, so the events time kernel execution only
         H = cfg.n_heads
         kv_start_h = st.kv_start.cpu()
-        ev = []
-        for i in range(args.steps):
-            t = t_first + i
-            for li in range(cfg.n_layers):
-                kc, vc = st.cache.layer(li)
-                a = torch.cuda.Event(enable_timing=True)
-                b = torch.cuda.Event(enable_timing=True)
-                a.record()
-                K.attn_decode(st.sc.q, kc, vc, B, H, st.pmask, S, st.kv_start, t, None, st.ws,
-                              st.split_len, st.sc.attn)
-                b.record()
-                ev.append((a, b, t))
-        torch.cuda.synchronize()
-        durs = [a.elapsed_time(b) for a, b, _ in ev]
-        bytes_l = [decode_attention_bytes(B, H, t, kv_start_h, S) for _, _, t in ev]
-        attn_ms = sum(durs) / len(durs)
-        attn_bytes = sum(bytes_l) / len(bytes_l)
+        ts = [t_first + i for i in range(args.steps) for _ in range(cfg.n_layers)]
+        layers = [li for _ in range(args.steps) for li in range(cfg.n_layers)]
+        ta = Timer()
+        ta.start()
+        for t, li in zip(ts, layers):
+            kc, vc = st.cache.layer(li)
+            K.attn_decode(st.sc.q, kc, vc, B, H, st.pmask, S, st.kv_start, t, None, st.ws,
+                          st.split_len, st.sc.attn, row_holes=st.holes, row_order=st.order)
+        ta.stop()
+        attn_ms = ta.ms() / len(ts)
+        attn_bytes = sum(decode_attention_bytes(B, H, t, kv_start_h, S) for t in ts) / len(ts)
         achieved = attn_bytes / attn_ms / 1e6
+        durs = ts
 
         micro = None if args.no_micro else microbench(dev)
 

@@ -65,6 +65,20 @@ int mdl_embed_rmsnorm(const int64_t* ids, const int64_t* example_ids, const void
                       uint16_t* xs_out, float* rstd_out, void* stream);
 
 /*
+ * Decode-step entry: grid position of the token each row just emitted, then K1 on that token.
+ * Replaces: GridStateUpdater.update (src/inference.py:127-168) followed by the embedding and
+ *           blocks[0].ln1 of _decode_step (src/inference.py:433-437).
+ * Per row b: pos_out[b] = position of token[b] from the state (gx, gy, in_out), the state
+ * advances past it (the rule of mdl_grid_step), then x / xs / rstd as mdl_embed_rmsnorm with
+ * row_len = 1.  counters (int32[2], may be NULL) are incremented by one, as by mdl_grid_step.
+ */
+int mdl_decode_embed(const int64_t* token, const int64_t* example_ids, const void* tok_table,
+                     const void* ex_table, int table_dtype, int vocab, int n_examples, int batch,
+                     int d, const float* gamma, float eps, int32_t* gx, int32_t* gy,
+                     uint8_t* in_out, int max_x, int max_y, int64_t* pos_out, int32_t* counters,
+                     float* x_out, uint16_t* xs_out, float* rstd_out, void* stream);
+
+/*
  * Residual add fused with the next RMSNorm's reduction.
  * Replaces: the residual adds of TransformerBlock.forward (src/transformer.py:494-496),
  *           _prefill / _decode_step (src/inference.py:412-413, :455-456), the fc_down bias
@@ -134,15 +148,21 @@ int mdl_attn_prefill(const uint16_t* q, const uint16_t* k_cache, const uint16_t*
  * The query of row b sees slot j iff
  *   kv_start[b] <= j <= t, t = (seq_dev ? *seq_dev : seq_pos), and
  *   (j >= prompt_len || prompt_mask[b*prompt_len + j] != 0)   (prompt_mask may be NULL).
+ * row_holes (uint8 [batch], may be NULL): 0 promises that row b's prompt mask is set exactly
+ *   on [kv_start[b], prompt_len), so the kernel skips reading it (mdl_grid_init computes it).
+ * row_order (int32 [batch], may be NULL): a permutation of the rows giving the order their work
+ *   is dispatched in; longest-first (ascending kv_start) shortens the launch's tail.
  * workspace: fp32, at least mdl_attn_decode_workspace_bytes(...) bytes (may be NULL when
  *   that is 0).  split_len: slots per work item (multiple of 128, >= 128).
  */
 int64_t mdl_attn_decode_workspace_bytes(int batch, int n_heads, int cache_slots, int split_len);
 int mdl_attn_decode(const uint16_t* q, const uint16_t* k_cache, const uint16_t* v_cache,
                     int batch, int n_heads, int head_dim, int cache_slots,
-                    const uint8_t* prompt_mask, int prompt_len, const int32_t* kv_start,
-                    int seq_pos, const int32_t* seq_dev, float* workspace,
-                    int64_t workspace_bytes, int split_len, uint16_t* out, void* stream);
+                    const uint8_t* prompt_mask, int prompt_len, const uint8_t* row_holes,
+                    const int32_t* kv_start, const int32_t* row_order, int seq_pos,
+                    const int32_t* seq_dev,
+                    float* workspace, int64_t workspace_bytes, int split_len, uint16_t* out,
+                    void* stream);
 
 /*
  * Final RMSNorm + LM head + greedy argmax.
@@ -157,16 +177,31 @@ int mdl_lm_head(const float* x, const int32_t* row_index, int rows, int d, const
                 void* stream);
 
 /*
+ * Decode-step tail: final RMSNorm + LM head + greedy argmax + token commit in one launch.
+ * Replaces: lm_head(ln_f(x)) and argmax of _decode_step / generate_output
+ *           (src/inference.py:459, :610-611), generated.append and finished |= END
+ *           (src/inference.py:589-590, :622-626).
+ * token_out[b] = argmax; out_ids[b*out_ld + c] = token_out[b] with c = (counters ? counters[1]
+ * : col); finish_step[b] (may be NULL) = c - gen_base at the first END.  logits_out may be NULL.
+ */
+int mdl_decode_head(const float* x, int batch, int d, const float* gamma, float eps,
+                    const float* w_head, int vocab, float* logits_out, int64_t* token_out,
+                    int64_t* out_ids, int64_t out_ld, int col, const int32_t* counters,
+                    int32_t* finish_step, int gen_base, int end_id, void* stream);
+
+/*
  * Grid-state initialisation from the prompt.
  * Replaces: _derive_initial_state_from_prompt (src/inference.py:171-221) and the
  *           lengths-1 index of _prefill (src/inference.py:420-424).
  * ids int64 [batch, seq], pos int64 [batch, seq, 3], mask uint8 [batch, seq] or NULL (all valid).
  * Outputs per row: gx, gy (int32), in_out (uint8), kv_start = first valid index (seq if none),
- * last_row = b*seq + max(len-1, 0) (the row the reference's prefill reads its logits from).
+ * last_row = b*seq + max(len-1, 0) (the row the reference's prefill reads its logits from),
+ * row_holes = 1 if the valid positions are not the single run [kv_start, seq), else 0.
+ * kv_start / last_row / row_holes may each be NULL.
  */
 int mdl_grid_init(const int64_t* ids, const int64_t* pos, const uint8_t* mask, int batch,
                   int seq, int max_x, int max_y, int32_t* gx, int32_t* gy, uint8_t* in_out,
-                  int32_t* kv_start, int32_t* last_row, void* stream);
+                  int32_t* kv_start, int32_t* last_row, uint8_t* row_holes, void* stream);
 
 /*
  * One grid-state step: position of the token each row just emitted, then advance the state.

@@ -25,6 +25,8 @@ SIGNATURES: dict[str, tuple[object, list]] = {
     "mdl_error_string": (ctypes.c_char_p, [c_int]),
     "mdl_embed_rmsnorm": (c_int, [P, P, P, P, c_int, c_int, c_int, c_int, c_int, c_int, P,
                                   c_float, P, P, P, P]),
+    "mdl_decode_embed": (c_int, [P, P, P, P, c_int, c_int, c_int, c_int, c_int, P, c_float, P,
+                                 P, P, c_int, c_int, P, P, P, P, P, P]),
     "mdl_add_rmsnorm": (c_int, [P, P, P, c_int, c_int, P, c_float, P, P, P]),
     "mdl_qkv_rope_cache": (c_int, [P, c_int64, P, P, P, c_int, c_int, c_int, c_int, c_int, c_int,
                                    c_int, c_int, c_int, c_int, c_float, P, P, P, c_int, c_int, P,
@@ -32,10 +34,12 @@ SIGNATURES: dict[str, tuple[object, list]] = {
     "mdl_swiglu": (c_int, [P, c_int64, P, P, P, c_int, c_int, P, P]),
     "mdl_attn_prefill": (c_int, [P, P, P, c_int, c_int, c_int, c_int, c_int, P, P, c_int, P, P]),
     "mdl_attn_decode_workspace_bytes": (c_int64, [c_int, c_int, c_int, c_int]),
-    "mdl_attn_decode": (c_int, [P, P, P, c_int, c_int, c_int, c_int, P, c_int, P, c_int, P, P,
-                                c_int64, c_int, P, P]),
+    "mdl_attn_decode": (c_int, [P, P, P, c_int, c_int, c_int, c_int, P, c_int, P, P, P, c_int,
+                                P, P, c_int64, c_int, P, P]),
     "mdl_lm_head": (c_int, [P, P, c_int, c_int, P, c_float, P, c_int, P, P, P]),
-    "mdl_grid_init": (c_int, [P, P, P, c_int, c_int, c_int, c_int, P, P, P, P, P, P]),
+    "mdl_decode_head": (c_int, [P, c_int, c_int, P, c_float, P, c_int, P, P, P, c_int64, c_int,
+                                P, P, c_int, c_int, P]),
+    "mdl_grid_init": (c_int, [P, P, P, c_int, c_int, c_int, c_int, P, P, P, P, P, P, P]),
     "mdl_grid_step": (c_int, [P, c_int, c_int, c_int, P, P, P, P, P, P]),
     "mdl_decode_commit": (c_int, [P, c_int, P, c_int64, c_int, P, P, c_int, c_int, P]),
 }

@@ -7,10 +7,13 @@
 // arithmetic, so each lane keeps 2*U 16-byte loads in flight.  Scores are reduced over the 8
 // lanes of a group with 3 xor-shuffles; every group keeps its own online-softmax state (max, sum,
 // 8 accumulators) in the log2 domain.  At the end the 8 groups, then the 4 waves (LDS), then the
-// splits (second kernel) are merged with the usual max-rescaled sums.
+// splits (second kernel) are merged with the usual max-rescaled sums.  K and V are streamed with
+// non-temporal loads (read once per launch; keeps the projection weights cached between layers).
 //
 // Slot j of row b is visible iff kv_start[b] <= j <= t and (j >= prompt_len or
 // prompt_mask[b, j]), the decode mask of the reference (prompt mask, then every generated slot).
+// row_holes[b] == 0 (from mdl_grid_init) says the prompt mask of row b is one contiguous run
+// starting at kv_start[b]; such rows skip the per-slot mask reads.
 #include "common.h"
 
 namespace mdl {
@@ -34,12 +37,17 @@ template <int U>
 __global__ __launch_bounds__(256) void attn_decode_kernel(
     const uint16_t* __restrict__ q, const uint16_t* __restrict__ kc,
     const uint16_t* __restrict__ vc, int n_heads, int slots, const uint8_t* __restrict__ pmask,
-    int plen, const int32_t* __restrict__ kv_start, int seq_pos,
-    const int32_t* __restrict__ seq_dev, int n_split, int split_len, float* __restrict__ ws,
-    uint16_t* __restrict__ out) {
-  const int bh = blockIdx.x;
+    int plen, const uint8_t* __restrict__ row_holes, const int32_t* __restrict__ kv_start,
+    const int32_t* __restrict__ row_order, int seq_pos, const int32_t* __restrict__ seq_dev,
+    int n_split, int split_len, float* __restrict__ ws, uint16_t* __restrict__ out) {
+  // blocks are dispatched in blockIdx order; row_order lists the rows longest-first so the
+  // short rows fill the tail of the launch
+  const int ri = blockIdx.x / n_heads;
+  const int n_rows = gridDim.x / n_heads;
+  // a caller's bad permutation entry is clamped into range: wrong rows, never a wild address
+  const int b = row_order ? min(max(row_order[ri], 0), n_rows - 1) : ri;
+  const int bh = b * n_heads + (blockIdx.x - ri * n_heads);
   const int split = blockIdx.y;
-  const int b = bh / n_heads;
   const int wave = threadIdx.x >> 6;
   const int lane = threadIdx.x & 63;
   const int grp = lane >> 3;
@@ -63,7 +71,9 @@ __global__ __launch_bounds__(256) void attn_decode_kernel(
     for (int i = 0; i < 8; ++i) qf[i] *= kLog2e;
     const uint16_t* K = kc + static_cast<int64_t>(bh) * slots * kHeadDim + sub * 8;
     const uint16_t* V = vc + static_cast<int64_t>(bh) * slots * kHeadDim + sub * 8;
-    const uint8_t* pm = pmask ? pmask + static_cast<int64_t>(b) * plen : nullptr;
+    // rows whose prompt mask is one contiguous run from kv_start need no per-slot mask reads
+    const bool dense = row_holes && row_holes[b] == 0;
+    const uint8_t* pm = (pmask && !dense) ? pmask + static_cast<int64_t>(b) * plen : nullptr;
 
     for (int base = lo + wave * 8 * U; base < hi; base += 4 * 8 * U) {
       uint4 kr[U], vr[U];
@@ -73,8 +83,8 @@ __global__ __launch_bounds__(256) void attn_decode_kernel(
         const int j = base + u * 8 + grp;
         ok[u] = j < hi;
         if (ok[u]) {
-          kr[u] = *reinterpret_cast<const uint4*>(K + static_cast<int64_t>(j) * kHeadDim);
-          vr[u] = *reinterpret_cast<const uint4*>(V + static_cast<int64_t>(j) * kHeadDim);
+          kr[u] = load_nt16(K + static_cast<int64_t>(j) * kHeadDim);
+          vr[u] = load_nt16(V + static_cast<int64_t>(j) * kHeadDim);
           if (pm && j < plen) ok[u] = pm[j] != 0;
         } else {
           kr[u] = make_uint4(0, 0, 0, 0);
@@ -208,9 +218,11 @@ extern "C" int64_t mdl_attn_decode_workspace_bytes(int batch, int n_heads, int c
 extern "C" int mdl_attn_decode(const uint16_t* q, const uint16_t* k_cache,
                                const uint16_t* v_cache, int batch, int n_heads, int head_dim,
                                int cache_slots, const uint8_t* prompt_mask, int prompt_len,
-                               const int32_t* kv_start, int seq_pos, const int32_t* seq_dev,
-                               float* workspace, int64_t workspace_bytes, int split_len,
-                               uint16_t* out, void* stream) {
+                               const uint8_t* row_holes, const int32_t* kv_start,
+                               const int32_t* row_order, int seq_pos,
+                               const int32_t* seq_dev, float* workspace,
+                               int64_t workspace_bytes, int split_len, uint16_t* out,
+                               void* stream) {
   if (!q || !k_cache || !v_cache || !out) return MDL_ERR_NULL;
   if (head_dim != kHeadDim) return MDL_ERR_HEAD_DIM;
   if (batch < 0 || n_heads <= 0 || cache_slots <= 0 || prompt_len < 0 ||
@@ -227,8 +239,8 @@ extern "C" int mdl_attn_decode(const uint16_t* q, const uint16_t* k_cache,
   hipStream_t s = static_cast<hipStream_t>(stream);
   const int n_bh = batch * n_heads;
   attn_decode_kernel<kUnroll><<<dim3(n_bh, ns), 256, 0, s>>>(
-      q, k_cache, v_cache, n_heads, cache_slots, prompt_mask, prompt_len, kv_start, seq_pos,
-      seq_dev, ns, split_len, workspace, out);
+      q, k_cache, v_cache, n_heads, cache_slots, prompt_mask, prompt_len, row_holes, kv_start,
+      row_order, seq_pos, seq_dev, ns, split_len, workspace, out);
   if (ns > 1)
     attn_decode_combine_kernel<<<dim3((n_bh + 3) / 4), 256, 0, s>>>(workspace, n_bh, n_heads,
                                                                      ns, out);

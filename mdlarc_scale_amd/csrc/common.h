@@ -66,6 +66,17 @@ __device__ __forceinline__ void split8(const float* f, uint4& hi, uint4& lo) {
   split_bf2(f[6], f[7], hi.w, lo.w);
 }
 
+// 16-byte streaming load with the non-temporal hint.  Data read once per kernel (the KV cache
+// in decode attention) then does not displace what later kernels reuse from the caches (the
+// projection weights), and on MI355X the stream itself runs faster: decode attention measured
+// 6.75 TB/s with it against 5.9 TB/s with plain loads.
+typedef unsigned int u32x4_t __attribute__((ext_vector_type(4)));
+
+__device__ __forceinline__ uint4 load_nt16(const void* p) {
+  const u32x4_t v = __builtin_nontemporal_load(reinterpret_cast<const u32x4_t*>(p));
+  return make_uint4(v.x, v.y, v.z, v.w);
+}
+
 __device__ __forceinline__ void load8f(const float* p, float* f) {
   const float4 a = *reinterpret_cast<const float4*>(p);
   const float4 b = *reinterpret_cast<const float4*>(p + 4);

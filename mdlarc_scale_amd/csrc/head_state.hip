@@ -1,35 +1,36 @@
-// Final RMSNorm + LM head + greedy argmax, grid-state position tracking and token commit.
+// Final RMSNorm + LM head + greedy argmax (+ token commit), grid-state initialisation and
+// stepping, token commit.
 //
 // These are the per-step bookkeeping kernels of batched greedy decode: everything the reference
 // does between two decode steps on tiny [B] / [B, 14] tensors (about 40 eager launches) becomes
-// three launches that keep state on the device, so a decode step needs no host round trip.
+// a couple of launches that keep state on the device, so a decode step needs no host round trip.
 #include "common.h"
+#include "grid.h"
 
 namespace mdl {
 
 constexpr int kVmax = 32;
 
-// One wavefront per output row.  The lane keeps 4-channel chunks of x in registers, reduces the
-// sum of squares, then accumulates all vocab dot products at once and reduces them together.
-template <int NC>
-__global__ __launch_bounds__(256) void lm_head_kernel(const float* __restrict__ x,
-                                                      const int32_t* __restrict__ row_index,
-                                                      int rows, int d,
-                                                      const float* __restrict__ gamma, float eps,
-                                                      const float* __restrict__ w, int vocab,
-                                                      float* __restrict__ logits,
-                                                      int64_t* __restrict__ token) {
-  const int lane = threadIdx.x & 63;
-  const int r = blockIdx.x * 4 + (threadIdx.x >> 6);
-  if (r >= rows) return;
-  const int64_t m = row_index ? row_index[r] : r;
-  const float* xr = x + m * d;
+// One wavefront per output row.  The lane keeps NC 4-channel chunks of x * gamma in registers,
+// reduces the sum of squares, accumulates its partial dot product with every vocab row, then
+// reduces all NV partials at once with a reduce-scatter butterfly: at level k (xor 32 >> k) a
+// lane keeps one half of its values and adds the partner's copy of that half, so log2(NV)
+// levels of NV/2, NV/4, ... exchanges plus 6 - log2(NV) plain levels (NV - 1 + 6 - log2(NV)
+// shuffles in all, instead of NV full wave reductions) leave lane l holding the logit of vocab
+// slot l >> (6 - log2(NV)).  The argmax is then one (value, index) wave reduction that keeps the
+// first index on ties (torch argmax).
+template <int NC, int NV>
+__device__ __forceinline__ void head_row(const float* __restrict__ xr, int lane, int d,
+                                         const float* __restrict__ gamma, float eps,
+                                         const float* __restrict__ w, int vocab, float& logit,
+                                         int& slot, int& best) {
+  constexpr int LOG_NV = NV == 16 ? 4 : 5;
   float v[NC][4];
   float ss = 0.f;
 #pragma unroll
   for (int i = 0; i < NC; ++i) {
     const int e = 4 * (lane + 64 * i);
-    if (e < d) {
+    if (i < NC - 1 || e < d) {
       const float4 a = *reinterpret_cast<const float4*>(xr + e);
       const float4 gm = *reinterpret_cast<const float4*>(gamma + e);
       ss += a.x * a.x + a.y * a.y + a.z * a.z + a.w * a.w;
@@ -38,64 +39,117 @@ __global__ __launch_bounds__(256) void lm_head_kernel(const float* __restrict__ 
       v[i][0] = v[i][1] = v[i][2] = v[i][3] = 0.f;
     }
   }
+  // Slots t >= vocab re-read the last vocab row (an L1 hit) instead of branching around their
+  // loads: with the loads unconditional all NV x NC of them are in flight at once, where a
+  // per-row branch serialises them into NV dependent memory round trips.  Those slots never
+  // reach the logits or the argmax.
+  float acc[NV];
+#pragma unroll
+  for (int t = 0; t < NV; ++t) {
+    acc[t] = 0.f;
+    const float* wr = w + static_cast<int64_t>(t < vocab ? t : vocab - 1) * d;
+#pragma unroll
+    for (int i = 0; i < NC; ++i) {
+      const int e = 4 * (lane + 64 * i);
+      if (i < NC - 1 || e < d) {
+        const float4 wv = *reinterpret_cast<const float4*>(wr + e);
+        acc[t] += v[i][0] * wv.x + v[i][1] * wv.y + v[i][2] * wv.z + v[i][3] * wv.w;
+      }
+    }
+  }
   ss = wave_sum(ss);
   const float rs = rsqrtf(ss / static_cast<float>(d) + eps);
-  float acc[kVmax];
 #pragma unroll
-  for (int t = 0; t < kVmax; ++t) {
-    acc[t] = 0.f;
-    if (t < vocab) {
+  for (int lvl = 0; lvl < LOG_NV; ++lvl) {
+    const int half = NV >> (lvl + 1);
+    const int mask = 32 >> lvl;
+    const bool up = (lane & mask) != 0;
 #pragma unroll
-      for (int i = 0; i < NC; ++i) {
-        const int e = 4 * (lane + 64 * i);
-        if (e < d) {
-          const float4 wv = *reinterpret_cast<const float4*>(w + static_cast<int64_t>(t) * d + e);
-          acc[t] += v[i][0] * wv.x + v[i][1] * wv.y + v[i][2] * wv.z + v[i][3] * wv.w;
-        }
-      }
-      acc[t] = wave_sum(acc[t]) * rs;
-    }
-  }
-  if (lane == 0) {
-    int best = 0;
-    float bv = acc[0];
-#pragma unroll
-    for (int t = 1; t < kVmax; ++t) {
-      if (t < vocab && acc[t] > bv) {   // strict: first index wins ties
-        bv = acc[t];
-        best = t;
+    for (int k = 0; k < NV / 2; ++k) {
+      if (k < half) {
+        const float keep = up ? acc[half + k] : acc[k];
+        const float send = up ? acc[k] : acc[half + k];
+        acc[k] = keep + __shfl_xor(send, mask, kWave);
       }
     }
-    if (token) token[r] = best;
   }
-  if (logits && lane < vocab) {
-    float val = 0.f;
+  float tot = acc[0];
 #pragma unroll
-    for (int t = 0; t < kVmax; ++t)
-      if (t == lane) val = acc[t];
-    logits[static_cast<int64_t>(r) * vocab + lane] = val;
+  for (int mask = 32 >> LOG_NV; mask > 0; mask >>= 1) tot += __shfl_xor(tot, mask, kWave);
+  slot = lane >> (6 - LOG_NV);
+  logit = tot * rs;
+  float bv = slot < vocab ? logit : -INFINITY;
+  int bi = slot;
+#pragma unroll
+  for (int mask = 32; mask > 0; mask >>= 1) {
+    const float ov = __shfl_xor(bv, mask, kWave);
+    const int oi = __shfl_xor(bi, mask, kWave);
+    if (ov > bv || (ov == bv && oi < bi)) {
+      bv = ov;
+      bi = oi;
+    }
+  }
+  best = bi;
+}
+
+// Logits (optional) and argmax of rows r: x row = row_index ? row_index[r] : r.  With out_ids
+// the kernel also commits the token (the decode-step tail): out_ids[r, c] = token,
+// c = counters ? counters[1] : col, and records the first END per row in finish.
+template <int NC, int NV>
+__global__ __launch_bounds__(256) void head_kernel(
+    const float* __restrict__ x, const int32_t* __restrict__ row_index, int rows, int d,
+    const float* __restrict__ gamma, float eps, const float* __restrict__ w, int vocab,
+    float* __restrict__ logits, int64_t* __restrict__ token, int64_t* __restrict__ out_ids,
+    int64_t ld, int col, const int32_t* __restrict__ counters, int32_t* __restrict__ finish,
+    int gen_base, int64_t end_id) {
+  const int lane = threadIdx.x & 63;
+  const int r = blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (r >= rows) return;
+  const int64_t m = row_index ? row_index[r] : r;
+  float logit;
+  int slot, best;
+  head_row<NC, NV>(x + m * d, lane, d, gamma, eps, w, vocab, logit, slot, best);
+  constexpr int kGroup = NV == 16 ? 4 : 2;          // lanes holding the same vocab slot
+  if (logits && (lane & (kGroup - 1)) == 0 && slot < vocab)
+    logits[static_cast<int64_t>(r) * vocab + slot] = logit;
+  if (lane != 0) return;
+  if (token) token[r] = best;
+  if (out_ids) {
+    const int c = counters ? counters[1] : col;
+    if (c < 0 || c >= ld) return;   // more steps than output columns: never write outside
+    out_ids[static_cast<int64_t>(r) * ld + c] = best;
+    if (finish && best == end_id && finish[r] < 0) finish[r] = c - gen_base;
   }
 }
 
-constexpr int64_t kStart = 10, kNewline = 11, kSep = 12, kEnd = 13;
-
-__device__ __forceinline__ int64_t clampi(int64_t v, int64_t lo, int64_t hi) {
-  return v < lo ? lo : (v > hi ? hi : v);
-}
-
-__global__ void grid_init_kernel(const int64_t* __restrict__ ids, const int64_t* __restrict__ pos,
-                                 const uint8_t* __restrict__ mask, int batch, int seq, int max_x,
-                                 int max_y, int32_t* gx, int32_t* gy, uint8_t* io,
-                                 int32_t* kv_start, int32_t* last_row) {
-  const int b = blockIdx.x * blockDim.x + threadIdx.x;
+__global__ __launch_bounds__(256) void grid_init_kernel(
+    const int64_t* __restrict__ ids, const int64_t* __restrict__ pos,
+    const uint8_t* __restrict__ mask, int batch, int seq, int max_x, int max_y, int32_t* gx,
+    int32_t* gy, uint8_t* io, int32_t* kv_start, int32_t* last_row, uint8_t* row_holes) {
+  // one wavefront per batch row: the lanes scan the mask row together
+  const int lane = threadIdx.x & 63;
+  const int b = blockIdx.x * 4 + (threadIdx.x >> 6);
   if (b >= batch) return;
   int n = 0, first = seq;
-  for (int j = 0; j < seq; ++j) {
-    if (!mask || mask[static_cast<int64_t>(b) * seq + j]) {
-      if (n == 0) first = j;
-      ++n;
+  if (mask) {
+    const uint8_t* mr = mask + static_cast<int64_t>(b) * seq;
+    for (int j = lane; j < seq; j += kWave) {
+      if (mr[j]) {
+        ++n;
+        first = min(first, j);
+      }
     }
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) {
+      n += __shfl_xor(n, o, kWave);
+      first = min(first, __shfl_xor(first, o, kWave));
+    }
+  } else {
+    n = seq;
+    first = 0;
   }
+  if (lane != 0) return;
+  // the reference reads the token at index len-1 of each row, a right-padding index
   const int last = n > 0 ? n - 1 : 0;
   const int64_t row = static_cast<int64_t>(b) * seq + last;
   const int64_t t = ids[row];
@@ -121,6 +175,8 @@ __global__ void grid_init_kernel(const int64_t* __restrict__ ids, const int64_t*
   io[b] = out ? 1 : 0;
   if (kv_start) kv_start[b] = first;
   if (last_row) last_row[b] = static_cast<int32_t>(row);
+  // valid positions form one run [first, seq) iff there are seq - first of them
+  if (row_holes) row_holes[b] = (n == seq - first) ? 0 : 1;
 }
 
 __global__ void grid_step_kernel(const int64_t* __restrict__ token, int batch, int max_x,
@@ -132,28 +188,12 @@ __global__ void grid_step_kernel(const int64_t* __restrict__ token, int batch, i
     counters[1] = counters[1] + 1;
   }
   if (b >= batch) return;
-  const int64_t t = token[b];
-  const bool st = t == kStart, sp = t == kSep, en = t == kEnd, nl = t == kNewline;
-  int64_t x = gx[b], y = gy[b];
-  bool out = io[b] != 0;
-  int64_t z = out ? 3 : 1;
-  if (st) z = 0;
-  if (sp) z = 2;
-  if (en) z = 4;
-  pos_out[b * 3 + 0] = (st || sp || en || nl) ? 0 : clampi(x, 0, max_x);
-  pos_out[b * 3 + 1] = (st || sp || en) ? 0 : clampi(y, 0, max_y);
-  pos_out[b * 3 + 2] = z;
-  if (st || sp) x = y = 0;
-  if (st) out = false;
-  if (sp) out = true;
-  if (nl) {
-    x = 0;
-    y = y + 1 < max_y ? y + 1 : max_y;
-  }
-  if (t < 10) x = x + 1 < max_x ? x + 1 : max_x;
-  gx[b] = static_cast<int32_t>(clampi(x, 0, max_x));
-  gy[b] = static_cast<int32_t>(clampi(y, 0, max_y));
-  io[b] = out ? 1 : 0;
+  int32_t x = gx[b], y = gy[b];
+  uint8_t o = io[b];
+  grid_position_step(token[b], max_x, max_y, x, y, o, pos_out + static_cast<int64_t>(b) * 3);
+  gx[b] = x;
+  gy[b] = y;
+  io[b] = o;
 }
 
 __global__ void decode_commit_kernel(const int64_t* __restrict__ token, int batch,
@@ -169,11 +209,45 @@ __global__ void decode_commit_kernel(const int64_t* __restrict__ token, int batc
   if (finish && t == end_id && finish[b] < 0) finish[b] = c - gen_base;
 }
 
+template <int NC>
+struct LaunchHead {
+  static void run(int nv, dim3 grid, hipStream_t s, const float* x, const int32_t* row_index,
+                  int rows, int d, const float* gamma, float eps, const float* w, int vocab,
+                  float* logits, int64_t* token, int64_t* out_ids, int64_t ld, int col,
+                  const int32_t* counters, int32_t* finish, int gen_base, int64_t end_id) {
+    if (nv == 16)
+      head_kernel<NC, 16><<<grid, 256, 0, s>>>(x, row_index, rows, d, gamma, eps, w, vocab,
+                                               logits, token, out_ids, ld, col, counters, finish,
+                                               gen_base, end_id);
+    else
+      head_kernel<NC, 32><<<grid, 256, 0, s>>>(x, row_index, rows, d, gamma, eps, w, vocab,
+                                               logits, token, out_ids, ld, col, counters, finish,
+                                               gen_base, end_id);
+  }
+};
+
+int launch_head(const float* x, const int32_t* row_index, int rows, int d, const float* gamma,
+                float eps, const float* w, int vocab, float* logits, int64_t* token,
+                int64_t* out_ids, int64_t ld, int col, const int32_t* counters, int32_t* finish,
+                int gen_base, int64_t end_id, hipStream_t s) {
+  const dim3 grid((rows + 3) / 4);
+  const int nv = vocab <= 16 ? 16 : 32;
+#define MDL_HEAD(N)                                                                            \
+  case N:                                                                                      \
+    LaunchHead<N>::run(nv, grid, s, x, row_index, rows, d, gamma, eps, w, vocab, logits, token, \
+                       out_ids, ld, col, counters, finish, gen_base, end_id);                  \
+    break;
+  switch ((d + 255) / 256) { MDL_HEAD(1) MDL_HEAD(2) MDL_HEAD(3) MDL_HEAD(4) MDL_HEAD(5)
+                             MDL_HEAD(6) MDL_HEAD(7) MDL_HEAD(8) }
+#undef MDL_HEAD
+  return launch_status();
+}
+
 }  // namespace mdl
 
 using namespace mdl;
 
-extern "C" int mdl_version(void) { return 100; }
+extern "C" int mdl_version(void) { return 101; }
 
 extern "C" const char* mdl_error_string(int code) {
   switch (code) {
@@ -197,30 +271,37 @@ extern "C" int mdl_lm_head(const float* x, const int32_t* row_index, int rows, i
     return MDL_ERR_SHAPE;
   if (!aligned16(x) || !aligned16(gamma) || !aligned16(w_head)) return MDL_ERR_ALIGN;
   if (rows == 0) return MDL_OK;
-  const dim3 grid((rows + 3) / 4);
-  hipStream_t s = static_cast<hipStream_t>(stream);
-#define MDL_HEAD(N)                                                                      \
-  case N:                                                                                \
-    lm_head_kernel<N><<<grid, 256, 0, s>>>(x, row_index, rows, d, gamma, eps, w_head, vocab, \
-                                           logits_out, token_out);                       \
-    break;
-  switch ((d + 255) / 256) { MDL_HEAD(1) MDL_HEAD(2) MDL_HEAD(3) MDL_HEAD(4) MDL_HEAD(5)
-                             MDL_HEAD(6) MDL_HEAD(7) MDL_HEAD(8) }
-#undef MDL_HEAD
-  return launch_status();
+  return launch_head(x, row_index, rows, d, gamma, eps, w_head, vocab, logits_out, token_out,
+                     nullptr, 0, 0, nullptr, nullptr, 0, 0, static_cast<hipStream_t>(stream));
+}
+
+extern "C" int mdl_decode_head(const float* x, int batch, int d, const float* gamma, float eps,
+                               const float* w_head, int vocab, float* logits_out,
+                               int64_t* token_out, int64_t* out_ids, int64_t out_ld, int col,
+                               const int32_t* counters, int32_t* finish_step, int gen_base,
+                               int end_id, void* stream) {
+  if (!x || !gamma || !w_head || !token_out || !out_ids) return MDL_ERR_NULL;
+  if (batch < 0 || d <= 0 || d % 4 != 0 || d > 2048 || vocab <= 0 || vocab > kVmax ||
+      out_ld <= 0 || (!counters && (col < 0 || col >= out_ld)))
+    return MDL_ERR_SHAPE;
+  if (!aligned16(x) || !aligned16(gamma) || !aligned16(w_head)) return MDL_ERR_ALIGN;
+  if (batch == 0) return MDL_OK;
+  return launch_head(x, nullptr, batch, d, gamma, eps, w_head, vocab, logits_out, token_out,
+                     out_ids, out_ld, col, counters, finish_step, gen_base, end_id,
+                     static_cast<hipStream_t>(stream));
 }
 
 extern "C" int mdl_grid_init(const int64_t* ids, const int64_t* pos, const uint8_t* mask,
                              int batch, int seq, int max_x, int max_y, int32_t* gx, int32_t* gy,
                              uint8_t* in_out, int32_t* kv_start, int32_t* last_row,
-                             void* stream) {
+                             uint8_t* row_holes, void* stream) {
   if (!ids || !pos || !gx || !gy || !in_out) return MDL_ERR_NULL;
   if (batch < 0 || seq <= 0 || max_x < 0 || max_y < 0 ||
       static_cast<int64_t>(batch) * seq > INT32_MAX)
     return MDL_ERR_SHAPE;
   if (batch == 0) return MDL_OK;
-  grid_init_kernel<<<dim3((batch + 63) / 64), 64, 0, static_cast<hipStream_t>(stream)>>>(
-      ids, pos, mask, batch, seq, max_x, max_y, gx, gy, in_out, kv_start, last_row);
+  grid_init_kernel<<<dim3((batch + 3) / 4), 256, 0, static_cast<hipStream_t>(stream)>>>(
+      ids, pos, mask, batch, seq, max_x, max_y, gx, gy, in_out, kv_start, last_row, row_holes);
   return launch_status();
 }
 

@@ -1,16 +1,20 @@
-// K1 (token/example embedding gather + RMSNorm) and the residual-add + RMSNorm kernel.
+// K1 (token/example embedding gather + RMSNorm), the residual-add + RMSNorm kernel and the fused
+// decode-step embedding (grid position + K1).
 //
 // One wavefront owns one token row; a 256-thread block holds 4 rows.  A lane owns NC chunks of
 // 4 consecutive channels (chunk c = lane + 64*i), so every global access is a fully coalesced
 // 16-byte (fp32) or 8-byte (bf16) vector per lane and the row's sum of squares is one wave64
 // shuffle reduction.  Everything stays in registers between the reduction and the stores, so a
-// row is read once and written once.
+// row is read once and written once.  gamma is loaded before the row so its latency overlaps the
+// row loads; optional inputs / outputs are template flags, so no runtime branch sits between the
+// loads and the stores.
 //
 // Outputs per row: the fp32 residual x, rstd = 1/sqrt(mean(x^2)+eps) and xs = split(x * gamma),
 // the GEMM input of the next projection as a hi|lo bf16 pair (2d values, see common.h).  The
 // RMSNorm multiply by rstd is deferred to the consumer of that GEMM (K2 for q/k/v, K3 for
 // gate/up), which is exact algebra: (x * rstd * gamma) @ W^T == rstd * ((x * gamma) @ W^T).
 #include "common.h"
+#include "grid.h"
 
 namespace mdl {
 
@@ -30,46 +34,59 @@ __device__ __forceinline__ void load4<uint16_t>(const uint16_t* p, float* f) {
   f[2] = bf2f(v.y & 0xffffu); f[3] = bf2f(v.y >> 16);
 }
 
-// x row (fp32) at xo, split(x * gamma) at xs (hi) and xs + d (lo); xs may be NULL.
-__device__ __forceinline__ void store_row(float* xo, uint16_t* xs, int d, const float* gamma,
-                                          int e, const float* v) {
-  *reinterpret_cast<float4*>(xo + e) = make_float4(v[0], v[1], v[2], v[3]);
-  if (xs) {
-    const float4 g = *reinterpret_cast<const float4*>(gamma + e);
-    const float t[4] = {v[0] * g.x, v[1] * g.y, v[2] * g.z, v[3] * g.w};
-    uint2 hi, lo;
-    split4(t, hi, lo);
-    *reinterpret_cast<uint2*>(xs + e) = hi;
-    *reinterpret_cast<uint2*>(xs + d + e) = lo;
+// Chunk i (channels e..e+3) lies inside the row.  Only the last chunk can stick out, and only
+// when d is not a multiple of 256 (TAIL): per-chunk runtime guards on every chunk cost about a
+// fifth of the bandwidth of these kernels, so full rows carry none.
+template <int NC, bool TAIL>
+__device__ __forceinline__ bool in_row(int i, int e, int d) {
+  return !TAIL || i < NC - 1 || e < d;
+}
+
+template <int NC, bool TAIL>
+__device__ __forceinline__ void load_gamma(const float* gamma, int lane, int d, float (*g)[4]) {
+#pragma unroll
+  for (int i = 0; i < NC; ++i) {
+    const int e = 4 * (lane + 64 * i);
+    if (in_row<NC, TAIL>(i, e, d)) load4<float>(gamma + e, g[i]);
   }
 }
 
-template <int NC, typename TT>
-__global__ __launch_bounds__(256) void embed_rmsnorm_kernel(
-    const int64_t* __restrict__ ids, const int64_t* __restrict__ ex_ids,
-    const TT* __restrict__ tok, const TT* __restrict__ ex, int vocab, int n_ex, int rows,
-    int row_len, int d, const float* __restrict__ gamma, float eps, float* __restrict__ x_out,
-    uint16_t* __restrict__ xs_out, float* __restrict__ rstd_out) {
-  const int lane = threadIdx.x & 63;
-  const int64_t m = static_cast<int64_t>(blockIdx.x) * 4 + (threadIdx.x >> 6);
-  if (m >= rows) return;
-  int64_t t = ids[m];
-  t = t < 0 ? 0 : (t >= vocab ? vocab - 1 : t);
-  const TT* trow = tok + t * d;
-  const TT* erow = nullptr;
-  if (ex_ids) {
-    int64_t e = ex_ids[m / row_len];
-    e = e < 0 ? 0 : (e >= n_ex ? n_ex - 1 : e);
-    erow = ex + e * d;
+// rstd of the row held in v, then x (fp32) and split(x * gamma) stores.
+template <int NC, bool TAIL, bool HAS_XS>
+__device__ __forceinline__ void finish_row(int lane, int d, float eps, const float (*v)[4],
+                                           const float (*g)[4], float ss, float* xo,
+                                           uint16_t* xs, float* rstd_out) {
+  ss = wave_sum(ss);
+  const float r = rsqrtf(ss / static_cast<float>(d) + eps);
+#pragma unroll
+  for (int i = 0; i < NC; ++i) {
+    const int e = 4 * (lane + 64 * i);
+    if (in_row<NC, TAIL>(i, e, d)) {
+      *reinterpret_cast<float4*>(xo + e) = make_float4(v[i][0], v[i][1], v[i][2], v[i][3]);
+      if (HAS_XS) {
+        const float t[4] = {v[i][0] * g[i][0], v[i][1] * g[i][1], v[i][2] * g[i][2],
+                            v[i][3] * g[i][3]};
+        uint2 hi, lo;
+        split4(t, hi, lo);
+        *reinterpret_cast<uint2*>(xs + e) = hi;
+        *reinterpret_cast<uint2*>(xs + d + e) = lo;
+      }
+    }
   }
-  float v[NC][4];
+  if (lane == 0) *rstd_out = r;
+}
+
+// x = tok[t] (+ ex[e]) for one row into v; returns the row's partial sum of squares.
+template <int NC, bool TAIL, typename TT, bool HAS_EX>
+__device__ __forceinline__ float gather_row(const TT* trow, const TT* erow, int lane, int d,
+                                            float (*v)[4]) {
   float ss = 0.f;
 #pragma unroll
   for (int i = 0; i < NC; ++i) {
     const int e = 4 * (lane + 64 * i);
-    if (e < d) {
+    if (in_row<NC, TAIL>(i, e, d)) {
       load4<TT>(trow + e, v[i]);
-      if (erow) {
+      if (HAS_EX) {
         float w[4];
         load4<TT>(erow + e, w);
 #pragma unroll
@@ -79,19 +96,67 @@ __global__ __launch_bounds__(256) void embed_rmsnorm_kernel(
       for (int j = 0; j < 4; ++j) ss += v[i][j] * v[i][j];
     }
   }
-  ss = wave_sum(ss);
-  const float r = rsqrtf(ss / static_cast<float>(d) + eps);
-  float* xo = x_out + m * d;
-  uint16_t* xs = xs_out ? xs_out + m * 2 * d : nullptr;
-#pragma unroll
-  for (int i = 0; i < NC; ++i) {
-    const int e = 4 * (lane + 64 * i);
-    if (e < d) store_row(xo, xs, d, gamma, e, v[i]);
-  }
-  if (lane == 0) rstd_out[m] = r;
+  return ss;
 }
 
-template <int NC>
+__device__ __forceinline__ int64_t clamp_id(int64_t t, int n) {
+  return t < 0 ? 0 : (t >= n ? n - 1 : t);
+}
+
+template <int NC, bool TAIL, typename TT, bool HAS_EX, bool HAS_XS>
+__global__ __launch_bounds__(256) void embed_rmsnorm_kernel(
+    const int64_t* __restrict__ ids, const int64_t* __restrict__ ex_ids,
+    const TT* __restrict__ tok, const TT* __restrict__ ex, int vocab, int n_ex, int rows,
+    int row_len, int d, const float* __restrict__ gamma, float eps, float* __restrict__ x_out,
+    uint16_t* __restrict__ xs_out, float* __restrict__ rstd_out) {
+  const int lane = threadIdx.x & 63;
+  const int64_t m = static_cast<int64_t>(blockIdx.x) * 4 + (threadIdx.x >> 6);
+  if (m >= rows) return;
+  float g[NC][4], v[NC][4];
+  if (HAS_XS) load_gamma<NC, TAIL>(gamma, lane, d, g);
+  const TT* trow = tok + clamp_id(ids[m], vocab) * d;
+  const TT* erow = HAS_EX ? ex + clamp_id(ex_ids[m / row_len], n_ex) * d : nullptr;
+  const float ss = gather_row<NC, TAIL, TT, HAS_EX>(trow, erow, lane, d, v);
+  finish_row<NC, TAIL, HAS_XS>(lane, d, eps, v, g, ss, x_out + m * d,
+                         HAS_XS ? xs_out + m * 2 * d : nullptr, rstd_out + m);
+}
+
+// Decode step entry: lane 0 of each row's wave turns the token the row just emitted into its 3D
+// position (grid.h) and advances the row's grid state, then the wave embeds the token as K1.
+template <int NC, bool TAIL, typename TT, bool HAS_EX>
+__global__ __launch_bounds__(256) void decode_embed_kernel(
+    const int64_t* __restrict__ token, const int64_t* __restrict__ ex_ids,
+    const TT* __restrict__ tok, const TT* __restrict__ ex, int vocab, int n_ex, int batch, int d,
+    const float* __restrict__ gamma, float eps, int32_t* __restrict__ gx,
+    int32_t* __restrict__ gy, uint8_t* __restrict__ gio, int max_x, int max_y,
+    int64_t* __restrict__ pos_out, int32_t* __restrict__ counters, float* __restrict__ x_out,
+    uint16_t* __restrict__ xs_out, float* __restrict__ rstd_out) {
+  const int lane = threadIdx.x & 63;
+  if (counters && blockIdx.x == 0 && threadIdx.x == 0) {
+    counters[0] = counters[0] + 1;
+    counters[1] = counters[1] + 1;
+  }
+  const int64_t m = static_cast<int64_t>(blockIdx.x) * 4 + (threadIdx.x >> 6);
+  if (m >= batch) return;
+  float g[NC][4], v[NC][4];
+  load_gamma<NC, TAIL>(gamma, lane, d, g);
+  const int64_t t = token[m];
+  if (lane == 0) {
+    int32_t x = gx[m], y = gy[m];
+    uint8_t io = gio[m];
+    grid_position_step(t, max_x, max_y, x, y, io, pos_out + m * 3);
+    gx[m] = x;
+    gy[m] = y;
+    gio[m] = io;
+  }
+  const TT* trow = tok + clamp_id(t, vocab) * d;
+  const TT* erow = HAS_EX ? ex + clamp_id(ex_ids[m], n_ex) * d : nullptr;
+  const float ss = gather_row<NC, TAIL, TT, HAS_EX>(trow, erow, lane, d, v);
+  finish_row<NC, TAIL, true>(lane, d, eps, v, g, ss, x_out + m * d, xs_out + m * 2 * d,
+                       rstd_out + m);
+}
+
+template <int NC, bool TAIL, bool HAS_DELTA, bool HAS_BIAS, bool HAS_XS>
 __global__ __launch_bounds__(256) void add_rmsnorm_kernel(
     float* __restrict__ x, const float* __restrict__ delta, const float* __restrict__ bias,
     int rows, int d, const float* __restrict__ gamma, float eps, uint16_t* __restrict__ xs_out,
@@ -99,22 +164,23 @@ __global__ __launch_bounds__(256) void add_rmsnorm_kernel(
   const int lane = threadIdx.x & 63;
   const int64_t m = static_cast<int64_t>(blockIdx.x) * 4 + (threadIdx.x >> 6);
   if (m >= rows) return;
+  float g[NC][4], v[NC][4];
+  if (HAS_XS) load_gamma<NC, TAIL>(gamma, lane, d, g);
   float* xr = x + m * d;
-  const float* dr = delta ? delta + m * d : nullptr;
-  float v[NC][4];
+  const float* dr = HAS_DELTA ? delta + m * d : nullptr;
   float ss = 0.f;
 #pragma unroll
   for (int i = 0; i < NC; ++i) {
     const int e = 4 * (lane + 64 * i);
-    if (e < d) {
+    if (in_row<NC, TAIL>(i, e, d)) {
       load4<float>(xr + e, v[i]);
-      if (dr) {
+      if (HAS_DELTA) {
         float w[4];
         load4<float>(dr + e, w);
 #pragma unroll
         for (int j = 0; j < 4; ++j) v[i][j] += w[j];
       }
-      if (bias) {
+      if (HAS_BIAS) {
         float w[4];
         load4<float>(bias + e, w);
 #pragma unroll
@@ -124,31 +190,102 @@ __global__ __launch_bounds__(256) void add_rmsnorm_kernel(
       for (int j = 0; j < 4; ++j) ss += v[i][j] * v[i][j];
     }
   }
-  ss = wave_sum(ss);
-  const float r = rsqrtf(ss / static_cast<float>(d) + eps);
-  uint16_t* xs = xs_out ? xs_out + m * 2 * d : nullptr;
-#pragma unroll
-  for (int i = 0; i < NC; ++i) {
-    const int e = 4 * (lane + 64 * i);
-    if (e < d) store_row(xr, xs, d, gamma, e, v[i]);
-  }
-  if (lane == 0) rstd_out[m] = r;
+  finish_row<NC, TAIL, HAS_XS>(lane, d, eps, v, g, ss, xr, HAS_XS ? xs_out + m * 2 * d : nullptr,
+                         rstd_out + m);
 }
 
 constexpr int kMaxChunks = 8;  // d <= 2048
 
-template <typename TT>
-static void launch_embed(int nc, dim3 grid, hipStream_t s, const int64_t* ids, const int64_t* ex_ids,
-                         const TT* tok, const TT* ex, int vocab, int n_ex, int rows, int row_len,
-                         int d, const float* gamma, float eps, float* x, uint16_t* xs, float* r) {
-#define MDL_EMB(N)                                                                          \
-  case N:                                                                                   \
-    embed_rmsnorm_kernel<N, TT><<<grid, 256, 0, s>>>(ids, ex_ids, tok, ex, vocab, n_ex, rows, \
-                                                     row_len, d, gamma, eps, x, xs, r);      \
+// Instantiate F<NC, TAIL>::run for a row of d channels: NC = ceil(d / 256) chunks per lane,
+// TAIL = the last chunk is partial.
+template <template <int, bool> class F, typename... A>
+void dispatch_nc(int d, A&&... a) {
+  const bool tail = d % 256 != 0;
+#define MDL_NC(N)                     \
+  case N:                             \
+    if (tail) F<N, true>::run(a...);  \
+    else F<N, false>::run(a...);      \
     break;
-  switch (nc) { MDL_EMB(1) MDL_EMB(2) MDL_EMB(3) MDL_EMB(4) MDL_EMB(5) MDL_EMB(6) MDL_EMB(7)
-                MDL_EMB(8) }
+  switch ((d + 255) / 256) {
+    MDL_NC(1) MDL_NC(2) MDL_NC(3) MDL_NC(4) MDL_NC(5) MDL_NC(6) MDL_NC(7)
+    default: if (tail) F<8, true>::run(a...); else F<8, false>::run(a...); break;
+  }
+#undef MDL_NC
+}
+
+template <int NC, bool TAIL>
+struct LaunchEmbed {
+  template <typename TT>
+  static void run(dim3 grid, hipStream_t s, bool has_ex, bool has_xs, const int64_t* ids,
+                  const int64_t* ex_ids, const TT* tok, const TT* ex, int vocab, int n_ex,
+                  int rows, int row_len, int d, const float* gamma, float eps, float* x,
+                  uint16_t* xs, float* r) {
+#define MDL_EMB(E, X)                                                                         \
+  embed_rmsnorm_kernel<NC, TAIL, TT, E, X><<<grid, 256, 0, s>>>(ids, ex_ids, tok, ex, vocab, n_ex,  \
+                                                          rows, row_len, d, gamma, eps, x, xs, \
+                                                          r)
+    if (has_ex && has_xs) MDL_EMB(true, true);
+    else if (has_ex) MDL_EMB(true, false);
+    else if (has_xs) MDL_EMB(false, true);
+    else MDL_EMB(false, false);
 #undef MDL_EMB
+  }
+};
+
+template <int NC, bool TAIL>
+struct LaunchDecodeEmbed {
+  template <typename TT>
+  static void run(dim3 grid, hipStream_t s, bool has_ex, const int64_t* token,
+                  const int64_t* ex_ids, const TT* tok, const TT* ex, int vocab, int n_ex,
+                  int batch, int d, const float* gamma, float eps, int32_t* gx, int32_t* gy,
+                  uint8_t* gio, int max_x, int max_y, int64_t* pos, int32_t* counters, float* x,
+                  uint16_t* xs, float* r) {
+    if (has_ex)
+      decode_embed_kernel<NC, TAIL, TT, true><<<grid, 256, 0, s>>>(
+          token, ex_ids, tok, ex, vocab, n_ex, batch, d, gamma, eps, gx, gy, gio, max_x, max_y,
+          pos, counters, x, xs, r);
+    else
+      decode_embed_kernel<NC, TAIL, TT, false><<<grid, 256, 0, s>>>(
+          token, ex_ids, tok, ex, vocab, n_ex, batch, d, gamma, eps, gx, gy, gio, max_x, max_y,
+          pos, counters, x, xs, r);
+  }
+};
+
+template <int NC, bool TAIL>
+struct LaunchAdd {
+  static void run(dim3 grid, hipStream_t s, float* x, const float* delta, const float* bias,
+                  int rows, int d, const float* gamma, float eps, uint16_t* xs, float* r) {
+    const int key = (delta ? 4 : 0) | (bias ? 2 : 0) | (xs ? 1 : 0);
+#define MDL_ADD(D, B, X)                                                                       \
+  add_rmsnorm_kernel<NC, TAIL, D, B, X><<<grid, 256, 0, s>>>(x, delta, bias, rows, d, gamma, eps, xs, \
+                                                       r)
+    switch (key) {
+      case 7: MDL_ADD(true, true, true); break;
+      case 6: MDL_ADD(true, true, false); break;
+      case 5: MDL_ADD(true, false, true); break;
+      case 4: MDL_ADD(true, false, false); break;
+      case 3: MDL_ADD(false, true, true); break;
+      case 2: MDL_ADD(false, true, false); break;
+      case 1: MDL_ADD(false, false, true); break;
+      default: MDL_ADD(false, false, false); break;
+    }
+#undef MDL_ADD
+  }
+};
+
+// host-side checks shared by the two embedding entry points
+inline int check_tables(const void* tok_table, const void* ex_table, bool use_ex, int table_dtype,
+                        int vocab, int n_examples, int d) {
+  if (!tok_table || (use_ex && !ex_table)) return MDL_ERR_NULL;
+  if (d <= 0 || d % 4 != 0 || d > 4 * 64 * kMaxChunks || vocab <= 0 ||
+      (use_ex && n_examples <= 0))
+    return MDL_ERR_SHAPE;
+  if (table_dtype != MDL_DTYPE_F32 && table_dtype != MDL_DTYPE_BF16) return MDL_ERR_DTYPE;
+  const bool f32 = table_dtype == MDL_DTYPE_F32;
+  if (!(f32 ? aligned16(tok_table) : aligned8(tok_table)) ||
+      (use_ex && !(f32 ? aligned16(ex_table) : aligned8(ex_table))))
+    return MDL_ERR_ALIGN;
+  return MDL_OK;
 }
 
 }  // namespace mdl
@@ -160,30 +297,57 @@ extern "C" int mdl_embed_rmsnorm(const int64_t* ids, const int64_t* example_ids,
                                  int vocab, int n_examples, int rows, int row_len, int d,
                                  const float* gamma, float eps, float* x_out, uint16_t* xs_out,
                                  float* rstd_out, void* stream) {
-  if (!ids || !tok_table || !gamma || !x_out || !rstd_out) return MDL_ERR_NULL;
-  if (example_ids && !ex_table) return MDL_ERR_NULL;
-  if (rows < 0 || row_len <= 0 || d <= 0 || d % 4 != 0 || d > 4 * 64 * kMaxChunks ||
-      vocab <= 0 || (example_ids && n_examples <= 0))
-    return MDL_ERR_SHAPE;
-  if (table_dtype != MDL_DTYPE_F32 && table_dtype != MDL_DTYPE_BF16) return MDL_ERR_DTYPE;
-  const bool f32 = table_dtype == MDL_DTYPE_F32;
-  if (!aligned16(x_out) || !aligned16(gamma) || (xs_out && !aligned8(xs_out)) ||
-      !(f32 ? aligned16(tok_table) : aligned8(tok_table)) ||
-      (ex_table && !(f32 ? aligned16(ex_table) : aligned8(ex_table))))
+  if (!ids || !gamma || !x_out || !rstd_out) return MDL_ERR_NULL;
+  const bool use_ex = example_ids != nullptr;
+  const int tc = check_tables(tok_table, ex_table, use_ex, table_dtype, vocab, n_examples, d);
+  if (tc != MDL_OK) return tc;
+  if (rows < 0 || row_len <= 0) return MDL_ERR_SHAPE;
+  if (!aligned16(x_out) || !aligned16(gamma) || (xs_out && !aligned8(xs_out)))
     return MDL_ERR_ALIGN;
   if (rows == 0) return MDL_OK;
-  const int nc = (d + 255) / 256;
   const dim3 grid((rows + 3) / 4);
   hipStream_t s = static_cast<hipStream_t>(stream);
-  if (f32)
-    launch_embed<float>(nc, grid, s, ids, example_ids, static_cast<const float*>(tok_table),
-                        static_cast<const float*>(ex_table), vocab, n_examples, rows, row_len, d,
-                        gamma, eps, x_out, xs_out, rstd_out);
+  if (table_dtype == MDL_DTYPE_F32)
+    dispatch_nc<LaunchEmbed>(d, grid, s, use_ex, xs_out != nullptr, ids, example_ids,
+                             static_cast<const float*>(tok_table),
+                             static_cast<const float*>(ex_table), vocab, n_examples, rows,
+                             row_len, d, gamma, eps, x_out, xs_out, rstd_out);
   else
-    launch_embed<uint16_t>(nc, grid, s, ids, example_ids,
-                           static_cast<const uint16_t*>(tok_table),
-                           static_cast<const uint16_t*>(ex_table), vocab, n_examples, rows,
-                           row_len, d, gamma, eps, x_out, xs_out, rstd_out);
+    dispatch_nc<LaunchEmbed>(d, grid, s, use_ex, xs_out != nullptr, ids, example_ids,
+                             static_cast<const uint16_t*>(tok_table),
+                             static_cast<const uint16_t*>(ex_table), vocab, n_examples, rows,
+                             row_len, d, gamma, eps, x_out, xs_out, rstd_out);
+  return launch_status();
+}
+
+extern "C" int mdl_decode_embed(const int64_t* token, const int64_t* example_ids,
+                                const void* tok_table, const void* ex_table, int table_dtype,
+                                int vocab, int n_examples, int batch, int d, const float* gamma,
+                                float eps, int32_t* gx, int32_t* gy, uint8_t* in_out, int max_x,
+                                int max_y, int64_t* pos_out, int32_t* counters, float* x_out,
+                                uint16_t* xs_out, float* rstd_out, void* stream) {
+  if (!token || !gamma || !gx || !gy || !in_out || !pos_out || !x_out || !xs_out || !rstd_out)
+    return MDL_ERR_NULL;
+  const bool use_ex = example_ids != nullptr;
+  const int tc = check_tables(tok_table, ex_table, use_ex, table_dtype, vocab, n_examples, d);
+  if (tc != MDL_OK) return tc;
+  if (batch < 0 || max_x < 0 || max_y < 0) return MDL_ERR_SHAPE;
+  if (!aligned16(x_out) || !aligned16(gamma) || !aligned8(xs_out)) return MDL_ERR_ALIGN;
+  if (batch == 0) return MDL_OK;
+  const dim3 grid((batch + 3) / 4);
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  if (table_dtype == MDL_DTYPE_F32)
+    dispatch_nc<LaunchDecodeEmbed>(d, grid, s, use_ex, token, example_ids,
+                                   static_cast<const float*>(tok_table),
+                                   static_cast<const float*>(ex_table), vocab, n_examples, batch,
+                                   d, gamma, eps, gx, gy, in_out, max_x, max_y, pos_out, counters,
+                                   x_out, xs_out, rstd_out);
+  else
+    dispatch_nc<LaunchDecodeEmbed>(d, grid, s, use_ex, token, example_ids,
+                                   static_cast<const uint16_t*>(tok_table),
+                                   static_cast<const uint16_t*>(ex_table), vocab, n_examples,
+                                   batch, d, gamma, eps, gx, gy, in_out, max_x, max_y, pos_out,
+                                   counters, x_out, xs_out, rstd_out);
   return launch_status();
 }
 
@@ -196,15 +360,7 @@ extern "C" int mdl_add_rmsnorm(float* x, const float* delta, const float* bias, 
       (bias && !aligned16(bias)) || (xs_out && !aligned8(xs_out)))
     return MDL_ERR_ALIGN;
   if (rows == 0) return MDL_OK;
-  const dim3 grid((rows + 3) / 4);
-  hipStream_t s = static_cast<hipStream_t>(stream);
-#define MDL_ADD(N)                                                                         \
-  case N:                                                                                  \
-    add_rmsnorm_kernel<N><<<grid, 256, 0, s>>>(x, delta, bias, rows, d, gamma, eps, xs_out, \
-                                               rstd_out);                                  \
-    break;
-  switch ((d + 255) / 256) { MDL_ADD(1) MDL_ADD(2) MDL_ADD(3) MDL_ADD(4) MDL_ADD(5) MDL_ADD(6)
-                             MDL_ADD(7) MDL_ADD(8) }
-#undef MDL_ADD
+  dispatch_nc<LaunchAdd>(d, dim3((rows + 3) / 4), static_cast<hipStream_t>(stream),
+                         x, delta, bias, rows, d, gamma, eps, xs_out, rstd_out);
   return launch_status();
 }

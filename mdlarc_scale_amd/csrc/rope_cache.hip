@@ -1,14 +1,14 @@
 // K2 -- RMSNorm scale + Q/K/V split + 3D RoPE + static-cache write, one pass over the qkv GEMM
 // output.
 //
-// qkv is the fp32 output of the projection GEMM (the GEMM accumulates in fp32 and returns it
-// unrounded).  Work item = 8 consecutive values of one token's qkv row (two 16-byte loads).
-// Items are numbered token-major, so a wavefront reads 2 KiB of contiguous qkv and writes q
-// (contiguous) or a 128-byte head row of the K/V cache per 8 lanes.  The 8 values are 4
-// interleaved RoPE pairs of
-// one head, rotated in fp32 with the per-axis cos/sin tables of the reference
-// (RotaryEmbedding3D._build_cache); pair j of a head uses axis x for j < px, y for
-// px <= j < px+py and z otherwise, exactly the split of RotaryEmbedding3D.apply_rotary.
+// qkv is the fp32 output of the projection GEMM (unrounded fp32 accumulators).  One wavefront
+// owns one token (a 256-thread block holds 4 tokens).  Lane l owns RoPE pair j = l % 32 of the
+// heads h = l / 32, l / 32 + 2, ...: it looks its cos/sin up once (pair j rotates with axis x
+// for j < px, y for px <= j < px+py and z otherwise, the split of RotaryEmbedding3D.apply_rotary)
+// and applies it to that pair of q and of k of each of its heads.  A half-wave therefore reads
+// 256 contiguous bytes of one head and writes 128 contiguous bytes of q or of one cache row;
+// v (no rotation) is streamed as float4 per lane.  Rotation (a, b) -> (a c - b s, b c + a s) is
+// the interleaved-pair form of _rotate_half.
 #include "common.h"
 
 namespace mdl {
@@ -23,63 +23,56 @@ __global__ __launch_bounds__(256) void qkv_rope_cache_kernel(
     int seq, int n_heads, float q_scale, uint16_t* __restrict__ q_out,
     uint16_t* __restrict__ kc, uint16_t* __restrict__ vc, int slots, int slot0,
     const int32_t* __restrict__ slot_dev) {
+  const int lane = threadIdx.x & 63;
+  const int64_t m = static_cast<int64_t>(blockIdx.x) * 4 + (threadIdx.x >> 6);
+  if (m >= rows) return;
+  const int j = lane & 31, first_head = lane >> 5;
   const int d = n_heads * kHeadDim;
-  const int per_region = d / 8;
-  const int per_tok = 3 * per_region;
-  const int64_t idx = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
-  if (idx >= rows * per_tok) return;
-  const int64_t m = idx / per_tok;
-  const int c = static_cast<int>(idx - m * per_tok);
-  const int region = c / per_region;            // 0 q, 1 k, 2 v
-  const int cc = c - region * per_region;
-  const int h = cc >> 3;
-  const int dim0 = (cc & 7) * 8;
 
-  float f[8];
-  load8f(qkv + m * ld + c * 8, f);
-  const float r = rstd ? rstd[m] : 1.f;
-#pragma unroll
-  for (int i = 0; i < 8; ++i) f[i] *= r;
-
-  if (region < 2) {
-    const int64_t* p = pos + m * 3;
-    int64_t cx = p[0], cy = p[1], cz = p[2];
-    cx = cx < 0 ? 0 : (cx >= ra.max_x ? ra.max_x - 1 : cx);
-    cy = cy < 0 ? 0 : (cy >= ra.max_y ? ra.max_y - 1 : cy);
-    cz = cz < 0 ? 0 : (cz >= ra.max_z ? ra.max_z - 1 : cz);
-    const int off_y = 2 * ra.max_x * ra.px;
-    const int off_z = off_y + 2 * ra.max_y * ra.py;
-#pragma unroll
-    for (int k = 0; k < 4; ++k) {
-      const int j = (dim0 >> 1) + k;
-      int base, half, jj;
-      if (j < ra.px) {
-        half = ra.max_x * ra.px; base = static_cast<int>(cx) * ra.px; jj = j;
-      } else if (j < ra.px + ra.py) {
-        half = ra.max_y * ra.py; base = off_y + static_cast<int>(cy) * ra.py; jj = j - ra.px;
-      } else {
-        half = ra.max_z * ra.pz; base = off_z + static_cast<int>(cz) * ra.pz;
-        jj = j - ra.px - ra.py;
-      }
-      const float cs = tab[base + jj];
-      const float sn = tab[base + half + jj];
-      const float a = f[2 * k], b = f[2 * k + 1];
-      f[2 * k] = a * cs - b * sn;
-      f[2 * k + 1] = b * cs + a * sn;
-    }
-  }
-  if (region == 0) {
-#pragma unroll
-    for (int i = 0; i < 8; ++i) f[i] *= q_scale;
-    *reinterpret_cast<uint4*>(q_out + m * d + h * kHeadDim + dim0) = pack8(f);
+  // table segment of pair j: [cos_x | sin_x | cos_y | sin_y | cos_z | sin_z], axis-major
+  int axis, n_pos, pairs, jj, off;
+  if (j < ra.px) {
+    axis = 0; n_pos = ra.max_x; pairs = ra.px; jj = j; off = 0;
+  } else if (j < ra.px + ra.py) {
+    axis = 1; n_pos = ra.max_y; pairs = ra.py; jj = j - ra.px; off = 2 * ra.max_x * ra.px;
   } else {
-    const int64_t b = m / seq;
-    const int s = static_cast<int>(m - b * seq);
-    const int slot = (slot_dev ? *slot_dev : slot0) + s;
-    if (slot < 0 || slot >= slots) return;       // host guarantees range; never write outside
-    uint16_t* dst = (region == 1 ? kc : vc) +
-                    ((b * n_heads + h) * static_cast<int64_t>(slots) + slot) * kHeadDim + dim0;
-    *reinterpret_cast<uint4*>(dst) = pack8(f);
+    axis = 2; n_pos = ra.max_z; pairs = ra.pz; jj = j - ra.px - ra.py;
+    off = 2 * ra.max_x * ra.px + 2 * ra.max_y * ra.py;
+  }
+  int64_t p = pos[m * 3 + axis];
+  p = p < 0 ? 0 : (p >= n_pos ? n_pos - 1 : p);
+  const int ti = off + static_cast<int>(p) * pairs + jj;
+  const float cs = tab[ti];
+  const float sn = tab[ti + n_pos * pairs];
+  const float r = rstd ? rstd[m] : 1.f;
+
+  const float* row = qkv + m * ld;
+  const int64_t b = m / seq;
+  const int slot = (slot_dev ? *slot_dev : slot0) + static_cast<int>(m - b * seq);
+  const bool in_cache = slot >= 0 && slot < slots;   // host guarantees range; never write outside
+  uint16_t* qrow = q_out + m * d;
+  const int64_t head_stride = static_cast<int64_t>(slots) * kHeadDim;
+  const int64_t cache_row = (b * n_heads * static_cast<int64_t>(slots) + slot) * kHeadDim;
+
+  for (int h = first_head; h < n_heads; h += 2) {
+    const int c = h * kHeadDim + 2 * j;
+    const float2 qa = *reinterpret_cast<const float2*>(row + c);
+    const float2 ka = *reinterpret_cast<const float2*>(row + d + c);
+    const float q0 = qa.x * r, q1 = qa.y * r, k0 = ka.x * r, k1 = ka.y * r;
+    *reinterpret_cast<uint32_t*>(qrow + c) =
+        pack_bf2((q0 * cs - q1 * sn) * q_scale, (q1 * cs + q0 * sn) * q_scale);
+    if (in_cache)
+      *reinterpret_cast<uint32_t*>(kc + cache_row + h * head_stride + 2 * j) =
+          pack_bf2(k0 * cs - k1 * sn, k1 * cs + k0 * sn);
+  }
+  if (!in_cache) return;
+  for (int idx = lane; idx < d / 4; idx += 64) {
+    const float4 v = *reinterpret_cast<const float4*>(row + 2 * d + 4 * idx);
+    const int hv = (4 * idx) / kHeadDim, dm = (4 * idx) % kHeadDim;
+    uint2 o;
+    o.x = pack_bf2(v.x * r, v.y * r);
+    o.y = pack_bf2(v.z * r, v.w * r);
+    *reinterpret_cast<uint2*>(vc + cache_row + hv * head_stride + dm) = o;
   }
 }
 
@@ -105,9 +98,8 @@ extern "C" int mdl_qkv_rope_cache(const float* qkv, int64_t qkv_ld, const float*
     return MDL_ERR_ALIGN;
   const int64_t rows = static_cast<int64_t>(batch) * seq;
   if (rows == 0) return MDL_OK;
-  const int64_t items = rows * 3 * n_heads * 8;
   const RopeArgs ra{max_x, max_y, max_z, px, py, pz};
-  qkv_rope_cache_kernel<<<dim3(static_cast<unsigned>((items + 255) / 256)), 256, 0,
+  qkv_rope_cache_kernel<<<dim3(static_cast<unsigned>((rows + 3) / 4)), 256, 0,
                           static_cast<hipStream_t>(stream)>>>(
       qkv, qkv_ld, rstd, pos, rope_tab, ra, rows, seq, n_heads, q_scale, q_out, k_cache,
       v_cache, cache_slots, slot0, slot_dev);

@@ -102,11 +102,17 @@ class Scratch:
                        delta=e(rows, d, dt=f), gu=e(rows, 2 * d_ff, dt=f), h=e(rows, 2 * d_ff))
 
 
+DECODE_MIN_BLOCKS = 2048   # 8 four-wave blocks per CU on 256 CUs
+
+
 def choose_split_len(n_bh: int, slots: int) -> int:
-    """Slots per decode-attention work item: aim for >= 8192 items, multiples of 128."""
-    n_split = max(1, -(-8192 // max(n_bh, 1)))
+    """Slots per decode-attention work item (a multiple of 128).  One chunk per (row, head) once
+    B*H alone gives DECODE_MIN_BLOCKS blocks -- splitting further only adds the partial-merge
+    pass (measured at config 2: 3,072 (b, h) pairs, one chunk each, is the fastest) -- and just
+    enough chunks to reach that count for small batches."""
+    n_split = max(1, -(-DECODE_MIN_BLOCKS // max(n_bh, 1)))
     per = -(-slots // n_split)
-    return max(256, -(-per // 128) * 128)
+    return max(128, -(-per // 128) * 128)
 
 
 class HipEngine:

@@ -219,6 +219,8 @@ class DecodeState:
     pmask: torch.Tensor         # [B, S] uint8 prompt mask
     kv_start: torch.Tensor      # [B] int32 first valid prompt slot
     last_row: torch.Tensor      # [B] int32 prefill row the first token is read from
+    holes: torch.Tensor         # [B] uint8 1 if the prompt mask has holes after kv_start
+    order: torch.Tensor         # [B] int32 rows by descending prompt length (attention dispatch)
     gx: torch.Tensor
     gy: torch.Tensor
     gio: torch.Tensor
@@ -251,7 +253,11 @@ class Generator:
         i32 = lambda: torch.empty(B, dtype=torch.int32, device=dev)  # noqa: E731
         gx, gy, kv_start, last_row = i32(), i32(), i32(), i32()
         gio = torch.empty(B, dtype=torch.uint8, device=dev)
-        K.grid_init(input_ids, positions_3d, pmask, gx, gy, gio, kv_start, last_row)
+        holes = torch.empty(B, dtype=torch.uint8, device=dev)
+        K.grid_init(input_ids, positions_3d, pmask, gx, gy, gio, kv_start, last_row,
+                    row_holes=holes)
+        # longest rows first: the decode-attention launch dispatches them before the short ones
+        order = torch.argsort(kv_start, stable=True).to(torch.int32)
         split = choose_split_len(B * H, total)
         nbytes = K.attn_decode_workspace_bytes(B, H, total, split)
         ws = torch.empty(max(nbytes // 4, 1), dtype=torch.float32, device=dev) if nbytes else None
@@ -259,7 +265,7 @@ class Generator:
         out_ids[:, :S] = input_ids
         return DecodeState(
             B=B, S=S, total=total, ex=example_ids, pmask=pmask, kv_start=kv_start,
-            last_row=last_row, gx=gx, gy=gy, gio=gio,
+            last_row=last_row, holes=holes, order=order, gx=gx, gy=gy, gio=gio,
             pos=torch.empty(B, 3, dtype=torch.int64, device=dev),
             tok=torch.empty(B, dtype=torch.int64, device=dev),
             counters=torch.tensor([S - 1, S], dtype=torch.int32, device=dev),
@@ -278,16 +284,18 @@ class Generator:
         K.lm_head(sc.x, st.last_row, st.B, W.ln_f, W.eps, W.head, st.logits, st.tok)
         st.cache.seq_len = st.S
 
-    def decode_layers(self, st: DecodeState, W: PackedWeights, want_logits: bool) -> None:
-        """``_decode_step`` (src/inference.py:427-459) for the token in ``st.tok`` at the
-        position in ``st.pos``; K/V go to slot counters[0]; greedy token back into ``st.tok``."""
+    def _embed_inputs(self, st: DecodeState):
+        cfg = self.model.config
+        tok_tab, ex_tab = self.eng._tables()
+        use_ex = st.ex if cfg.use_example_embedding else None
+        return tok_tab, (ex_tab if use_ex is not None else None), use_ex
+
+    def _layers(self, st: DecodeState, W: PackedWeights) -> None:
+        """Every layer of ``_decode_step`` (src/inference.py:437-456) for the embedded token in
+        ``st.sc``: K/V of the new token go to slot counters[0]; leaves the residual in sc.x."""
         cfg = self.model.config
         sc, B = st.sc, st.B
         H = cfg.n_heads
-        tok_tab, ex_tab = self.eng._tables()
-        use_ex = st.ex if cfg.use_example_embedding else None
-        K.embed_rmsnorm(st.tok, use_ex, tok_tab, ex_tab if use_ex is not None else None, 1,
-                        W.ln1[0], W.eps, sc.x, sc.xs, sc.rstd)
         qs = softmax_scale(cfg.d_model // H)
         slot = st.counters[0:1]
         for li in range(cfg.n_layers):
@@ -296,17 +304,31 @@ class Generator:
             K.qkv_rope_cache(sc.qkv, sc.rstd, st.pos, W.rope_tab, W.rope_geom, B, 1, H, qs,
                              sc.q, kc, vc, slot_dev=slot)
             K.attn_decode(sc.q, kc, vc, B, H, st.pmask, st.S, st.kv_start, 0, slot, st.ws,
-                          st.split_len, sc.attn)
+                          st.split_len, sc.attn, row_holes=st.holes, row_order=st.order)
             self.eng._mlp(W, li, sc)
-        K.lm_head(sc.x, None, B, W.ln_f, W.eps, W.head, st.logits if want_logits else None,
+
+    def decode_layers(self, st: DecodeState, W: PackedWeights, want_logits: bool) -> None:
+        """``_decode_step`` (src/inference.py:427-459) for the token in ``st.tok`` at the
+        position in ``st.pos``; K/V go to slot counters[0]; greedy token back into ``st.tok``
+        (the host-launched path of sampling / constrained decoding)."""
+        sc = st.sc
+        tok_tab, ex_tab, use_ex = self._embed_inputs(st)
+        K.embed_rmsnorm(st.tok, use_ex, tok_tab, ex_tab, 1, W.ln1[0], W.eps, sc.x, sc.xs,
+                        sc.rstd)
+        self._layers(st, W)
+        K.lm_head(sc.x, None, st.B, W.ln_f, W.eps, W.head, st.logits if want_logits else None,
                   st.tok)
 
     def greedy_step(self, st: DecodeState, W: PackedWeights, stop_on_end: bool) -> None:
-        """One full device-side decode step of greedy generation."""
-        K.grid_step(st.tok, st.gx, st.gy, st.gio, st.pos, st.counters)
-        self.decode_layers(st, W, want_logits=False)
-        K.decode_commit(st.tok, st.out_ids, 0, st.counters, st.finish if stop_on_end else None,
-                        st.S, END_TOKEN_ID)
+        """One full device-side decode step of greedy generation: grid position + embedding,
+        the layers, then LM head + argmax + commit."""
+        sc = st.sc
+        tok_tab, ex_tab, use_ex = self._embed_inputs(st)
+        K.decode_embed(st.tok, use_ex, tok_tab, ex_tab, W.ln1[0], W.eps, st.gx, st.gy, st.gio,
+                       st.pos, st.counters, sc.x, sc.xs, sc.rstd)
+        self._layers(st, W)
+        K.decode_head(sc.x, W.ln_f, W.eps, W.head, None, st.tok, st.out_ids, 0, st.counters,
+                      st.finish if stop_on_end else None, st.S, END_TOKEN_ID)
 
     def capture_greedy(self, st: DecodeState, W: PackedWeights,
                        stop_on_end: bool) -> torch.cuda.CUDAGraph:

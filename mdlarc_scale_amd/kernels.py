@@ -77,6 +77,37 @@ def embed_rmsnorm(ids: torch.Tensor, example_ids: torch.Tensor | None, tok_table
         _stream()), "mdl_embed_rmsnorm")
 
 
+def decode_embed(token: torch.Tensor, example_ids: torch.Tensor | None, tok_table: torch.Tensor,
+                 ex_table: torch.Tensor | None, gamma: torch.Tensor, eps: float,
+                 gx: torch.Tensor, gy: torch.Tensor, in_out: torch.Tensor, pos_out: torch.Tensor,
+                 counters: torch.Tensor | None, x_out: torch.Tensor, xs_out: torch.Tensor,
+                 rstd_out: torch.Tensor, max_x: int = 30, max_y: int = 29) -> None:
+    """Grid position of each row's emitted token (state advanced), then K1 on that token."""
+    batch = token.numel()
+    vocab, d = tok_table.shape
+    _need(token, "token", I64)
+    _need(example_ids, "example_ids", I64, batch, optional=True)
+    _need(tok_table, "tok_table", tok_table.dtype)
+    if example_ids is not None:
+        _need(ex_table, "ex_table", tok_table.dtype)
+        if ex_table.shape[1] != d:
+            raise ValueError("example table width differs from token table width")
+    for name, t, dt in (("gx", gx, I32), ("gy", gy, I32), ("in_out", in_out, U8)):
+        _need(t, name, dt, batch)
+    _need(pos_out, "pos_out", I64, batch * 3)
+    _need(counters, "counters", I32, 2, optional=True)
+    _need(gamma, "gamma", F32, d)
+    _need(x_out, "x_out", F32, batch * d)
+    _need(xs_out, "xs_out", BF16, batch * 2 * d)
+    _need(rstd_out, "rstd_out", F32, batch)
+    n_ex = ex_table.shape[0] if ex_table is not None else 0
+    _lib.check(_lib.lib().mdl_decode_embed(
+        _p(token), _p(example_ids), _p(tok_table), _p(ex_table), table_dtype_code(tok_table),
+        vocab, n_ex, batch, d, _p(gamma), eps, _p(gx), _p(gy), _p(in_out), max_x, max_y,
+        _p(pos_out), _p(counters), _p(x_out), _p(xs_out), _p(rstd_out), _stream()),
+        "mdl_decode_embed")
+
+
 def add_rmsnorm(x: torch.Tensor, delta: torch.Tensor | None, bias: torch.Tensor | None,
                 gamma: torch.Tensor, eps: float, xs_out: torch.Tensor | None,
                 rstd_out: torch.Tensor) -> None:
@@ -162,8 +193,12 @@ def attn_decode_workspace_bytes(batch: int, n_heads: int, slots: int, split_len:
 def attn_decode(q: torch.Tensor, k_cache: torch.Tensor, v_cache: torch.Tensor, batch: int,
                 n_heads: int, prompt_mask: torch.Tensor | None, prompt_len: int,
                 kv_start: torch.Tensor | None, seq_pos: int, seq_dev: torch.Tensor | None,
-                workspace: torch.Tensor | None, split_len: int, out: torch.Tensor) -> None:
-    """out: split [batch, 2*n_heads*64] bf16."""
+                workspace: torch.Tensor | None, split_len: int, out: torch.Tensor,
+                row_holes: torch.Tensor | None = None,
+                row_order: torch.Tensor | None = None) -> None:
+    """out: split [batch, 2*n_heads*64] bf16.  row_holes (uint8 [batch], from grid_init):
+    rows marked 0 skip the prompt-mask reads.  row_order (int32 [batch]): permutation giving
+    the dispatch order of the rows (longest first)."""
     n = batch * n_heads * HEAD_DIM
     _need(q, "q", BF16, n)
     _need(out, "out", BF16, 2 * n)
@@ -172,14 +207,17 @@ def attn_decode(q: torch.Tensor, k_cache: torch.Tensor, v_cache: torch.Tensor, b
         if c.dim() != 4 or c.shape[0] != batch or c.shape[1] != n_heads or c.shape[3] != 64:
             raise ValueError(f"{name} must be [batch, n_heads, slots, 64]")
     _need(prompt_mask, "prompt_mask", U8, batch * prompt_len, optional=True)
+    _need(row_holes, "row_holes", U8, batch, optional=True)
     _need(kv_start, "kv_start", I32, batch, optional=True)
+    _need(row_order, "row_order", I32, batch, optional=True)
     _need(seq_dev, "seq_dev", I32, 1, optional=True)
     _need(workspace, "workspace", F32, optional=True)
     ws_bytes = 0 if workspace is None else workspace.numel() * 4
     _lib.check(_lib.lib().mdl_attn_decode(
         _p(q), _p(k_cache), _p(v_cache), batch, n_heads, HEAD_DIM, k_cache.shape[2],
-        _p(prompt_mask), prompt_len, _p(kv_start), seq_pos, _p(seq_dev), _p(workspace),
-        ws_bytes, split_len, _p(out), _stream()), "mdl_attn_decode")
+        _p(prompt_mask), prompt_len, _p(row_holes), _p(kv_start), _p(row_order), seq_pos,
+        _p(seq_dev),
+        _p(workspace), ws_bytes, split_len, _p(out), _stream()), "mdl_attn_decode")
 
 
 def lm_head(x: torch.Tensor, row_index: torch.Tensor | None, rows: int, gamma: torch.Tensor,
@@ -200,9 +238,33 @@ def lm_head(x: torch.Tensor, row_index: torch.Tensor | None, rows: int, gamma: t
         _p(token_out), _stream()), "mdl_lm_head")
 
 
+def decode_head(x: torch.Tensor, gamma: torch.Tensor, eps: float, w_head: torch.Tensor,
+                logits_out: torch.Tensor | None, token_out: torch.Tensor, out_ids: torch.Tensor,
+                col: int, counters: torch.Tensor | None, finish_step: torch.Tensor | None,
+                gen_base: int, end_id: int) -> None:
+    """ln_f + LM head + argmax into token_out, committed to out_ids[:, counters[1] or col]."""
+    batch, d = x.shape
+    vocab = w_head.shape[0]
+    _need(x, "x", F32)
+    _need(gamma, "gamma", F32, d)
+    _need(w_head, "w_head", F32, vocab * d)
+    _need(logits_out, "logits_out", F32, batch * vocab, optional=True)
+    _need(token_out, "token_out", I64, batch)
+    _need(out_ids, "out_ids", I64)
+    if out_ids.dim() != 2 or out_ids.shape[0] != batch:
+        raise ValueError("out_ids must be [batch, columns]")
+    _need(counters, "counters", I32, 2, optional=True)
+    _need(finish_step, "finish_step", I32, batch, optional=True)
+    _lib.check(_lib.lib().mdl_decode_head(
+        _p(x), batch, d, _p(gamma), eps, _p(w_head), vocab, _p(logits_out), _p(token_out),
+        _p(out_ids), out_ids.shape[1], col, _p(counters), _p(finish_step), gen_base, end_id,
+        _stream()), "mdl_decode_head")
+
+
 def grid_init(ids: torch.Tensor, pos: torch.Tensor, mask: torch.Tensor | None, gx: torch.Tensor,
               gy: torch.Tensor, in_out: torch.Tensor, kv_start: torch.Tensor | None,
-              last_row: torch.Tensor | None, max_x: int = 30, max_y: int = 29) -> None:
+              last_row: torch.Tensor | None, max_x: int = 30, max_y: int = 29,
+              row_holes: torch.Tensor | None = None) -> None:
     batch, seq = ids.shape
     _need(ids, "ids", I64)
     _need(pos, "pos", I64, batch * seq * 3)
@@ -212,9 +274,10 @@ def grid_init(ids: torch.Tensor, pos: torch.Tensor, mask: torch.Tensor | None, g
     _need(in_out, "in_out", U8, batch)
     _need(kv_start, "kv_start", I32, batch, optional=True)
     _need(last_row, "last_row", I32, batch, optional=True)
+    _need(row_holes, "row_holes", U8, batch, optional=True)
     _lib.check(_lib.lib().mdl_grid_init(
         _p(ids), _p(pos), _p(mask), batch, seq, max_x, max_y, _p(gx), _p(gy), _p(in_out),
-        _p(kv_start), _p(last_row), _stream()), "mdl_grid_init")
+        _p(kv_start), _p(last_row), _p(row_holes), _stream()), "mdl_grid_init")
 
 
 def grid_step(token: torch.Tensor, gx: torch.Tensor, gy: torch.Tensor, in_out: torch.Tensor,

@@ -49,7 +49,7 @@ def test_argument_errors_are_reported_before_any_launch():
     assert L.mdl_swiglu(fake + 2, 16, None, None, None, 1, 8, fake, None) == -2
     assert L.mdl_qkv_rope_cache(fake, 192, None, fake, fake, 1, 4, 1, 64, 32, 32, 8, 10, 10, 12,
                                 0.125, fake, fake, fake, 4, 1, None, None) == -5
-    assert L.mdl_attn_decode(fake, fake, fake, 1, 1, 64, 1024, None, 0, None, 5, None, None, 0,
-                             128, fake, None) == -6
+    assert L.mdl_attn_decode(fake, fake, fake, 1, 1, 64, 1024, None, 0, None, None, None, 5,
+                             None, None, 0, 128, fake, None) == -6
     with pytest.raises(RuntimeError, match="head_dim"):
         _lib.check(-4, "probe")

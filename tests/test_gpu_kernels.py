@@ -256,11 +256,22 @@ def test_attn_decode(split_len, with_mask):
     ws_n = K().attn_decode_workspace_bytes(B, H, slots, split_len) // 4
     ws = torch.empty(max(ws_n, 1), device=DEV) if ws_n else None
     out = torch.empty(B, 2 * H * 64, device=DEV, dtype=torch.bfloat16)
-    for dev_seq in (False, True):
+    holes = None
+    if pm is not None:
+        # rows without holes skip the mask; row 2 has one and must keep reading it
+        holes = torch.tensor([0 if (not pm[b].any() or bool(pm[b, int(kv_start[b]):].all()))
+                              else 1 for b in range(B)], dtype=torch.uint8)
+        assert holes[2] == 1 and holes.sum() == 1
+        holes = holes.to(DEV)
+    order = torch.tensor([3, 0, 4, 2, 1], dtype=torch.int32, device=DEV)
+    for dev_seq, use_holes, use_order in ((False, False, False), (True, False, True),
+                                          (True, True, True)):
         seq_dev = torch.tensor([t], dtype=torch.int32, device=DEV) if dev_seq else None
         K().attn_decode(q.to(DEV), kc.to(DEV), vc.to(DEV), B, H,
                         None if pm is None else pm.to(torch.uint8).to(DEV), S if pm is not None
-                        else 0, kv_start, t, seq_dev, ws, split_len, out)
+                        else 0, kv_start, t, seq_dev, ws, split_len, out,
+                        row_holes=holes if use_holes else None,
+                        row_order=order if use_order else None)
         torch.cuda.synchronize()
         keymask = torch.ones(B, t + 1, dtype=torch.bool)
         if pm is not None:
@@ -326,8 +337,9 @@ def test_grid_kernels_match_reference_golden():
     kvs = torch.empty(B, dtype=torch.int32, device=DEV)
     last = torch.empty(B, dtype=torch.int32, device=DEV)
     mask = torch.from_numpy(gs["p_mask"])
+    holes = torch.empty(B, dtype=torch.uint8, device=DEV)
     K().grid_init(torch.from_numpy(gs["p_ids"]).to(DEV), torch.from_numpy(gs["p_pos"]).to(DEV),
-                  mask.to(torch.uint8).to(DEV), ox, oy, oio, kvs, last)
+                  mask.to(torch.uint8).to(DEV), ox, oy, oio, kvs, last, row_holes=holes)
     init = np.stack([ox.cpu().numpy(), oy.cpu().numpy(), oio.cpu().numpy()], 1).astype(np.int64)
     assert np.array_equal(init, gs["init"])
     L = mask.shape[1]
@@ -335,6 +347,76 @@ def test_grid_kernels_match_reference_golden():
     first = torch.where(n_valid > 0, mask.float().argmax(1), torch.full((B,), L))
     assert torch.equal(kvs.cpu().long(), first)
     assert torch.equal(last.cpu().long(), torch.arange(B) * L + (n_valid - 1).clamp(min=0))
+    # a row has holes iff its valid positions are not exactly [first, L)
+    want = torch.tensor([0 if n_valid[b] == L - first[b] else 1 for b in range(B)],
+                        dtype=torch.uint8)
+    assert torch.equal(holes.cpu(), want)
+    assert want.sum() > 0 and (want == 0).sum() > 0          # the fixture exercises both kinds
+
+
+@pytest.mark.parametrize("d,with_ex", [(256, True), (768, True), (1280, False)])
+def test_decode_embed_equals_grid_step_plus_embed(d, with_ex):
+    """The fused decode-step entry equals mdl_grid_step followed by mdl_embed_rmsnorm."""
+    g = torch.Generator().manual_seed(d)
+    B, V, NE = 37, 14, 9
+    tok = torch.randn(V, d, generator=g).to(torch.bfloat16).to(DEV)
+    ex = torch.randn(NE, d, generator=g).to(torch.bfloat16).to(DEV)
+    gamma = (1 + 0.1 * torch.randn(d, generator=g)).to(DEV)
+    ex_ids = torch.randint(0, NE, (B,), generator=g).to(DEV) if with_ex else None
+    state0 = (torch.randint(0, 33, (B,), generator=g).to(torch.int32),
+              torch.randint(0, 31, (B,), generator=g).to(torch.int32),
+              torch.randint(0, 2, (B,), generator=g).to(torch.uint8))
+    outs = []
+    for fused in (False, True):
+        gx, gy, io = (s.clone().to(DEV) for s in state0)
+        counters = torch.tensor([3, 7], dtype=torch.int32, device=DEV)
+        pos = torch.empty(B, 3, dtype=torch.int64, device=DEV)
+        x = torch.empty(B, d, device=DEV)
+        xs = torch.empty(B, 2 * d, device=DEV, dtype=torch.bfloat16)
+        r = torch.empty(B, device=DEV)
+        for step in range(5):
+            token = torch.randint(0, V, (B,), generator=torch.Generator().manual_seed(step)).to(DEV)
+            if fused:
+                K().decode_embed(token, ex_ids, tok, ex if with_ex else None, gamma, 1e-5, gx, gy,
+                                 io, pos, counters, x, xs, r)
+            else:
+                K().grid_step(token, gx, gy, io, pos, counters)
+                K().embed_rmsnorm(token, ex_ids, tok, ex if with_ex else None, 1, gamma, 1e-5, x,
+                                  xs, r)
+        torch.cuda.synchronize()
+        outs.append([t.cpu() for t in (gx, gy, io, counters, pos, x, xs, r)])
+    for a, b in zip(*outs):
+        assert torch.equal(a, b)
+    assert outs[1][3].tolist() == [8, 12]
+
+
+@pytest.mark.parametrize("d,V", [(128, 14), (768, 14), (1280, 14), (256, 20)])
+def test_decode_head_equals_lm_head_plus_commit(d, V):
+    g = torch.Generator().manual_seed(d + V)
+    B, cols = 45, 16
+    x = (torch.randn(B, d, generator=g) * 2).to(DEV)
+    gamma = (1 + 0.1 * torch.randn(d, generator=g)).to(DEV)
+    w = (torch.randn(V, d, generator=g) / math.sqrt(d)).to(DEV)
+    w[V - 1] = w[2]                                  # exact tie: first index must win
+    ref_logits = torch.empty(B, V, device=DEV)
+    ref_tok = torch.empty(B, dtype=torch.int64, device=DEV)
+    K().lm_head(x, None, B, gamma, 1e-5, w, ref_logits, ref_tok)
+    out_ref = torch.full((B, cols), -1, dtype=torch.int64, device=DEV)
+    fin_ref = torch.full((B,), -1, dtype=torch.int32, device=DEV)
+    counters = torch.tensor([0, 9], dtype=torch.int32, device=DEV)
+    K().decode_commit(ref_tok, out_ref, 0, counters, fin_ref, 4, 2)
+    logits = torch.empty(B, V, device=DEV)
+    tok = torch.empty(B, dtype=torch.int64, device=DEV)
+    out = torch.full((B, cols), -1, dtype=torch.int64, device=DEV)
+    fin = torch.full((B,), -1, dtype=torch.int32, device=DEV)
+    K().decode_head(x, gamma, 1e-5, w, logits, tok, out, 0, counters, fin, 4, 2)
+    torch.cuda.synchronize()
+    assert torch.equal(tok.cpu(), ref_tok.cpu())
+    assert torch.equal(out.cpu(), out_ref.cpu()) and torch.equal(fin.cpu(), fin_ref.cpu())
+    assert (fin.cpu() == 5).sum() == (tok.cpu() == 2).sum()      # token 2 stands for END here
+    ref = rp.rmsnorm(x.cpu().double(), gamma.cpu().double(), 1e-5) @ w.cpu().double().T
+    assert torch.allclose(logits.cpu().double(), ref, atol=2e-5, rtol=1e-5)
+    assert not bool((tok.cpu() == V - 1).any())      # the tied duplicate of slot 2 never wins
 
 
 def test_decode_commit():
@@ -367,6 +449,6 @@ def test_capi_rejects_bad_arguments_before_launch():
     assert L.mdl_swiglu(x.data_ptr() + 2, 16, None, None, None, 1, 8, x.data_ptr(), None) == -2
     # workspace too small for a multi-split decode
     assert L.mdl_attn_decode(x.data_ptr(), x.data_ptr(), x.data_ptr(), 1, 1, 64, 1024, None, 0,
-                             None, 5, None, None, 0, 128, x.data_ptr(), None) == -6
+                             None, None, None, 5, None, None, 0, 128, x.data_ptr(), None) == -6
     with pytest.raises(RuntimeError, match="head_dim"):
         _lib.check(-4, "probe")
