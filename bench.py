@@ -92,19 +92,22 @@ def recorded_traffic(kernel: str, workload: str):
     return None, None
 
 
-def decode_attention_bytes(B, H, t, kv_start, S):
-    """Algorithmic bytes of one decode-attention launch at cache position t: every row reads the
-    K and V rows of the slots it attends (kv_start[b]..t, 2 x 64 bf16 per head each), its q
-    (64 bf16 per head), writes the split output (2 x 64 bf16 per head) and reads its prompt mask
-    bytes once."""
+def decode_attention_bytes(B, H, t, kv_start, S, holes):
+    """Algorithmic bytes of one fused decode-attention launch (mdl_attn_decode_rope) at cache
+    position t: every (row, head) reads its q/k/v slice of the fp32 qkv row (3 x 64 x 4 B),
+    writes the token's K and V into slot t (2 x 128 B), reads the K and V rows of the slots it
+    attends (kv_start[b]..t, 2 x 128 B each) and writes the split output (2 x 128 B); rows whose
+    prompt mask has holes also read their mask bytes."""
     import torch
 
-    n = (t + 1 - kv_start.to(torch.int64)).clamp(min=0)
+    ks = kv_start.to(torch.int64)
+    n = (t + 1 - ks).clamp(min=0)
     kv = int(n.sum()) * H * 64 * 2 * 2
-    q = B * H * 64 * 2
+    qkv_in = B * H * 3 * 64 * 4
+    kv_out = B * H * 2 * 64 * 2
     out = B * H * 64 * 2 * 2
-    mask = int((S - kv_start.to(torch.int64)).clamp(min=0).sum())
-    return kv + q + out + mask
+    mask = int(((S - ks).clamp(min=0) * holes.to(torch.int64)).sum())
+    return kv + qkv_in + kv_out + out + mask
 
 
 def microbench(dev):
@@ -184,7 +187,15 @@ def microbench(dev):
     return res
 
 
-def cpu_baseline(model_state, cfg, st, ex, t0, seconds):
+def snapshot_decode_state(st, ex):
+    """Host copy of what the CPU baseline continues from: the cache (bf16 -> fp32), the current
+    token, the grid state and the masks."""
+    return dict(B=st.B, S=st.S, total=st.total, cache=st.cache.cache.cpu().float(),
+                tok=st.tok.cpu(), gx=st.gx.cpu(), gy=st.gy.cpu(), gio=st.gio.cpu(),
+                pmask=st.pmask.cpu().bool(), ex=ex.cpu())
+
+
+def cpu_baseline(model_state, cfg, snap, t0, seconds):
     """fp32 CPU oracle decoding the same B rows from the GPU's cache contents (upcast to fp32)
     for as many steps as fit in ``seconds`` (at least 2)."""
     import torch
@@ -194,13 +205,13 @@ def cpu_baseline(model_state, cfg, st, ex, t0, seconds):
     ocfg = rp.OracleConfig(cfg.d_model, cfg.n_heads, cfg.n_layers, cfg.d_ff, cfg.num_examples,
                            cfg.max_seq_len)
     om = rp.OracleModel(ocfg, model_state, dtype=torch.float32)
-    B, S, total = st.B, st.S, st.total
-    cache = st.cache.cache.cpu().float()
-    tok = st.tok.cpu()
-    grid = rp.GridState(st.gx.cpu(), st.gy.cpu(), st.gio.cpu())
+    B, S, total = snap["B"], snap["S"], snap["total"]
+    cache = snap["cache"]
+    tok = snap["tok"]
+    grid = rp.GridState(snap["gx"], snap["gy"], snap["gio"])
     key_mask = torch.ones(B, total, dtype=torch.bool)
-    key_mask[:, :S] = st.pmask.cpu().bool()
-    exc = ex.cpu()
+    key_mask[:, :S] = snap["pmask"]
+    exc = snap["ex"]
     steps, t = 0, t0
     start = time.perf_counter()
     while t + 1 < total:
@@ -297,30 +308,38 @@ def main() -> int:
         wall_s = time.perf_counter() - wall0
         timed_ms = tm.ms()
 
-        # decode attention: re-issue the timed region's launches (every layer at every cache
-        # position t of the timed steps) back to back on the launching stream, between one pair
-        # of HIP events; the queue never drains, so the events time kernel execution only
+        # the CPU baseline continues from this state; take it before the re-launches below
+        # rewrite the slots they attend to
+        snap = snapshot_decode_state(st, ex_d) if args.cpu_seconds > 0 else None
+
+        # decode attention (the fused mdl_attn_decode_rope the step runs): re-issue the timed
+        # region's launches (every layer at every cache position t of the timed steps) back to
+        # back on the launching stream, between one pair of HIP events; the queue never drains,
+        # so the events time kernel execution only
         H = cfg.n_heads
-        kv_start_h = st.kv_start.cpu()
+        kv_start_h, holes_h = st.kv_start.cpu(), st.holes.cpu()
         ts = [t_first + i for i in range(args.steps) for _ in range(cfg.n_layers)]
         layers = [li for _ in range(args.steps) for li in range(cfg.n_layers)]
+        qs = 1.0 / 8.0
         ta = Timer()
         ta.start()
         for t, li in zip(ts, layers):
             kc, vc = st.cache.layer(li)
-            K.attn_decode(st.sc.q, kc, vc, B, H, st.pmask, S, st.kv_start, t, None, st.ws,
-                          st.split_len, st.sc.attn, row_holes=st.holes, row_order=st.order)
+            K.attn_decode_rope(st.sc.qkv, st.sc.rstd, st.pos, W.rope_tab, W.rope_geom, qs, kc,
+                               vc, B, H, st.pmask, S, st.kv_start, t, None, st.ws, st.split_len,
+                               st.sc.attn, row_holes=st.holes, row_order=st.order)
         ta.stop()
         attn_ms = ta.ms() / len(ts)
-        attn_bytes = sum(decode_attention_bytes(B, H, t, kv_start_h, S) for t in ts) / len(ts)
+        attn_bytes = sum(decode_attention_bytes(B, H, t, kv_start_h, S, holes_h)
+                         for t in ts) / len(ts)
         achieved = attn_bytes / attn_ms / 1e6
         durs = ts
 
         micro = None if args.no_micro else microbench(dev)
 
         cpu = None
-        if args.cpu_seconds > 0:
-            cpu = cpu_baseline(model_state, cfg, st, ex, S + args.warmup + args.steps,
+        if snap is not None:
+            cpu = cpu_baseline(model_state, cfg, snap, S + args.warmup + args.steps,
                                args.cpu_seconds)
 
     n_valid = mask.sum(1)
@@ -353,7 +372,8 @@ def main() -> int:
             "graph": not args.eager, "workload_seed": spec.seed,
         },
         "roofline": {
-            "kernel": "attn_decode_kernel (+ attn_decode_combine_kernel)",
+            "kernel": "attn_decode_kernel<4, true> (mdl_attn_decode_rope: K2 + decode "
+                      "attention, one split per (row, head) at this shape)",
             "bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS,
             "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": traffic,
             "traffic_source": traffic_src,

@@ -165,6 +165,23 @@ int mdl_attn_decode(const uint16_t* q, const uint16_t* k_cache, const uint16_t* 
                     void* stream);
 
 /*
+ * K2 + K4b fused for the decode step: mdl_qkv_rope_cache (seq = 1, slot t) followed by
+ * mdl_attn_decode, in one launch.  Each (row, head) block rotates its head's q and k of the
+ * decode token from qkv (fp32 [batch, 3*d], row stride qkv_ld), writes k / v into cache slot t
+ * (t = seq_dev ? *seq_dev : seq_pos) and attends as mdl_attn_decode.  q is rounded to bf16 as
+ * mdl_qkv_rope_cache rounds it.  Arguments as in those two entry points.
+ * Replaces: the same reference ops as mdl_qkv_rope_cache and mdl_attn_decode, for one token.
+ */
+int mdl_attn_decode_rope(const float* qkv, int64_t qkv_ld, const float* rstd, const int64_t* pos,
+                         const float* rope_tab, int max_x, int max_y, int max_z, int px, int py,
+                         int pz, float q_scale, uint16_t* k_cache, uint16_t* v_cache, int batch,
+                         int n_heads, int head_dim, int cache_slots, const uint8_t* prompt_mask,
+                         int prompt_len, const uint8_t* row_holes, const int32_t* kv_start,
+                         const int32_t* row_order, int seq_pos, const int32_t* seq_dev,
+                         float* workspace, int64_t workspace_bytes, int split_len, uint16_t* out,
+                         void* stream);
+
+/*
  * Final RMSNorm + LM head + greedy argmax.
  * Replaces: model.lm_head(model.ln_f(x)) in _prefill / _decode_step (src/inference.py:417-424,
  *           :459) including the x[b, lengths-1] row pick, and logits.argmax(-1)

@@ -36,6 +36,9 @@ SIGNATURES: dict[str, tuple[object, list]] = {
     "mdl_attn_decode_workspace_bytes": (c_int64, [c_int, c_int, c_int, c_int]),
     "mdl_attn_decode": (c_int, [P, P, P, c_int, c_int, c_int, c_int, P, c_int, P, P, P, c_int,
                                 P, P, c_int64, c_int, P, P]),
+    "mdl_attn_decode_rope": (c_int, [P, c_int64, P, P, P, c_int, c_int, c_int, c_int, c_int,
+                                     c_int, c_float, P, P, c_int, c_int, c_int, c_int, P, c_int,
+                                     P, P, P, c_int, P, P, c_int64, c_int, P, P]),
     "mdl_lm_head": (c_int, [P, P, c_int, c_int, P, c_float, P, c_int, P, P, P]),
     "mdl_decode_head": (c_int, [P, c_int, c_int, P, c_float, P, c_int, P, P, P, c_int64, c_int,
                                 P, P, c_int, c_int, P]),

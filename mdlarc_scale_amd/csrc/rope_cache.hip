@@ -10,12 +10,9 @@
 // v (no rotation) is streamed as float4 per lane.  Rotation (a, b) -> (a c - b s, b c + a s) is
 // the interleaved-pair form of _rotate_half.
 #include "common.h"
+#include "rope.h"
 
 namespace mdl {
-
-struct RopeArgs {
-  int max_x, max_y, max_z, px, py, pz;
-};
 
 __global__ __launch_bounds__(256) void qkv_rope_cache_kernel(
     const float* __restrict__ qkv, int64_t ld, const float* __restrict__ rstd,
@@ -29,21 +26,8 @@ __global__ __launch_bounds__(256) void qkv_rope_cache_kernel(
   const int j = lane & 31, first_head = lane >> 5;
   const int d = n_heads * kHeadDim;
 
-  // table segment of pair j: [cos_x | sin_x | cos_y | sin_y | cos_z | sin_z], axis-major
-  int axis, n_pos, pairs, jj, off;
-  if (j < ra.px) {
-    axis = 0; n_pos = ra.max_x; pairs = ra.px; jj = j; off = 0;
-  } else if (j < ra.px + ra.py) {
-    axis = 1; n_pos = ra.max_y; pairs = ra.py; jj = j - ra.px; off = 2 * ra.max_x * ra.px;
-  } else {
-    axis = 2; n_pos = ra.max_z; pairs = ra.pz; jj = j - ra.px - ra.py;
-    off = 2 * ra.max_x * ra.px + 2 * ra.max_y * ra.py;
-  }
-  int64_t p = pos[m * 3 + axis];
-  p = p < 0 ? 0 : (p >= n_pos ? n_pos - 1 : p);
-  const int ti = off + static_cast<int>(p) * pairs + jj;
-  const float cs = tab[ti];
-  const float sn = tab[ti + n_pos * pairs];
+  float cs, sn;
+  rope_cos_sin(j, pos + m * 3, tab, ra, cs, sn);
   const float r = rstd ? rstd[m] : 1.f;
 
   const float* row = qkv + m * ld;

@@ -301,10 +301,10 @@ class Generator:
         for li in range(cfg.n_layers):
             kc, vc = st.cache.layer(li)
             gemm_f32(sc.xs, W.qkv[li], sc.qkv)
-            K.qkv_rope_cache(sc.qkv, sc.rstd, st.pos, W.rope_tab, W.rope_geom, B, 1, H, qs,
-                             sc.q, kc, vc, slot_dev=slot)
-            K.attn_decode(sc.q, kc, vc, B, H, st.pmask, st.S, st.kv_start, 0, slot, st.ws,
-                          st.split_len, sc.attn, row_holes=st.holes, row_order=st.order)
+            # RMSNorm scale + split + 3D RoPE + cache write fused into the attention launch
+            K.attn_decode_rope(sc.qkv, sc.rstd, st.pos, W.rope_tab, W.rope_geom, qs, kc, vc, B,
+                               H, st.pmask, st.S, st.kv_start, 0, slot, st.ws, st.split_len,
+                               sc.attn, row_holes=st.holes, row_order=st.order)
             self.eng._mlp(W, li, sc)
 
     def decode_layers(self, st: DecodeState, W: PackedWeights, want_logits: bool) -> None:

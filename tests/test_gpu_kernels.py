@@ -284,6 +284,52 @@ def test_attn_decode(split_len, with_mask):
             f"max err {(got.double() - ref).abs().max().item():.3e}"
 
 
+@pytest.mark.parametrize("split_len", [128, 384, 1024])
+def test_attn_decode_rope_equals_k2_then_decode(split_len):
+    """The fused decode launch writes the same K/V into slot t (to 1 bf16 ulp of the rotation's
+    rounding) and returns the same attention as mdl_qkv_rope_cache + mdl_attn_decode."""
+    from mdlarc_scale_amd.transformer import RotaryEmbedding3D
+
+    g = torch.Generator().manual_seed(split_len)
+    B, H, slots, S, t = 6, 3, 900, 400, 777
+    d = 64 * H
+    qkv = torch.randn(B, 3 * d, generator=g).to(DEV)
+    rstd = (0.5 + torch.rand(B, generator=g)).to(DEV)
+    pos = torch.randint(0, 35, (B, 3), generator=g).to(DEV)
+    rope = RotaryEmbedding3D(64, 32, 32, 8)
+    tab, geom = rope.device_table(DEV), (32, 32, 8, rope.px, rope.py, rope.pz)
+    kc0 = bf(torch.randn(B, H, slots, 64, generator=g)).to(DEV)
+    vc0 = bf(torch.randn(B, H, slots, 64, generator=g)).to(DEV)
+    pm = _masks(B, S, "left", g)
+    pm[1, 300:310] = False
+    kv_start = torch.where(pm.any(1), pm.float().argmax(1), torch.full((B,), S))
+    kv_start = kv_start.to(torch.int32).to(DEV)
+    pm = pm.to(torch.uint8).to(DEV)
+    seq_dev = torch.tensor([t], dtype=torch.int32, device=DEV)
+    ws_n = K().attn_decode_workspace_bytes(B, H, slots, split_len) // 4
+    ws = torch.empty(max(ws_n, 1), device=DEV) if ws_n else None
+    order = torch.argsort(kv_start).to(torch.int32)
+    # unfused reference path
+    kc1, vc1 = kc0.clone(), vc0.clone()
+    q = torch.empty(B, d, device=DEV, dtype=torch.bfloat16)
+    out1 = torch.empty(B, 2 * d, device=DEV, dtype=torch.bfloat16)
+    K().qkv_rope_cache(qkv, rstd, pos, tab, geom, B, 1, H, 0.125, q, kc1, vc1, slot_dev=seq_dev)
+    K().attn_decode(q, kc1, vc1, B, H, pm, S, kv_start, 0, seq_dev, ws, split_len, out1,
+                    row_order=order)
+    # fused
+    kc2, vc2 = kc0.clone(), vc0.clone()
+    out2 = torch.empty_like(out1)
+    K().attn_decode_rope(qkv, rstd, pos, tab, geom, 0.125, kc2, vc2, B, H, pm, S, kv_start, 0,
+                         seq_dev, ws, split_len, out2, row_order=order)
+    torch.cuda.synchronize()
+    others = torch.ones(slots, dtype=torch.bool)
+    others[t] = False
+    assert torch.equal(kc1[:, :, others.to(DEV)], kc2[:, :, others.to(DEV)])
+    assert torch.equal(vc1, vc2)
+    close_bf16(kc2[:, :, t], kc1[:, :, t].float(), atol=1e-6, rtol=8e-3)
+    assert torch.allclose(unsplit(out2), unsplit(out1), rtol=2e-3, atol=2e-4)
+
+
 # ---------------------------------------------------------------------------- head + state
 
 @pytest.mark.parametrize("d", [128, 768, 1280])
