@@ -1,180 +1,250 @@
 // K4a -- prefill / full-sequence attention on bf16 MFMA (gfx950 v_mfma_f32_16x16x32_bf16).
 //
-// Block = 4 wavefronts = 64 queries of one (b, h); wave w owns queries q0+16w .. q0+16w+15.
-// Key tiles of 64 are staged in LDS: K row-major (A operand of S^T = K Q^T), V transposed
-// (A operand of O^T = V^T P^T).  Working with S^T instead of S makes the MFMA accumulator of the
-// scores (lane = one query, 4 keys per 16-key block) exactly the B-operand layout P^T needs for
-// the second product, so probabilities never leave registers:
+// Block = 4 wavefronts = 128 queries of one (b, h); wave w owns queries q0+32w .. q0+32w+31 as
+// two groups of 16 (j = 0, 1).  Key tiles of 64 are staged in LDS row-major, K and V alike.
+// Working with S^T = K Q^T instead of S makes the MFMA accumulator of the scores (lane = one
+// query, 4 keys per 16-key block) exactly the B-operand layout P^T needs in O^T = V^T P^T, so the
+// probabilities never leave registers:
 //   score block nb (keys 16nb..16nb+15), lane (c = lane%16, g = lane/16) holds keys 16nb+4g+i,
-//   i = 0..3, of query c.  The P^T operand of k-step kk takes blocks 2kk and 2kk+1, element j of
-//   group g = key 32kk + (j<4 ? 4g+j : 16+4g+j-4).  V^T is stored in LDS with its keys permuted
-//   into that same order, so the A operand of each k-step is one 16-byte LDS read.
-// An MFMA pairs element j of lane group g in A with element j of group g in B, whatever k that
-// is inside the instruction, so any common key order of the two operands is exact.
+//   i = 0..3, of query c.  The P^T operand of k-step kk takes blocks 2kk and 2kk+1: element e of
+//   lane group g is key 32kk + (e<4 ? 4g+e : 16+4g+e-4).
+// The matching V^T operand comes straight from the row-major V tile through two transposing LDS
+// reads (ds_read_b64_tr_b16): within each 16-lane group, lane i receives element i&3 of the 8-byte
+// rows addressed by lanes 4k + (i>>2), k = 0..3.  Lane c of group g addresses key row
+// 32kk + 4g + c/4 (and +16), dims 16db + 4(c%4) .. +3, which yields exactly V^T[dim 16db + c] over
+// the key order above.  An MFMA pairs element e of lane group g in A with element e of group g in
+// B whatever k that is inside the instruction, so any common key order of the operands is exact.
+// Each A operand read from LDS (K rows, V^T rows) feeds both query groups' MFMAs.
 //
-// Online softmax in the log2 domain, fp32 throughout; the per-lane partial row sums are merged
-// across the 4 lane groups once at the end.  Queries with no visible key produce 0.  The output
-// (the out-projection GEMM input) is written as a hi|lo bf16 pair per row, see common.h.
+// Masking: wave 0 folds key validity (inside [kv_start, S) and the key mask) of the tile into a
+// 64-bit ballot in LDS.  Tiles that are fully valid and entirely in the past of the wave's queries
+// skip all per-element work; the others AND the ballot with the causal prefix of each query.
+//
+// Online softmax in the log2 domain, fp32 (v_exp_f32 directly: results below 2^-126 flush to 0,
+// which no softmax weight of a visible key can reach relative to the row maximum).  The row sums
+// come from one more MFMA per k-step against a ones operand, so they sum the same bf16-rounded
+// probabilities the PV product uses.  Queries with no visible key produce 0.  The output (the
+// out-projection GEMM input) is written as a hi|lo bf16 pair per row, see common.h.
+//
+// Block order: block i runs on XCD i % 8; each (b, h) is pinned to one XCD, whose L2 then serves
+// all of that head's query tiles, and heads are dealt round-robin over the XCDs so that rows of
+// different lengths spread evenly.  Within a head the latest (most expensive) query tile runs
+// first.
 #include "common.h"
 
 namespace mdl {
 
 typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
+typedef __bf16 bf16x4_t __attribute__((ext_vector_type(4)));
 typedef float f32x4_t __attribute__((ext_vector_type(4)));
+typedef short s16x4_t __attribute__((ext_vector_type(4)));
 
-constexpr int kBM = 64;          // queries per block
+constexpr int kQW = 32;          // queries per wave
+constexpr int kBM = 4 * kQW;     // queries per block
 constexpr int kBN = 64;          // keys per tile
 constexpr int kLds = 72;         // LDS row stride (bf16 elements): 144 B rows, 16 B aligned
+constexpr int kXcds = 8;
 constexpr float kLog2eP = 1.4426950408889634f;
 
 __device__ __forceinline__ bf16x8_t as_bf16x8(uint4 v) { return __builtin_bit_cast(bf16x8_t, v); }
 
-// LDS position of key `k` (0..63) inside a transposed V row (see file comment).
-__device__ __forceinline__ int vt_pos(int k) {
-  const int nb = k >> 4, w = k & 15;
-  return 32 * (nb >> 1) + 8 * (w >> 2) + 4 * (nb & 1) + (w & 3);
+__device__ __forceinline__ s16x4_t lds_read_tr16(const uint16_t* p) {
+  return __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+      (__attribute__((address_space(3))) s16x4_t*)(p));
 }
 
-__global__ __launch_bounds__(256) void attn_prefill_kernel(
+__global__ __launch_bounds__(256, 3) void attn_prefill_kernel(
     const uint16_t* __restrict__ q, const uint16_t* __restrict__ kc,
     const uint16_t* __restrict__ vc, int S, int H, int slots, const uint8_t* __restrict__ kmask,
-    const int32_t* __restrict__ kv_start, int causal, uint16_t* __restrict__ out) {
-  const int qt = blockIdx.x, h = blockIdx.y, b = blockIdx.z;
+    const int32_t* __restrict__ kv_start, int causal, uint16_t* __restrict__ out, int nqt,
+    int n_bh) {
+  const int slot = blockIdx.x / kXcds;
+  const int kq = slot / nqt;
+  const int bh = blockIdx.x % kXcds + kXcds * kq;
+  if (bh >= n_bh) return;                       // padding blocks of the last round exit
+  const int qt = nqt - 1 - (slot - kq * nqt);
+  const int b = bh / H, h = bh - b * H;
   const int tid = threadIdx.x;
   const int wave = tid >> 6, lane = tid & 63, c16 = lane & 15, g = lane >> 4;
   const int q0 = qt * kBM;
 
   __shared__ __attribute__((aligned(16))) uint16_t Ks[kBN * kLds];
-  __shared__ __attribute__((aligned(16))) uint16_t Vt[kHeadDim * kLds];
-  __shared__ uint8_t Ms[kBN];
+  __shared__ __attribute__((aligned(16))) uint16_t Vs[kBN * kLds];
+  __shared__ uint64_t Mw;
 
-  const int qi = q0 + 16 * wave + c16;
-  bf16x8_t qf[2];
-  if (qi < S) {
-    const uint16_t* qp = q + ((static_cast<int64_t>(b) * S + qi) * H + h) * kHeadDim;
-    qf[0] = as_bf16x8(*reinterpret_cast<const uint4*>(qp + 8 * g));
-    qf[1] = as_bf16x8(*reinterpret_cast<const uint4*>(qp + 32 + 8 * g));
-  } else {
-    qf[0] = as_bf16x8(make_uint4(0, 0, 0, 0));
-    qf[1] = qf[0];
+  const int wq0 = q0 + kQW * wave;
+  int qi[2];
+  bf16x8_t qf[2][2];
+#pragma unroll
+  for (int j = 0; j < 2; ++j) {
+    qi[j] = wq0 + 16 * j + c16;
+    if (qi[j] < S) {
+      const uint16_t* qp = q + ((static_cast<int64_t>(b) * S + qi[j]) * H + h) * kHeadDim;
+      qf[j][0] = as_bf16x8(*reinterpret_cast<const uint4*>(qp + 8 * g));
+      qf[j][1] = as_bf16x8(*reinterpret_cast<const uint4*>(qp + 32 + 8 * g));
+    } else {
+      qf[j][0] = as_bf16x8(make_uint4(0, 0, 0, 0));
+      qf[j][1] = qf[j][0];
+    }
   }
 
   const int64_t head_off = (static_cast<int64_t>(b) * H + h) * slots * kHeadDim;
   const uint16_t* Kg = kc + head_off;
   const uint16_t* Vg = vc + head_off;
-  const int kstart = kv_start ? kv_start[b] : 0;
+  const int kstart = kv_start ? min(max(kv_start[b], 0), S) : 0;
   const int kt0 = (kstart / kBN) * kBN;
   const int kend = causal ? min(S, q0 + kBM) : S;
+  const uint8_t* mrow = kmask ? kmask + static_cast<int64_t>(b) * S : nullptr;
+  const bf16x8_t ones = as_bf16x8(make_uint4(0x3f803f80u, 0x3f803f80u, 0x3f803f80u, 0x3f803f80u));
 
-  float m_run = -INFINITY, l_run = 0.f;
-  f32x4_t o[4];
+  float m_run[2] = {-INFINITY, -INFINITY};
+  f32x4_t lsum[2], o[2][4];
 #pragma unroll
-  for (int db = 0; db < 4; ++db) o[db] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+  for (int j = 0; j < 2; ++j) {
+    lsum[j] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int db = 0; db < 4; ++db) o[j][db] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+  }
 
   for (int kt = kt0; kt < kend; kt += kBN) {
-    __syncthreads();   // the previous tile's LDS readers are done
+    // stage the tile: 64 keys x 128 B of K and of V, 16 B per lane per load
+    uint4 pk[2], pv[2];
 #pragma unroll
     for (int rep = 0; rep < 2; ++rep) {
       const int ch = tid + rep * 256;
       const int key = ch >> 3, d0 = (ch & 7) * 8;
       const int kj = kt + key;
-      uint4 kv = make_uint4(0, 0, 0, 0), vv = make_uint4(0, 0, 0, 0);
+      pk[rep] = make_uint4(0, 0, 0, 0);
+      pv[rep] = pk[rep];
       if (kj < S) {
-        kv = *reinterpret_cast<const uint4*>(Kg + static_cast<int64_t>(kj) * kHeadDim + d0);
-        vv = *reinterpret_cast<const uint4*>(Vg + static_cast<int64_t>(kj) * kHeadDim + d0);
-      }
-      *reinterpret_cast<uint4*>(&Ks[key * kLds + d0]) = kv;
-      const int p = vt_pos(key);
-      const uint32_t w4[4] = {vv.x, vv.y, vv.z, vv.w};
-#pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        Vt[(d0 + 2 * i) * kLds + p] = static_cast<uint16_t>(w4[i] & 0xffffu);
-        Vt[(d0 + 2 * i + 1) * kLds + p] = static_cast<uint16_t>(w4[i] >> 16);
+        pk[rep] = *reinterpret_cast<const uint4*>(Kg + static_cast<int64_t>(kj) * kHeadDim + d0);
+        pv[rep] = *reinterpret_cast<const uint4*>(Vg + static_cast<int64_t>(kj) * kHeadDim + d0);
       }
     }
-    if (tid < kBN) {
-      const int kj = kt + tid;
-      Ms[tid] = (kj < S && kj >= kstart &&
-                 (!kmask || kmask[static_cast<int64_t>(b) * S + kj] != 0)) ? 1 : 0;
+    bool key_ok = false;
+    if (wave == 0) {
+      const int kj = kt + lane;
+      key_ok = kj < S && kj >= kstart && (!mrow || mrow[kj] != 0);
+    }
+    __syncthreads();   // the previous tile's LDS readers are done
+#pragma unroll
+    for (int rep = 0; rep < 2; ++rep) {
+      const int ch = tid + rep * 256;
+      const int key = ch >> 3, d0 = (ch & 7) * 8;
+      *reinterpret_cast<uint4*>(&Ks[key * kLds + d0]) = pk[rep];
+      *reinterpret_cast<uint4*>(&Vs[key * kLds + d0]) = pv[rep];
+    }
+    if (wave == 0) {
+      const uint64_t bal = __ballot(key_ok);
+      if (lane == 0) Mw = bal;
     }
     __syncthreads();
+    if (causal && kt > wq0 + kQW - 1) continue;   // the whole tile is in this wave's future
+    const uint64_t mw = Mw;
 
-    // S^T = K Q^T for 4 blocks of 16 keys
-    f32x4_t sc[4];
+    // S^T = K Q^T: 4 blocks of 16 keys for both query groups
+    f32x4_t sc[2][4];
 #pragma unroll
     for (int nb = 0; nb < 4; ++nb) {
-      sc[nb] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+      sc[0][nb] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+      sc[1][nb] = sc[0][nb];
 #pragma unroll
       for (int kk = 0; kk < 2; ++kk) {
         const bf16x8_t a = as_bf16x8(
             *reinterpret_cast<const uint4*>(&Ks[(nb * 16 + c16) * kLds + 32 * kk + 8 * g]));
-        sc[nb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, qf[kk], sc[nb], 0, 0, 0);
+        sc[0][nb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, qf[0][kk], sc[0][nb], 0, 0, 0);
+        sc[1][nb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, qf[1][kk], sc[1][nb], 0, 0, 0);
       }
     }
 
-    float s[4][4];
-    float tmax = -INFINITY;
+    const bool full = (mw == ~0ull) && (!causal || kt + kBN - 1 <= wq0);
+    if (!full) {
 #pragma unroll
-    for (int nb = 0; nb < 4; ++nb) {
+      for (int j = 0; j < 2; ++j) {
+        uint64_t vis = mw;
+        if (causal) {
+          const int x = qi[j] - kt;    // offset of the last key query qi[j] may see
+          vis &= x >= 63 ? ~0ull : (x < 0 ? 0ull : (2ull << x) - 1ull);
+        }
+        vis >>= 4 * g;
+        const uint32_t lo = static_cast<uint32_t>(vis), hi = static_cast<uint32_t>(vis >> 32);
 #pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        const int kl = nb * 16 + 4 * g + i;
-        const bool ok = Ms[kl] && (!causal || kt + kl <= qi);
-        s[nb][i] = ok ? sc[nb][i] * kLog2eP : -INFINITY;
-        tmax = fmaxf(tmax, s[nb][i]);
+        for (int nb = 0; nb < 4; ++nb)
+#pragma unroll
+          for (int i = 0; i < 4; ++i) {
+            const uint32_t word = nb < 2 ? lo : hi;
+            if (!((word >> (16 * (nb & 1) + i)) & 1u)) sc[j][nb][i] = -INFINITY;
+          }
       }
     }
-    tmax = fmaxf(tmax, __shfl_xor(tmax, 16, kWave));
-    tmax = fmaxf(tmax, __shfl_xor(tmax, 32, kWave));
-    const float mnew = fmaxf(m_run, tmax);
-    const float alpha = (mnew == -INFINITY) ? 1.f : exp2f(m_run - mnew);
-    float psum = 0.f;
-#pragma unroll
-    for (int nb = 0; nb < 4; ++nb) {
-#pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        const float p = (mnew == -INFINITY) ? 0.f : exp2f(s[nb][i] - mnew);
-        s[nb][i] = p;
-        psum += p;
-      }
-    }
-    l_run = l_run * alpha + psum;
-    m_run = mnew;
-#pragma unroll
-    for (int db = 0; db < 4; ++db) o[db] *= alpha;
 
-    // O^T += V^T P^T, two k-steps of 32 keys
+    bf16x8_t pb[2][2];
+#pragma unroll
+    for (int j = 0; j < 2; ++j) {
+      float tmax = -INFINITY;
+#pragma unroll
+      for (int nb = 0; nb < 4; ++nb)
+#pragma unroll
+        for (int i = 0; i < 4; ++i) tmax = fmaxf(tmax, sc[j][nb][i]);
+      tmax = fmaxf(tmax, __shfl_xor(tmax, 16, kWave));
+      tmax = fmaxf(tmax, __shfl_xor(tmax, 32, kWave));
+      const float mnew = fmaxf(m_run[j], tmax * kLog2eP);
+      const float mb = (mnew == -INFINITY) ? 0.f : mnew;   // no visible key yet: p = 0
+      const float alpha = __builtin_amdgcn_exp2f(m_run[j] - mb);
+      m_run[j] = mnew;
+      lsum[j] *= alpha;
+#pragma unroll
+      for (int db = 0; db < 4; ++db) o[j][db] *= alpha;
+#pragma unroll
+      for (int nb = 0; nb < 4; ++nb)
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+          sc[j][nb][i] = __builtin_amdgcn_exp2f(fmaf(sc[j][nb][i], kLog2eP, -mb));
+#pragma unroll
+      for (int kk = 0; kk < 2; ++kk)
+        pb[j][kk] = bf16x8_t{(__bf16)sc[j][2 * kk][0], (__bf16)sc[j][2 * kk][1],
+                             (__bf16)sc[j][2 * kk][2], (__bf16)sc[j][2 * kk][3],
+                             (__bf16)sc[j][2 * kk + 1][0], (__bf16)sc[j][2 * kk + 1][1],
+                             (__bf16)sc[j][2 * kk + 1][2], (__bf16)sc[j][2 * kk + 1][3]};
+    }
+
+    // O^T += V^T P^T and the row sums, two k-steps of 32 keys
 #pragma unroll
     for (int kk = 0; kk < 2; ++kk) {
-      uint4 pw;
-      pw.x = pack_bf2(s[2 * kk][0], s[2 * kk][1]);
-      pw.y = pack_bf2(s[2 * kk][2], s[2 * kk][3]);
-      pw.z = pack_bf2(s[2 * kk + 1][0], s[2 * kk + 1][1]);
-      pw.w = pack_bf2(s[2 * kk + 1][2], s[2 * kk + 1][3]);
-      const bf16x8_t pb = as_bf16x8(pw);
 #pragma unroll
       for (int db = 0; db < 4; ++db) {
-        const bf16x8_t a = as_bf16x8(
-            *reinterpret_cast<const uint4*>(&Vt[(16 * db + c16) * kLds + 32 * kk + 8 * g]));
-        o[db] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, pb, o[db], 0, 0, 0);
+        const int r0 = 32 * kk + 4 * g + (c16 >> 2);
+        const int cc = 16 * db + 4 * (c16 & 3);
+        const s16x4_t lo4 = lds_read_tr16(&Vs[r0 * kLds + cc]);
+        const s16x4_t hi4 = lds_read_tr16(&Vs[(r0 + 16) * kLds + cc]);
+        const bf16x8_t a = __builtin_bit_cast(
+            bf16x8_t, __builtin_shufflevector(lo4, hi4, 0, 1, 2, 3, 4, 5, 6, 7));
+        o[0][db] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, pb[0][kk], o[0][db], 0, 0, 0);
+        o[1][db] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, pb[1][kk], o[1][db], 0, 0, 0);
       }
+      lsum[0] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ones, pb[0][kk], lsum[0], 0, 0, 0);
+      lsum[1] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ones, pb[1][kk], lsum[1], 0, 0, 0);
     }
   }
 
-  float l = l_run + __shfl_xor(l_run, 16, kWave);
-  l += __shfl_xor(l, 32, kWave);
-  if (qi < S) {
-    // output row (b, qi) holds 2*H*64 bf16: hi of every head, then lo of every head
+  // output row (b, qi) holds 2*H*64 bf16: hi of every head, then lo of every head
+  const int64_t d = static_cast<int64_t>(H) * kHeadDim;
+#pragma unroll
+  for (int j = 0; j < 2; ++j) {
+    if (qi[j] >= S) continue;
+    const float l = lsum[j][0];     // every row of the ones product holds the query's sum
     const float inv = l > 0.f ? 1.f / l : 0.f;
-    const int64_t d = static_cast<int64_t>(H) * kHeadDim;
-    uint16_t* op = out + (static_cast<int64_t>(b) * S + qi) * 2 * d + h * kHeadDim;
+    uint16_t* op = out + (static_cast<int64_t>(b) * S + qi[j]) * 2 * d + h * kHeadDim;
 #pragma unroll
     for (int db = 0; db < 4; ++db) {
-      const float t[4] = {o[db][0] * inv, o[db][1] * inv, o[db][2] * inv, o[db][3] * inv};
-      uint2 hi, lo;
-      split4(t, hi, lo);
-      *reinterpret_cast<uint2*>(op + 16 * db + 4 * g) = hi;
-      *reinterpret_cast<uint2*>(op + d + 16 * db + 4 * g) = lo;
+      const float t[4] = {o[j][db][0] * inv, o[j][db][1] * inv, o[j][db][2] * inv,
+                          o[j][db][3] * inv};
+      // v_cvt_pk_bf16_f32 rounds to nearest even, as f2bf does for every non-NaN value
+      const bf16x4_t hv = {(__bf16)t[0], (__bf16)t[1], (__bf16)t[2], (__bf16)t[3]};
+      const bf16x4_t lv = {(__bf16)(t[0] - (float)hv[0]), (__bf16)(t[1] - (float)hv[1]),
+                           (__bf16)(t[2] - (float)hv[2]), (__bf16)(t[3] - (float)hv[3])};
+      *reinterpret_cast<bf16x4_t*>(op + 16 * db + 4 * g) = hv;
+      *reinterpret_cast<bf16x4_t*>(op + d + 16 * db + 4 * g) = lv;
     }
   }
 }
@@ -196,8 +266,13 @@ extern "C" int mdl_attn_prefill(const uint16_t* q, const uint16_t* k_cache,
   if (!aligned16(q) || !aligned16(k_cache) || !aligned16(v_cache) || !aligned8(out))
     return MDL_ERR_ALIGN;
   if (batch == 0 || seq == 0) return MDL_OK;
-  const dim3 grid((seq + kBM - 1) / kBM, n_heads, batch);
-  attn_prefill_kernel<<<grid, 256, 0, static_cast<hipStream_t>(stream)>>>(
-      q, k_cache, v_cache, seq, n_heads, cache_slots, key_mask, kv_start, causal ? 1 : 0, out);
+  const int64_t heads = static_cast<int64_t>(batch) * n_heads;
+  const int64_t nqt = (seq + kBM - 1) / kBM;
+  const int64_t blocks = (heads + kXcds - 1) / kXcds * kXcds * nqt;
+  if (blocks > 0x7fffffff) return MDL_ERR_SHAPE;
+  attn_prefill_kernel<<<static_cast<unsigned>(blocks), 256, 0,
+                        static_cast<hipStream_t>(stream)>>>(
+      q, k_cache, v_cache, seq, n_heads, cache_slots, key_mask, kv_start, causal ? 1 : 0, out,
+      static_cast<int>(nqt), static_cast<int>(heads));
   return launch_status();
 }

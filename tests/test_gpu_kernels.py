@@ -235,6 +235,48 @@ def test_attn_prefill(S, kind, causal):
     close_bf16(unsplit(out).view(B, S, H, 64).transpose(1, 2), ref, atol=8e-3, rtol=2e-2)
 
 
+@pytest.mark.parametrize("causal", [True, False])
+def test_attn_prefill_many_heads(causal):
+    """B*H = 35 heads (several rounds of the 8-XCD block order, with padding blocks) over
+    S = 700: six query tiles, ragged left padding, holes in one row, one row with no key."""
+    g = torch.Generator().manual_seed(700 + causal)
+    B, H, S, slots = 7, 5, 700, 768
+    q = bf(torch.randn(B, S, H, 64, generator=g) * 0.125)
+    kc = bf(torch.randn(B, H, slots, 64, generator=g))
+    vc = bf(torch.randn(B, H, slots, 64, generator=g))
+    mask = torch.ones(B, S, dtype=torch.bool)
+    for b, n in enumerate([700, 1, 63, 64, 129, 450, 0]):
+        mask[b, :S - n] = False
+    mask[4, 600:611] = False
+    first = torch.where(mask.any(1), mask.float().argmax(1), torch.full((B,), S))
+    out = torch.empty(B * S, 2 * H * 64, device=DEV, dtype=torch.bfloat16)
+    K().attn_prefill(q.to(DEV), kc.to(DEV), vc.to(DEV), B, S, H, mask.to(torch.uint8).to(DEV),
+                     first.to(torch.int32).to(DEV), causal, out)
+    torch.cuda.synchronize()
+    ref = rp.attention((q.float() * 8).transpose(1, 2), kc[:, :, :S].float(), vc[:, :, :S].float(),
+                       mask, causal)
+    close_bf16(unsplit(out).view(B, S, H, 64).transpose(1, 2), ref, atol=8e-3, rtol=2e-2)
+
+
+def test_attn_prefill_kv_start_clamped():
+    """kv_start values outside [0, S] act as 0 (every key) and S (no key), never as addresses."""
+    g = torch.Generator().manual_seed(91)
+    B, H, S, slots = 3, 2, 150, 160
+    q = bf(torch.randn(B, S, H, 64, generator=g) * 0.125)
+    kc = bf(torch.randn(B, H, slots, 64, generator=g))
+    vc = bf(torch.randn(B, H, slots, 64, generator=g))
+    kv = torch.tensor([-1000, 10_000, 5], dtype=torch.int32)
+    out = torch.empty(B * S, 2 * H * 64, device=DEV, dtype=torch.bfloat16)
+    K().attn_prefill(q.to(DEV), kc.to(DEV), vc.to(DEV), B, S, H, None, kv.to(DEV), True, out)
+    torch.cuda.synchronize()
+    mask = torch.ones(B, S, dtype=torch.bool)
+    mask[1] = False
+    mask[2, :5] = False
+    ref = rp.attention((q.float() * 8).transpose(1, 2), kc[:, :, :S].float(), vc[:, :, :S].float(),
+                       mask, True)
+    close_bf16(unsplit(out).view(B, S, H, 64).transpose(1, 2), ref, atol=8e-3, rtol=2e-2)
+
+
 # ---------------------------------------------------------------------------- K4b decode
 
 @pytest.mark.parametrize("split_len", [128, 256, 4096])
