@@ -180,6 +180,16 @@ def microbench(dev):
     nbytes = N * (2 * F * 4 + 4 + 2 * F * 2)
     res["k3_swiglu"] = dict(ms=ms, bytes=nbytes, gbs=nbytes / ms / 1e6)
     del gu, h
+
+    # residual add (+ fc_down bias) + next RMSNorm: x += delta + b in place, rstd, split(x*gamma)
+    x = [torch.randn(N, d, generator=g).to(dev) for _ in range(sets)]
+    delta = [torch.randn(N, d, generator=g).to(dev) for _ in range(sets)]
+    bias = (0.1 * torch.randn(d, generator=g)).to(dev)
+    xs = [torch.empty(N, 2 * d, device=dev, dtype=torch.bfloat16) for _ in range(sets)]
+    ms = timeit(lambda i: K.add_rmsnorm(x[i], delta[i], bias, gamma, 1e-5, xs[i], rstd[i]))
+    nbytes = N * (d * 4 * 2 + d * 4 + d * 2 * 2 + 4)
+    res["add_rmsnorm"] = dict(ms=ms, bytes=nbytes, gbs=nbytes / ms / 1e6)
+    del x, delta, xs, rstd
     for v in res.values():
         v["frac_of_peak"] = round(v["gbs"] / HBM_PEAK_GBS, 4)
         v["ms"] = round(v["ms"], 5)

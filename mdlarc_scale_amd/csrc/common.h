@@ -14,16 +14,17 @@ constexpr int kHeadDim = 64;
 // ---- bf16 <-> f32 (bf16 stored as raw 16-bit words) ------------------------------------------
 __device__ __forceinline__ float bf2f(uint32_t h16) { return __uint_as_float(h16 << 16); }
 
-// Round-to-nearest-even, NaN kept quiet (same rounding torch uses for .to(bfloat16)).
+// f32 -> bf16 with v_cvt_pk_bf16_f32: round to nearest even (the rounding torch uses for
+// .to(bfloat16)), NaN stays NaN.  One VALU op per pair; a bit-twiddling rounding with a NaN test
+// compiles to exec-masked branches around every value.
+typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
+
 __device__ __forceinline__ uint32_t f2bf(float f) {
-  uint32_t u = __float_as_uint(f);
-  if ((u & 0x7fffffffu) > 0x7f800000u) return (u >> 16) | 0x40u;
-  u += 0x7fffu + ((u >> 16) & 1u);
-  return u >> 16;
+  return __builtin_bit_cast(uint16_t, static_cast<__bf16>(f));
 }
 
 __device__ __forceinline__ uint32_t pack_bf2(float lo, float hi) {
-  return f2bf(lo) | (f2bf(hi) << 16);
+  return __builtin_bit_cast(uint32_t, bf16x2_t{static_cast<__bf16>(lo), static_cast<__bf16>(hi)});
 }
 
 // 8 bf16 held in a uint4 -> 8 floats
@@ -47,9 +48,9 @@ __device__ __forceinline__ uint4 pack8(const float* f) {
 // the bf16 GEMM then returns (hi + lo) . w, i.e. v to about 2^-17 relative instead of the 2^-9
 // of a single bf16 rounding; the same buffer read as [2M, K] gives hi.w and lo.w as row pairs.
 __device__ __forceinline__ void split_bf2(float a, float b, uint32_t& hi, uint32_t& lo) {
-  const uint32_t ha = f2bf(a), hb = f2bf(b);
-  hi = ha | (hb << 16);
-  lo = f2bf(a - bf2f(ha)) | (f2bf(b - bf2f(hb)) << 16);
+  const bf16x2_t h = {static_cast<__bf16>(a), static_cast<__bf16>(b)};
+  hi = __builtin_bit_cast(uint32_t, h);
+  lo = pack_bf2(a - static_cast<float>(h[0]), b - static_cast<float>(h[1]));
 }
 
 // 4 floats -> hi (uint2) and lo (uint2)
@@ -75,6 +76,51 @@ typedef unsigned int u32x4_t __attribute__((ext_vector_type(4)));
 __device__ __forceinline__ uint4 load_nt16(const void* p) {
   const u32x4_t v = __builtin_nontemporal_load(reinterpret_cast<const u32x4_t*>(p));
   return make_uint4(v.x, v.y, v.z, v.w);
+}
+
+// ---- streaming activations -------------------------------------------------------------------
+// A whole prompt batch's activations (hundreds of MB) cannot stay in L2 / the 256 MB MALL until
+// their consumer reads them, so the memory-bound kernels read and write them with the
+// non-temporal hint when the host asks for it (NT = true; measured on MI355X: K2 5.5 -> 6.2 TB/s,
+// both hints together).  Outputs below kStreamBytes (the decode step's) keep the default policy,
+// so the next GEMM still finds them in cache.
+constexpr int64_t kStreamBytes = int64_t{64} << 20;
+
+typedef float f32x4_vt __attribute__((ext_vector_type(4)));
+typedef unsigned int u32x2_t __attribute__((ext_vector_type(2)));
+
+template <bool NT>
+__device__ __forceinline__ float4 ld_f4(const float* p) {
+  if constexpr (NT) {
+    const f32x4_vt v = __builtin_nontemporal_load(reinterpret_cast<const f32x4_vt*>(p));
+    return make_float4(v.x, v.y, v.z, v.w);
+  } else {
+    return *reinterpret_cast<const float4*>(p);
+  }
+}
+
+template <bool NT>
+__device__ __forceinline__ void st_f4(float* p, float4 v) {
+  if constexpr (NT)
+    __builtin_nontemporal_store(f32x4_vt{v.x, v.y, v.z, v.w}, reinterpret_cast<f32x4_vt*>(p));
+  else
+    *reinterpret_cast<float4*>(p) = v;
+}
+
+template <bool NT>
+__device__ __forceinline__ void st_u2(void* p, uint2 v) {
+  if constexpr (NT)
+    __builtin_nontemporal_store(u32x2_t{v.x, v.y}, reinterpret_cast<u32x2_t*>(p));
+  else
+    *reinterpret_cast<uint2*>(p) = v;
+}
+
+template <bool NT>
+__device__ __forceinline__ void st_u4(void* p, uint4 v) {
+  if constexpr (NT)
+    __builtin_nontemporal_store(u32x4_t{v.x, v.y, v.z, v.w}, reinterpret_cast<u32x4_t*>(p));
+  else
+    *reinterpret_cast<uint4*>(p) = v;
 }
 
 __device__ __forceinline__ void load8f(const float* p, float* f) {

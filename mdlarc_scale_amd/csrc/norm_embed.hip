@@ -13,6 +13,10 @@
 // the GEMM input of the next projection as a hi|lo bf16 pair (2d values, see common.h).  The
 // RMSNorm multiply by rstd is deferred to the consumer of that GEMM (K2 for q/k/v, K3 for
 // gate/up), which is exact algebra: (x * rstd * gamma) @ W^T == rstd * ((x * gamma) @ W^T).
+//
+// Prompt-sized add+RMSNorm passes read and write with the non-temporal hint (common.h,
+// kStreamBytes; measured 5.75 -> 6.26 TB/s).  K1 keeps the default policy: the hint on its
+// stores measured 5.9 -> 5.6 TB/s.
 #include "common.h"
 #include "grid.h"
 
@@ -51,8 +55,8 @@ __device__ __forceinline__ void load_gamma(const float* gamma, int lane, int d, 
   }
 }
 
-// rstd of the row held in v, then x (fp32) and split(x * gamma) stores.
-template <int NC, bool TAIL, bool HAS_XS>
+// rstd of the row held in v, then x (fp32) and split(x * gamma) stores (non-temporal if NT).
+template <int NC, bool TAIL, bool HAS_XS, bool NT>
 __device__ __forceinline__ void finish_row(int lane, int d, float eps, const float (*v)[4],
                                            const float (*g)[4], float ss, float* xo,
                                            uint16_t* xs, float* rstd_out) {
@@ -62,14 +66,14 @@ __device__ __forceinline__ void finish_row(int lane, int d, float eps, const flo
   for (int i = 0; i < NC; ++i) {
     const int e = 4 * (lane + 64 * i);
     if (in_row<NC, TAIL>(i, e, d)) {
-      *reinterpret_cast<float4*>(xo + e) = make_float4(v[i][0], v[i][1], v[i][2], v[i][3]);
+      st_f4<NT>(xo + e, make_float4(v[i][0], v[i][1], v[i][2], v[i][3]));
       if (HAS_XS) {
         const float t[4] = {v[i][0] * g[i][0], v[i][1] * g[i][1], v[i][2] * g[i][2],
                             v[i][3] * g[i][3]};
         uint2 hi, lo;
         split4(t, hi, lo);
-        *reinterpret_cast<uint2*>(xs + e) = hi;
-        *reinterpret_cast<uint2*>(xs + d + e) = lo;
+        st_u2<NT>(xs + e, hi);
+        st_u2<NT>(xs + d + e, lo);
       }
     }
   }
@@ -117,8 +121,8 @@ __global__ __launch_bounds__(256) void embed_rmsnorm_kernel(
   const TT* trow = tok + clamp_id(ids[m], vocab) * d;
   const TT* erow = HAS_EX ? ex + clamp_id(ex_ids[m / row_len], n_ex) * d : nullptr;
   const float ss = gather_row<NC, TAIL, TT, HAS_EX>(trow, erow, lane, d, v);
-  finish_row<NC, TAIL, HAS_XS>(lane, d, eps, v, g, ss, x_out + m * d,
-                         HAS_XS ? xs_out + m * 2 * d : nullptr, rstd_out + m);
+  finish_row<NC, TAIL, HAS_XS, false>(lane, d, eps, v, g, ss, x_out + m * d,
+                                      HAS_XS ? xs_out + m * 2 * d : nullptr, rstd_out + m);
 }
 
 // Decode step entry: lane 0 of each row's wave turns the token the row just emitted into its 3D
@@ -152,11 +156,11 @@ __global__ __launch_bounds__(256) void decode_embed_kernel(
   const TT* trow = tok + clamp_id(t, vocab) * d;
   const TT* erow = HAS_EX ? ex + clamp_id(ex_ids[m], n_ex) * d : nullptr;
   const float ss = gather_row<NC, TAIL, TT, HAS_EX>(trow, erow, lane, d, v);
-  finish_row<NC, TAIL, true>(lane, d, eps, v, g, ss, x_out + m * d, xs_out + m * 2 * d,
-                       rstd_out + m);
+  finish_row<NC, TAIL, true, false>(lane, d, eps, v, g, ss, x_out + m * d, xs_out + m * 2 * d,
+                                    rstd_out + m);
 }
 
-template <int NC, bool TAIL, bool HAS_DELTA, bool HAS_BIAS, bool HAS_XS>
+template <int NC, bool TAIL, bool HAS_DELTA, bool HAS_BIAS, bool HAS_XS, bool NT>
 __global__ __launch_bounds__(256) void add_rmsnorm_kernel(
     float* __restrict__ x, const float* __restrict__ delta, const float* __restrict__ bias,
     int rows, int d, const float* __restrict__ gamma, float eps, uint16_t* __restrict__ xs_out,
@@ -173,12 +177,11 @@ __global__ __launch_bounds__(256) void add_rmsnorm_kernel(
   for (int i = 0; i < NC; ++i) {
     const int e = 4 * (lane + 64 * i);
     if (in_row<NC, TAIL>(i, e, d)) {
-      load4<float>(xr + e, v[i]);
+      const float4 xv = ld_f4<NT>(xr + e);
+      v[i][0] = xv.x; v[i][1] = xv.y; v[i][2] = xv.z; v[i][3] = xv.w;
       if (HAS_DELTA) {
-        float w[4];
-        load4<float>(dr + e, w);
-#pragma unroll
-        for (int j = 0; j < 4; ++j) v[i][j] += w[j];
+        const float4 w = ld_f4<NT>(dr + e);
+        v[i][0] += w.x; v[i][1] += w.y; v[i][2] += w.z; v[i][3] += w.w;
       }
       if (HAS_BIAS) {
         float w[4];
@@ -190,8 +193,8 @@ __global__ __launch_bounds__(256) void add_rmsnorm_kernel(
       for (int j = 0; j < 4; ++j) ss += v[i][j] * v[i][j];
     }
   }
-  finish_row<NC, TAIL, HAS_XS>(lane, d, eps, v, g, ss, xr, HAS_XS ? xs_out + m * 2 * d : nullptr,
-                         rstd_out + m);
+  finish_row<NC, TAIL, HAS_XS, NT>(lane, d, eps, v, g, ss, xr,
+                                   HAS_XS ? xs_out + m * 2 * d : nullptr, rstd_out + m);
 }
 
 constexpr int kMaxChunks = 8;  // d <= 2048
@@ -221,9 +224,8 @@ struct LaunchEmbed {
                   int rows, int row_len, int d, const float* gamma, float eps, float* x,
                   uint16_t* xs, float* r) {
 #define MDL_EMB(E, X)                                                                         \
-  embed_rmsnorm_kernel<NC, TAIL, TT, E, X><<<grid, 256, 0, s>>>(ids, ex_ids, tok, ex, vocab, n_ex,  \
-                                                          rows, row_len, d, gamma, eps, x, xs, \
-                                                          r)
+  embed_rmsnorm_kernel<NC, TAIL, TT, E, X><<<grid, 256, 0, s>>>(                              \
+      ids, ex_ids, tok, ex, vocab, n_ex, rows, row_len, d, gamma, eps, x, xs, r)
     if (has_ex && has_xs) MDL_EMB(true, true);
     else if (has_ex) MDL_EMB(true, false);
     else if (has_xs) MDL_EMB(false, true);
@@ -253,12 +255,20 @@ struct LaunchDecodeEmbed {
 
 template <int NC, bool TAIL>
 struct LaunchAdd {
-  static void run(dim3 grid, hipStream_t s, float* x, const float* delta, const float* bias,
-                  int rows, int d, const float* gamma, float eps, uint16_t* xs, float* r) {
+  static void run(dim3 grid, hipStream_t s, bool nt, float* x, const float* delta,
+                  const float* bias, int rows, int d, const float* gamma, float eps, uint16_t* xs,
+                  float* r) {
+    if (nt) go<true>(grid, s, x, delta, bias, rows, d, gamma, eps, xs, r);
+    else go<false>(grid, s, x, delta, bias, rows, d, gamma, eps, xs, r);
+  }
+
+  template <bool NT>
+  static void go(dim3 grid, hipStream_t s, float* x, const float* delta, const float* bias,
+                 int rows, int d, const float* gamma, float eps, uint16_t* xs, float* r) {
     const int key = (delta ? 4 : 0) | (bias ? 2 : 0) | (xs ? 1 : 0);
-#define MDL_ADD(D, B, X)                                                                       \
-  add_rmsnorm_kernel<NC, TAIL, D, B, X><<<grid, 256, 0, s>>>(x, delta, bias, rows, d, gamma, eps, xs, \
-                                                       r)
+#define MDL_ADD(D, B, X)                                                                     \
+  add_rmsnorm_kernel<NC, TAIL, D, B, X, NT><<<grid, 256, 0, s>>>(x, delta, bias, rows, d, gamma, \
+                                                                 eps, xs, r)
     switch (key) {
       case 7: MDL_ADD(true, true, true); break;
       case 6: MDL_ADD(true, true, false); break;
@@ -360,7 +370,9 @@ extern "C" int mdl_add_rmsnorm(float* x, const float* delta, const float* bias, 
       (bias && !aligned16(bias)) || (xs_out && !aligned8(xs_out)))
     return MDL_ERR_ALIGN;
   if (rows == 0) return MDL_OK;
-  dispatch_nc<LaunchAdd>(d, dim3((rows + 3) / 4), static_cast<hipStream_t>(stream),
+  const bool nt = static_cast<int64_t>(rows) * d * (8 + (delta ? 4 : 0) + (xs_out ? 4 : 0)) >=
+                  kStreamBytes;
+  dispatch_nc<LaunchAdd>(d, dim3((rows + 3) / 4), static_cast<hipStream_t>(stream), nt,
                          x, delta, bias, rows, d, gamma, eps, xs_out, rstd_out);
   return launch_status();
 }

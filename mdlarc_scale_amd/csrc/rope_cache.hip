@@ -60,6 +60,64 @@ __global__ __launch_bounds__(256) void qkv_rope_cache_kernel(
   }
 }
 
+// Same work with the whole qkv row in flight at once, for H % 4 == 0 (every configured model):
+// lane l owns the NCH = 3H/4 float4 chunks c = l + 64 i of the row.  A chunk's four channels sit
+// at dims 4 (l % 16) .. +3 of their head, i.e. RoPE pairs 2 (l % 16) and 2 (l % 16) + 1 for every
+// chunk of the lane, so one cos/sin lookup pair per token serves all of them, and chunk i belongs
+// to q, k or v for i / (H/4) = 0, 1, 2.  All NCH loads are issued before the first store;
+// prompt-sized batches stream with the non-temporal hint (common.h, kStreamBytes).
+template <int NCH, bool NT>
+__global__ __launch_bounds__(256) void qkv_rope_cache_vec_kernel(
+    const float* __restrict__ qkv, int64_t ld, const float* __restrict__ rstd,
+    const int64_t* __restrict__ pos, const float* __restrict__ tab, RopeArgs ra, int64_t rows,
+    int seq, float q_scale, uint16_t* __restrict__ q_out, uint16_t* __restrict__ kc,
+    uint16_t* __restrict__ vc, int slots, int slot0, const int32_t* __restrict__ slot_dev) {
+  constexpr int kH = 4 * NCH / 3, kD = kH * kHeadDim, kPart = NCH / 3;
+  const int lane = threadIdx.x & 63;
+  const int64_t m = static_cast<int64_t>(blockIdx.x) * 4 + (threadIdx.x >> 6);
+  if (m >= rows) return;
+  const float* row = qkv + m * ld;
+  float4 v[NCH];
+#pragma unroll
+  for (int i = 0; i < NCH; ++i)
+    v[i] = ld_f4<NT>(row + 4 * (lane + 64 * i));
+
+  float cs0, sn0, cs1, sn1;
+  rope_cos_sin(2 * (lane & 15), pos + m * 3, tab, ra, cs0, sn0);
+  rope_cos_sin(2 * (lane & 15) + 1, pos + m * 3, tab, ra, cs1, sn1);
+  const float r = rstd ? rstd[m] : 1.f;
+  const int64_t b = m / seq;
+  const int slot = (slot_dev ? *slot_dev : slot0) + static_cast<int>(m - b * seq);
+  const bool in_cache = slot >= 0 && slot < slots;   // host guarantees range; never write outside
+  const int64_t head_stride = static_cast<int64_t>(slots) * kHeadDim;
+  const int64_t cache_row = (b * kH * static_cast<int64_t>(slots) + slot) * kHeadDim;
+
+#pragma unroll
+  for (int i = 0; i < NCH; ++i) {
+    const int e = 4 * (lane + 64 * i) - (i / kPart) * kD;   // channel inside the q/k/v part
+    const float a0 = v[i].x * r, a1 = v[i].y * r, a2 = v[i].z * r, a3 = v[i].w * r;
+    if (i < kPart) {
+      uint2 o;
+      o.x = pack_bf2((a0 * cs0 - a1 * sn0) * q_scale, (a1 * cs0 + a0 * sn0) * q_scale);
+      o.y = pack_bf2((a2 * cs1 - a3 * sn1) * q_scale, (a3 * cs1 + a2 * sn1) * q_scale);
+      st_u2<NT>(q_out + m * kD + e, o);
+    } else if (in_cache) {
+      uint2 o;
+      uint16_t* dst;
+      if (i < 2 * kPart) {
+        o.x = pack_bf2(a0 * cs0 - a1 * sn0, a1 * cs0 + a0 * sn0);
+        o.y = pack_bf2(a2 * cs1 - a3 * sn1, a3 * cs1 + a2 * sn1);
+        dst = kc;
+      } else {
+        o.x = pack_bf2(a0, a1);
+        o.y = pack_bf2(a2, a3);
+        dst = vc;
+      }
+      st_u2<NT>(dst + cache_row + (e / kHeadDim) * head_stride + e % kHeadDim, o);
+    }
+  }
+}
+
 }  // namespace mdl
 
 using namespace mdl;
@@ -83,9 +141,28 @@ extern "C" int mdl_qkv_rope_cache(const float* qkv, int64_t qkv_ld, const float*
   const int64_t rows = static_cast<int64_t>(batch) * seq;
   if (rows == 0) return MDL_OK;
   const RopeArgs ra{max_x, max_y, max_z, px, py, pz};
-  qkv_rope_cache_kernel<<<dim3(static_cast<unsigned>((rows + 3) / 4)), 256, 0,
-                          static_cast<hipStream_t>(stream)>>>(
-      qkv, qkv_ld, rstd, pos, rope_tab, ra, rows, seq, n_heads, q_scale, q_out, k_cache,
-      v_cache, cache_slots, slot0, slot_dev);
+  const dim3 grid(static_cast<unsigned>((rows + 3) / 4));
+  const hipStream_t st = static_cast<hipStream_t>(stream);
+  const bool nt = rows * n_heads * kHeadDim * 18 >= kStreamBytes;
+#define MDL_K2_VEC(NCH)                                                                        \
+  if (nt)                                                                                     \
+    qkv_rope_cache_vec_kernel<NCH, true><<<grid, 256, 0, st>>>(                               \
+        qkv, qkv_ld, rstd, pos, rope_tab, ra, rows, seq, q_scale, q_out, k_cache, v_cache,    \
+        cache_slots, slot0, slot_dev);                                                        \
+  else                                                                                        \
+    qkv_rope_cache_vec_kernel<NCH, false><<<grid, 256, 0, st>>>(                              \
+        qkv, qkv_ld, rstd, pos, rope_tab, ra, rows, seq, q_scale, q_out, k_cache, v_cache,    \
+        cache_slots, slot0, slot_dev)
+  switch (n_heads) {
+    case 4: MDL_K2_VEC(3); break;
+    case 12: MDL_K2_VEC(9); break;
+    case 16: MDL_K2_VEC(12); break;
+    case 20: MDL_K2_VEC(15); break;
+    default:
+      qkv_rope_cache_kernel<<<grid, 256, 0, st>>>(qkv, qkv_ld, rstd, pos, rope_tab, ra, rows,
+                                                  seq, n_heads, q_scale, q_out, k_cache,
+                                                  v_cache, cache_slots, slot0, slot_dev);
+  }
+#undef MDL_K2_VEC
   return launch_status();
 }

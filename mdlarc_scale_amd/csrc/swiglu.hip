@@ -5,11 +5,13 @@
 // up half, 2x32 bytes of fp32 bias (L2 resident) and two 16-byte stores of h as a hi|lo bf16
 // pair ([rows, 2*d_ff], hi in [0, d_ff), lo in [d_ff, 2*d_ff)), so each wavefront streams 2 KiB
 // per input operand with no reuse -- a pure HBM-bound pass.  rstd applies ln2's RMSNorm
-// multiply deferred past the GEMM.
+// multiply deferred past the GEMM.  Prompt-sized batches store h with the non-temporal hint
+// (common.h, kStreamBytes; measured 5.83 -> 5.97 TB/s); the same hint on the loads costs 10%.
 #include "common.h"
 
 namespace mdl {
 
+template <bool NT>
 __global__ __launch_bounds__(256) void swiglu_kernel(const float* __restrict__ gu, int64_t ld,
                                                      const float* __restrict__ rstd,
                                                      const float* __restrict__ bg,
@@ -49,8 +51,8 @@ __global__ __launch_bounds__(256) void swiglu_kernel(const float* __restrict__ g
   uint4 hi, lo;
   split8(o, hi, lo);
   uint16_t* hr = h + m * 2 * d_ff + c;
-  *reinterpret_cast<uint4*>(hr) = hi;
-  *reinterpret_cast<uint4*>(hr + d_ff) = lo;
+  st_u4<NT>(hr, hi);
+  st_u4<NT>(hr + d_ff, lo);
 }
 
 }  // namespace mdl
@@ -68,8 +70,13 @@ extern "C" int mdl_swiglu(const float* gate_up, int64_t ld, const float* rstd,
     return MDL_ERR_ALIGN;
   if (rows == 0) return MDL_OK;
   const int64_t items = static_cast<int64_t>(rows) * (d_ff / 8);
-  swiglu_kernel<<<dim3(static_cast<unsigned>((items + 255) / 256)), 256, 0,
-                  static_cast<hipStream_t>(stream)>>>(gate_up, ld, rstd, bias_gate, bias_up,
-                                                      rows, d_ff, h_out);
+  const dim3 grid(static_cast<unsigned>((items + 255) / 256));
+  const hipStream_t st = static_cast<hipStream_t>(stream);
+  if (static_cast<int64_t>(rows) * d_ff * 12 >= kStreamBytes)
+    swiglu_kernel<true><<<grid, 256, 0, st>>>(gate_up, ld, rstd, bias_gate, bias_up, rows, d_ff,
+                                              h_out);
+  else
+    swiglu_kernel<false><<<grid, 256, 0, st>>>(gate_up, ld, rstd, bias_gate, bias_up, rows, d_ff,
+                                               h_out);
   return launch_status();
 }

@@ -114,7 +114,8 @@ def test_add_rmsnorm(d):
 
 # ---------------------------------------------------------------------------- K2
 
-@pytest.mark.parametrize("H,S,slot0", [(2, 1, 5), (4, 33, 0), (12, 64, 10), (20, 7, 100)])
+@pytest.mark.parametrize("H,S,slot0", [(2, 1, 5), (4, 33, 0), (12, 64, 10), (16, 5, 3),
+                                        (20, 7, 100)])
 def test_qkv_rope_cache(H, S, slot0):
     d = 64 * H
     B, slots = 3, 200
@@ -148,9 +149,10 @@ def test_qkv_rope_cache(H, S, slot0):
     assert bool((vc[:, :, untouched.to(DEV)] == 7).all())
 
 
-def test_qkv_rope_cache_device_slot():
-    H, B, slots = 2, 4, 50
-    d = 128
+@pytest.mark.parametrize("H", [2, 4])       # generic kernel, whole-row kernel
+def test_qkv_rope_cache_device_slot(H):
+    B, slots = 4, 50
+    d = 64 * H
     qkv = torch.randn(B, 3 * d).to(DEV)
     from mdlarc_scale_amd.transformer import RotaryEmbedding3D
 
@@ -196,6 +198,75 @@ def test_swiglu(F):
     K().swiglu(gu.to(DEV), None, None, None, h2)
     torch.cuda.synchronize()
     check_split(h2, rp.silu(gu[:, :F].double()) * gu[:, F:].double(), rtol=1e-5, atol=1e-6)
+
+
+# ---------------------------------------------------------------------------- streaming paths
+
+def test_streaming_paths_bit_identical():
+    """Batches of 64 MiB or more go through the non-temporal load/store instantiations of K1,
+    add+RMSNorm, K2 and K3.  The cache hint cannot change arithmetic: the first rows of a large
+    batch must equal, bit for bit, the same rows run as a small (default-policy) batch."""
+    g = torch.Generator(device=DEV).manual_seed(5)
+    d, H, F, V, NE = 768, 12, 2048, 14, 9
+    big, small = 12_288, 37                       # K1 at d=768: 12288*768*8 B = 75 MB
+
+    def both(run):
+        outs = [run(n) for n in (big, small)]
+        torch.cuda.synchronize()
+        for ob, os_ in zip(*outs):
+            assert torch.equal(ob[:os_.shape[0]], os_)
+
+    tok = torch.randn(V, d, device=DEV, generator=g).to(torch.bfloat16)
+    ex = torch.randn(NE, d, device=DEV, generator=g).to(torch.bfloat16)
+    gamma = 1 + 0.1 * torch.randn(d, device=DEV, generator=g)
+    ids = torch.randint(0, V, (big,), device=DEV, generator=g)
+    ex_ids = torch.randint(0, NE, (big,), device=DEV, generator=g)
+
+    def k1(n):
+        x = torch.empty(n, d, device=DEV)
+        xs = torch.empty(n, 2 * d, device=DEV, dtype=torch.bfloat16)
+        r = torch.empty(n, device=DEV)
+        K().embed_rmsnorm(ids[:n], ex_ids[:n], tok, ex, 1, gamma, 1e-5, x, xs, r)
+        return x, xs, r
+    both(k1)
+
+    x0 = torch.randn(big, d, device=DEV, generator=g)
+    delta = torch.randn(big, d, device=DEV, generator=g)
+    bias = 0.1 * torch.randn(d, device=DEV, generator=g)
+
+    def add(n):
+        x = x0[:n].clone()
+        xs = torch.empty(n, 2 * d, device=DEV, dtype=torch.bfloat16)
+        r = torch.empty(n, device=DEV)
+        K().add_rmsnorm(x, delta[:n], bias, gamma, 1e-5, xs, r)
+        return x, xs, r
+    both(add)
+
+    gu = torch.randn(big, 2 * F, device=DEV, generator=g)
+    rs = 0.5 + torch.rand(big, device=DEV, generator=g)
+    bg = 0.1 * torch.randn(F, device=DEV, generator=g)
+
+    def k3(n):
+        h = torch.empty(n, 2 * F, device=DEV, dtype=torch.bfloat16)
+        K().swiglu(gu[:n], rs[:n], bg, bg, h)
+        return (h,)
+    both(k3)
+
+    from mdlarc_scale_amd.transformer import RotaryEmbedding3D
+
+    rope = RotaryEmbedding3D(64, 32, 32, 8)
+    geom = (32, 32, 8, rope.px, rope.py, rope.pz)
+    qkv = torch.randn(big, 3 * d, device=DEV, generator=g)
+    pos = torch.randint(0, 30, (big, 3), device=DEV, generator=g)
+
+    def k2(n):                                    # one row of n tokens: cache [1, H, n, 64]
+        q = torch.empty(n, d, device=DEV, dtype=torch.bfloat16)
+        kc = torch.zeros(1, H, n, 64, device=DEV, dtype=torch.bfloat16)
+        vc = torch.zeros_like(kc)
+        K().qkv_rope_cache(qkv[:n], rs[:n], pos[:n], rope.device_table(DEV), geom, 1, n, H,
+                           0.125, q, kc, vc, slot0=0)
+        return q, kc[0].transpose(0, 1), vc[0].transpose(0, 1)
+    both(k2)
 
 
 # ---------------------------------------------------------------------------- K4a prefill
