@@ -7,7 +7,7 @@ colour variants, prompts of 300-1800 tokens left-padded into one batch, a 2,048-
 cache, greedy decode up to 930 tokens (capped by the cache at 2048 - S_pad, as the reference's
 ``max_total_len`` does).
 
-    python bench.py [--gpus 1] [--steps K] [--warmup W]
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--config small_b256|medium_b128|large_b64]
 
 A *step* is one greedy decode step of the whole B=256 batch (grid state -> embedding -> 4 layers
 -> LM head / argmax -> commit), replayed from the captured HIP graph the product path uses.  The
@@ -24,6 +24,12 @@ Also reported on the same JSON line:
 * ``microbench``: BASELINE config 1 -- the fused norm / RoPE / SwiGLU kernels at N=65,536
   tokens, d=768, F=2048, GB/s against the 8 TB/s HBM peak (buffer sets rotated so the 256 MB
   MALL cannot hold the working set).
+* ``prefill_attention``: the prefill attention kernel alone over one layer of the batch's cache
+  (its real masks and left padding), re-launched back to back; TFLOP/s of the valid causal
+  (query, key) pairs against the 2.5 PFLOP/s dense bf16 MFMA peak.
+
+``--config medium_b128`` / ``large_b64`` run BASELINE configs 3 and 4 the same way (their own
+metric name; no microbench; the CPU baseline only with an explicit ``--cpu-seconds``).
 """
 
 from __future__ import annotations
@@ -42,6 +48,17 @@ if ROOT not in sys.path:
 HBM_PEAK_GBS = 8000.0          # MI355X HBM3E
 BF16_PEAK_TFLOPS = 2500.0      # MI355X dense bf16 MFMA
 METRIC = "greedy decode tokens/s at small, B=256; fused-kernel HBM GB/s as % of peak"
+WORKLOADS = {
+    "small_b256": "BASELINE config 2: small TinyTransformer (d=768, 12 heads, 4 layers, "
+                  "d_ff=2048) bf16, random init seed 0, B=256 greedy decode "
+                  "(32 tasks x 8 dihedral+colour variants, left-padded)",
+    "medium_b128": "BASELINE config 3: medium TinyTransformer (d=1024, 16 heads, 8 layers, "
+                   "d_ff=2752) bf16, random init seed 0, B=128 greedy decode (16 tasks x 8 "
+                   "variants, 4-5 demo pairs, prompts 1500-3500 tokens, 4096-slot cache)",
+    "large_b64": "BASELINE config 4: large TinyTransformer (d=1280, 20 heads, 12 layers, "
+                 "d_ff=3392) bf16, random init seed 0, B=64 greedy decode (8 tasks x 8 "
+                 "variants, 5 demo pairs, prompts 5000-5726 tokens, 6656-slot cache)",
+}
 
 
 def _args():
@@ -49,8 +66,12 @@ def _args():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=128)
     ap.add_argument("--warmup", type=int, default=8)
-    ap.add_argument("--cpu-seconds", type=float, default=15.0,
-                    help="time bound of the CPU-baseline sample (0 disables it)")
+    ap.add_argument("--config", default="small_b256",
+                    choices=["small_b256", "medium_b128", "large_b64"],
+                    help="BASELINE workload (default: config 2, the headline metric)")
+    ap.add_argument("--cpu-seconds", type=float, default=None,
+                    help="time bound of the CPU-baseline sample (0 disables it; default 15 s "
+                         "for small_b256, off for the larger configs)")
     ap.add_argument("--no-micro", action="store_true", help="skip the config-1 microbench")
     ap.add_argument("--eager", action="store_true",
                     help="launch every kernel from the host instead of replaying a HIP graph")
@@ -252,11 +273,12 @@ def main() -> int:
         return 2
     import torch
 
-    from mdlarc_scale_amd import _lib, create_small_model
+    from mdlarc_scale_amd import _lib
     from mdlarc_scale_amd import kernels as K
     from mdlarc_scale_amd import inference as I
     from mdlarc_scale_amd.data import END_TOKEN_ID
     from mdlarc_scale_amd.engine import engine_for
+    from mdlarc_scale_amd.transformer import MODEL_SIZES, create_model
     from mdlarc_scale_amd.workload import SPECS, build_prompts, left_pad
 
     if not torch.cuda.is_available():
@@ -264,7 +286,10 @@ def main() -> int:
         return 1
     _lib.lib()
     dev = torch.device("cuda:0")
-    spec = SPECS["small_b256"]
+    spec = SPECS[args.config]
+    headline = spec.name == "small_b256"
+    if args.cpu_seconds is None:
+        args.cpu_seconds = 15.0 if headline else 0.0
     t_build = time.perf_counter()
     prompts = build_prompts(spec)
     ids, pos, mask = left_pad(prompts)
@@ -274,8 +299,8 @@ def main() -> int:
     host_build_s = time.perf_counter() - t_build
 
     torch.manual_seed(0)
-    model = create_small_model(dropout=0.0, max_seq_len=spec.cache_slots)
-    model = model.to(torch.bfloat16)                 # bf16 model
+    model = create_model(**MODEL_SIZES[spec.preset], dropout=0.0, max_seq_len=spec.cache_slots)
+    model = model.to(torch.bfloat16)                 # bf16 models
     model_state = {k: v.float().clone() for k, v in model.state_dict().items()}
     model = model.to(dev).eval()
     cfg = model.config
@@ -345,19 +370,35 @@ def main() -> int:
         achieved = attn_bytes / attn_ms / 1e6
         durs = ts
 
-        micro = None if args.no_micro else microbench(dev)
+        # prefill attention alone: one layer's launch over the batch's own masks and cache,
+        # with synthetic q (the kernel's time does not depend on values)
+        n_valid = mask.sum(1)
+        pa_flops = 4 * 64 * H * int((n_valid * (n_valid + 1) // 2).sum())
+        qp = (torch.randn(B * S, H * 64, device=dev) * 0.125).to(torch.bfloat16)
+        op = torch.empty(B * S, 2 * H * 64, device=dev, dtype=torch.bfloat16)
+        kc0, vc0 = st.cache.layer(0)
+        K.attn_prefill(qp, kc0, vc0, B, S, H, st.pmask, st.kv_start, True, op)
+        reps = 10
+        tpa = Timer()
+        tpa.start()
+        for _ in range(reps):
+            K.attn_prefill(qp, kc0, vc0, B, S, H, st.pmask, st.kv_start, True, op)
+        tpa.stop()
+        pa_ms = tpa.ms() / reps
+        del qp, op
+
+        micro = None if (args.no_micro or not headline) else microbench(dev)
 
         cpu = None
         if snap is not None:
             cpu = cpu_baseline(model_state, cfg, snap, S + args.warmup + args.steps,
                                args.cpu_seconds)
 
-    n_valid = mask.sum(1)
-    prefill_flops = cfg.n_layers * 4 * 64 * H * int((n_valid * (n_valid + 1) // 2).sum())
+    prefill_flops = cfg.n_layers * pa_flops
     traffic, traffic_src = recorded_traffic("attn_decode_kernel", spec.name)
     value = B * args.steps / (timed_ms / 1e3)
     out = {
-        "metric": METRIC,
+        "metric": METRIC if headline else f"greedy decode tokens/s at {spec.preset}, B={B}",
         "value": round(value, 1),
         "unit": "tokens/s",
         "n_gpus": 1,
@@ -370,10 +411,8 @@ def main() -> int:
         "dtype": "bf16",
         "data": "synthetic",
         "config": {
-            "workload": "BASELINE config 2: small TinyTransformer (d=768, 12 heads, 4 layers, "
-                        "d_ff=2048) bf16, random init seed 0, B=256 greedy decode "
-                        "(32 tasks x 8 dihedral+colour variants, left-padded)",
-            "model": "small", "global_batch": B, "seq_len": S, "cache_slots": total,
+            "workload": WORKLOADS[spec.name],
+            "model": spec.preset, "global_batch": B, "seq_len": S, "cache_slots": total,
             "decode_steps_available": max_new - 1, "timed_cache_fill": [t_first,
                                                                         t_first + args.steps],
             "prompt_len_min": int(n_valid.min()), "prompt_len_mean": round(float(
@@ -395,6 +434,13 @@ def main() -> int:
             "ms": round(prefill_ms, 3), "tokens": int(n_valid.sum()), "padded_tokens": B * S,
             "tokens_per_s": round(int(n_valid.sum()) / (prefill_ms / 1e3), 1),
             "attention_causal_tflop": round(prefill_flops / 1e12, 3),
+        },
+        "prefill_attention": {
+            "kernel": "attn_prefill_kernel (mdl_attn_prefill, bf16 MFMA)", "bound": "mfma",
+            "ms_per_layer": round(pa_ms, 4), "tflop_per_layer": round(pa_flops / 1e12, 4),
+            "achieved": round(pa_flops / pa_ms / 1e9, 1), "peak": BF16_PEAK_TFLOPS,
+            "unit": "TFLOP/s", "frac": round(pa_flops / pa_ms / 1e9 / BF16_PEAK_TFLOPS, 4),
+            "flops": "valid causal (query, key) pairs x 4 x 64 (QK^T and PV)",
         },
         "microbench": micro,
         "wall_s_timed": round(wall_s, 4),
