@@ -211,14 +211,20 @@ int mdl_decode_head(const float* x, int batch, int d, const float* gamma, float 
  * Replaces: _derive_initial_state_from_prompt (src/inference.py:171-221) and the
  *           lengths-1 index of _prefill (src/inference.py:420-424).
  * ids int64 [batch, seq], pos int64 [batch, seq, 3], mask uint8 [batch, seq] or NULL (all valid).
+ * row_shift int32 [batch] or NULL (all 0): for rows that the reference would have left-padded in
+ *   a narrower batch of width L, the extra left padding seq - L of this batch; the reference's
+ *   index len-1 in its own batch is index row_shift[b] + len-1 here (clamped into the row).
+ *   Several such batches (the reference's chunks of 16) then run as one with identical results.
  * Outputs per row: gx, gy (int32), in_out (uint8), kv_start = first valid index (seq if none),
- * last_row = b*seq + max(len-1, 0) (the row the reference's prefill reads its logits from),
- * row_holes = 1 if the valid positions are not the single run [kv_start, seq), else 0.
- * kv_start / last_row / row_holes may each be NULL.
+ * last_row = b*seq + row_shift[b] + max(len-1, 0) (the row the reference's prefill reads its
+ * logits from; the grid state derives from the same token), row_holes = 1 if the valid positions
+ * are not the single run [kv_start, seq), else 0.  kv_start / last_row / row_holes may each be
+ * NULL.
  */
-int mdl_grid_init(const int64_t* ids, const int64_t* pos, const uint8_t* mask, int batch,
-                  int seq, int max_x, int max_y, int32_t* gx, int32_t* gy, uint8_t* in_out,
-                  int32_t* kv_start, int32_t* last_row, uint8_t* row_holes, void* stream);
+int mdl_grid_init(const int64_t* ids, const int64_t* pos, const uint8_t* mask,
+                  const int32_t* row_shift, int batch, int seq, int max_x, int max_y, int32_t* gx,
+                  int32_t* gy, uint8_t* in_out, int32_t* kv_start, int32_t* last_row,
+                  uint8_t* row_holes, void* stream);
 
 /*
  * One grid-state step: position of the token each row just emitted, then advance the state.

@@ -42,7 +42,7 @@ SIGNATURES: dict[str, tuple[object, list]] = {
     "mdl_lm_head": (c_int, [P, P, c_int, c_int, P, c_float, P, c_int, P, P, P]),
     "mdl_decode_head": (c_int, [P, c_int, c_int, P, c_float, P, c_int, P, P, P, c_int64, c_int,
                                 P, P, c_int, c_int, P]),
-    "mdl_grid_init": (c_int, [P, P, P, c_int, c_int, c_int, c_int, P, P, P, P, P, P, P]),
+    "mdl_grid_init": (c_int, [P, P, P, P, c_int, c_int, c_int, c_int, P, P, P, P, P, P, P]),
     "mdl_grid_step": (c_int, [P, c_int, c_int, c_int, P, P, P, P, P, P]),
     "mdl_decode_commit": (c_int, [P, c_int, P, c_int64, c_int, P, P, c_int, c_int, P]),
 }

@@ -124,7 +124,8 @@ __global__ __launch_bounds__(256) void head_kernel(
 
 __global__ __launch_bounds__(256) void grid_init_kernel(
     const int64_t* __restrict__ ids, const int64_t* __restrict__ pos,
-    const uint8_t* __restrict__ mask, int batch, int seq, int max_x, int max_y, int32_t* gx,
+    const uint8_t* __restrict__ mask, const int32_t* __restrict__ row_shift, int batch, int seq,
+    int max_x, int max_y, int32_t* gx,
     int32_t* gy, uint8_t* io, int32_t* kv_start, int32_t* last_row, uint8_t* row_holes) {
   // one wavefront per batch row: the lanes scan the mask row together
   const int lane = threadIdx.x & 63;
@@ -149,8 +150,10 @@ __global__ __launch_bounds__(256) void grid_init_kernel(
     first = 0;
   }
   if (lane != 0) return;
-  // the reference reads the token at index len-1 of each row, a right-padding index
-  const int last = n > 0 ? n - 1 : 0;
+  // the reference reads the token at index len-1 of each row, a right-padding index, in the
+  // batch it padded the row in; row_shift maps that index into this (wider) batch
+  const int shift = row_shift ? row_shift[b] : 0;
+  const int last = clampi(shift + (n > 0 ? n - 1 : 0), 0, seq - 1);
   const int64_t row = static_cast<int64_t>(b) * seq + last;
   const int64_t t = ids[row];
   int64_t x = pos[row * 3], y = pos[row * 3 + 1];
@@ -292,16 +295,17 @@ extern "C" int mdl_decode_head(const float* x, int batch, int d, const float* ga
 }
 
 extern "C" int mdl_grid_init(const int64_t* ids, const int64_t* pos, const uint8_t* mask,
-                             int batch, int seq, int max_x, int max_y, int32_t* gx, int32_t* gy,
-                             uint8_t* in_out, int32_t* kv_start, int32_t* last_row,
-                             uint8_t* row_holes, void* stream) {
+                             const int32_t* row_shift, int batch, int seq, int max_x, int max_y,
+                             int32_t* gx, int32_t* gy, uint8_t* in_out, int32_t* kv_start,
+                             int32_t* last_row, uint8_t* row_holes, void* stream) {
   if (!ids || !pos || !gx || !gy || !in_out) return MDL_ERR_NULL;
   if (batch < 0 || seq <= 0 || max_x < 0 || max_y < 0 ||
       static_cast<int64_t>(batch) * seq > INT32_MAX)
     return MDL_ERR_SHAPE;
   if (batch == 0) return MDL_OK;
   grid_init_kernel<<<dim3((batch + 3) / 4), 256, 0, static_cast<hipStream_t>(stream)>>>(
-      ids, pos, mask, batch, seq, max_x, max_y, gx, gy, in_out, kv_start, last_row, row_holes);
+      ids, pos, mask, row_shift, batch, seq, max_x, max_y, gx, gy, in_out, kv_start, last_row,
+      row_holes);
   return launch_status();
 }
 

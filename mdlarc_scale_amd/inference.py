@@ -243,7 +243,11 @@ class Generator:
         self.model = model
         self.eng = engine_for(model)
 
-    def prepare(self, input_ids, positions_3d, example_ids, prompt_mask, total) -> DecodeState:
+    def prepare(self, input_ids, positions_3d, example_ids, prompt_mask, total,
+                row_shift: torch.Tensor | None = None) -> DecodeState:
+        """Device state for generating up to ``total`` columns.  ``row_shift`` (int32 [B]) maps
+        each row's lengths-1 index from the narrower batch the reference padded it in (see
+        ``mdl_grid_init``)."""
         cfg = self.model.config
         dev = input_ids.device
         B, S = input_ids.shape
@@ -255,7 +259,7 @@ class Generator:
         gio = torch.empty(B, dtype=torch.uint8, device=dev)
         holes = torch.empty(B, dtype=torch.uint8, device=dev)
         K.grid_init(input_ids, positions_3d, pmask, gx, gy, gio, kv_start, last_row,
-                    row_holes=holes)
+                    row_holes=holes, row_shift=row_shift)
         # longest rows first: the decode-attention launch dispatches them before the short ones
         order = torch.argsort(kv_start, stable=True).to(torch.int32)
         split = choose_split_len(B * H, total)
@@ -360,9 +364,28 @@ def generate_output(model: TinyTransformer, input_ids: torch.Tensor, positions_3
     if attention_mask is not None and tuple(attention_mask.shape) != (B, S):
         raise ValueError("attention_mask must have shape [batch, seq_len]")
     total = min(S + max_new_tokens, cfg.max_seq_len)
-    max_new = total - S
-    if max_new <= 0:
+    if total - S <= 0:
         return input_ids
+    out_ids, finish, produced = _generate(model, input_ids, positions_3d, example_ids,
+                                          attention_mask, total, temperature, top_k, stop_on_end,
+                                          constraints)
+    g = produced
+    if stop_on_end:
+        fin = finish.cpu()
+        if bool((fin >= 0).all()):
+            g = min(g, int(fin.max()) + 1)
+    return out_ids[:, :S + g]
+
+
+def _generate(model: TinyTransformer, input_ids, positions_3d, example_ids, attention_mask,
+              total: int, temperature: float, top_k: int | None, stop_on_end: bool,
+              constraints: DecodingConstraints | None, row_shift: torch.Tensor | None = None):
+    """Prefill + decode of up to ``total - S`` tokens.  Returns (out_ids [B, S + produced],
+    finish [B] int32 = generated index of each row's first END or -1, produced).  The loop stops
+    early once every row has emitted END (checked every SYNC_EVERY greedy steps), so
+    ``produced`` may exceed the reference's count; callers trim."""
+    B, S = input_ids.shape
+    max_new = total - S
     eng = engine_for(model)
     dev = eng._check_device(input_ids)
     ids = input_ids.to(torch.int64).contiguous()
@@ -374,10 +397,12 @@ def generate_output(model: TinyTransformer, input_ids: torch.Tensor, positions_3
     else:
         prompt_mask = attention_mask.to(device=dev, dtype=torch.bool)
     eng._validate_ids(ids, ex)
+    if row_shift is not None:
+        row_shift = row_shift.to(device=dev, dtype=torch.int32).contiguous()
     gen = Generator(model)
     with torch.no_grad():
         W = eng.packed(dev)
-        st = gen.prepare(ids, pos, ex, prompt_mask, total)
+        st = gen.prepare(ids, pos, ex, prompt_mask, total, row_shift)
         gen.prefill(st, W, ids, pos)
         eager = temperature > 0 or constraints is not None
         if eager:
@@ -404,12 +429,7 @@ def generate_output(model: TinyTransformer, input_ids: torch.Tensor, positions_3
                 if USE_GRAPHS and step + 1 < max_new:
                     graph = gen.capture_greedy(st, W, stop_on_end)
             produced += 1
-        g = produced
-        if stop_on_end:
-            fin = st.finish.cpu()
-            if bool((fin >= 0).all()):
-                g = min(g, int(fin.max()) + 1)
-    return st.out_ids[:, :S + g]
+    return st.out_ids[:, :S + produced], st.finish, produced
 
 
 # =============================================================================================
@@ -534,13 +554,16 @@ def predict_with_augmentations(model: TinyTransformer, task: dict, test_idx: int
                                sample_top_k: int | None = None, constrain_decoding: bool = False,
                                palette_penalty: float = 2.0, shape_penalty: float = 2.0,
                                batched: bool = True, use_compile: bool = False,
-                               max_batch_size: int = 16):
+                               max_batch_size: int = 16, fuse_chunks: bool = True):
     """All dihedral x colour-permutation predictions for AAIVR voting
     (src/inference.py:697-920): list of (grid | None, dihedral_idx, perm_tuple | None).
 
-    ``batched`` runs the prompts in left-padded chunks of ``max_batch_size`` (the reference's
-    16, which also fixes each chunk's padding and hence its ``lengths-1`` rows); otherwise one
-    prompt at a time."""
+    The reference runs the prompts in left-padded chunks of ``max_batch_size`` (16) when
+    ``batched``, otherwise one prompt at a time; the chunking is part of its results (each
+    chunk's padding fixes its ``lengths-1`` rows, and a chunk stops when all of its rows have
+    emitted END).  With greedy decoding and ``fuse_chunks`` (the default) every chunk runs in
+    ONE batch with those semantics kept per row (``_predict_fused``); sampling, whose random
+    draws depend on the batch, keeps the chunk loop, as does ``fuse_chunks=False``."""
     del use_compile
     model.eval()
     num_samples = max(1, num_samples)
@@ -549,6 +572,9 @@ def predict_with_augmentations(model: TinyTransformer, task: dict, test_idx: int
     variants = _build_variants(task, test_idx, use_train_examples, num_color_perms, num_samples,
                                constrain_decoding, base_palette, base_shape)
     chunk = max_batch_size if batched else 1
+    if fuse_chunks and sample_temperature <= 0 and len(variants) > 1:
+        return _predict_fused(model, variants, chunk, device, example_id, max_output_tokens,
+                              constrain_decoding, palette_penalty, shape_penalty)
     preds = []
     for c0 in range(0, len(variants), chunk):
         part = variants[c0:c0 + chunk]
@@ -572,6 +598,60 @@ def predict_with_augmentations(model: TinyTransformer, task: dict, test_idx: int
             seps = [j for j, t in enumerate(seq) if t == IO_SEP_TOKEN_ID]
             grid = decode_output_grid(seq[seps[-1]:]) if seps else None
             preds.append((grid, v.dihedral, v.perm))
+    return preds
+
+
+def _predict_fused(model: TinyTransformer, variants: list[_Variant], chunk: int, device,
+                   example_id: int, max_output_tokens: int, constrain: bool,
+                   palette_penalty: float, shape_penalty: float):
+    """Greedy predictions of every variant from one generation over all of them, equal to the
+    reference's loop over left-padded chunks of ``chunk`` rows (src/inference.py:829-918).
+
+    Row i of chunk c (padded there to width L_c, here to the batch-wide S):
+    * its prefill logits and initial grid state come from the reference's index lengths-1 in its
+      chunk, i.e. index S - L_c + lengths-1 here (``mdl_grid_init`` row_shift; the extra left
+      pads are END tokens at (0, 0, 0) whose hidden states equal the chunk's own pads);
+    * it keeps the first g_c generated tokens, where the chunk's budget is
+      b_c = min(L_c + max_output_tokens, max_seq_len) - L_c and g_c = min(b_c, 1 + the latest
+      first-END index over the chunk's rows), b_c if a row never emits END: the reference stops
+      a chunk once all of its rows have emitted END, and keeps what finished rows produced until
+      then;
+    * greedy rows never interact (attention, norms and the argmax are per row; constraints are
+      per row), so the tokens themselves do not depend on the batch.
+    The one generation runs until every row has emitted END or the largest budget is spent, so
+    every row has at least its g_c tokens."""
+    cfg = model.config
+    n = len(variants)
+    lens = [len(v.tokens) for v in variants]
+    widths = [max(lens[c0:c0 + chunk]) for c0 in range(0, n, chunk)]
+    budgets = [min(w + max_output_tokens, cfg.max_seq_len) - w for w in widths]
+    ids, pos, mask = left_pad_batch([v.tokens for v in variants], device)
+    S = ids.shape[1]
+    gen_max = max(budgets)
+    gen = torch.empty(n, 0, dtype=torch.int64)
+    fin = torch.full((n,), -1, dtype=torch.int32)
+    if gen_max > 0:
+        shift = torch.tensor([S - widths[i // chunk] for i in range(n)], dtype=torch.int32)
+        constraints = (_chunk_constraints(variants, device, palette_penalty, shape_penalty, True)
+                       if constrain else None)
+        ex = torch.full((n,), example_id, dtype=torch.long, device=device)
+        with torch.no_grad():
+            out_ids, finish, _ = _generate(model, ids, pos, ex, mask, S + gen_max, 0.0, None, True,
+                                           constraints, row_shift=shift)
+        gen = out_ids[:, S:].cpu()
+        fin = finish.cpu()
+    preds = []
+    for c, c0 in enumerate(range(0, n, chunk)):
+        rows = range(c0, min(c0 + chunk, n))
+        f = fin[c0:c0 + chunk]
+        g = budgets[c]
+        if g > 0 and bool((f >= 0).all()):
+            g = min(g, int(f.max()) + 1)
+        for i in rows:
+            seq = variants[i].tokens + gen[i, :max(g, 0)].tolist()
+            seps = [j for j, t in enumerate(seq) if t == IO_SEP_TOKEN_ID]
+            grid = decode_output_grid(seq[seps[-1]:]) if seps else None
+            preds.append((grid, variants[i].dihedral, variants[i].perm))
     return preds
 
 

@@ -300,7 +300,10 @@ def decode_head(x: torch.Tensor, gamma: torch.Tensor, eps: float, w_head: torch.
 def grid_init(ids: torch.Tensor, pos: torch.Tensor, mask: torch.Tensor | None, gx: torch.Tensor,
               gy: torch.Tensor, in_out: torch.Tensor, kv_start: torch.Tensor | None,
               last_row: torch.Tensor | None, max_x: int = 30, max_y: int = 29,
-              row_holes: torch.Tensor | None = None) -> None:
+              row_holes: torch.Tensor | None = None,
+              row_shift: torch.Tensor | None = None) -> None:
+    """row_shift (int32 [batch]): extra left padding of each row relative to the batch the
+    reference padded it in (its lengths-1 index moves by that much); None = 0."""
     batch, seq = ids.shape
     _need(ids, "ids", I64)
     _need(pos, "pos", I64, batch * seq * 3)
@@ -311,9 +314,10 @@ def grid_init(ids: torch.Tensor, pos: torch.Tensor, mask: torch.Tensor | None, g
     _need(kv_start, "kv_start", I32, batch, optional=True)
     _need(last_row, "last_row", I32, batch, optional=True)
     _need(row_holes, "row_holes", U8, batch, optional=True)
+    _need(row_shift, "row_shift", I32, batch, optional=True)
     _lib.check(_lib.lib().mdl_grid_init(
-        _p(ids), _p(pos), _p(mask), batch, seq, max_x, max_y, _p(gx), _p(gy), _p(in_out),
-        _p(kv_start), _p(last_row), _p(row_holes), _stream()), "mdl_grid_init")
+        _p(ids), _p(pos), _p(mask), _p(row_shift), batch, seq, max_x, max_y, _p(gx), _p(gy),
+        _p(in_out), _p(kv_start), _p(last_row), _p(row_holes), _stream()), "mdl_grid_init")
 
 
 def grid_step(token: torch.Tensor, gx: torch.Tensor, gy: torch.Tensor, in_out: torch.Tensor,

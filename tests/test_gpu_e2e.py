@@ -263,3 +263,35 @@ def test_predict_with_augmentations_pipeline():
     assert len(preds) == 16
     assert [p[1] for p in preds[::2]] == list(range(8))
     assert preds[0][2] is None and preds[1][2] is not None
+
+
+@pytest.mark.parametrize("fixture,batched,chunk", [("e2e_micro_stop", True, 16),
+                                                   ("e2e_micro_stop", True, 5),
+                                                   ("e2e_micro_stop", False, 1),
+                                                   ("e2e_micro", False, 1)])
+def test_fused_augmentations_equal_chunk_loop(fixture, batched, chunk, monkeypatch):
+    """One fused generation over every augmented prompt returns exactly what the reference's
+    chunk-by-chunk loop returns (src/inference.py:829-918): per row, the chunk's lengths-1 index,
+    the chunk's token budget under max_seq_len and the chunk's stop step (all of its rows emitted
+    END).  The test grid 1x5 becomes 5x1 under half the dihedral transforms, so prompts differ in
+    length and chunks in width and budget; the golden stop model ends rows at many different steps
+    (the CPU oracle's chunk loop on this task gives 5-9 distinct output lengths), the other model
+    never emits END and runs into each row's max_seq_len budget.  The raw token streams are
+    compared (decode_output_grid replaced by the identity)."""
+    from mdlarc_scale_amd import inference as inf
+
+    m = _model_from_fixture(load_e2e(fixture))
+    task = {"train": [{"input": [[1, 2, 3, 4, 5, 6]], "output": [[6], [5], [4], [3], [2], [1]]},
+                      {"input": [[7, 0], [0, 7]], "output": [[0, 7], [7, 0]]}],
+            "test": [{"input": [[1, 0, 2, 0, 3]]}]}
+    monkeypatch.setattr(inf, "decode_output_grid", lambda toks: tuple(toks))
+    kw = dict(example_id=1, num_color_perms=3, max_output_tokens=130, batched=batched,
+              max_batch_size=chunk)
+    fused = inf.predict_with_augmentations(m, task, 0, DEV, **kw)
+    loop = inf.predict_with_augmentations(m, task, 0, DEV, fuse_chunks=False, **kw)
+    assert len(fused) == len(loop) == 24
+    print(f"fused augmentations ({fixture}, chunk {chunk}): "
+          f"{len({len(p[0]) for p in loop})} distinct output lengths over {len(loop)} rows")
+    for (gf, df, pf), (gl, dl, pl) in zip(fused, loop):
+        assert (df, pf) == (dl, pl)
+        assert gf == gl

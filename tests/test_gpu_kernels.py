@@ -513,6 +513,46 @@ def test_grid_kernels_match_reference_golden():
     assert want.sum() > 0 and (want == 0).sum() > 0          # the fixture exercises both kinds
 
 
+def test_grid_init_row_shift_equals_chunk_padding():
+    """Rows left-padded together in one wide batch with row_shift = S - L_c give exactly the
+    grid state and lengths-1 row that grid_init gives on each chunk padded to its own width L_c
+    (including rows whose lengths-1 index falls in the padding)."""
+    from mdlarc_scale_amd.inference import left_pad_batch
+
+    rng = np.random.default_rng(11)
+    chunk = 4
+    prompts = []
+    for i in range(11):
+        n = int(rng.integers(1, 40))
+        toks = [10] + [int(t) for t in rng.integers(0, 14, n)]      # START + random tokens
+        prompts.append(toks)
+    def run(ps, shift=None):
+        ids, pos, mask = left_pad_batch(ps, DEV)
+        B = len(ps)
+        o = [torch.empty(B, dtype=torch.int32, device=DEV) for _ in range(2)]
+        io = torch.empty(B, dtype=torch.uint8, device=DEV)
+        last = torch.empty(B, dtype=torch.int32, device=DEV)
+        K().grid_init(ids, pos, mask.to(torch.uint8), o[0], o[1], io, None, last,
+                      row_shift=None if shift is None else shift.to(DEV))
+        return o[0].cpu(), o[1].cpu(), io.cpu(), last.cpu(), ids.cpu(), ids.shape[1]
+    gx, gy, io, last, ids, S = run(prompts)
+    widths = [max(len(p) for p in prompts[c:c + chunk]) for c in range(0, len(prompts), chunk)]
+    shift = torch.tensor([S - widths[i // chunk] for i in range(len(prompts))], dtype=torch.int32)
+    sx, sy, sio, slast, _, _ = run(prompts, shift)
+    hit_pad = 0
+    for c0 in range(0, len(prompts), chunk):
+        cx, cy, cio, clast, cids, L = run(prompts[c0:c0 + chunk])
+        for j in range(cx.shape[0]):
+            b = c0 + j
+            assert (sx[b], sy[b], sio[b]) == (cx[j], cy[j], cio[j]), f"row {b}"
+            lc = int(clast[j]) - j * L                       # index inside the chunk's padding
+            assert int(slast[b]) - b * S == S - L + lc
+            assert int(ids.view(-1)[slast[b]]) == int(cids.view(-1)[clast[j]])
+            hit_pad += int(lc < L - len(prompts[b]))
+    assert hit_pad > 0                                       # some index lands in the padding
+    assert not torch.equal(slast, last)                      # the shift moved some rows
+
+
 @pytest.mark.parametrize("d,with_ex", [(256, True), (768, True), (1280, False)])
 def test_decode_embed_equals_grid_step_plus_embed(d, with_ex):
     """The fused decode-step entry equals mdl_grid_step followed by mdl_embed_rmsnorm."""
