@@ -75,6 +75,10 @@ def _args():
     ap.add_argument("--no-micro", action="store_true", help="skip the config-1 microbench")
     ap.add_argument("--eager", action="store_true",
                     help="launch every kernel from the host instead of replaying a HIP graph")
+    ap.add_argument("--augment", action="store_true",
+                    help="also time predict_with_augmentations on one task of the workload: "
+                         "8 dihedral x 8 colour variants in one fused generation against the "
+                         "reference's loop over chunks of 16 (same predictions required)")
     return ap.parse_args()
 
 
@@ -215,6 +219,36 @@ def microbench(dev):
         v["frac_of_peak"] = round(v["gbs"] / HBM_PEAK_GBS, 4)
         v["ms"] = round(v["ms"], 5)
         v["gbs"] = round(v["gbs"], 1)
+    return res
+
+
+def augmentation_bench(model, dev, spec):
+    """predict_with_augmentations (the caller of the path, src/inference.py:697-920) on one
+    synthetic task of ``spec``: 64 prompts (8 dihedral x 8 colour permutations), greedy, the
+    workload's decode budget.  Fused (one generation, per-row chunk semantics) against the chunk
+    loop of 16 rows; wall seconds of one call each after a warm call, host prompt building and
+    grid decoding included."""
+    import torch
+
+    from mdlarc_scale_amd import inference as I
+    from mdlarc_scale_amd.workload import task_dict
+
+    task = task_dict(spec)
+    kw = dict(num_color_perms=8, max_output_tokens=spec.max_new)
+    res = {}
+    preds = {}
+    for name, fuse in (("fused", True), ("chunks_of_16", False)):
+        I.predict_with_augmentations(model, task, 0, dev, fuse_chunks=fuse, **kw)
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        preds[name] = I.predict_with_augmentations(model, task, 0, dev, fuse_chunks=fuse, **kw)
+        torch.cuda.synchronize()
+        res[f"{name}_s"] = round(time.perf_counter() - t0, 4)
+    n_tok = [len(v.tokens) for v in I._build_variants(task, 0, True, 8, 1, False, None, None)]
+    res.update(variants=len(preds["fused"]), prompt_len_min=min(n_tok),
+               prompt_len_max=max(n_tok), max_output_tokens=spec.max_new,
+               speedup=round(res["chunks_of_16_s"] / res["fused_s"], 2),
+               identical_predictions=preds["fused"] == preds["chunks_of_16"])
     return res
 
 
@@ -388,6 +422,7 @@ def main() -> int:
         del qp, op
 
         micro = None if (args.no_micro or not headline) else microbench(dev)
+        augment = augmentation_bench(model, dev, spec) if args.augment else None
 
         cpu = None
         if snap is not None:
@@ -443,6 +478,7 @@ def main() -> int:
             "flops": "valid causal (query, key) pairs x 4 x 64 (QK^T and PV)",
         },
         "microbench": micro,
+        **({"augmentation": augment} if augment is not None else {}),
         "wall_s_timed": round(wall_s, 4),
         "host_prompt_build_s": round(host_build_s, 3),
     }

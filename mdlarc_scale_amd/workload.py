@@ -118,6 +118,25 @@ def build_prompts(spec: WorkloadSpec) -> list[list[int]]:
     return prompts
 
 
+def task_dict(spec: WorkloadSpec, seed: int | None = None) -> dict:
+    """One ARC-format task ({"train": [{"input", "output"}, ...], "test": [{"input"}]}) drawn
+    like ``build_prompts``' tasks: every dihedral variant of its prompt lies in
+    ``spec.prompt_len``.  Input of the augmentation caller (predict_with_augmentations)."""
+    rng = np.random.default_rng(spec.seed if seed is None else seed)
+    lo, hi = spec.prompt_len
+    for _attempt in range(MAX_DRAWS):
+        grids = _draw_task(rng, spec)
+        n_special = 3 * (len(grids) // 2) + 2
+        n_tok = sum(g.shape[0] * (g.shape[1] + 1) for g in grids) + n_special
+        n_tok_t = sum(g.shape[1] * (g.shape[0] + 1) for g in grids) + n_special
+        if lo <= min(n_tok, n_tok_t) and max(n_tok, n_tok_t) <= hi:
+            pairs = [{"input": grids[i].tolist(), "output": grids[i + 1].tolist()}
+                     for i in range(0, len(grids) - 1, 2)]
+            return {"train": pairs, "test": [{"input": grids[-1].tolist()}]}
+    raise RuntimeError(f"{spec.name}: no task within {spec.prompt_len} tokens after {MAX_DRAWS} "
+                       f"draws")
+
+
 def left_pad(prompts: list[list[int]]) -> tuple[torch.Tensor, torch.Tensor, torch.Tensor]:
     """Left-pad with END and position (0,0,0); bool mask of real tokens (src/inference.py:
     877-890).  Returns CPU tensors ids [B,S], pos [B,S,3], mask [B,S]."""
