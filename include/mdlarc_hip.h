@@ -43,6 +43,28 @@ extern "C" {
 #define MDL_DTYPE_F32 0
 #define MDL_DTYPE_BF16 1
 
+/*
+ * Soft decoding constraints on a row's logits, applied before the argmax in the order of
+ * _apply_logit_constraints (src/inference.py:285-364; DecodingConstraints :37-43):
+ *   1. logit v = -inf for every bit v set in disallow_mask (disallow_tokens);
+ *   2. colours 0-9 with palette_mask[r*10 + c] == 0 lose palette_penalty;
+ *   3. rows with a target shape (target_shape[r] = (h, w), both >= 0), grid state (x, y) =
+ *      (grid_x[r], grid_y[r]) after the current token: x >= w -> colours lose shape_penalty;
+ *      x < w -> NEWLINE loses it; y >= h -> colours and NEWLINE lose it (once more).
+ * Each subtraction is a separate fp32 operation, as in the reference.  palette_mask and
+ * target_shape may be NULL (that constraint is off); grid_x / grid_y are required with
+ * target_shape.
+ */
+typedef struct mdl_logit_constraints {
+  uint32_t disallow_mask;
+  const uint8_t* palette_mask;  /* uint8 [rows, 10] */
+  float palette_penalty;
+  const int32_t* target_shape;  /* int32 [rows, 2] */
+  const int32_t* grid_x;        /* int32 [rows] */
+  const int32_t* grid_y;        /* int32 [rows] */
+  float shape_penalty;
+} mdl_logit_constraints;
+
 /* Library version (major*100 + minor) and a static string for an error code. */
 int mdl_version(void);
 const char* mdl_error_string(int code);
@@ -188,10 +210,12 @@ int mdl_attn_decode_rope(const float* qkv, int64_t qkv_ld, const float* rstd, co
  *           (src/inference.py:573-574, :610-611; first index on ties).
  * Row r uses x[row_index ? row_index[r] : r].  logits_out fp32 [rows, vocab] and token_out
  * int64 [rows] may each be NULL.  w_head fp32 [vocab, d], gamma fp32 [d].  vocab <= 32.
+ * constraints (may be NULL) are applied to row r's logits before the argmax; logits_out then
+ * holds the constrained logits.
  */
 int mdl_lm_head(const float* x, const int32_t* row_index, int rows, int d, const float* gamma,
                 float eps, const float* w_head, int vocab, float* logits_out, int64_t* token_out,
-                void* stream);
+                const mdl_logit_constraints* constraints, void* stream);
 
 /*
  * Decode-step tail: final RMSNorm + LM head + greedy argmax + token commit in one launch.
@@ -200,11 +224,14 @@ int mdl_lm_head(const float* x, const int32_t* row_index, int rows, int d, const
  *           (src/inference.py:589-590, :622-626).
  * token_out[b] = argmax; out_ids[b*out_ld + c] = token_out[b] with c = (counters ? counters[1]
  * : col); finish_step[b] (may be NULL) = c - gen_base at the first END.  logits_out may be NULL.
+ * constraints (may be NULL) as for mdl_lm_head, with the grid state the step's mdl_decode_embed
+ * advanced (so constrained greedy decoding replays from a captured graph too).
  */
 int mdl_decode_head(const float* x, int batch, int d, const float* gamma, float eps,
                     const float* w_head, int vocab, float* logits_out, int64_t* token_out,
                     int64_t* out_ids, int64_t out_ld, int col, const int32_t* counters,
-                    int32_t* finish_step, int gen_base, int end_id, void* stream);
+                    int32_t* finish_step, int gen_base, int end_id,
+                    const mdl_logit_constraints* constraints, void* stream);
 
 /*
  * Grid-state initialisation from the prompt.

@@ -19,6 +19,17 @@ LIB_PATH = _PKG / "libmdlarc_hip.so"
 HEADER = _PKG.parent / "include" / "mdlarc_hip.h"
 
 P = c_void_p
+
+
+class LogitConstraints(ctypes.Structure):
+    """``mdl_logit_constraints`` (include/mdlarc_hip.h), field for field."""
+
+    _fields_ = [("disallow_mask", ctypes.c_uint32), ("palette_mask", c_void_p),
+                ("palette_penalty", c_float), ("target_shape", c_void_p), ("grid_x", c_void_p),
+                ("grid_y", c_void_p), ("shape_penalty", c_float)]
+
+
+CONS = ctypes.POINTER(LogitConstraints)
 # argtypes per entry point, in header order
 SIGNATURES: dict[str, tuple[object, list]] = {
     "mdl_version": (c_int, []),
@@ -39,9 +50,9 @@ SIGNATURES: dict[str, tuple[object, list]] = {
     "mdl_attn_decode_rope": (c_int, [P, c_int64, P, P, P, c_int, c_int, c_int, c_int, c_int,
                                      c_int, c_float, P, P, c_int, c_int, c_int, c_int, P, c_int,
                                      P, P, P, c_int, P, P, c_int64, c_int, P, P]),
-    "mdl_lm_head": (c_int, [P, P, c_int, c_int, P, c_float, P, c_int, P, P, P]),
+    "mdl_lm_head": (c_int, [P, P, c_int, c_int, P, c_float, P, c_int, P, P, CONS, P]),
     "mdl_decode_head": (c_int, [P, c_int, c_int, P, c_float, P, c_int, P, P, P, c_int64, c_int,
-                                P, P, c_int, c_int, P]),
+                                P, P, c_int, c_int, CONS, P]),
     "mdl_grid_init": (c_int, [P, P, P, P, c_int, c_int, c_int, c_int, P, P, P, P, P, P, P]),
     "mdl_grid_step": (c_int, [P, c_int, c_int, c_int, P, P, P, P, P, P]),
     "mdl_decode_commit": (c_int, [P, c_int, P, c_int64, c_int, P, P, c_int, c_int, P]),

@@ -11,6 +11,38 @@ namespace mdl {
 
 constexpr int kVmax = 32;
 
+// mdl_logit_constraints by value in the kernel arguments (a captured graph keeps them).
+struct HeadCons {
+  uint32_t disallow;
+  const uint8_t* palette;
+  float palette_penalty;
+  const int32_t* shape;
+  const int32_t* gx;
+  const int32_t* gy;
+  float shape_penalty;
+};
+
+// Row r's logit of vocab slot `slot` after the constraints, in the reference's order of
+// operations (one fp32 subtraction per penalty).
+__device__ __forceinline__ float constrain(float v, int slot, int r, const HeadCons& c) {
+  if ((c.disallow >> slot) & 1u) v = -INFINITY;
+  const bool colour = slot < 10, newline = slot == kNewline;
+  if (c.palette && colour && c.palette[static_cast<int64_t>(r) * 10 + slot] == 0)
+    v = v - c.palette_penalty;
+  if (c.shape) {
+    const int th = c.shape[2 * static_cast<int64_t>(r)];
+    const int tw = c.shape[2 * static_cast<int64_t>(r) + 1];
+    if (th >= 0 && tw >= 0) {
+      const int x = c.gx[r], y = c.gy[r];
+      if (x >= tw && colour) v = v - c.shape_penalty;
+      if (x < tw && newline) v = v - c.shape_penalty;
+      if (y >= th && colour) v = v - c.shape_penalty;
+      if (y >= th && newline) v = v - c.shape_penalty;
+    }
+  }
+  return v;
+}
+
 // One wavefront per output row.  The lane keeps NC 4-channel chunks of x * gamma in registers,
 // reduces the sum of squares, accumulates its partial dot product with every vocab row, then
 // reduces all NV partials at once with a reduce-scatter butterfly: at level k (xor 32 >> k) a
@@ -22,8 +54,9 @@ constexpr int kVmax = 32;
 template <int NC, int NV>
 __device__ __forceinline__ void head_row(const float* __restrict__ xr, int lane, int d,
                                          const float* __restrict__ gamma, float eps,
-                                         const float* __restrict__ w, int vocab, float& logit,
-                                         int& slot, int& best) {
+                                         const float* __restrict__ w, int vocab, int r,
+                                         const HeadCons& cons, float& logit, int& slot,
+                                         int& best) {
   constexpr int LOG_NV = NV == 16 ? 4 : 5;
   float v[NC][4];
   float ss = 0.f;
@@ -78,6 +111,7 @@ __device__ __forceinline__ void head_row(const float* __restrict__ xr, int lane,
   for (int mask = 32 >> LOG_NV; mask > 0; mask >>= 1) tot += __shfl_xor(tot, mask, kWave);
   slot = lane >> (6 - LOG_NV);
   logit = tot * rs;
+  if (slot < vocab) logit = constrain(logit, slot, r, cons);
   float bv = slot < vocab ? logit : -INFINITY;
   int bi = slot;
 #pragma unroll
@@ -101,14 +135,14 @@ __global__ __launch_bounds__(256) void head_kernel(
     const float* __restrict__ gamma, float eps, const float* __restrict__ w, int vocab,
     float* __restrict__ logits, int64_t* __restrict__ token, int64_t* __restrict__ out_ids,
     int64_t ld, int col, const int32_t* __restrict__ counters, int32_t* __restrict__ finish,
-    int gen_base, int64_t end_id) {
+    int gen_base, int64_t end_id, HeadCons cons) {
   const int lane = threadIdx.x & 63;
   const int r = blockIdx.x * 4 + (threadIdx.x >> 6);
   if (r >= rows) return;
   const int64_t m = row_index ? row_index[r] : r;
   float logit;
   int slot, best;
-  head_row<NC, NV>(x + m * d, lane, d, gamma, eps, w, vocab, logit, slot, best);
+  head_row<NC, NV>(x + m * d, lane, d, gamma, eps, w, vocab, r, cons, logit, slot, best);
   constexpr int kGroup = NV == 16 ? 4 : 2;          // lanes holding the same vocab slot
   if (logits && (lane & (kGroup - 1)) == 0 && slot < vocab)
     logits[static_cast<int64_t>(r) * vocab + slot] = logit;
@@ -217,28 +251,35 @@ struct LaunchHead {
   static void run(int nv, dim3 grid, hipStream_t s, const float* x, const int32_t* row_index,
                   int rows, int d, const float* gamma, float eps, const float* w, int vocab,
                   float* logits, int64_t* token, int64_t* out_ids, int64_t ld, int col,
-                  const int32_t* counters, int32_t* finish, int gen_base, int64_t end_id) {
+                  const int32_t* counters, int32_t* finish, int gen_base, int64_t end_id,
+                  const HeadCons& cons) {
     if (nv == 16)
       head_kernel<NC, 16><<<grid, 256, 0, s>>>(x, row_index, rows, d, gamma, eps, w, vocab,
                                                logits, token, out_ids, ld, col, counters, finish,
-                                               gen_base, end_id);
+                                               gen_base, end_id, cons);
     else
       head_kernel<NC, 32><<<grid, 256, 0, s>>>(x, row_index, rows, d, gamma, eps, w, vocab,
                                                logits, token, out_ids, ld, col, counters, finish,
-                                               gen_base, end_id);
+                                               gen_base, end_id, cons);
   }
 };
 
 int launch_head(const float* x, const int32_t* row_index, int rows, int d, const float* gamma,
                 float eps, const float* w, int vocab, float* logits, int64_t* token,
                 int64_t* out_ids, int64_t ld, int col, const int32_t* counters, int32_t* finish,
-                int gen_base, int64_t end_id, hipStream_t s) {
+                int gen_base, int64_t end_id, const mdl_logit_constraints* c, hipStream_t s) {
+  HeadCons cons{0u, nullptr, 0.f, nullptr, nullptr, nullptr, 0.f};
+  if (c) {
+    if (c->target_shape && (!c->grid_x || !c->grid_y)) return MDL_ERR_NULL;
+    cons = HeadCons{c->disallow_mask, c->palette_mask, c->palette_penalty, c->target_shape,
+                    c->grid_x, c->grid_y, c->shape_penalty};
+  }
   const dim3 grid((rows + 3) / 4);
   const int nv = vocab <= 16 ? 16 : 32;
 #define MDL_HEAD(N)                                                                            \
   case N:                                                                                      \
     LaunchHead<N>::run(nv, grid, s, x, row_index, rows, d, gamma, eps, w, vocab, logits, token, \
-                       out_ids, ld, col, counters, finish, gen_base, end_id);                  \
+                       out_ids, ld, col, counters, finish, gen_base, end_id, cons);            \
     break;
   switch ((d + 255) / 256) { MDL_HEAD(1) MDL_HEAD(2) MDL_HEAD(3) MDL_HEAD(4) MDL_HEAD(5)
                              MDL_HEAD(6) MDL_HEAD(7) MDL_HEAD(8) }
@@ -250,7 +291,7 @@ int launch_head(const float* x, const int32_t* row_index, int rows, int d, const
 
 using namespace mdl;
 
-extern "C" int mdl_version(void) { return 101; }
+extern "C" int mdl_version(void) { return 102; }
 
 extern "C" const char* mdl_error_string(int code) {
   switch (code) {
@@ -268,21 +309,24 @@ extern "C" const char* mdl_error_string(int code) {
 
 extern "C" int mdl_lm_head(const float* x, const int32_t* row_index, int rows, int d,
                            const float* gamma, float eps, const float* w_head, int vocab,
-                           float* logits_out, int64_t* token_out, void* stream) {
+                           float* logits_out, int64_t* token_out,
+                           const mdl_logit_constraints* constraints, void* stream) {
   if (!x || !gamma || !w_head) return MDL_ERR_NULL;
   if (rows < 0 || d <= 0 || d % 4 != 0 || d > 2048 || vocab <= 0 || vocab > kVmax)
     return MDL_ERR_SHAPE;
   if (!aligned16(x) || !aligned16(gamma) || !aligned16(w_head)) return MDL_ERR_ALIGN;
   if (rows == 0) return MDL_OK;
   return launch_head(x, row_index, rows, d, gamma, eps, w_head, vocab, logits_out, token_out,
-                     nullptr, 0, 0, nullptr, nullptr, 0, 0, static_cast<hipStream_t>(stream));
+                     nullptr, 0, 0, nullptr, nullptr, 0, 0, constraints,
+                     static_cast<hipStream_t>(stream));
 }
 
 extern "C" int mdl_decode_head(const float* x, int batch, int d, const float* gamma, float eps,
                                const float* w_head, int vocab, float* logits_out,
                                int64_t* token_out, int64_t* out_ids, int64_t out_ld, int col,
                                const int32_t* counters, int32_t* finish_step, int gen_base,
-                               int end_id, void* stream) {
+                               int end_id, const mdl_logit_constraints* constraints,
+                               void* stream) {
   if (!x || !gamma || !w_head || !token_out || !out_ids) return MDL_ERR_NULL;
   if (batch < 0 || d <= 0 || d % 4 != 0 || d > 2048 || vocab <= 0 || vocab > kVmax ||
       out_ld <= 0 || (!counters && (col < 0 || col >= out_ld)))
@@ -290,7 +334,7 @@ extern "C" int mdl_decode_head(const float* x, int batch, int d, const float* ga
   if (!aligned16(x) || !aligned16(gamma) || !aligned16(w_head)) return MDL_ERR_ALIGN;
   if (batch == 0) return MDL_OK;
   return launch_head(x, nullptr, batch, d, gamma, eps, w_head, vocab, logits_out, token_out,
-                     out_ids, out_ld, col, counters, finish_step, gen_base, end_id,
+                     out_ids, out_ld, col, counters, finish_step, gen_base, end_id, constraints,
                      static_cast<hipStream_t>(stream));
 }
 

@@ -41,6 +41,9 @@ from .engine import engine_for, gemm_f32
 from .transformer import TinyTransformer, softmax_scale
 
 SYNC_EVERY = 8
+# Greedy constrained decoding applies the constraints inside the head kernel (and replays the
+# captured step); False routes it through the host torch restatement between launches instead.
+FUSED_CONSTRAINTS = True
 # Replay greedy decode steps from one captured HIP graph (False: launch every kernel from the host
 # each step; same kernels, same results).
 USE_GRAPHS = True
@@ -91,9 +94,23 @@ def apply_logit_constraints(logits: torch.Tensor, gx: torch.Tensor, gy: torch.Te
         row_full = (has & (x >= tw)).to(logits.dtype) * pen
         row_open = (has & (x < tw)).to(logits.dtype) * pen
         past_end = (has & (y >= th)).to(logits.dtype) * pen
-        logits[:, :10] -= (row_full + past_end)[:, None]
-        logits[:, NEWLINE_TOKEN_ID] -= row_open + past_end
+        # one subtraction per penalty, in the reference's order (it rounds each separately)
+        logits[:, :10] -= row_full[:, None]
+        logits[:, NEWLINE_TOKEN_ID] -= row_open
+        logits[:, :10] -= past_end[:, None]
+        logits[:, NEWLINE_TOKEN_ID] -= past_end
     return logits
+
+
+def _head_constraints(c: DecodingConstraints, st) -> K.HeadConstraints:
+    """The constraints of one generation in the head kernels' device form, bound to the decode
+    state's grid position (the state after the current token, as at src/inference.py:586-611).
+    Shapes normalise as in the host path: a single row broadcasts, other mismatches drop that
+    constraint."""
+    dev = st.gx.device
+    return K.HeadConstraints(c.disallow_tokens, _per_row(c.palette_mask, st.B, 10, dev),
+                             c.palette_penalty, _per_row(c.target_shape, st.B, 2, dev),
+                             st.gx, st.gy, c.shape_penalty)
 
 
 def _pick(logits: torch.Tensor, temperature: float, top_k: int | None) -> torch.Tensor:
@@ -278,14 +295,16 @@ class Generator:
             cache=cache, sc=Scratch.alloc(B, cfg.d_model, cfg.d_ff, dev), ws=ws,
             split_len=split)
 
-    def prefill(self, st: DecodeState, W: PackedWeights, input_ids, positions_3d) -> None:
+    def prefill(self, st: DecodeState, W: PackedWeights, input_ids, positions_3d,
+                cons: K.HeadConstraints | None = None) -> None:
         """``_prefill`` (src/inference.py:383-424): all layers over the prompt, K/V into slots
-        [0, S), logits of row lengths-1 into ``st.logits`` and its argmax into ``st.tok``."""
+        [0, S), logits of row lengths-1 into ``st.logits`` and its argmax into ``st.tok``
+        (after ``cons``, the fused logit constraints, when given)."""
         cfg = self.model.config
         sc = Scratch.alloc(st.B * st.S, cfg.d_model, cfg.d_ff, input_ids.device)
         self.eng.run_prompt(W, input_ids, positions_3d, st.ex, st.pmask, st.kv_start, True,
                             st.cache.layer, sc)
-        K.lm_head(sc.x, st.last_row, st.B, W.ln_f, W.eps, W.head, st.logits, st.tok)
+        K.lm_head(sc.x, st.last_row, st.B, W.ln_f, W.eps, W.head, st.logits, st.tok, cons)
         st.cache.seq_len = st.S
 
     def _embed_inputs(self, st: DecodeState):
@@ -323,19 +342,20 @@ class Generator:
         K.lm_head(sc.x, None, st.B, W.ln_f, W.eps, W.head, st.logits if want_logits else None,
                   st.tok)
 
-    def greedy_step(self, st: DecodeState, W: PackedWeights, stop_on_end: bool) -> None:
+    def greedy_step(self, st: DecodeState, W: PackedWeights, stop_on_end: bool,
+                    cons: K.HeadConstraints | None = None) -> None:
         """One full device-side decode step of greedy generation: grid position + embedding,
-        the layers, then LM head + argmax + commit."""
+        the layers, then LM head (+ logit constraints) + argmax + commit."""
         sc = st.sc
         tok_tab, ex_tab, use_ex = self._embed_inputs(st)
         K.decode_embed(st.tok, use_ex, tok_tab, ex_tab, W.ln1[0], W.eps, st.gx, st.gy, st.gio,
                        st.pos, st.counters, sc.x, sc.xs, sc.rstd)
         self._layers(st, W)
         K.decode_head(sc.x, W.ln_f, W.eps, W.head, None, st.tok, st.out_ids, 0, st.counters,
-                      st.finish if stop_on_end else None, st.S, END_TOKEN_ID)
+                      st.finish if stop_on_end else None, st.S, END_TOKEN_ID, cons)
 
-    def capture_greedy(self, st: DecodeState, W: PackedWeights,
-                       stop_on_end: bool) -> torch.cuda.CUDAGraph:
+    def capture_greedy(self, st: DecodeState, W: PackedWeights, stop_on_end: bool,
+                       cons: K.HeadConstraints | None = None) -> torch.cuda.CUDAGraph:
         """Record ``greedy_step`` into a HIP graph.  Every buffer it touches is preallocated in
         ``st`` and the cache slot / output column advance through ``st.counters`` on the device,
         so one recording replays as every later step.  Capturing launches nothing; the caller
@@ -343,7 +363,7 @@ class Generator:
         The step records no memset nodes."""
         g = torch.cuda.CUDAGraph()
         with torch.cuda.graph(g):
-            self.greedy_step(st, W, stop_on_end)
+            self.greedy_step(st, W, stop_on_end, cons)
         return g
 
 
@@ -403,8 +423,11 @@ def _generate(model: TinyTransformer, input_ids, positions_3d, example_ids, atte
     with torch.no_grad():
         W = eng.packed(dev)
         st = gen.prepare(ids, pos, ex, prompt_mask, total, row_shift)
-        gen.prefill(st, W, ids, pos)
-        eager = temperature > 0 or constraints is not None
+        # sampling runs on the host between launches; greedy decoding (constrained or not) is
+        # one device-side step replayed from a captured graph, constraints fused into the head
+        eager = temperature > 0 or (constraints is not None and not FUSED_CONSTRAINTS)
+        cons = None if (eager or constraints is None) else _head_constraints(constraints, st)
+        gen.prefill(st, W, ids, pos, cons)
         if eager:
             apply_logit_constraints(st.logits, st.gx, st.gy, constraints)
             st.tok.copy_(_pick(st.logits, temperature, top_k))
@@ -425,9 +448,9 @@ def _generate(model: TinyTransformer, input_ids, positions_3d, example_ids, atte
             elif graph is not None:
                 graph.replay()
             else:
-                gen.greedy_step(st, W, stop_on_end)
+                gen.greedy_step(st, W, stop_on_end, cons)
                 if USE_GRAPHS and step + 1 < max_new:
-                    graph = gen.capture_greedy(st, W, stop_on_end)
+                    graph = gen.capture_greedy(st, W, stop_on_end, cons)
             produced += 1
     return st.out_ids[:, :S + produced], st.finish, produced
 

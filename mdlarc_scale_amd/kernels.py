@@ -256,9 +256,42 @@ def attn_decode_rope(qkv: torch.Tensor, rstd: torch.Tensor, pos: torch.Tensor,
         _p(workspace), ws_bytes, split_len, _p(out), _stream()), "mdl_attn_decode_rope")
 
 
+class HeadConstraints:
+    """Device form of DecodingConstraints for the head kernels (``mdl_logit_constraints``):
+    keeps the tensors it points at alive for as long as the launches (or a captured graph)
+    use them.  palette uint8/bool [rows, 10] and target_shape int [rows, 2] may be None; gx / gy
+    are the decode state's grid position (int32 [rows]), read at launch time."""
+
+    def __init__(self, disallow_tokens, palette: torch.Tensor | None, palette_penalty: float,
+                 target_shape: torch.Tensor | None, gx: torch.Tensor, gy: torch.Tensor,
+                 shape_penalty: float):
+        rows = gx.numel()
+        self.palette = None if palette is None else palette.to(torch.uint8).contiguous()
+        self.shape = None if target_shape is None else target_shape.to(torch.int32).contiguous()
+        _need(self.palette, "palette", U8, rows * 10, optional=True)
+        _need(self.shape, "target_shape", I32, rows * 2, optional=True)
+        _need(gx, "gx", I32, rows)
+        _need(gy, "gy", I32, rows)
+        self.gx, self.gy, self.rows = gx, gy, rows
+        mask = 0
+        for t in disallow_tokens:
+            if not 0 <= int(t) < 32:
+                raise ValueError(f"disallowed token {t} outside the head's 32 vocab slots")
+            mask |= 1 << int(t)
+        addr = lambda t: None if t is None else t.data_ptr()  # noqa: E731
+        self.struct = _lib.LogitConstraints(mask, addr(self.palette), float(palette_penalty),
+                                            addr(self.shape), addr(gx), addr(gy),
+                                            float(shape_penalty))
+
+    def ref(self, rows: int):
+        if rows != self.rows:
+            raise ValueError(f"constraints built for {self.rows} rows, launch has {rows}")
+        return ctypes.byref(self.struct)
+
+
 def lm_head(x: torch.Tensor, row_index: torch.Tensor | None, rows: int, gamma: torch.Tensor,
             eps: float, w_head: torch.Tensor, logits_out: torch.Tensor | None,
-            token_out: torch.Tensor | None) -> None:
+            token_out: torch.Tensor | None, constraints: HeadConstraints | None = None) -> None:
     d = x.shape[-1]
     vocab = w_head.shape[0]
     _need(x, "x", F32)
@@ -271,14 +304,16 @@ def lm_head(x: torch.Tensor, row_index: torch.Tensor | None, rows: int, gamma: t
     _need(token_out, "token_out", I64, rows, optional=True)
     _lib.check(_lib.lib().mdl_lm_head(
         _p(x), _p(row_index), rows, d, _p(gamma), eps, _p(w_head), vocab, _p(logits_out),
-        _p(token_out), _stream()), "mdl_lm_head")
+        _p(token_out), None if constraints is None else constraints.ref(rows), _stream()),
+        "mdl_lm_head")
 
 
 def decode_head(x: torch.Tensor, gamma: torch.Tensor, eps: float, w_head: torch.Tensor,
                 logits_out: torch.Tensor | None, token_out: torch.Tensor, out_ids: torch.Tensor,
                 col: int, counters: torch.Tensor | None, finish_step: torch.Tensor | None,
-                gen_base: int, end_id: int) -> None:
-    """ln_f + LM head + argmax into token_out, committed to out_ids[:, counters[1] or col]."""
+                gen_base: int, end_id: int, constraints: HeadConstraints | None = None) -> None:
+    """ln_f + LM head (+ constraints) + argmax into token_out, committed to
+    out_ids[:, counters[1] or col]."""
     batch, d = x.shape
     vocab = w_head.shape[0]
     _need(x, "x", F32)
@@ -294,7 +329,7 @@ def decode_head(x: torch.Tensor, gamma: torch.Tensor, eps: float, w_head: torch.
     _lib.check(_lib.lib().mdl_decode_head(
         _p(x), batch, d, _p(gamma), eps, _p(w_head), vocab, _p(logits_out), _p(token_out),
         _p(out_ids), out_ids.shape[1], col, _p(counters), _p(finish_step), gen_base, end_id,
-        _stream()), "mdl_decode_head")
+        None if constraints is None else constraints.ref(batch), _stream()), "mdl_decode_head")
 
 
 def grid_init(ids: torch.Tensor, pos: torch.Tensor, mask: torch.Tensor | None, gx: torch.Tensor,

@@ -265,11 +265,13 @@ def test_predict_with_augmentations_pipeline():
     assert preds[0][2] is None and preds[1][2] is not None
 
 
-@pytest.mark.parametrize("fixture,batched,chunk", [("e2e_micro_stop", True, 16),
-                                                   ("e2e_micro_stop", True, 5),
-                                                   ("e2e_micro_stop", False, 1),
-                                                   ("e2e_micro", False, 1)])
-def test_fused_augmentations_equal_chunk_loop(fixture, batched, chunk, monkeypatch):
+@pytest.mark.parametrize("fixture,batched,chunk,constrain", [("e2e_micro_stop", True, 16, False),
+                                                             ("e2e_micro_stop", True, 5, False),
+                                                             ("e2e_micro_stop", False, 1, False),
+                                                             ("e2e_micro", False, 1, False),
+                                                             ("e2e_micro_stop", True, 5, True),
+                                                             ("e2e_micro", False, 1, True)])
+def test_fused_augmentations_equal_chunk_loop(fixture, batched, chunk, constrain, monkeypatch):
     """One fused generation over every augmented prompt returns exactly what the reference's
     chunk-by-chunk loop returns (src/inference.py:829-918): per row, the chunk's lengths-1 index,
     the chunk's token budget under max_seq_len and the chunk's stop step (all of its rows emitted
@@ -286,7 +288,7 @@ def test_fused_augmentations_equal_chunk_loop(fixture, batched, chunk, monkeypat
             "test": [{"input": [[1, 0, 2, 0, 3]]}]}
     monkeypatch.setattr(inf, "decode_output_grid", lambda toks: tuple(toks))
     kw = dict(example_id=1, num_color_perms=3, max_output_tokens=130, batched=batched,
-              max_batch_size=chunk)
+              max_batch_size=chunk, constrain_decoding=constrain)
     fused = inf.predict_with_augmentations(m, task, 0, DEV, **kw)
     loop = inf.predict_with_augmentations(m, task, 0, DEV, fuse_chunks=False, **kw)
     assert len(fused) == len(loop) == 24
@@ -362,3 +364,33 @@ def test_config2_slice_decode_vs_oracle():
     assert err <= 2e-2
     _near_tie_ok(ref, got.argmax(-1), ref.argmax(-1), err)
     assert agree >= 0.995 or _first_divergence_is_tie(out, tr, S, err)
+
+
+def test_constrained_greedy_fused_equals_host_path(monkeypatch):
+    """Greedy constrained decoding with the palette / shape / disallow constraints fused into the
+    head kernels (and the step replayed from a captured graph) returns exactly the tokens of the
+    host restatement of _apply_logit_constraints between launches (src/inference.py:285-364,
+    :586-611); the constraints change the tokens."""
+    from mdlarc_scale_amd import inference as inf
+
+    m = _model_from_fixture(load_e2e("e2e_micro"))
+    rng = np.random.default_rng(9)
+    ids, pos, mask = _left_pad(_random_prompts(rng, 6, 2, 1, 4))
+    g = torch.Generator().manual_seed(9)
+    pal = torch.rand(6, 10, generator=g) < 0.5
+    pal[0] = True
+    shape = torch.randint(1, 5, (6, 2), generator=g)
+    shape[1] = -1
+    cons = inf.DecodingConstraints(palette_mask=pal.to(DEV), target_shape=shape.to(DEV))
+    outs = {}
+    for fused in (True, False):
+        monkeypatch.setattr(inf, "FUSED_CONSTRAINTS", fused)
+        with torch.no_grad():
+            outs[fused] = inf.generate_output(m, ids.to(DEV), pos.to(DEV), None, mask.to(DEV),
+                                              max_new_tokens=40, constraints=cons).cpu()
+    with torch.no_grad():
+        free = inf.generate_output(m, ids.to(DEV), pos.to(DEV), None, mask.to(DEV),
+                                   max_new_tokens=40).cpu()
+    assert torch.equal(outs[True], outs[False])
+    n = min(free.shape[1], outs[True].shape[1])
+    assert not torch.equal(free[:, :n], outs[True][:, :n])
