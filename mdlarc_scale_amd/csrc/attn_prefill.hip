@@ -53,6 +53,19 @@ __device__ __forceinline__ s16x4_t lds_read_tr16(const uint16_t* p) {
       (__attribute__((address_space(3))) s16x4_t*)(p));
 }
 
+// Maximum over lanes l, l^16, l^32, l^48 (one query's four lane groups) with gfx950's VALU lane
+// swaps: v_permlane16_swap / v_permlane32_swap of a value with itself return {x[l], x[l^16]} /
+// {x[l], x[l^32]} (checked on the GPU).  Replaces two ds_bpermute round trips through the LDS
+// unit on the softmax's critical path (measured 3% on the whole kernel, bit-identical).
+__device__ __forceinline__ float max_over_groups(float v) {
+  const auto a = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false,
+                                                  false);
+  v = fmaxf(__uint_as_float(a[0]), __uint_as_float(a[1]));
+  const auto b = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false,
+                                                  false);
+  return fmaxf(__uint_as_float(b[0]), __uint_as_float(b[1]));
+}
+
 __global__ __launch_bounds__(256, 3) void attn_prefill_kernel(
     const uint16_t* __restrict__ q, const uint16_t* __restrict__ kc,
     const uint16_t* __restrict__ vc, int S, int H, int slots, const uint8_t* __restrict__ kmask,
@@ -186,8 +199,7 @@ __global__ __launch_bounds__(256, 3) void attn_prefill_kernel(
       for (int nb = 0; nb < 4; ++nb)
 #pragma unroll
         for (int i = 0; i < 4; ++i) tmax = fmaxf(tmax, sc[j][nb][i]);
-      tmax = fmaxf(tmax, __shfl_xor(tmax, 16, kWave));
-      tmax = fmaxf(tmax, __shfl_xor(tmax, 32, kWave));
+      tmax = max_over_groups(tmax);
       const float mnew = fmaxf(m_run[j], tmax * kLog2eP);
       const float mb = (mnew == -INFINITY) ? 0.f : mnew;   // no visible key yet: p = 0
       const float alpha = __builtin_amdgcn_exp2f(m_run[j] - mb);
