@@ -6,6 +6,7 @@ The kernels live in ``libmdlarc_hip.so`` (C ABI, include/mdlarc_hip.h), built in
 ``python -m mdlarc_scale_amd.build``.
 """
 
+from .checkpoint import load_model_from_checkpoint  # noqa: F401
 from .data import (  # noqa: F401
     DIHEDRAL_TRANSFORMS,
     END_TOKEN_ID,
