@@ -254,6 +254,26 @@ int mdl_grid_init(const int64_t* ids, const int64_t* pos, const uint8_t* mask,
                   uint8_t* row_holes, void* stream);
 
 /*
+ * Augmented prompts of one task, built on the device and left-padded into one batch.
+ * Replaces: the prompt construction of _predict_augmentations_batched (src/inference.py:794-827,
+ *           :877-890): dihedral transforms (src/data.py:224-233), colour permutations (:257-278),
+ *           encode_example (:75-93), compute_positions_3d (:124-175) and the END / (0,0,0) left
+ *           padding.
+ * cells uint8 [n_cells]: every grid of the task row-major in its own orientation, concatenated;
+ * grids int32 [n_grids, 3] = (offset into cells, h, w) in the order in0, out0, in1, out1, ...,
+ *   test_in (n_grids odd);
+ * variants int32 [batch, 2] = (dihedral index 0-7, row of perms); perms int32 [n_perms, 10];
+ * lengths int32 [batch]: each variant's prompt length (sum of its grids' h'(w'+1) plus the
+ *   START / IO_SEP / END tokens), seq >= max(lengths).
+ * Outputs: ids int64 [batch, seq], pos int64 [batch, seq, 3], mask uint8 [batch, seq]; row b's
+ * prompt occupies columns [seq - lengths[b], seq).
+ */
+int mdl_build_prompts(const uint8_t* cells, int64_t n_cells, const int32_t* grids, int n_grids,
+                      const int32_t* variants, int batch, const int32_t* perms, int n_perms,
+                      const int32_t* lengths, int seq, int64_t* ids_out, int64_t* pos_out,
+                      uint8_t* mask_out, void* stream);
+
+/*
  * One grid-state step: position of the token each row just emitted, then advance the state.
  * Replaces: GridStateUpdater.update (src/inference.py:127-168).
  * token int64 [batch] -> pos_out int64 [batch, 3].  counters (int32[2], may be NULL) are

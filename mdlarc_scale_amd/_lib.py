@@ -54,6 +54,8 @@ SIGNATURES: dict[str, tuple[object, list]] = {
     "mdl_decode_head": (c_int, [P, c_int, c_int, P, c_float, P, c_int, P, P, P, c_int64, c_int,
                                 P, P, c_int, c_int, CONS, P]),
     "mdl_grid_init": (c_int, [P, P, P, P, c_int, c_int, c_int, c_int, P, P, P, P, P, P, P]),
+    "mdl_build_prompts": (c_int, [P, c_int64, P, c_int, P, c_int, P, c_int, P, c_int, P, P, P,
+                                  P]),
     "mdl_grid_step": (c_int, [P, c_int, c_int, c_int, P, P, P, P, P, P]),
     "mdl_decode_commit": (c_int, [P, c_int, P, c_int64, c_int, P, P, c_int, c_int, P]),
 }

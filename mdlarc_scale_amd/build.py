@@ -30,6 +30,7 @@ SOURCES = [
     "attn_decode.hip",
     "attn_prefill.hip",
     "head_state.hip",
+    "prompt_build.hip",
 ]
 
 FLAGS = [

@@ -44,6 +44,9 @@ SYNC_EVERY = 8
 # Greedy constrained decoding applies the constraints inside the head kernel (and replays the
 # captured step); False routes it through the host torch restatement between launches instead.
 FUSED_CONSTRAINTS = True
+# The fused augmentation caller builds its prompts on the device (mdl_build_prompts); False
+# tokenises them on the host.
+DEVICE_PROMPTS = True
 # Replay greedy decode steps from one captured HIP graph (False: launch every kernel from the host
 # each step; same kernels, same results).
 USE_GRAPHS = True
@@ -514,17 +517,19 @@ def _transform_shape(shape, dihedral_idx: int):
 
 @dataclass
 class _Variant:
-    tokens: list[int]
+    tokens: list[int] | None     # None when the prompt is built on the device
     dihedral: int
     perm: tuple[int, ...] | None
     palette: set[int] | None
     shape: tuple[int, int] | None
+    perm_row: int = 0            # row of generate_color_permutations(num_color_perms, 42)
 
 
 def _build_variants(task, test_idx, use_train_examples, num_color_perms, num_samples,
-                    constrain, base_palette, base_shape) -> list[_Variant]:
+                    constrain, base_palette, base_shape, tokenize: bool = True) -> list[_Variant]:
     """Every dihedral x colour-permutation prompt, in the reference's order
-    (src/inference.py:794-827)."""
+    (src/inference.py:794-827); ``tokenize=False`` keeps only the variant's description (the
+    device builds the prompts, ``_device_prompts``)."""
     pairs = task["train"] if use_train_examples else []
     test_in = task["test"][test_idx]["input"]
     perms = generate_color_permutations(num_color_perms, seed=42)
@@ -539,6 +544,10 @@ def _build_variants(task, test_idx, use_train_examples, num_color_perms, num_sam
             palette = None
             if base_palette is not None:
                 palette = {int(perm[c]) for c in base_palette} if pi > 0 else base_palette
+            ptuple = tuple(int(v) for v in perm) if pi > 0 else None
+            if not tokenize:
+                out += [_Variant(None, di, ptuple, palette, shape, pi) for _ in range(num_samples)]
+                continue
             if pi > 0:
                 ins_p = [apply_color_perm_grid(g, perm) for g in ins]
                 outs_p = [apply_color_perm_grid(g, perm) for g in outs]
@@ -549,9 +558,46 @@ def _build_variants(task, test_idx, use_train_examples, num_color_perms, num_sam
             for a, b in zip(ins_p, outs_p, strict=True):
                 toks += encode_example(a, b)
             toks += encode_example(tin_p, None)
-            ptuple = tuple(int(v) for v in perm) if pi > 0 else None
-            out += [_Variant(toks, di, ptuple, palette, shape) for _ in range(num_samples)]
+            out += [_Variant(toks, di, ptuple, palette, shape, pi) for _ in range(num_samples)]
     return out
+
+
+def _task_grids(task, test_idx, use_train_examples) -> list | None:
+    """[in0, out0, ..., test_in] as int arrays, or None when a grid is not rectangular (only the
+    host tokeniser handles those)."""
+    pairs = task["train"] if use_train_examples else []
+    grids = [g for p in pairs for g in (p["input"], p["output"])] + [task["test"][test_idx]["input"]]
+    out = []
+    for g in grids:
+        if g and any(len(r) != len(g[0]) for r in g):
+            return None
+        out.append(np.asarray(g, dtype=np.int64).reshape(len(g), len(g[0]) if g else 0))
+    return out
+
+
+def _device_prompts(grids: list, variants: list[_Variant], num_color_perms: int, device):
+    """The variants' prompts built on the device (mdl_build_prompts), left-padded: ids, pos,
+    mask and the per-row prompt lengths.  A transposing dihedral swaps a grid's h and w; a grid
+    of h x w is h*(w+1) tokens; each pair adds START / IO_SEP / END, the test START / IO_SEP."""
+    swaps = (1, 3, 6, 7)
+    n_pairs = (len(grids) - 1) // 2
+    seg = lambda g, d: (g.shape[1] * (g.shape[0] + 1) if d in swaps       # noqa: E731
+                        else g.shape[0] * (g.shape[1] + 1))
+    lengths = [3 * n_pairs + 2 + sum(seg(g, v.dihedral) for g in grids) for v in variants]
+    S = max(lengths)
+    offs = np.cumsum([0] + [g.size for g in grids])
+    cells = np.concatenate([g.reshape(-1) for g in grids] + [np.zeros(1, np.int64)]) % 10
+    meta = np.array([[offs[i], g.shape[0], g.shape[1]] for i, g in enumerate(grids)], np.int32)
+    perms = generate_color_permutations(num_color_perms, seed=42).astype(np.int32)
+    var = np.array([[v.dihedral, v.perm_row] for v in variants], dtype=np.int32)
+    to = lambda a: torch.from_numpy(np.ascontiguousarray(a)).to(device)   # noqa: E731
+    B = len(variants)
+    ids = torch.empty(B, S, dtype=torch.int64, device=device)
+    pos = torch.empty(B, S, 3, dtype=torch.int64, device=device)
+    mask = torch.empty(B, S, dtype=torch.uint8, device=device)
+    K.build_prompts(to(cells.astype(np.uint8)), to(meta), to(var), to(perms),
+                    to(np.array(lengths, dtype=np.int32)), ids, pos, mask)
+    return ids, pos, mask.bool(), lengths
 
 
 def left_pad_batch(prompts: list[list[int]], device) -> tuple[torch.Tensor, ...]:
@@ -592,12 +638,17 @@ def predict_with_augmentations(model: TinyTransformer, task: dict, test_idx: int
     num_samples = max(1, num_samples)
     base_palette = _collect_palette(task, test_idx) if constrain_decoding else None
     base_shape = _infer_output_shape(task) if constrain_decoding else None
-    variants = _build_variants(task, test_idx, use_train_examples, num_color_perms, num_samples,
-                               constrain_decoding, base_palette, base_shape)
     chunk = max_batch_size if batched else 1
-    if fuse_chunks and sample_temperature <= 0 and len(variants) > 1:
+    fused = fuse_chunks and sample_temperature <= 0 and 8 * num_color_perms * num_samples > 1
+    grids = (_task_grids(task, test_idx, use_train_examples)
+             if fused and DEVICE_PROMPTS else None)
+    variants = _build_variants(task, test_idx, use_train_examples, num_color_perms, num_samples,
+                               constrain_decoding, base_palette, base_shape,
+                               tokenize=grids is None)
+    if fused:
         return _predict_fused(model, variants, chunk, device, example_id, max_output_tokens,
-                              constrain_decoding, palette_penalty, shape_penalty)
+                              constrain_decoding, palette_penalty, shape_penalty, grids,
+                              num_color_perms)
     preds = []
     for c0 in range(0, len(variants), chunk):
         part = variants[c0:c0 + chunk]
@@ -626,7 +677,8 @@ def predict_with_augmentations(model: TinyTransformer, task: dict, test_idx: int
 
 def _predict_fused(model: TinyTransformer, variants: list[_Variant], chunk: int, device,
                    example_id: int, max_output_tokens: int, constrain: bool,
-                   palette_penalty: float, shape_penalty: float):
+                   palette_penalty: float, shape_penalty: float, grids: list | None = None,
+                   num_color_perms: int = 0):
     """Greedy predictions of every variant from one generation over all of them, equal to the
     reference's loop over left-padded chunks of ``chunk`` rows (src/inference.py:829-918).
 
@@ -642,13 +694,20 @@ def _predict_fused(model: TinyTransformer, variants: list[_Variant], chunk: int,
     * greedy rows never interact (attention, norms and the argmax are per row; constraints are
       per row), so the tokens themselves do not depend on the batch.
     The one generation runs until every row has emitted END or the largest budget is spent, so
-    every row has at least its g_c tokens."""
+    every row has at least its g_c tokens.
+
+    With ``grids`` (the task's rectangular grids) the prompts are built on the device
+    (``mdl_build_prompts``); otherwise from the variants' host tokens.  Every prompt ends with
+    IO_SEP, so a row's grid is decoded from its generated tokens alone."""
     cfg = model.config
     n = len(variants)
-    lens = [len(v.tokens) for v in variants]
+    if grids is not None:
+        ids, pos, mask, lens = _device_prompts(grids, variants, num_color_perms, device)
+    else:
+        lens = [len(v.tokens) for v in variants]
+        ids, pos, mask = left_pad_batch([v.tokens for v in variants], device)
     widths = [max(lens[c0:c0 + chunk]) for c0 in range(0, n, chunk)]
     budgets = [min(w + max_output_tokens, cfg.max_seq_len) - w for w in widths]
-    ids, pos, mask = left_pad_batch([v.tokens for v in variants], device)
     S = ids.shape[1]
     gen_max = max(budgets)
     gen = torch.empty(n, 0, dtype=torch.int64)
@@ -671,10 +730,10 @@ def _predict_fused(model: TinyTransformer, variants: list[_Variant], chunk: int,
         if g > 0 and bool((f >= 0).all()):
             g = min(g, int(f.max()) + 1)
         for i in rows:
-            seq = variants[i].tokens + gen[i, :max(g, 0)].tolist()
+            seq = [IO_SEP_TOKEN_ID] + gen[i, :max(g, 0)].tolist()   # the prompt's last token on
             seps = [j for j, t in enumerate(seq) if t == IO_SEP_TOKEN_ID]
-            grid = decode_output_grid(seq[seps[-1]:]) if seps else None
-            preds.append((grid, variants[i].dihedral, variants[i].perm))
+            preds.append((decode_output_grid(seq[seps[-1]:]), variants[i].dihedral,
+                          variants[i].perm))
     return preds
 
 

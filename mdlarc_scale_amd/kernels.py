@@ -370,6 +370,30 @@ def grid_step(token: torch.Tensor, gx: torch.Tensor, gy: torch.Tensor, in_out: t
         _stream()), "mdl_grid_step")
 
 
+def build_prompts(cells: torch.Tensor, grids: torch.Tensor, variants: torch.Tensor,
+                  perms: torch.Tensor, lengths: torch.Tensor, ids_out: torch.Tensor,
+                  pos_out: torch.Tensor, mask_out: torch.Tensor) -> None:
+    """Augmented prompts of one task into the left-padded batch (mdl_build_prompts): cells uint8
+    (all grids row-major), grids int32 [n, 3] (offset, h, w), variants int32 [B, 2] (dihedral,
+    perm row), perms int32 [P, 10], lengths int32 [B]; ids int64 / pos int64 [B, S, 3] / mask
+    uint8 [B, S]."""
+    batch, seq = ids_out.shape
+    _need(cells, "cells", U8)
+    _need(grids, "grids", I32)
+    _need(variants, "variants", I32, batch * 2)
+    _need(perms, "perms", I32)
+    _need(lengths, "lengths", I32, batch)
+    _need(ids_out, "ids_out", I64, batch * seq)
+    _need(pos_out, "pos_out", I64, batch * seq * 3)
+    _need(mask_out, "mask_out", U8, batch * seq)
+    if grids.dim() != 2 or grids.shape[1] != 3 or perms.dim() != 2 or perms.shape[1] != 10:
+        raise ValueError("grids must be [n, 3] and perms [P, 10]")
+    _lib.check(_lib.lib().mdl_build_prompts(
+        _p(cells), cells.numel(), _p(grids), grids.shape[0], _p(variants), batch, _p(perms),
+        perms.shape[0], _p(lengths), seq, _p(ids_out), _p(pos_out), _p(mask_out), _stream()),
+        "mdl_build_prompts")
+
+
 def decode_commit(token: torch.Tensor, out_ids: torch.Tensor, col: int,
                   counters: torch.Tensor | None, finish_step: torch.Tensor | None,
                   gen_base: int, end_id: int) -> None:

@@ -668,6 +668,38 @@ def test_head_constraints_equal_host_restatement():
         assert bool(cond.any())                              # every branch is exercised
 
 
+def test_build_prompts_equals_host_tokeniser():
+    """mdl_build_prompts (dihedral transform, colour permutation, tokens, 3D positions, left
+    padding on the device) equals the host path -- the data-format functions pinned by the
+    reference's own known-answer tests -- exactly, on random tasks: 0-3 demonstration pairs,
+    grids from 1x1 to 30x30, all 8 transforms x 3 colour permutations."""
+    from mdlarc_scale_amd import inference as inf
+
+    rng = np.random.default_rng(21)
+
+    def grid(h=None, w=None):
+        h = int(rng.integers(1, 31)) if h is None else h
+        w = int(rng.integers(1, 31)) if w is None else w
+        g = rng.integers(1, 10, size=(h, w))
+        g[rng.random((h, w)) < 0.5] = 0
+        return g.tolist()
+
+    for trial in range(7):
+        n_pairs = trial % 4
+        pairs = [{"input": grid(), "output": grid()} for _ in range(n_pairs)]
+        test_in = grid(1, 1) if trial == 5 else (grid(30, 30) if trial == 6 else grid())
+        task = {"train": pairs, "test": [{"input": test_in}]}
+        variants = inf._build_variants(task, 0, True, 3, 1, False, None, None)
+        ids_h, pos_h, mask_h = inf.left_pad_batch([v.tokens for v in variants], DEV)
+        grids = inf._task_grids(task, 0, True)
+        ids_d, pos_d, mask_d, lens = inf._device_prompts(grids, variants, 3, DEV)
+        torch.cuda.synchronize()
+        assert lens == [len(v.tokens) for v in variants]
+        assert torch.equal(ids_d.cpu(), ids_h.cpu()), f"trial {trial}: tokens"
+        assert torch.equal(pos_d.cpu(), pos_h.cpu()), f"trial {trial}: positions"
+        assert torch.equal(mask_d.cpu(), mask_h.cpu()), f"trial {trial}: mask"
+
+
 def test_decode_commit():
     B, cols = 6, 10
     out = torch.full((B, cols), -7, dtype=torch.int64, device=DEV)
