@@ -299,15 +299,18 @@ def test_fused_augmentations_equal_chunk_loop(fixture, batched, chunk, constrain
         assert gf == gl
 
 
-def test_config2_slice_decode_vs_oracle():
-    """The parity harness's 8-row slice of BASELINE config 2: the small model under the
-    reference's initialisation (torch.manual_seed(0)), weights rounded to bf16 once and shared
-    with the fp32 oracle, on 8 prompts of the config-2 workload spanning its lengths (436-1,763
-    tokens, left-padded to 1,763, 2,048-slot cache).  The decode path itself is teacher-forced
-    through the oracle's tokens -- grid step, fused K2 + decode attention over the static cache,
-    head -- and every step's logits must lie within 2e-2 max-abs of the oracle's (the prefill's
-    lengths-1 logits included); the free-running greedy tokens of generate_output (HIP graph)
-    must agree on >= 99.5% of positions, any divergence a near-tie."""
+@pytest.mark.parametrize("spec_name,rows,max_new", [("small_b256", 8, 24), ("medium_b128", 2, 8),
+                                                    ("large_b64", 1, 6)])
+def test_config_slice_decode_vs_oracle(spec_name, rows, max_new):
+    """Slices of BASELINE configs 2-4 at their real shapes (the parity harness's config-2 slice is
+    8 rows; configs 3 and 4 take 2 and 1 rows so that the fp32 CPU oracle finishes in seconds):
+    the preset under the reference's initialisation (torch.manual_seed(0)), weights rounded to
+    bf16 once and shared with the oracle, prompts of the config's workload spanning its lengths,
+    left-padded, the config's cache size.  The decode path itself is teacher-forced through the
+    oracle's tokens -- grid step, fused K2 + decode attention over the static cache, head -- and
+    every step's logits must lie within 2e-2 max-abs of the oracle's (the prefill's lengths-1
+    logits included); the free-running greedy tokens of generate_output (HIP graph) must agree
+    on >= 99.5% of positions, any divergence a near-tie."""
     from mdlarc_scale_amd import create_model, generate_output
     from mdlarc_scale_amd import kernels as Kn
     from mdlarc_scale_amd.engine import engine_for
@@ -315,13 +318,14 @@ def test_config2_slice_decode_vs_oracle():
     from mdlarc_scale_amd.transformer import MODEL_SIZES
     from mdlarc_scale_amd.workload import SPECS, build_prompts, left_pad
 
-    prompts = build_prompts(SPECS["small_b256"])
+    spec = SPECS[spec_name]
+    prompts = build_prompts(spec)
     order = sorted(range(len(prompts)), key=lambda i: len(prompts[i]))
-    sl = [prompts[order[round(k * (len(order) - 1) / 7)]] for k in range(8)]
+    sl = [prompts[order[round(k * (len(order) - 1) / max(rows - 1, 1))]] for k in range(rows)]
     ids, pos, mask = left_pad(sl)
     B, S = ids.shape
     torch.manual_seed(0)
-    m = create_model(**MODEL_SIZES["small"], dropout=0.0, max_seq_len=SPECS["small_b256"].cache_slots)
+    m = create_model(**MODEL_SIZES[spec.preset], dropout=0.0, max_seq_len=spec.cache_slots)
     with torch.no_grad():
         for p in m.parameters():
             p.copy_(p.to(torch.bfloat16).float())
@@ -331,7 +335,6 @@ def test_config2_slice_decode_vs_oracle():
     om = rp.OracleModel(rp.OracleConfig(c.d_model, c.n_heads, c.n_layers, c.d_ff, c.num_examples,
                                         c.max_seq_len), state)
     ex = torch.arange(B) * 3
-    max_new = 24
     tr = rp.generate_output(om, ids, pos, ex, mask, max_new)
     g = len(tr.step_logits)
     ref = torch.stack(tr.step_logits, 1)
@@ -359,7 +362,7 @@ def test_config2_slice_decode_vs_oracle():
                               max_new_tokens=max_new).cpu()
     n = min(out.shape[1], tr.tokens.shape[1])
     agree = (out[:, S:n] == tr.tokens[:, S:n]).float().mean().item()
-    print(f"config-2 slice (prompts {[len(p) for p in sl]}): teacher-forced decode logits "
+    print(f"{spec_name} slice (prompts {[len(p) for p in sl]}): teacher-forced decode logits "
           f"max-abs {err:.3e} over {g} steps, free-running agreement {agree:.4f}")
     assert err <= 2e-2
     _near_tie_ok(ref, got.argmax(-1), ref.argmax(-1), err)
