@@ -43,21 +43,31 @@ __device__ __forceinline__ float constrain(float v, int slot, int r, const HeadC
   return v;
 }
 
-// One wavefront per output row.  The lane keeps NC 4-channel chunks of x * gamma in registers,
-// reduces the sum of squares, accumulates its partial dot product with every vocab row, then
-// reduces all NV partials at once with a reduce-scatter butterfly: at level k (xor 32 >> k) a
-// lane keeps one half of its values and adds the partner's copy of that half, so log2(NV)
-// levels of NV/2, NV/4, ... exchanges plus 6 - log2(NV) plain levels (NV - 1 + 6 - log2(NV)
-// shuffles in all, instead of NV full wave reductions) leave lane l holding the logit of vocab
-// slot l >> (6 - log2(NV)).  The argmax is then one (value, index) wave reduction that keeps the
-// first index on ties (torch argmax).
+// One 256-thread block per output row; wave w owns vocab slots KW*w .. KW*w + KW-1 (KW = NV/4),
+// so a launch of B rows fills B blocks across the chip and each lane carries KW rows' worth of
+// weight loads (all in flight at once) rather than NV.  Every wave holds the row's NC 4-channel
+// chunks of x * gamma and its sum of squares; the lane's partial dot products with the wave's
+// KW vocab rows are reduced with a reduce-scatter butterfly (log2(KW) halving levels, then
+// 6 - log2(KW) plain levels) that leaves the logit of slot KW*w + (lane >> (6 - log2 KW)) in
+// every lane.  The logits, after the constraints, meet in LDS; wave 0 takes the argmax with the
+// first index winning ties (torch argmax) and commits the token.
+// Weight slots t >= vocab re-read the last vocab row (an L1 hit) instead of branching around
+// their loads, which would serialise them; those slots never reach the logits or the argmax.
 template <int NC, int NV>
-__device__ __forceinline__ void head_row(const float* __restrict__ xr, int lane, int d,
-                                         const float* __restrict__ gamma, float eps,
-                                         const float* __restrict__ w, int vocab, int r,
-                                         const HeadCons& cons, float& logit, int& slot,
-                                         int& best) {
-  constexpr int LOG_NV = NV == 16 ? 4 : 5;
+__global__ __launch_bounds__(256) void head_kernel(
+    const float* __restrict__ x, const int32_t* __restrict__ row_index, int rows, int d,
+    const float* __restrict__ gamma, float eps, const float* __restrict__ w, int vocab,
+    float* __restrict__ logits, int64_t* __restrict__ token, int64_t* __restrict__ out_ids,
+    int64_t ld, int col, const int32_t* __restrict__ counters, int32_t* __restrict__ finish,
+    int gen_base, int64_t end_id, HeadCons cons) {
+  constexpr int KW = NV / 4;                       // vocab slots per wave
+  constexpr int LOG_KW = KW == 4 ? 2 : 3;
+  __shared__ float lg[NV];
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int r = blockIdx.x;
+  if (r >= rows) return;
+  const int64_t m = row_index ? row_index[r] : r;
+  const float* xr = x + m * d;
   float v[NC][4];
   float ss = 0.f;
 #pragma unroll
@@ -72,33 +82,30 @@ __device__ __forceinline__ void head_row(const float* __restrict__ xr, int lane,
       v[i][0] = v[i][1] = v[i][2] = v[i][3] = 0.f;
     }
   }
-  // Slots t >= vocab re-read the last vocab row (an L1 hit) instead of branching around their
-  // loads: with the loads unconditional all NV x NC of them are in flight at once, where a
-  // per-row branch serialises them into NV dependent memory round trips.  Those slots never
-  // reach the logits or the argmax.
-  float acc[NV];
+  float acc[KW];
 #pragma unroll
-  for (int t = 0; t < NV; ++t) {
-    acc[t] = 0.f;
+  for (int k = 0; k < KW; ++k) {
+    const int t = KW * wave + k;
     const float* wr = w + static_cast<int64_t>(t < vocab ? t : vocab - 1) * d;
+    acc[k] = 0.f;
 #pragma unroll
     for (int i = 0; i < NC; ++i) {
       const int e = 4 * (lane + 64 * i);
       if (i < NC - 1 || e < d) {
         const float4 wv = *reinterpret_cast<const float4*>(wr + e);
-        acc[t] += v[i][0] * wv.x + v[i][1] * wv.y + v[i][2] * wv.z + v[i][3] * wv.w;
+        acc[k] += v[i][0] * wv.x + v[i][1] * wv.y + v[i][2] * wv.z + v[i][3] * wv.w;
       }
     }
   }
   ss = wave_sum(ss);
   const float rs = rsqrtf(ss / static_cast<float>(d) + eps);
 #pragma unroll
-  for (int lvl = 0; lvl < LOG_NV; ++lvl) {
-    const int half = NV >> (lvl + 1);
+  for (int lvl = 0; lvl < LOG_KW; ++lvl) {
+    const int half = KW >> (lvl + 1);
     const int mask = 32 >> lvl;
     const bool up = (lane & mask) != 0;
 #pragma unroll
-    for (int k = 0; k < NV / 2; ++k) {
+    for (int k = 0; k < KW / 2; ++k) {
       if (k < half) {
         const float keep = up ? acc[half + k] : acc[k];
         const float send = up ? acc[k] : acc[half + k];
@@ -108,14 +115,22 @@ __device__ __forceinline__ void head_row(const float* __restrict__ xr, int lane,
   }
   float tot = acc[0];
 #pragma unroll
-  for (int mask = 32 >> LOG_NV; mask > 0; mask >>= 1) tot += __shfl_xor(tot, mask, kWave);
-  slot = lane >> (6 - LOG_NV);
-  logit = tot * rs;
-  if (slot < vocab) logit = constrain(logit, slot, r, cons);
-  float bv = slot < vocab ? logit : -INFINITY;
-  int bi = slot;
+  for (int mask = 32 >> LOG_KW; mask > 0; mask >>= 1) tot += __shfl_xor(tot, mask, kWave);
+  const int slot = KW * wave + (lane >> (6 - LOG_KW));
+  if ((lane & ((64 >> LOG_KW) - 1)) == 0) {
+    float logit = tot * rs;
+    if (slot < vocab) {
+      logit = constrain(logit, slot, r, cons);
+      if (logits) logits[static_cast<int64_t>(r) * vocab + slot] = logit;
+    }
+    lg[slot] = slot < vocab ? logit : -INFINITY;
+  }
+  __syncthreads();
+  if (wave != 0) return;
+  float bv = lane < NV ? lg[lane] : -INFINITY;
+  int bi = lane;
 #pragma unroll
-  for (int mask = 32; mask > 0; mask >>= 1) {
+  for (int mask = NV / 2; mask > 0; mask >>= 1) {
     const float ov = __shfl_xor(bv, mask, kWave);
     const int oi = __shfl_xor(bi, mask, kWave);
     if (ov > bv || (ov == bv && oi < bi)) {
@@ -123,36 +138,13 @@ __device__ __forceinline__ void head_row(const float* __restrict__ xr, int lane,
       bi = oi;
     }
   }
-  best = bi;
-}
-
-// Logits (optional) and argmax of rows r: x row = row_index ? row_index[r] : r.  With out_ids
-// the kernel also commits the token (the decode-step tail): out_ids[r, c] = token,
-// c = counters ? counters[1] : col, and records the first END per row in finish.
-template <int NC, int NV>
-__global__ __launch_bounds__(256) void head_kernel(
-    const float* __restrict__ x, const int32_t* __restrict__ row_index, int rows, int d,
-    const float* __restrict__ gamma, float eps, const float* __restrict__ w, int vocab,
-    float* __restrict__ logits, int64_t* __restrict__ token, int64_t* __restrict__ out_ids,
-    int64_t ld, int col, const int32_t* __restrict__ counters, int32_t* __restrict__ finish,
-    int gen_base, int64_t end_id, HeadCons cons) {
-  const int lane = threadIdx.x & 63;
-  const int r = blockIdx.x * 4 + (threadIdx.x >> 6);
-  if (r >= rows) return;
-  const int64_t m = row_index ? row_index[r] : r;
-  float logit;
-  int slot, best;
-  head_row<NC, NV>(x + m * d, lane, d, gamma, eps, w, vocab, r, cons, logit, slot, best);
-  constexpr int kGroup = NV == 16 ? 4 : 2;          // lanes holding the same vocab slot
-  if (logits && (lane & (kGroup - 1)) == 0 && slot < vocab)
-    logits[static_cast<int64_t>(r) * vocab + slot] = logit;
   if (lane != 0) return;
-  if (token) token[r] = best;
+  if (token) token[r] = bi;
   if (out_ids) {
     const int c = counters ? counters[1] : col;
     if (c < 0 || c >= ld) return;   // more steps than output columns: never write outside
-    out_ids[static_cast<int64_t>(r) * ld + c] = best;
-    if (finish && best == end_id && finish[r] < 0) finish[r] = c - gen_base;
+    out_ids[static_cast<int64_t>(r) * ld + c] = bi;
+    if (finish && bi == end_id && finish[r] < 0) finish[r] = c - gen_base;
   }
 }
 
@@ -274,7 +266,7 @@ int launch_head(const float* x, const int32_t* row_index, int rows, int d, const
     cons = HeadCons{c->disallow_mask, c->palette_mask, c->palette_penalty, c->target_shape,
                     c->grid_x, c->grid_y, c->shape_penalty};
   }
-  const dim3 grid((rows + 3) / 4);
+  const dim3 grid(rows);
   const int nv = vocab <= 16 ? 16 : 32;
 #define MDL_HEAD(N)                                                                            \
   case N:                                                                                      \
