@@ -135,6 +135,22 @@ int mdl_qkv_rope_cache(const float* qkv, int64_t qkv_ld, const float* rstd,
                        void* stream);
 
 /*
+ * K2 over a packed token list (the prompt tokens of every row without their left padding).
+ * Replaces: the same reference ops as mdl_qkv_rope_cache over the rows of a left-padded batch,
+ *           for the tokens at or after each row's first valid position (src/inference.py:395-407;
+ *           the padding's K/V are never visible to a later query).
+ * qkv / rstd / pos / q_out hold n_tokens rows.  Token m belongs to batch row token_row[m] and
+ * writes its k / v into cache slot token_slot[m] of that row (nothing when token_slot[m] < 0,
+ * or outside [0, cache_slots) or a token_row outside [0, batch)).
+ */
+int mdl_qkv_rope_cache_packed(const float* qkv, int64_t qkv_ld, const float* rstd,
+                              const int64_t* pos, const float* rope_tab, int64_t n_tokens,
+                              const int32_t* token_row, const int32_t* token_slot, int batch,
+                              int n_heads, int head_dim, int max_x, int max_y, int max_z, int px,
+                              int py, int pz, float q_scale, uint16_t* q_out, uint16_t* k_cache,
+                              uint16_t* v_cache, int cache_slots, void* stream);
+
+/*
  * K3 -- SwiGLU gate: silu(gate) * up, with the RMSNorm multiply of ln2 and the fc biases.
  * Replaces: FeedForward.forward's silu(fc_gate(x)) * fc_up(x) (src/transformer.py:441-449).
  * gate_up: fp32 [rows, 2*d_ff] (row stride ld) = (x*gamma2) @ [W_gate; W_up]^T.
@@ -161,6 +177,20 @@ int mdl_attn_prefill(const uint16_t* q, const uint16_t* k_cache, const uint16_t*
                      int batch, int seq, int n_heads, int head_dim, int cache_slots,
                      const uint8_t* key_mask, const int32_t* kv_start, int causal,
                      uint16_t* out, void* stream);
+
+/*
+ * K4a over packed query rows: as mdl_attn_prefill, for the queries i >= kv_start[b] of each row
+ * only.  Query i of row b is row q_offset[b] + i - kv_start[b] of q (bf16 [rows, n_heads, 64])
+ * and of out (split bf16 [rows, 2*n_heads*64]); no other row of out is written.  Keys are the
+ * cache slots as in mdl_attn_prefill; slots before kv_start[b] are never read into a product.
+ * kv_start and q_offset are required; the caller sizes q / out to cover every row it names.
+ * Replaces: the same SDPA call as mdl_attn_prefill (src/inference.py:409), without the padding
+ *           queries: each sees no key, so its output is 0, which the caller supplies if needed.
+ */
+int mdl_attn_prefill_packed(const uint16_t* q, const uint16_t* k_cache, const uint16_t* v_cache,
+                            int batch, int seq, int n_heads, int head_dim, int cache_slots,
+                            const uint8_t* key_mask, const int32_t* kv_start,
+                            const int32_t* q_offset, int causal, uint16_t* out, void* stream);
 
 /*
  * K4b -- decode attention over the static cache (split-K flash decoding).

@@ -42,8 +42,13 @@ SIGNATURES: dict[str, tuple[object, list]] = {
     "mdl_qkv_rope_cache": (c_int, [P, c_int64, P, P, P, c_int, c_int, c_int, c_int, c_int, c_int,
                                    c_int, c_int, c_int, c_int, c_float, P, P, P, c_int, c_int, P,
                                    P]),
+    "mdl_qkv_rope_cache_packed": (c_int, [P, c_int64, P, P, P, c_int64, P, P, c_int, c_int, c_int,
+                                          c_int, c_int, c_int, c_int, c_int, c_int, c_float, P, P,
+                                          P, c_int, P]),
     "mdl_swiglu": (c_int, [P, c_int64, P, P, P, c_int, c_int, P, P]),
     "mdl_attn_prefill": (c_int, [P, P, P, c_int, c_int, c_int, c_int, c_int, P, P, c_int, P, P]),
+    "mdl_attn_prefill_packed": (c_int, [P, P, P, c_int, c_int, c_int, c_int, c_int, P, P, P,
+                                        c_int, P, P]),
     "mdl_attn_decode_workspace_bytes": (c_int64, [c_int, c_int, c_int, c_int]),
     "mdl_attn_decode": (c_int, [P, P, P, c_int, c_int, c_int, c_int, P, c_int, P, P, P, c_int,
                                 P, P, c_int64, c_int, P, P]),

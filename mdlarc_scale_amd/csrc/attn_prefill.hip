@@ -69,8 +69,8 @@ __device__ __forceinline__ float max_over_groups(float v) {
 __global__ __launch_bounds__(256, 3) void attn_prefill_kernel(
     const uint16_t* __restrict__ q, const uint16_t* __restrict__ kc,
     const uint16_t* __restrict__ vc, int S, int H, int slots, const uint8_t* __restrict__ kmask,
-    const int32_t* __restrict__ kv_start, int causal, uint16_t* __restrict__ out, int nqt,
-    int n_bh) {
+    const int32_t* __restrict__ kv_start, const int32_t* __restrict__ q_offset, int causal,
+    uint16_t* __restrict__ out, int nqt, int n_bh) {
   const int slot = blockIdx.x / kXcds;
   const int kq = slot / nqt;
   const int bh = blockIdx.x % kXcds + kXcds * kq;
@@ -80,6 +80,13 @@ __global__ __launch_bounds__(256, 3) void attn_prefill_kernel(
   const int tid = threadIdx.x;
   const int wave = tid >> 6, lane = tid & 63, c16 = lane & 15, g = lane >> 4;
   const int q0 = qt * kBM;
+  const int kstart = kv_start ? min(max(kv_start[b], 0), S) : 0;
+  // packed rows: query qi >= kstart of row b is row q_offset[b] + qi - kstart of q and out;
+  // queries before kstart are not part of the packed list and are neither read nor written
+  const int qlo = q_offset ? kstart : 0;
+  if (q0 + kBM <= qlo) return;                  // the whole query tile is before the row start
+  const int64_t qbase = q_offset ? static_cast<int64_t>(q_offset[b]) - kstart
+                                 : static_cast<int64_t>(b) * S;
 
   __shared__ __attribute__((aligned(16))) uint16_t Ks[kBN * kLds];
   __shared__ __attribute__((aligned(16))) uint16_t Vs[kBN * kLds];
@@ -91,8 +98,8 @@ __global__ __launch_bounds__(256, 3) void attn_prefill_kernel(
 #pragma unroll
   for (int j = 0; j < 2; ++j) {
     qi[j] = wq0 + 16 * j + c16;
-    if (qi[j] < S) {
-      const uint16_t* qp = q + ((static_cast<int64_t>(b) * S + qi[j]) * H + h) * kHeadDim;
+    if (qi[j] < S && qi[j] >= qlo) {
+      const uint16_t* qp = q + ((qbase + qi[j]) * H + h) * kHeadDim;
       qf[j][0] = as_bf16x8(*reinterpret_cast<const uint4*>(qp + 8 * g));
       qf[j][1] = as_bf16x8(*reinterpret_cast<const uint4*>(qp + 32 + 8 * g));
     } else {
@@ -104,7 +111,6 @@ __global__ __launch_bounds__(256, 3) void attn_prefill_kernel(
   const int64_t head_off = (static_cast<int64_t>(b) * H + h) * slots * kHeadDim;
   const uint16_t* Kg = kc + head_off;
   const uint16_t* Vg = vc + head_off;
-  const int kstart = kv_start ? min(max(kv_start[b], 0), S) : 0;
   const int kt0 = (kstart / kBN) * kBN;
   const int kend = causal ? min(S, q0 + kBM) : S;
   const uint8_t* mrow = kmask ? kmask + static_cast<int64_t>(b) * S : nullptr;
@@ -129,7 +135,7 @@ __global__ __launch_bounds__(256, 3) void attn_prefill_kernel(
       const int kj = kt + key;
       pk[rep] = make_uint4(0, 0, 0, 0);
       pv[rep] = pk[rep];
-      if (kj < S) {
+      if (kj < S && kj >= kstart) {    // slots before kstart may hold stale values
         pk[rep] = *reinterpret_cast<const uint4*>(Kg + static_cast<int64_t>(kj) * kHeadDim + d0);
         pv[rep] = *reinterpret_cast<const uint4*>(Vg + static_cast<int64_t>(kj) * kHeadDim + d0);
       }
@@ -243,10 +249,10 @@ __global__ __launch_bounds__(256, 3) void attn_prefill_kernel(
   const int64_t d = static_cast<int64_t>(H) * kHeadDim;
 #pragma unroll
   for (int j = 0; j < 2; ++j) {
-    if (qi[j] >= S) continue;
+    if (qi[j] >= S || qi[j] < qlo) continue;
     const float l = lsum[j][0];     // every row of the ones product holds the query's sum
     const float inv = l > 0.f ? 1.f / l : 0.f;
-    uint16_t* op = out + (static_cast<int64_t>(b) * S + qi[j]) * 2 * d + h * kHeadDim;
+    uint16_t* op = out + (qbase + qi[j]) * 2 * d + h * kHeadDim;
 #pragma unroll
     for (int db = 0; db < 4; ++db) {
       const float t[4] = {o[j][db][0] * inv, o[j][db][1] * inv, o[j][db][2] * inv,
@@ -265,11 +271,12 @@ __global__ __launch_bounds__(256, 3) void attn_prefill_kernel(
 
 using namespace mdl;
 
-extern "C" int mdl_attn_prefill(const uint16_t* q, const uint16_t* k_cache,
-                                const uint16_t* v_cache, int batch, int seq, int n_heads,
-                                int head_dim, int cache_slots, const uint8_t* key_mask,
-                                const int32_t* kv_start, int causal, uint16_t* out,
-                                void* stream) {
+namespace mdl {
+
+int launch_prefill(const uint16_t* q, const uint16_t* k_cache, const uint16_t* v_cache,
+                   int batch, int seq, int n_heads, int head_dim, int cache_slots,
+                   const uint8_t* key_mask, const int32_t* kv_start, const int32_t* q_offset,
+                   int causal, uint16_t* out, hipStream_t st) {
   if (!q || !k_cache || !v_cache || !out) return MDL_ERR_NULL;
   if (head_dim != kHeadDim) return MDL_ERR_HEAD_DIM;
   if (batch < 0 || seq < 0 || n_heads <= 0 || n_heads > 65535 || batch > 65535)
@@ -282,9 +289,31 @@ extern "C" int mdl_attn_prefill(const uint16_t* q, const uint16_t* k_cache,
   const int64_t nqt = (seq + kBM - 1) / kBM;
   const int64_t blocks = (heads + kXcds - 1) / kXcds * kXcds * nqt;
   if (blocks > 0x7fffffff) return MDL_ERR_SHAPE;
-  attn_prefill_kernel<<<static_cast<unsigned>(blocks), 256, 0,
-                        static_cast<hipStream_t>(stream)>>>(
-      q, k_cache, v_cache, seq, n_heads, cache_slots, key_mask, kv_start, causal ? 1 : 0, out,
-      static_cast<int>(nqt), static_cast<int>(heads));
+  attn_prefill_kernel<<<static_cast<unsigned>(blocks), 256, 0, st>>>(
+      q, k_cache, v_cache, seq, n_heads, cache_slots, key_mask, kv_start, q_offset,
+      causal ? 1 : 0, out, static_cast<int>(nqt), static_cast<int>(heads));
   return launch_status();
+}
+
+}  // namespace mdl
+
+extern "C" int mdl_attn_prefill(const uint16_t* q, const uint16_t* k_cache,
+                                const uint16_t* v_cache, int batch, int seq, int n_heads,
+                                int head_dim, int cache_slots, const uint8_t* key_mask,
+                                const int32_t* kv_start, int causal, uint16_t* out,
+                                void* stream) {
+  return launch_prefill(q, k_cache, v_cache, batch, seq, n_heads, head_dim, cache_slots,
+                        key_mask, kv_start, nullptr, causal, out,
+                        static_cast<hipStream_t>(stream));
+}
+
+extern "C" int mdl_attn_prefill_packed(const uint16_t* q, const uint16_t* k_cache,
+                                       const uint16_t* v_cache, int batch, int seq, int n_heads,
+                                       int head_dim, int cache_slots, const uint8_t* key_mask,
+                                       const int32_t* kv_start, const int32_t* q_offset,
+                                       int causal, uint16_t* out, void* stream) {
+  if (!kv_start || !q_offset) return MDL_ERR_NULL;
+  return launch_prefill(q, k_cache, v_cache, batch, seq, n_heads, head_dim, cache_slots,
+                        key_mask, kv_start, q_offset, causal, out,
+                        static_cast<hipStream_t>(stream));
 }

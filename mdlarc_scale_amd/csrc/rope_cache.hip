@@ -14,12 +14,30 @@
 
 namespace mdl {
 
+// Cache row (batch row b) and slot of token m: token m of a [batch, seq] prompt goes to slot
+// (slot_dev ? *slot_dev : slot0) + m % seq of row m / seq; a packed token list names both per
+// token (tok_row / tok_slot; a negative slot writes nothing).
+__device__ __forceinline__ void token_slot(int64_t m, int seq, int slot0,
+                                           const int32_t* __restrict__ slot_dev,
+                                           const int32_t* __restrict__ tok_row,
+                                           const int32_t* __restrict__ tok_slot, int64_t& b,
+                                           int& slot) {
+  if (tok_slot) {
+    b = tok_row[m];
+    slot = tok_slot[m];
+  } else {
+    b = m / seq;
+    slot = (slot_dev ? *slot_dev : slot0) + static_cast<int>(m - b * seq);
+  }
+}
+
 __global__ __launch_bounds__(256) void qkv_rope_cache_kernel(
     const float* __restrict__ qkv, int64_t ld, const float* __restrict__ rstd,
     const int64_t* __restrict__ pos, const float* __restrict__ tab, RopeArgs ra, int64_t rows,
     int seq, int n_heads, float q_scale, uint16_t* __restrict__ q_out,
     uint16_t* __restrict__ kc, uint16_t* __restrict__ vc, int slots, int slot0,
-    const int32_t* __restrict__ slot_dev) {
+    const int32_t* __restrict__ slot_dev, const int32_t* __restrict__ tok_row,
+    const int32_t* __restrict__ tok_slot, int64_t batch) {
   const int lane = threadIdx.x & 63;
   const int64_t m = static_cast<int64_t>(blockIdx.x) * 4 + (threadIdx.x >> 6);
   if (m >= rows) return;
@@ -31,9 +49,11 @@ __global__ __launch_bounds__(256) void qkv_rope_cache_kernel(
   const float r = rstd ? rstd[m] : 1.f;
 
   const float* row = qkv + m * ld;
-  const int64_t b = m / seq;
-  const int slot = (slot_dev ? *slot_dev : slot0) + static_cast<int>(m - b * seq);
-  const bool in_cache = slot >= 0 && slot < slots;   // host guarantees range; never write outside
+  int64_t b;
+  int slot;
+  token_slot(m, seq, slot0, slot_dev, tok_row, tok_slot, b, slot);
+  // host guarantees the range; never write outside
+  const bool in_cache = slot >= 0 && slot < slots && b >= 0 && b < batch;
   uint16_t* qrow = q_out + m * d;
   const int64_t head_stride = static_cast<int64_t>(slots) * kHeadDim;
   const int64_t cache_row = (b * n_heads * static_cast<int64_t>(slots) + slot) * kHeadDim;
@@ -71,7 +91,8 @@ __global__ __launch_bounds__(256) void qkv_rope_cache_vec_kernel(
     const float* __restrict__ qkv, int64_t ld, const float* __restrict__ rstd,
     const int64_t* __restrict__ pos, const float* __restrict__ tab, RopeArgs ra, int64_t rows,
     int seq, float q_scale, uint16_t* __restrict__ q_out, uint16_t* __restrict__ kc,
-    uint16_t* __restrict__ vc, int slots, int slot0, const int32_t* __restrict__ slot_dev) {
+    uint16_t* __restrict__ vc, int slots, int slot0, const int32_t* __restrict__ slot_dev,
+    const int32_t* __restrict__ tok_row, const int32_t* __restrict__ tok_slot, int64_t batch) {
   constexpr int kH = 4 * NCH / 3, kD = kH * kHeadDim, kPart = NCH / 3;
   const int lane = threadIdx.x & 63;
   const int64_t m = static_cast<int64_t>(blockIdx.x) * 4 + (threadIdx.x >> 6);
@@ -86,9 +107,11 @@ __global__ __launch_bounds__(256) void qkv_rope_cache_vec_kernel(
   rope_cos_sin(2 * (lane & 15), pos + m * 3, tab, ra, cs0, sn0);
   rope_cos_sin(2 * (lane & 15) + 1, pos + m * 3, tab, ra, cs1, sn1);
   const float r = rstd ? rstd[m] : 1.f;
-  const int64_t b = m / seq;
-  const int slot = (slot_dev ? *slot_dev : slot0) + static_cast<int>(m - b * seq);
-  const bool in_cache = slot >= 0 && slot < slots;   // host guarantees range; never write outside
+  int64_t b;
+  int slot;
+  token_slot(m, seq, slot0, slot_dev, tok_row, tok_slot, b, slot);
+  // host guarantees the range; never write outside
+  const bool in_cache = slot >= 0 && slot < slots && b >= 0 && b < batch;
   const int64_t head_stride = static_cast<int64_t>(slots) * kHeadDim;
   const int64_t cache_row = (b * kH * static_cast<int64_t>(slots) + slot) * kHeadDim;
 
@@ -122,37 +145,25 @@ __global__ __launch_bounds__(256) void qkv_rope_cache_vec_kernel(
 
 using namespace mdl;
 
-extern "C" int mdl_qkv_rope_cache(const float* qkv, int64_t qkv_ld, const float* rstd,
-                                  const int64_t* pos, const float* rope_tab, int batch, int seq,
-                                  int n_heads, int head_dim, int max_x, int max_y, int max_z,
-                                  int px, int py, int pz, float q_scale, uint16_t* q_out,
-                                  uint16_t* k_cache, uint16_t* v_cache, int cache_slots,
-                                  int slot0, const int32_t* slot_dev, void* stream) {
-  if (!qkv || !pos || !rope_tab || !q_out || !k_cache || !v_cache) return MDL_ERR_NULL;
-  if (head_dim != kHeadDim) return MDL_ERR_HEAD_DIM;
-  if (batch < 0 || seq <= 0 || n_heads <= 0 || max_x <= 0 || max_y <= 0 || max_z <= 0 ||
-      px < 0 || py < 0 || pz < 0 || px + py + pz != kHeadDim / 2 || qkv_ld < 3 * n_heads * 64)
-    return MDL_ERR_SHAPE;
-  if (cache_slots <= 0 || (!slot_dev && (slot0 < 0 || slot0 + seq > cache_slots)))
-    return MDL_ERR_CACHE;
-  if (!aligned16(qkv) || qkv_ld % 4 != 0 || !aligned16(q_out) || !aligned16(k_cache) ||
-      !aligned16(v_cache) || !aligned4(rope_tab))
-    return MDL_ERR_ALIGN;
-  const int64_t rows = static_cast<int64_t>(batch) * seq;
+namespace mdl {
+
+int launch_k2(const float* qkv, int64_t qkv_ld, const float* rstd, const int64_t* pos,
+              const float* rope_tab, int64_t rows, int seq, int n_heads, const RopeArgs& ra,
+              float q_scale, uint16_t* q_out, uint16_t* k_cache, uint16_t* v_cache,
+              int cache_slots, int slot0, const int32_t* slot_dev, const int32_t* tok_row,
+              const int32_t* tok_slot, int64_t batch, hipStream_t st) {
   if (rows == 0) return MDL_OK;
-  const RopeArgs ra{max_x, max_y, max_z, px, py, pz};
   const dim3 grid(static_cast<unsigned>((rows + 3) / 4));
-  const hipStream_t st = static_cast<hipStream_t>(stream);
   const bool nt = rows * n_heads * kHeadDim * 18 >= kStreamBytes;
 #define MDL_K2_VEC(NCH)                                                                        \
   if (nt)                                                                                     \
     qkv_rope_cache_vec_kernel<NCH, true><<<grid, 256, 0, st>>>(                               \
         qkv, qkv_ld, rstd, pos, rope_tab, ra, rows, seq, q_scale, q_out, k_cache, v_cache,    \
-        cache_slots, slot0, slot_dev);                                                        \
+        cache_slots, slot0, slot_dev, tok_row, tok_slot, batch);                              \
   else                                                                                        \
     qkv_rope_cache_vec_kernel<NCH, false><<<grid, 256, 0, st>>>(                              \
         qkv, qkv_ld, rstd, pos, rope_tab, ra, rows, seq, q_scale, q_out, k_cache, v_cache,    \
-        cache_slots, slot0, slot_dev)
+        cache_slots, slot0, slot_dev, tok_row, tok_slot, batch)
   switch (n_heads) {
     case 4: MDL_K2_VEC(3); break;
     case 12: MDL_K2_VEC(9); break;
@@ -161,8 +172,62 @@ extern "C" int mdl_qkv_rope_cache(const float* qkv, int64_t qkv_ld, const float*
     default:
       qkv_rope_cache_kernel<<<grid, 256, 0, st>>>(qkv, qkv_ld, rstd, pos, rope_tab, ra, rows,
                                                   seq, n_heads, q_scale, q_out, k_cache,
-                                                  v_cache, cache_slots, slot0, slot_dev);
+                                                  v_cache, cache_slots, slot0, slot_dev, tok_row,
+                                                  tok_slot, batch);
   }
 #undef MDL_K2_VEC
   return launch_status();
+}
+
+int check_k2(const float* qkv, int64_t qkv_ld, const int64_t* pos, const float* rope_tab,
+             int n_heads, int head_dim, int max_x, int max_y, int max_z, int px, int py, int pz,
+             const uint16_t* q_out, const uint16_t* k_cache, const uint16_t* v_cache) {
+  if (!qkv || !pos || !rope_tab || !q_out || !k_cache || !v_cache) return MDL_ERR_NULL;
+  if (head_dim != kHeadDim) return MDL_ERR_HEAD_DIM;
+  if (n_heads <= 0 || max_x <= 0 || max_y <= 0 || max_z <= 0 || px < 0 || py < 0 || pz < 0 ||
+      px + py + pz != kHeadDim / 2 || qkv_ld < 3 * n_heads * 64)
+    return MDL_ERR_SHAPE;
+  if (!aligned16(qkv) || qkv_ld % 4 != 0 || !aligned16(q_out) || !aligned16(k_cache) ||
+      !aligned16(v_cache) || !aligned4(rope_tab))
+    return MDL_ERR_ALIGN;
+  return MDL_OK;
+}
+
+}  // namespace mdl
+
+extern "C" int mdl_qkv_rope_cache(const float* qkv, int64_t qkv_ld, const float* rstd,
+                                  const int64_t* pos, const float* rope_tab, int batch, int seq,
+                                  int n_heads, int head_dim, int max_x, int max_y, int max_z,
+                                  int px, int py, int pz, float q_scale, uint16_t* q_out,
+                                  uint16_t* k_cache, uint16_t* v_cache, int cache_slots,
+                                  int slot0, const int32_t* slot_dev, void* stream) {
+  const int c = check_k2(qkv, qkv_ld, pos, rope_tab, n_heads, head_dim, max_x, max_y, max_z, px,
+                         py, pz, q_out, k_cache, v_cache);
+  if (c != MDL_OK) return c;
+  if (batch < 0 || seq <= 0) return MDL_ERR_SHAPE;
+  if (cache_slots <= 0 || (!slot_dev && (slot0 < 0 || slot0 + seq > cache_slots)))
+    return MDL_ERR_CACHE;
+  const RopeArgs ra{max_x, max_y, max_z, px, py, pz};
+  return launch_k2(qkv, qkv_ld, rstd, pos, rope_tab, static_cast<int64_t>(batch) * seq, seq,
+                   n_heads, ra, q_scale, q_out, k_cache, v_cache, cache_slots, slot0, slot_dev,
+                   nullptr, nullptr, batch, static_cast<hipStream_t>(stream));
+}
+
+extern "C" int mdl_qkv_rope_cache_packed(const float* qkv, int64_t qkv_ld, const float* rstd,
+                                         const int64_t* pos, const float* rope_tab,
+                                         int64_t n_tokens, const int32_t* token_row,
+                                         const int32_t* token_slot, int batch, int n_heads,
+                                         int head_dim, int max_x, int max_y, int max_z, int px,
+                                         int py, int pz, float q_scale, uint16_t* q_out,
+                                         uint16_t* k_cache, uint16_t* v_cache, int cache_slots,
+                                         void* stream) {
+  const int c = check_k2(qkv, qkv_ld, pos, rope_tab, n_heads, head_dim, max_x, max_y, max_z, px,
+                         py, pz, q_out, k_cache, v_cache);
+  if (c != MDL_OK) return c;
+  if (!token_row || !token_slot) return MDL_ERR_NULL;
+  if (n_tokens < 0 || batch < 0 || cache_slots <= 0) return MDL_ERR_SHAPE;
+  const RopeArgs ra{max_x, max_y, max_z, px, py, pz};
+  return launch_k2(qkv, qkv_ld, rstd, pos, rope_tab, n_tokens, 1, n_heads, ra, q_scale, q_out,
+                   k_cache, v_cache, cache_slots, 0, nullptr, token_row, token_slot, batch,
+                   static_cast<hipStream_t>(stream));
 }

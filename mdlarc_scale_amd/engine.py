@@ -30,6 +30,7 @@ from __future__ import annotations
 
 from dataclasses import dataclass
 
+import numpy as np
 import torch
 
 from . import kernels as K
@@ -100,6 +101,56 @@ class Scratch:
         return Scratch(x=e(rows, d, dt=f), xs=e(rows, 2 * d), rstd=e(rows, dt=f),
                        qkv=e(rows, 3 * d, dt=f), q=e(rows, d), attn=e(rows, 2 * d),
                        delta=e(rows, d, dt=f), gu=e(rows, 2 * d_ff, dt=f), h=e(rows, 2 * d_ff))
+
+
+@dataclass
+class PackedPrompt:
+    """The tokens of a left-padded [B, S] prompt batch with the padding left out.
+
+    Row b contributes its tokens j in [kv_start[b], S) (slots j of its cache row), in order, at
+    packed rows q_offset[b] .. q_offset[b] + S - kv_start[b] - 1; ``n_valid`` rows in all.  The
+    reference reads its logits at index lengths-1 of each left-padded row, which is a padding
+    token when a row is shorter than its padding: such a token is appended after the valid ones
+    (cache slot -1, never written).  A padding query sees no key, so its attention output is 0
+    and its hidden state depends on its own embedding only; the extra rows reproduce exactly
+    that.  ``head_row[b]`` is the packed row whose logits row b reports."""
+
+    gather: torch.Tensor       # int32 [T]: flat index b*S + j into the [B, S] inputs
+    token_row: torch.Tensor    # int32 [T]
+    token_slot: torch.Tensor   # int32 [T] (-1 on the extra rows)
+    q_offset: torch.Tensor     # int32 [B]
+    head_row: torch.Tensor     # int32 [B]
+    n_valid: int
+    n_tokens: int
+
+
+def pack_prompt(kv_start: np.ndarray, last_row: np.ndarray, batch: int, seq: int,
+                device: torch.device) -> PackedPrompt:
+    """PackedPrompt of a batch whose rows start at ``kv_start`` (first valid index) and report
+    logits at flat row ``last_row`` (b*S + index), both host int arrays of length ``batch``."""
+    if batch * seq >= 2 ** 31:
+        raise ValueError("packed prompts index [B, S] with int32; B*S must stay below 2^31")
+    kv = np.clip(np.asarray(kv_start, dtype=np.int64), 0, seq)
+    last = np.asarray(last_row, dtype=np.int64) - np.arange(batch, dtype=np.int64) * seq
+    if last.size and (last.min() < 0 or last.max() >= seq):
+        raise ValueError("last_row must lie inside its own row")
+    n = seq - kv
+    off = np.concatenate([[0], np.cumsum(n)[:-1]]).astype(np.int64)
+    n_valid = int(n.sum())
+    rows = np.repeat(np.arange(batch, dtype=np.int64), n)
+    slot = np.arange(n_valid, dtype=np.int64) - np.repeat(off, n) + np.repeat(kv, n)
+    inside = last >= kv
+    extra = np.nonzero(~inside)[0]
+    head = np.where(inside, off + last - kv, 0)
+    head[extra] = n_valid + np.arange(extra.size)
+    total = n_valid + extra.size
+    host = np.concatenate([rows * seq + slot, extra * seq + last[extra], rows, extra, slot,
+                           np.full(extra.size, -1), off, head]).astype(np.int32)
+    dev = torch.from_numpy(host).to(device)
+    t, b = total, batch
+    return PackedPrompt(gather=dev[0:t], token_row=dev[t:2 * t], token_slot=dev[2 * t:3 * t],
+                        q_offset=dev[3 * t:3 * t + b], head_row=dev[3 * t + b:3 * t + 2 * b],
+                        n_valid=n_valid, n_tokens=total)
 
 
 DECODE_MIN_BLOCKS = 2048   # 8 four-wave blocks per CU on 256 CUs
@@ -181,6 +232,35 @@ class HipEngine:
             K.qkv_rope_cache(sc.qkv, sc.rstd, pos, W.rope_tab, W.rope_geom, B, S, H, qs, sc.q,
                              kc, vc, slot0=0)
             K.attn_prefill(sc.q, kc, vc, B, S, H, key_mask, kv_start, causal, sc.attn)
+            self._mlp(W, li, sc)
+
+    def run_packed(self, W: PackedWeights, ids: torch.Tensor, pos: torch.Tensor,
+                   ex_ids: torch.Tensor | None, key_mask: torch.Tensor | None,
+                   kv_start: torch.Tensor, pk: PackedPrompt, kv_layers, sc: Scratch) -> None:
+        """``run_prompt`` (causal) over the packed tokens ``pk`` of the [B, S] batch ``ids`` /
+        ``pos``: every GEMM and elementwise kernel sees pk.n_tokens rows instead of B*S.  K/V of
+        the valid tokens go to their slots; leaves the final residual in ``sc.x`` (packed rows).
+        ``sc`` must hold pk.n_tokens rows."""
+        cfg = self.cfg
+        B, S = ids.shape
+        H, d = cfg.n_heads, cfg.d_model
+        tok, ex = self._tables()
+        use_ex = ex_ids is not None and cfg.use_example_embedding
+        ids_p = ids.reshape(-1).index_select(0, pk.gather)
+        pos_p = pos.reshape(-1, 3).index_select(0, pk.gather)
+        ex_p = ex_ids.reshape(-1).index_select(0, pk.token_row) if use_ex else None
+        K.embed_rmsnorm(ids_p, ex_p, tok, ex if use_ex else None, 1, W.ln1[0], W.eps, sc.x,
+                        sc.xs, sc.rstd)
+        if pk.n_tokens > pk.n_valid:
+            sc.attn[pk.n_valid:pk.n_tokens].zero_()   # padding queries: no visible key
+        qs = softmax_scale(d // H)
+        for li in range(cfg.n_layers):
+            kc, vc = kv_layers(li)
+            gemm_f32(sc.xs, W.qkv[li], sc.qkv)
+            K.qkv_rope_cache_packed(sc.qkv, sc.rstd, pos_p, W.rope_tab, W.rope_geom,
+                                    pk.token_row, pk.token_slot, H, qs, sc.q, kc, vc)
+            K.attn_prefill_packed(sc.q, kc, vc, B, S, H, key_mask, kv_start, pk.q_offset,
+                                  pk.n_valid, True, sc.attn)
             self._mlp(W, li, sc)
 
     def _mlp(self, W: PackedWeights, li: int, sc: Scratch) -> None:

@@ -37,6 +37,7 @@ from .data import (
     generate_color_permutations,
 )
 from .engine import GRID_MAX_X, GRID_MAX_Y, HipEngine, PackedWeights, Scratch, choose_split_len
+from .engine import pack_prompt
 from .engine import engine_for, gemm_f32
 from .transformer import TinyTransformer, softmax_scale
 
@@ -50,6 +51,10 @@ DEVICE_PROMPTS = True
 # Replay greedy decode steps from one captured HIP graph (False: launch every kernel from the host
 # each step; same kernels, same results).
 USE_GRAPHS = True
+# Prefill runs over the prompt tokens without their left padding (packed rows); False runs every
+# layer over the whole padded [B, S] batch.  Logits and cache contents agree to fp32 rounding (the
+# GEMMs see a different row count).
+PACKED_PREFILL = True
 
 
 # =============================================================================================
@@ -304,10 +309,21 @@ class Generator:
         [0, S), logits of row lengths-1 into ``st.logits`` and its argmax into ``st.tok``
         (after ``cons``, the fused logit constraints, when given)."""
         cfg = self.model.config
-        sc = Scratch.alloc(st.B * st.S, cfg.d_model, cfg.d_ff, input_ids.device)
-        self.eng.run_prompt(W, input_ids, positions_3d, st.ex, st.pmask, st.kv_start, True,
-                            st.cache.layer, sc)
-        K.lm_head(sc.x, st.last_row, st.B, W.ln_f, W.eps, W.head, st.logits, st.tok, cons)
+        dev = input_ids.device
+        if PACKED_PREFILL:
+            # one small device->host read of the row starts; the padding then costs nothing
+            starts = torch.stack([st.kv_start, st.last_row]).cpu().numpy()
+            pk = pack_prompt(starts[0], starts[1], st.B, st.S, dev)
+            sc = Scratch.alloc(pk.n_tokens, cfg.d_model, cfg.d_ff, dev)
+            self.eng.run_packed(W, input_ids, positions_3d, st.ex, st.pmask, st.kv_start, pk,
+                                st.cache.layer, sc)
+            head_row = pk.head_row
+        else:
+            sc = Scratch.alloc(st.B * st.S, cfg.d_model, cfg.d_ff, dev)
+            self.eng.run_prompt(W, input_ids, positions_3d, st.ex, st.pmask, st.kv_start, True,
+                                st.cache.layer, sc)
+            head_row = st.last_row
+        K.lm_head(sc.x, head_row, st.B, W.ln_f, W.eps, W.head, st.logits, st.tok, cons)
         st.cache.seq_len = st.S
 
     def _embed_inputs(self, st: DecodeState):

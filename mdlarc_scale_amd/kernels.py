@@ -152,6 +152,36 @@ def qkv_rope_cache(qkv: torch.Tensor, rstd: torch.Tensor | None, pos: torch.Tens
         _p(slot_dev), _stream()), "mdl_qkv_rope_cache")
 
 
+def qkv_rope_cache_packed(qkv: torch.Tensor, rstd: torch.Tensor | None, pos: torch.Tensor,
+                          rope_tab: torch.Tensor,
+                          rope_geom: tuple[int, int, int, int, int, int],
+                          token_row: torch.Tensor, token_slot: torch.Tensor, n_heads: int,
+                          q_scale: float, q_out: torch.Tensor, k_cache: torch.Tensor,
+                          v_cache: torch.Tensor) -> None:
+    """``qkv_rope_cache`` over a packed token list: token m goes to batch row token_row[m],
+    cache slot token_slot[m] (no cache write when negative)."""
+    rows, d = token_row.numel(), n_heads * HEAD_DIM
+    _need(qkv, "qkv", F32, rows * 3 * d)
+    if qkv.dim() != 2 or qkv.shape[1] != 3 * d:
+        raise ValueError(f"qkv must be [rows, {3 * d}]")
+    _need(rstd, "rstd", F32, rows, optional=True)
+    _need(pos, "pos", I64, rows * 3)
+    _need(rope_tab, "rope_tab", F32)
+    _need(q_out, "q_out", BF16, rows * d)
+    _need(token_row, "token_row", I32, rows)
+    _need(token_slot, "token_slot", I32, rows)
+    for name, c in (("k_cache", k_cache), ("v_cache", v_cache)):
+        _need(c, name, BF16)
+        if c.dim() != 4 or c.shape[1] != n_heads or c.shape[3] != 64:
+            raise ValueError(f"{name} must be [batch, n_heads, slots, 64]")
+    batch, slots = k_cache.shape[0], k_cache.shape[2]
+    mx, my, mz, px, py, pz = rope_geom
+    _lib.check(_lib.lib().mdl_qkv_rope_cache_packed(
+        _p(qkv), qkv.shape[1], _p(rstd), _p(pos), _p(rope_tab), rows, _p(token_row),
+        _p(token_slot), batch, n_heads, HEAD_DIM, mx, my, mz, px, py, pz, q_scale, _p(q_out),
+        _p(k_cache), _p(v_cache), slots, _stream()), "mdl_qkv_rope_cache_packed")
+
+
 def swiglu(gate_up: torch.Tensor, rstd: torch.Tensor | None, bias_gate: torch.Tensor | None,
            bias_up: torch.Tensor | None, h_out: torch.Tensor) -> None:
     """h = silu(rstd*g + b_g) * (rstd*u + b_u) from fp32 gate|up, written as split [rows, 2F]."""
@@ -184,6 +214,29 @@ def attn_prefill(q: torch.Tensor, k_cache: torch.Tensor, v_cache: torch.Tensor, 
         _p(q), _p(k_cache), _p(v_cache), batch, seq, n_heads, HEAD_DIM, k_cache.shape[2],
         _p(key_mask), _p(kv_start), 1 if causal else 0, _p(out), _stream()),
         "mdl_attn_prefill")
+
+
+def attn_prefill_packed(q: torch.Tensor, k_cache: torch.Tensor, v_cache: torch.Tensor,
+                        batch: int, seq: int, n_heads: int, key_mask: torch.Tensor | None,
+                        kv_start: torch.Tensor, q_offset: torch.Tensor, n_rows: int,
+                        causal: bool, out: torch.Tensor) -> None:
+    """Packed query rows: query i >= kv_start[b] of row b is row q_offset[b] + i - kv_start[b]
+    of q ([n_rows, n_heads*64]) and out (split [n_rows, 2*n_heads*64]).  The caller guarantees
+    q_offset[b] + seq - kv_start[b] <= n_rows for every row."""
+    n = n_rows * n_heads * HEAD_DIM
+    _need(q, "q", BF16, n)
+    _need(out, "out", BF16, 2 * n)
+    for name, c in (("k_cache", k_cache), ("v_cache", v_cache)):
+        _need(c, name, BF16)
+        if c.dim() != 4 or c.shape[0] != batch or c.shape[1] != n_heads or c.shape[3] != 64:
+            raise ValueError(f"{name} must be [batch, n_heads, slots, 64]")
+    _need(key_mask, "key_mask", U8, batch * seq, optional=True)
+    _need(kv_start, "kv_start", I32, batch)
+    _need(q_offset, "q_offset", I32, batch)
+    _lib.check(_lib.lib().mdl_attn_prefill_packed(
+        _p(q), _p(k_cache), _p(v_cache), batch, seq, n_heads, HEAD_DIM, k_cache.shape[2],
+        _p(key_mask), _p(kv_start), _p(q_offset), 1 if causal else 0, _p(out), _stream()),
+        "mdl_attn_prefill_packed")
 
 
 def attn_decode_workspace_bytes(batch: int, n_heads: int, slots: int, split_len: int) -> int:

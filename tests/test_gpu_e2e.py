@@ -397,3 +397,48 @@ def test_constrained_greedy_fused_equals_host_path(monkeypatch):
     assert torch.equal(outs[True], outs[False])
     n = min(free.shape[1], outs[True].shape[1])
     assert not torch.equal(free[:, :n], outs[True][:, :n])
+
+
+def test_packed_prefill_equals_padded(monkeypatch):
+    """Prefill over the packed token list (left padding left out, the padding tokens that the
+    lengths-1 index names appended) against prefill over the whole padded batch: first-step logits
+    equal to GEMM rounding (the GEMMs see another row count), every valid cache slot equal to one
+    bf16 ulp, the same first token unless the two best logits are tied to that rounding.  Half
+    the rows are shorter than their padding, so their logits come from extra rows.  (Generation
+    on the packed path is checked against the oracle and the golden traces.)"""
+    from mdlarc_scale_amd import create_model
+    from mdlarc_scale_amd import inference as inf
+    from mdlarc_scale_amd.transformer import MODEL_SIZES
+
+    torch.manual_seed(4)
+    m = create_model(**MODEL_SIZES["small"], dropout=0.0, max_seq_len=2048).to(DEV).eval()
+    rng = np.random.default_rng(44)
+    prompts = _random_prompts(rng, 4, 3, 3, 9) + _random_prompts(rng, 4, 1, 1, 2)
+    ids, pos, mask = _left_pad(prompts)
+    ids, pos, mask = ids.to(DEV), pos.to(DEV), mask.to(DEV)
+    B, S = ids.shape
+    ex = torch.arange(B, device=DEV)
+    kv = (S - mask.sum(1)).cpu()
+    assert int(((S - kv) * 2 < S).sum()) >= 2        # rows whose lengths-1 index is padding
+    res = {}
+    for packed in (True, False):
+        monkeypatch.setattr(inf, "PACKED_PREFILL", packed)
+        gen = inf.Generator(m)
+        with torch.no_grad():
+            W = gen.eng.packed(ids.device)
+            st = gen.prepare(ids, pos, ex, mask, S + 8)
+            gen.prefill(st, W, ids, pos)
+        torch.cuda.synchronize()
+        res[packed] = (st.logits.cpu(), st.tok.cpu(), st.cache)
+    lp, tp, cp = res[True]
+    lq, tq, cq = res[False]
+    err = (lp - lq).abs().max().item()
+    print(f"packed vs padded prefill: logits max-abs {err:.3e}")
+    assert err <= 1e-3
+    _near_tie_ok(lq, tp, tq, err)
+    for li in range(m.config.n_layers):
+        for a, b in zip(cp.layer(li), cq.layer(li)):
+            for r in range(B):
+                k0 = int(kv[r])
+                x, y = a[r, :, k0:S].float(), b[r, :, k0:S].float()
+                assert bool(((x - y).abs() <= 2 ** -7 * y.abs() + 1e-6).all())

@@ -348,6 +348,86 @@ def test_attn_prefill_kv_start_clamped():
     close_bf16(unsplit(out).view(B, S, H, 64).transpose(1, 2), ref, atol=8e-3, rtol=2e-2)
 
 
+def _pack(kv, B, S):
+    from mdlarc_scale_amd.engine import pack_prompt
+
+    lengths = S - np.asarray(kv)
+    last = np.arange(B) * S + np.maximum(lengths - 1, 0)
+    return pack_prompt(np.asarray(kv), last, B, S, torch.device(DEV))
+
+
+@pytest.mark.parametrize("H", [4, 12, 5])        # whole-row kernels and the per-head kernel
+def test_qkv_rope_cache_packed_equals_padded(H):
+    """The packed list (each row from its first valid token, plus the padding tokens that the
+    lengths-1 index names) writes the q rows and cache slots the padded launch writes for those
+    tokens, bit for bit, and no slot before a row's start."""
+    d, S, slots = 64 * H, 37, 48
+    kv = [0, 20, 37, 5]
+    B = len(kv)
+    g = torch.Generator().manual_seed(H)
+    qkv = torch.randn(B * S, 3 * d, generator=g).to(DEV)
+    rstd = (0.5 + torch.rand(B * S, generator=g)).to(DEV)
+    pos = torch.randint(0, 31, (B * S, 3), generator=g).to(DEV)
+    from mdlarc_scale_amd.transformer import RotaryEmbedding3D
+
+    rope = RotaryEmbedding3D(64, 32, 32, 8)
+    tab, geom = rope.device_table(DEV), (32, 32, 8, rope.px, rope.py, rope.pz)
+    q_pad = torch.empty(B * S, d, device=DEV, dtype=torch.bfloat16)
+    kc_pad = torch.full((B, H, slots, 64), 7.0, device=DEV, dtype=torch.bfloat16)
+    vc_pad = torch.full_like(kc_pad, 7.0)
+    K().qkv_rope_cache(qkv, rstd, pos, tab, geom, B, S, H, 0.125, q_pad, kc_pad, vc_pad)
+    pk = _pack(kv, B, S)
+    gi = pk.gather.long()
+    q_pk = torch.empty(pk.n_tokens, d, device=DEV, dtype=torch.bfloat16)
+    kc_pk = torch.full_like(kc_pad, 7.0)
+    vc_pk = torch.full_like(kc_pad, 7.0)
+    K().qkv_rope_cache_packed(qkv[gi].contiguous(), rstd[gi].contiguous(), pos[gi].contiguous(),
+                              tab, geom, pk.token_row, pk.token_slot, H, 0.125, q_pk, kc_pk,
+                              vc_pk)
+    torch.cuda.synchronize()
+    assert pk.n_tokens == pk.n_valid + 2          # rows 1 and 2 read inside their padding
+    assert torch.equal(q_pk, q_pad[gi])
+    for b, k0 in enumerate(kv):
+        assert torch.equal(kc_pk[b, :, k0:S], kc_pad[b, :, k0:S])
+        assert torch.equal(vc_pk[b, :, k0:S], vc_pad[b, :, k0:S])
+        assert bool((kc_pk[b, :, :k0] == 7).all()) and bool((vc_pk[b, :, :k0] == 7).all())
+        assert bool((kc_pk[b, :, S:] == 7).all()) and bool((vc_pk[b, :, S:] == 7).all())
+
+
+@pytest.mark.parametrize("causal", [True, False])
+def test_attn_prefill_packed_equals_padded(causal):
+    """Packed query rows give the padded launch's outputs for every query at or after its row's
+    start, bit for bit; cache slots before a row's start hold NaN and never reach a product; no
+    row outside the packed range is written."""
+    g = torch.Generator().manual_seed(31 + causal)
+    B, H, S, slots = 6, 3, 300, 320
+    q = bf(torch.randn(B, S, H, 64, generator=g) * 0.125).to(DEV)
+    kc = bf(torch.randn(B, H, slots, 64, generator=g)).to(DEV)
+    vc = bf(torch.randn(B, H, slots, 64, generator=g)).to(DEV)
+    kv = [0, 299, 170, 300, 64, 1]
+    mask = torch.ones(B, S, dtype=torch.bool)
+    for b, k0 in enumerate(kv):
+        mask[b, :k0] = False
+    mask[4, 200:230] = False                       # holes inside a row
+    mask8 = mask.to(torch.uint8).to(DEV)
+    kv_dev = torch.tensor(kv, dtype=torch.int32, device=DEV)
+    out_pad = torch.empty(B * S, 2 * H * 64, device=DEV, dtype=torch.bfloat16)
+    K().attn_prefill(q, kc, vc, B, S, H, mask8, kv_dev, causal, out_pad)
+    pk = _pack(kv, B, S)
+    gi = pk.gather[:pk.n_valid].long()
+    kc_nan, vc_nan = kc.clone(), vc.clone()
+    for b, k0 in enumerate(kv):
+        kc_nan[b, :, :k0] = float("nan")
+        vc_nan[b, :, :k0] = float("nan")
+    q_pk = q.reshape(B * S, H * 64)[gi].contiguous()
+    out_pk = torch.full((pk.n_valid + 5, 2 * H * 64), 3.0, device=DEV, dtype=torch.bfloat16)
+    K().attn_prefill_packed(q_pk, kc_nan, vc_nan, B, S, H, mask8, kv_dev, pk.q_offset,
+                            pk.n_valid, causal, out_pk)
+    torch.cuda.synchronize()
+    assert torch.equal(out_pk[:pk.n_valid], out_pad[gi])
+    assert bool((out_pk[pk.n_valid:] == 3).all())
+
+
 # ---------------------------------------------------------------------------- K4b decode
 
 @pytest.mark.parametrize("split_len", [128, 256, 4096])
