@@ -25,8 +25,9 @@ Also reported on the same JSON line:
   tokens, d=768, F=2048, GB/s against the 8 TB/s HBM peak (buffer sets rotated so the 256 MB
   MALL cannot hold the working set).
 * ``prefill_attention``: the prefill attention kernel alone over one layer of the batch's cache
-  (its real masks and left padding), re-launched back to back; TFLOP/s of the valid causal
-  (query, key) pairs against the 2.5 PFLOP/s dense bf16 MFMA peak.
+  (its real masks and left padding, packed query rows as the prefill launches it), re-launched
+  back to back; TFLOP/s of the valid causal (query, key) pairs against the 2.5 PFLOP/s dense
+  bf16 MFMA peak.
 
 ``--config medium_b128`` / ``large_b64`` run BASELINE configs 3 and 4 the same way (their own
 metric name; no microbench; the CPU baseline only with an explicit ``--cpu-seconds``).
@@ -311,7 +312,7 @@ def main() -> int:
     from mdlarc_scale_amd import kernels as K
     from mdlarc_scale_amd import inference as I
     from mdlarc_scale_amd.data import END_TOKEN_ID
-    from mdlarc_scale_amd.engine import engine_for
+    from mdlarc_scale_amd.engine import engine_for, pack_prompt
     from mdlarc_scale_amd.transformer import MODEL_SIZES, create_model
     from mdlarc_scale_amd.workload import SPECS, build_prompts, left_pad
 
@@ -404,19 +405,27 @@ def main() -> int:
         achieved = attn_bytes / attn_ms / 1e6
         durs = ts
 
-        # prefill attention alone: one layer's launch over the batch's own masks and cache,
-        # with synthetic q (the kernel's time does not depend on values)
+        # prefill attention alone: one layer's launch as the prefill makes it (packed query
+        # rows) over the batch's own masks and cache, with synthetic q (the kernel's time does
+        # not depend on values)
         n_valid = mask.sum(1)
         pa_flops = 4 * 64 * H * int((n_valid * (n_valid + 1) // 2).sum())
-        qp = (torch.randn(B * S, H * 64, device=dev) * 0.125).to(torch.bfloat16)
-        op = torch.empty(B * S, 2 * H * 64, device=dev, dtype=torch.bfloat16)
+        starts = torch.stack([st.kv_start, st.last_row]).cpu().numpy()
+        pk = pack_prompt(starts[0], starts[1], B, S, dev)
+        qp = (torch.randn(pk.n_valid, H * 64, device=dev) * 0.125).to(torch.bfloat16)
+        op = torch.empty(pk.n_valid, 2 * H * 64, device=dev, dtype=torch.bfloat16)
         kc0, vc0 = st.cache.layer(0)
-        K.attn_prefill(qp, kc0, vc0, B, S, H, st.pmask, st.kv_start, True, op)
+
+        def prefill_attention():
+            K.attn_prefill_packed(qp, kc0, vc0, B, S, H, st.pmask, st.kv_start, pk.q_offset,
+                                  pk.n_valid, True, op)
+
+        prefill_attention()
         reps = 10
         tpa = Timer()
         tpa.start()
         for _ in range(reps):
-            K.attn_prefill(qp, kc0, vc0, B, S, H, st.pmask, st.kv_start, True, op)
+            prefill_attention()
         tpa.stop()
         pa_ms = tpa.ms() / reps
         del qp, op
@@ -471,7 +480,7 @@ def main() -> int:
             "attention_causal_tflop": round(prefill_flops / 1e12, 3),
         },
         "prefill_attention": {
-            "kernel": "attn_prefill_kernel (mdl_attn_prefill, bf16 MFMA)", "bound": "mfma",
+            "kernel": "attn_prefill_kernel (mdl_attn_prefill_packed, bf16 MFMA)", "bound": "mfma",
             "ms_per_layer": round(pa_ms, 4), "tflop_per_layer": round(pa_flops / 1e12, 4),
             "achieved": round(pa_flops / pa_ms / 1e9, 1), "peak": BF16_PEAK_TFLOPS,
             "unit": "TFLOP/s", "frac": round(pa_flops / pa_ms / 1e9 / BF16_PEAK_TFLOPS, 4),
