@@ -51,5 +51,14 @@ def test_argument_errors_are_reported_before_any_launch():
                                 0.125, fake, fake, fake, 4, 1, None, None) == -5
     assert L.mdl_attn_decode(fake, fake, fake, 1, 1, 64, 1024, None, 0, None, None, None, 5,
                              None, None, 0, 128, fake, None) == -6
+    # packed prefill: the per-row starts / offsets and the per-token rows / slots are required
+    assert L.mdl_attn_prefill_packed(fake, fake, fake, 1, 4, 1, 64, 4, None, None, fake, 1, fake,
+                                     None) == -1
+    assert L.mdl_attn_prefill_packed(fake, fake, fake, 1, 4, 1, 32, 4, None, fake, fake, 1, fake,
+                                     None) == -4
+    assert L.mdl_qkv_rope_cache_packed(fake, 192, None, fake, fake, 4, None, fake, 1, 1, 64, 32,
+                                       32, 8, 10, 10, 12, 0.125, fake, fake, fake, 4, None) == -1
+    assert L.mdl_qkv_rope_cache_packed(fake, 192, None, fake, fake, 4, fake, fake, 1, 1, 32, 32,
+                                       32, 8, 10, 10, 12, 0.125, fake, fake, fake, 4, None) == -4
     with pytest.raises(RuntimeError, match="head_dim"):
         _lib.check(-4, "probe")
