@@ -168,7 +168,7 @@ def test_reference_init_generate_vs_oracle(preset):
     """Reference initialisation (src/transformer.py:547-560) under torch.manual_seed(0), weights
     rounded to bf16 once and shared with the fp32 oracle: logits within 2e-2 max-abs at every
     decoded step (teacher-forced through the oracle's tokens) and >= 99.5% greedy agreement."""
-    from mdlarc_scale_amd import create_model, generate_output
+    from mdlarc_scale_amd import create_model
     from mdlarc_scale_amd.transformer import MODEL_SIZES
 
     torch.manual_seed(0)
@@ -181,7 +181,17 @@ def test_reference_init_generate_vs_oracle(preset):
     rng = np.random.default_rng(20261201)
     ids, pos, mask = _left_pad(_random_prompts(rng, 4, 3, 1, 8))
     ex = torch.tensor([0, 5, 17, 1279])
-    max_new = 48
+    _compare_with_oracle(m, state, ids, pos, ex, mask, 48, preset)
+
+
+def _compare_with_oracle(m, state, ids, pos, ex, mask, max_new, label):
+    """GPU generate_output against the fp32 oracle's: teacher-forced logits (the GPU forward
+    over the oracle's token stream) within 2e-2 max-abs at every decoded step with every
+    argmax difference a near-tie, and >= 99.5% free-running greedy agreement (or a near-tie at
+    each row's first divergence)."""
+    from mdlarc_scale_amd import generate_output
+
+    B = ids.shape[0]
     c = m.config
     ocfg = rp.OracleConfig(c.d_model, c.n_heads, c.n_layers, c.d_ff, c.num_examples,
                            c.max_seq_len)
@@ -196,18 +206,48 @@ def test_reference_init_generate_vs_oracle(preset):
     # teacher-forced logits: GPU forward over the oracle's token stream
     g = len(tr.step_logits)
     toks = tr.tokens[:, :S + g - 1]
-    tpos = torch.cat([pos, torch.stack(tr.step_positions, 1)], 1)
-    tmask = torch.cat([mask, torch.ones(4, g - 1, dtype=torch.bool)], 1)
+    tpos = torch.cat([pos, torch.stack(tr.step_positions, 1)], 1) if g > 1 else pos
+    tmask = torch.cat([mask, torch.ones(B, g - 1, dtype=torch.bool)], 1)
     with torch.no_grad():
         lg = m(toks.to(DEV), tpos.to(DEV), ex.to(DEV), tmask.to(DEV), True).float().cpu()
-    first = lg[torch.arange(4), mask.sum(1) - 1]
+    first = lg[torch.arange(B), mask.sum(1) - 1]
     steps = torch.cat([first[:, None], lg[:, S:S + g - 1]], 1)
     ref = torch.stack(tr.step_logits, 1)
     err = (steps - ref).abs().max().item()
-    print(f"{preset}: teacher-forced logits max-abs {err:.3e}, free-running agreement {agree:.4f}")
+    print(f"{label}: teacher-forced logits max-abs {err:.3e}, free-running agreement {agree:.4f}")
     assert err <= 2e-2
     _near_tie_ok(ref, steps.argmax(-1), ref.argmax(-1), err)
     assert agree >= 0.995 or _first_divergence_is_tie(out, tr, S, err)
+
+
+def test_generate_with_mask_holes_vs_oracle():
+    """Prompt masks with holes inside the valid run (the reference accepts any boolean mask,
+    src/inference.py:530-531, :557-558): the packed prefill keeps the holes as masked keys, decode
+    reads the mask per slot for rows with holes, and lengths-1 counts valid positions only, so it
+    moves left of the last token.  One row starts with a hole (its first valid position moves
+    right), one has none.  Tiny reference-initialised model against the fp32 oracle."""
+    from mdlarc_scale_amd import create_model
+    from mdlarc_scale_amd.transformer import MODEL_SIZES
+
+    torch.manual_seed(1)
+    m = create_model(**MODEL_SIZES["tiny"], dropout=0.0, max_seq_len=4096)
+    with torch.no_grad():
+        for p in m.parameters():
+            p.copy_(p.to(torch.bfloat16).float())
+    state = {k: v.clone() for k, v in m.state_dict().items()}
+    m = m.to(DEV).eval()
+    rng = np.random.default_rng(77)
+    ids, pos, mask = _left_pad(_random_prompts(rng, 5, 3, 1, 8))
+    for b in range(1, 5):
+        valid = mask[b].nonzero().flatten()
+        k = min(7, len(valid) - 2)
+        if k > 0:
+            mask[b, torch.from_numpy(rng.choice(valid[1:-1].numpy(), size=k, replace=False))] = False
+    first = mask[2].nonzero().flatten()[0]
+    mask[2, first:first + 3] = False                 # row 2 starts with holes
+    assert all(int(mask[b].sum()) > 0 for b in range(5))
+    ex = torch.tensor([3, 0, 9, 100, 1279])
+    _compare_with_oracle(m, state, ids, pos, ex, mask, 40, "holes")
 
 
 def _first_divergence_is_tie(out, tr, S, err):
