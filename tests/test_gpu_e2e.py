@@ -263,6 +263,45 @@ def _first_divergence_is_tie(out, tr, S, err):
     return True
 
 
+def test_generate_properties_of_the_reference_suite():
+    """The properties the reference's own tests pin for generate_output and predict_grid
+    (tests/test_inference.py): output length within [S, S + max_new] (:55-80); greedy
+    determinism across calls, also after an unrelated call of another shape in between (:82-98,
+    :301-363); a right-padded B=2 batch padded with token 0 and no mask (:100-123), whose prompt
+    comes back unchanged; predict_grid returns a grid (list of lists) or None (:155-214)."""
+    from mdlarc_scale_amd import create_tiny_model, generate_output, predict_grid
+
+    torch.manual_seed(0)
+    m = create_tiny_model(dropout=0.0).to(DEV).eval()
+    rng = np.random.default_rng(5)
+    ids, pos, mask = _left_pad(_random_prompts(rng, 3, 2, 1, 5))
+    ids, pos, mask = ids.to(DEV), pos.to(DEV), mask.to(DEV)
+    S = ids.shape[1]
+    with torch.no_grad():
+        a = generate_output(m, ids, pos, None, mask, max_new_tokens=25)
+        generate_output(m, ids[:1, -5:], pos[:1, -5:], max_new_tokens=7)
+        b = generate_output(m, ids, pos, None, mask, max_new_tokens=25)
+    assert S < a.shape[1] <= S + 25
+    assert torch.equal(a, b)
+    assert torch.equal(a[:, :S], ids)
+    p1 = odf.encode_example([[1, 2], [3, 4]], None)
+    p2 = odf.encode_example([[5]], None)
+    L = max(len(p1), len(p2))
+    ids2 = torch.zeros(2, L, dtype=torch.long)
+    pos2 = torch.zeros(2, L, 3, dtype=torch.long)
+    for r, p in enumerate((p1, p2)):
+        ids2[r, :len(p)] = torch.tensor(p)
+        pos2[r, :len(p)] = torch.from_numpy(odf.compute_positions_3d(p))
+    with torch.no_grad():
+        out2 = generate_output(m, ids2.to(DEV), pos2.to(DEV), max_new_tokens=10).cpu()
+    assert out2.shape[0] == 2 and L < out2.shape[1] <= L + 10
+    assert torch.equal(out2[:, :L], ids2)
+    assert int(out2.min()) >= 0 and int(out2.max()) < 14
+    g = predict_grid(m, [[[1, 2], [3, 4]]], [[[4, 3], [2, 1]]], [[5, 6], [7, 8]], DEV,
+                     max_output_tokens=20)
+    assert g is None or (isinstance(g, list) and all(isinstance(row, list) for row in g))
+
+
 @pytest.mark.parametrize("stop_on_end", [True, False])
 def test_graph_replay_matches_eager_launches(stop_on_end):
     """Greedy decode replayed from one captured HIP graph returns exactly the tokens of the
