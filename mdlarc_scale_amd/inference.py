@@ -146,7 +146,8 @@ class StaticKVCache:
                  head_dim: int, device: torch.device, dtype: torch.dtype = torch.bfloat16, *,
                  zero: bool = True):
         """``zero=False`` skips the initial fill: the generation path writes every slot before
-        any kernel reads it (prefill writes [0, S), each decode step writes its slot first)."""
+        any kernel reads it (prefill writes [kv_start, S) of each row, each decode step writes
+        its slot first, and no kernel reads a row's slots before its kv_start)."""
         self.batch_size, self.max_seq_len, self.n_layers = batch_size, max_seq_len, n_layers
         self.seq_len = 0
         alloc = torch.zeros if zero else torch.empty
