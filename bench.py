@@ -404,6 +404,10 @@ def main() -> int:
                          for t in ts) / len(ts)
         achieved = attn_bytes / attn_ms / 1e6
         durs = ts
+        # the launch's own choices (csrc/attn_decode.hip decode_impl): wave tiles of 64 slots
+        # once a work item can exceed 2,048 slots, else 32; ceil(total / split_len) splits
+        n_split = -(-total // st.split_len)
+        decode_nb = 4 if min(st.split_len, total) > 2048 else 2
 
         # prefill attention alone: one layer's launch as the prefill makes it (packed query
         # rows) over the batch's own masks and cache, with synthetic q (the kernel's time does
@@ -465,8 +469,9 @@ def main() -> int:
             "graph": not args.eager, "workload_seed": spec.seed,
         },
         "roofline": {
-            "kernel": "attn_decode_kernel<4, true> (mdl_attn_decode_rope: K2 + decode "
-                      "attention, one split per (row, head) at this shape)",
+            "kernel": f"attn_decode_kernel<true, {decode_nb}> (mdl_attn_decode_rope: K2 + "
+                      f"decode attention on bf16 MFMA, {16 * decode_nb}-slot wave tiles, "
+                      f"{n_split} split(s) per (row, head))",
             "bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS,
             "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": traffic,
             "traffic_source": traffic_src,

@@ -193,7 +193,9 @@ int mdl_attn_prefill_packed(const uint16_t* q, const uint16_t* k_cache, const ui
                             const int32_t* q_offset, int causal, uint16_t* out, void* stream);
 
 /*
- * K4b -- decode attention over the static cache (split-K flash decoding).
+ * K4b -- decode attention over the static cache (split-K flash decoding on bf16 MFMA: QK^T with
+ * K straight from HBM as the A operand, PV with V staged through LDS; the probabilities enter
+ * the PV product rounded to bf16).
  * Replaces: F.scaled_dot_product_attention in _decode_step (src/inference.py:452) with the
  *           mask rebuilt from full_attention_mask (src/inference.py:446-450, :557-558, :626).
  * q: bf16 [batch, n_heads, 64] (pre-scaled); out: split bf16 [batch, 2*n_heads*64].

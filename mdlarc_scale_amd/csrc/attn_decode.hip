@@ -1,25 +1,31 @@
-// K4b -- decode attention: one query per (row, head) against the static KV cache.
+// K4b -- decode attention: one query per (row, head) against the static KV cache, on bf16 MFMA.
 //
-// Split-K flash decoding.  Work item = (b*h, split): a 256-thread block streams `split_len`
-// cache slots of one head.  Inside a wavefront, lane = 8*grp + sub: the 8 lanes of a group own
-// one slot at a time and `sub` selects 8 of the 64 channels, so one 16-byte load per lane covers
-// 8 consecutive slots = 1 KiB of contiguous K (then V).  U slots per group are loaded before any
-// arithmetic, so each lane keeps 2*U 16-byte loads in flight.  Scores are reduced over the 8
-// lanes of a group with 3 xor-shuffles; every group keeps its own online-softmax state (max, sum,
-// 8 accumulators) in the log2 domain.  At the end the 8 groups, then the 4 waves (LDS), then the
-// splits (second kernel) are merged with the usual max-rescaled sums.  K and V are streamed with
-// non-temporal loads (read once per launch; keeps the projection weights cached between layers).
+// Split-K flash decoding.  Work item = (b*h, split): a 256-thread block attends over `split_len`
+// cache slots of one head; its 4 wavefronts take tiles of kT = 16 NB consecutive slots in turn
+// (NB = 2 or 4).  Per tile, on v_mfma_f32_16x16x32_bf16 (operand layouts in mfma.h):
+//   S^T = K q^T: the A operand is K itself -- lane (c, g) loads 16 bytes of slot row 16 nb + c at
+//     dims 32 kk + 8 g straight from HBM into registers, no staging needed; the B operand is q
+//     replicated over the 16 columns, so every lane ends up holding real scores (slots
+//     16 nb + 4 g + i) and the softmax needs no cross-lane gather beyond the 4-group max;
+//   O^T = V^T P^T: V is staged through the wave's own LDS tile (row-major, 144-byte rows) and read
+//     back transposed (ds_read_b64_tr_b16); P^T comes from the score accumulators, in the key
+//     order the transposing reads produce; the row sum is one more MFMA against ones, so it sums
+//     the same bf16-rounded probabilities the PV product uses.
+// The single query costs 15/16 of every MFMA, which is free: the kernel streams 256 bytes of K/V
+// per slot from HBM and does 2 x 128 useful flops per slot, so MFMA and VALU stay far below their
+// rates.  K and V use non-temporal loads (read once per launch; keeps the projection weights
+// cached between layers).  The 4 waves, then the splits (second kernel) merge with the usual
+// max-rescaled sums.
 //
 // Slot j of row b is visible iff kv_start[b] <= j <= t and (j >= prompt_len or
 // prompt_mask[b, j]), the decode mask of the reference (prompt mask, then every generated slot).
 // row_holes[b] == 0 (from mdl_grid_init) says the prompt mask of row b is one contiguous run
 // starting at kv_start[b]; such rows skip the per-slot mask reads.
-#include "common.h"
+#include "mfma.h"
 #include "rope.h"
 
 namespace mdl {
 
-constexpr float kLog2e = 1.4426950408889634f;
 constexpr int kPart = 2 + kHeadDim;   // m, l, acc[64] per split
 
 // Channel `lane` of head h = bh % n_heads of batch row b = bh / n_heads into the out-projection
@@ -45,12 +51,15 @@ struct RopeIn {
   float q_scale;
 };
 
+constexpr int kVld = 72;      // LDS row stride of a staged V tile (bf16): 144-byte rows
+
 // FUSED: the block first does K2's work for its own (row, head) -- wave 0 rotates q (lanes
 // 0-31, one pair each) and k (lanes 32-63) of the decode token, rounds q to bf16 exactly as K2
 // does and hands it to the other waves through LDS, and the block whose slot range holds t
 // writes the token's K/V into cache slot t -- then attends as the unfused kernel.  The cache
 // row is stored before the barrier and read after it, so the block sees its own write.
-template <int U, bool FUSED>
+// NB: 16-slot score blocks per wave tile.
+template <bool FUSED, int NB>
 __global__ __launch_bounds__(256) void attn_decode_kernel(
     const uint16_t* __restrict__ q, uint16_t* __restrict__ kc, uint16_t* __restrict__ vc,
     int n_heads, int slots, const uint8_t* __restrict__ pmask, int plen,
@@ -58,25 +67,23 @@ __global__ __launch_bounds__(256) void attn_decode_kernel(
     const int32_t* __restrict__ row_order, int seq_pos, const int32_t* __restrict__ seq_dev,
     int n_split, int split_len, float* __restrict__ ws, uint16_t* __restrict__ out,
     RopeIn rin) {
-  // blocks are dispatched in blockIdx order; row_order lists the rows longest-first so the
-  // short rows fill the tail of the launch
   const int ri = blockIdx.x / n_heads;
   const int n_rows = gridDim.x / n_heads;
-  // a caller's bad permutation entry is clamped into range: wrong rows, never a wild address
   const int b = row_order ? min(max(row_order[ri], 0), n_rows - 1) : ri;
   const int bh = b * n_heads + (blockIdx.x - ri * n_heads);
   const int split = blockIdx.y;
   const int wave = threadIdx.x >> 6;
   const int lane = threadIdx.x & 63;
-  const int grp = lane >> 3;
-  const int sub = lane & 7;
+  const int c16 = lane & 15, g = lane >> 4;
   const int t = seq_dev ? *seq_dev : seq_pos;
   const int start = kv_start ? kv_start[b] : 0;
   const int lo = start + split * split_len;
   const int hi = min(lo + split_len, min(t + 1, slots));
 
   __shared__ float red[4][kPart];
-  __shared__ float q_lds[FUSED ? kHeadDim : 1];
+  __shared__ __attribute__((aligned(16))) uint16_t q_lds[kHeadDim];
+  constexpr int kT = 16 * NB;   // slots per wave tile
+  __shared__ __attribute__((aligned(16))) uint16_t Vs[4][kT * kVld];
 
   if (FUSED) {
     if (wave == 0) {
@@ -95,9 +102,8 @@ __global__ __launch_bounds__(256) void attn_decode_kernel(
       const bool writes = t >= lo && t < lo + split_len && t < slots;
       const int64_t slot_row = (static_cast<int64_t>(bh) * slots + t) * kHeadDim;
       if (!is_k) {
-        const uint32_t qb = pack_bf2(y0 * rin.q_scale, y1 * rin.q_scale);
-        q_lds[2 * j] = bf2f(qb & 0xffffu);
-        q_lds[2 * j + 1] = bf2f(qb >> 16);
+        *reinterpret_cast<uint32_t*>(q_lds + 2 * j) = pack_bf2(y0 * rin.q_scale,
+                                                               y1 * rin.q_scale);
       } else if (writes) {
         *reinterpret_cast<uint32_t*>(kc + slot_row + 2 * j) = pack_bf2(y0, y1);
       }
@@ -113,99 +119,113 @@ __global__ __launch_bounds__(256) void attn_decode_kernel(
     __syncthreads();
   }
 
-  float m = -INFINITY, l = 0.f, acc[8];
+  float m = -INFINITY;
+  f32x4_t lsum = {0.f, 0.f, 0.f, 0.f}, o[4];
 #pragma unroll
-  for (int i = 0; i < 8; ++i) acc[i] = 0.f;
+  for (int db = 0; db < 4; ++db) o[db] = f32x4_t{0.f, 0.f, 0.f, 0.f};
 
   if (lo < hi) {
-    float qf[8];
-    if (FUSED) {
+    bf16x8_t qf[2];
 #pragma unroll
-      for (int i = 0; i < 8; ++i) qf[i] = q_lds[sub * 8 + i];
-    } else {
-      unpack8(*reinterpret_cast<const uint4*>(q + static_cast<int64_t>(bh) * kHeadDim + sub * 8),
-              qf);
-    }
-#pragma unroll
-    for (int i = 0; i < 8; ++i) qf[i] *= kLog2e;
-    const uint16_t* K = kc + static_cast<int64_t>(bh) * slots * kHeadDim + sub * 8;
-    const uint16_t* V = vc + static_cast<int64_t>(bh) * slots * kHeadDim + sub * 8;
-    // rows whose prompt mask is one contiguous run from kv_start need no per-slot mask reads
+    for (int kk = 0; kk < 2; ++kk)
+      qf[kk] = as_bf16x8(
+          FUSED ? *reinterpret_cast<const uint4*>(q_lds + 32 * kk + 8 * g)
+                : *reinterpret_cast<const uint4*>(q + static_cast<int64_t>(bh) * kHeadDim +
+                                                  32 * kk + 8 * g));
+    const bf16x8_t ones = bf16_ones8();
+    const uint16_t* K = kc + static_cast<int64_t>(bh) * slots * kHeadDim;
+    const uint16_t* V = vc + static_cast<int64_t>(bh) * slots * kHeadDim;
     const bool dense = row_holes && row_holes[b] == 0;
     const uint8_t* pm = (pmask && !dense) ? pmask + static_cast<int64_t>(b) * plen : nullptr;
+    uint16_t* Vw = Vs[wave];
 
-    for (int base = lo + wave * 8 * U; base < hi; base += 4 * 8 * U) {
-      uint4 kr[U], vr[U];
-      bool ok[U];
+    for (int base = lo + wave * kT; base < hi; base += 4 * kT) {
+      uint4 kf[NB][2], vr[2 * NB];
 #pragma unroll
-      for (int u = 0; u < U; ++u) {
-        const int j = base + u * 8 + grp;
-        ok[u] = j < hi;
-        if (ok[u]) {
-          kr[u] = load_nt16(K + static_cast<int64_t>(j) * kHeadDim);
-          vr[u] = load_nt16(V + static_cast<int64_t>(j) * kHeadDim);
-          if (pm && j < plen) ok[u] = pm[j] != 0;
-        } else {
-          kr[u] = make_uint4(0, 0, 0, 0);
-          vr[u] = make_uint4(0, 0, 0, 0);
-        }
+      for (int nb = 0; nb < NB; ++nb) {
+        const int key = base + 16 * nb + c16;
+#pragma unroll
+        for (int kk = 0; kk < 2; ++kk)
+          kf[nb][kk] = key < hi ? load_nt16(K + static_cast<int64_t>(key) * kHeadDim + 32 * kk +
+                                            8 * g)
+                                : make_uint4(0, 0, 0, 0);
       }
-      float s[U];
 #pragma unroll
-      for (int u = 0; u < U; ++u) {
-        float kf[8];
-        unpack8(kr[u], kf);
-        float a = 0.f;
-#pragma unroll
-        for (int i = 0; i < 8; ++i) a += qf[i] * kf[i];
-        a += __shfl_xor(a, 1, kWave);
-        a += __shfl_xor(a, 2, kWave);
-        a += __shfl_xor(a, 4, kWave);
-        s[u] = ok[u] ? a : -INFINITY;
+      for (int r = 0; r < 2 * NB; ++r) {
+        const int key = base + 8 * r + (lane >> 3);
+        vr[r] = key < hi ? load_nt16(V + static_cast<int64_t>(key) * kHeadDim + 8 * (lane & 7))
+                         : make_uint4(0, 0, 0, 0);
       }
-      float mx = m;
+      f32x4_t sc[NB];
 #pragma unroll
-      for (int u = 0; u < U; ++u) mx = fmaxf(mx, s[u]);
-      if (mx == -INFINITY) continue;
-      const float alpha = exp2f(m - mx);
-      l *= alpha;
+      for (int nb = 0; nb < NB; ++nb) {
+        sc[nb] = f32x4_t{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-      for (int i = 0; i < 8; ++i) acc[i] *= alpha;
-#pragma unroll
-      for (int u = 0; u < U; ++u) {
-        const float p = exp2f(s[u] - mx);
-        l += p;
-        float vf[8];
-        unpack8(vr[u], vf);
-#pragma unroll
-        for (int i = 0; i < 8; ++i) acc[i] += p * vf[i];
+        for (int kk = 0; kk < 2; ++kk)
+          sc[nb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf16x8(kf[nb][kk]), qf[kk],
+                                                           sc[nb], 0, 0, 0);
       }
-      m = mx;
+      // the previous tile's transposing reads of Vw are done before it is overwritten
+      __builtin_amdgcn_fence(__ATOMIC_ACQ_REL, "wavefront");
+      __builtin_amdgcn_wave_barrier();
+#pragma unroll
+      for (int r = 0; r < 2 * NB; ++r)
+        *reinterpret_cast<uint4*>(Vw + (8 * r + (lane >> 3)) * kVld + 8 * (lane & 7)) = vr[r];
+      // score block nb, element i of lane group g is slot base + 16 nb + 4 g + i
+      if (base + kT > hi || pm) {
+#pragma unroll
+        for (int nb = 0; nb < NB; ++nb)
+#pragma unroll
+          for (int i = 0; i < 4; ++i) {
+            const int key = base + 16 * nb + 4 * g + i;
+            const bool vis = key < hi && (!pm || key >= plen || pm[key] != 0);
+            if (!vis) sc[nb][i] = -INFINITY;
+          }
+      }
+      float tmax = -INFINITY;
+#pragma unroll
+      for (int nb = 0; nb < NB; ++nb)
+#pragma unroll
+        for (int i = 0; i < 4; ++i) tmax = fmaxf(tmax, sc[nb][i]);
+      tmax = max_over_groups(tmax);
+      const float mnew = fmaxf(m, tmax * kLog2eF);
+      const float mb = (mnew == -INFINITY) ? 0.f : mnew;
+      const float alpha = __builtin_amdgcn_exp2f(m - mb);
+      m = mnew;
+      lsum *= alpha;
+#pragma unroll
+      for (int db = 0; db < 4; ++db) o[db] *= alpha;
+#pragma unroll
+      for (int nb = 0; nb < NB; ++nb)
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+          sc[nb][i] = __builtin_amdgcn_exp2f(fmaf(sc[nb][i], kLog2eF, -mb));
+      bf16x8_t pb[NB / 2];
+#pragma unroll
+      for (int kk = 0; kk < NB / 2; ++kk) pb[kk] = pt_operand(sc[2 * kk], sc[2 * kk + 1]);
+      // the staged V tile is visible to the whole wave
+      __builtin_amdgcn_fence(__ATOMIC_ACQ_REL, "wavefront");
+      __builtin_amdgcn_wave_barrier();
+#pragma unroll
+      for (int kk = 0; kk < NB / 2; ++kk) {
+#pragma unroll
+        for (int db = 0; db < 4; ++db)
+          o[db] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(vt_operand(Vw, kVld, kk, db, c16, g),
+                                                          pb[kk], o[db], 0, 0, 0);
+        lsum = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ones, pb[kk], lsum, 0, 0, 0);
+      }
     }
   }
 
-  // merge the 8 slot groups of this wave
+  // every column of the replicated products holds the same values: lanes 0, 16, 32, 48 publish
+  if (c16 == 0) {
 #pragma unroll
-  for (int off = 8; off < 64; off <<= 1) {
-    const float mo = __shfl_xor(m, off, kWave);
-    const float lo2 = __shfl_xor(l, off, kWave);
-    const float mn = fmaxf(m, mo);
-    const float a = (m == -INFINITY) ? 0.f : exp2f(m - mn);
-    const float c = (mo == -INFINITY) ? 0.f : exp2f(mo - mn);
-    l = l * a + lo2 * c;
+    for (int db = 0; db < 4; ++db)
 #pragma unroll
-    for (int i = 0; i < 8; ++i) {
-      const float ao = __shfl_xor(acc[i], off, kWave);
-      acc[i] = acc[i] * a + ao * c;
-    }
-    m = mn;
-  }
-  if (grp == 0) {
-#pragma unroll
-    for (int i = 0; i < 8; ++i) red[wave][2 + sub * 8 + i] = acc[i];
-    if (sub == 0) {
+      for (int i = 0; i < 4; ++i) red[wave][2 + 16 * db + 4 * g + i] = o[db][i];
+    if (g == 0) {
       red[wave][0] = m;
-      red[wave][1] = l;
+      red[wave][1] = lsum[0];
     }
   }
   __syncthreads();
@@ -255,8 +275,11 @@ __global__ __launch_bounds__(256) void attn_decode_combine_kernel(const float* _
   store_split(out, bh, n_heads, lane, L > 0.f ? O / L : 0.f);
 }
 
-constexpr int kUnroll = 4;
-constexpr int kSlotsPerIter = 4 * 8 * kUnroll;   // slots a block consumes per loop trip
+constexpr int kSlotsPerIter = 128;   // split_len granularity
+// Work items that can exceed this many slots take 64-slot wave tiles, shorter ones 32-slot
+// tiles (measured: 32 is 1-3% faster at config 2's items of at most 2,048 slots, 64 faster at
+// configs 3 and 4, whose items run to 3,300-4,100 slots).
+constexpr int kLongItem = 2048;
 
 static int n_splits(int cache_slots, int split_len) {
   return (cache_slots + split_len - 1) / split_len;
@@ -298,14 +321,19 @@ static int decode_impl(bool fused, const RopeIn& rin, const uint16_t* q, uint16_
   hipStream_t s = static_cast<hipStream_t>(stream);
   const int n_bh = batch * n_heads;
   const dim3 grid(n_bh, ns);
-  if (fused)
-    attn_decode_kernel<kUnroll, true><<<grid, 256, 0, s>>>(
-        q, k_cache, v_cache, n_heads, cache_slots, prompt_mask, prompt_len, row_holes,
-        kv_start, row_order, seq_pos, seq_dev, ns, split_len, workspace, out, rin);
-  else
-    attn_decode_kernel<kUnroll, false><<<grid, 256, 0, s>>>(
-        q, k_cache, v_cache, n_heads, cache_slots, prompt_mask, prompt_len, row_holes,
-        kv_start, row_order, seq_pos, seq_dev, ns, split_len, workspace, out, rin);
+  const bool long_items = std::min(split_len, cache_slots) > kLongItem;
+#define MDL_DECODE(FUSED, NB)                                                                  \
+  attn_decode_kernel<FUSED, NB><<<grid, 256, 0, s>>>(                                          \
+      q, k_cache, v_cache, n_heads, cache_slots, prompt_mask, prompt_len, row_holes, kv_start, \
+      row_order, seq_pos, seq_dev, ns, split_len, workspace, out, rin)
+  if (fused) {
+    if (long_items) MDL_DECODE(true, 4);
+    else MDL_DECODE(true, 2);
+  } else {
+    if (long_items) MDL_DECODE(false, 4);
+    else MDL_DECODE(false, 2);
+  }
+#undef MDL_DECODE
   if (ns > 1)
     attn_decode_combine_kernel<<<dim3((n_bh + 3) / 4), 256, 0, s>>>(workspace, n_bh, n_heads,
                                                                      ns, out);

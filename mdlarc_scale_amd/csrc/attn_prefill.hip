@@ -30,41 +30,15 @@
 // all of that head's query tiles, and heads are dealt round-robin over the XCDs so that rows of
 // different lengths spread evenly.  Within a head the latest (most expensive) query tile runs
 // first.
-#include "common.h"
+#include "mfma.h"
 
 namespace mdl {
-
-typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
-typedef __bf16 bf16x4_t __attribute__((ext_vector_type(4)));
-typedef float f32x4_t __attribute__((ext_vector_type(4)));
-typedef short s16x4_t __attribute__((ext_vector_type(4)));
 
 constexpr int kQW = 32;          // queries per wave
 constexpr int kBM = 4 * kQW;     // queries per block
 constexpr int kBN = 64;          // keys per tile
 constexpr int kLds = 72;         // LDS row stride (bf16 elements): 144 B rows, 16 B aligned
 constexpr int kXcds = 8;
-constexpr float kLog2eP = 1.4426950408889634f;
-
-__device__ __forceinline__ bf16x8_t as_bf16x8(uint4 v) { return __builtin_bit_cast(bf16x8_t, v); }
-
-__device__ __forceinline__ s16x4_t lds_read_tr16(const uint16_t* p) {
-  return __builtin_amdgcn_ds_read_tr16_b64_v4i16(
-      (__attribute__((address_space(3))) s16x4_t*)(p));
-}
-
-// Maximum over lanes l, l^16, l^32, l^48 (one query's four lane groups) with gfx950's VALU lane
-// swaps: v_permlane16_swap / v_permlane32_swap of a value with itself return {x[l], x[l^16]} /
-// {x[l], x[l^32]} (checked on the GPU).  Replaces two ds_bpermute round trips through the LDS
-// unit on the softmax's critical path (measured 3% on the whole kernel, bit-identical).
-__device__ __forceinline__ float max_over_groups(float v) {
-  const auto a = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false,
-                                                  false);
-  v = fmaxf(__uint_as_float(a[0]), __uint_as_float(a[1]));
-  const auto b = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false,
-                                                  false);
-  return fmaxf(__uint_as_float(b[0]), __uint_as_float(b[1]));
-}
 
 __global__ __launch_bounds__(256, 3) void attn_prefill_kernel(
     const uint16_t* __restrict__ q, const uint16_t* __restrict__ kc,
@@ -114,7 +88,7 @@ __global__ __launch_bounds__(256, 3) void attn_prefill_kernel(
   const int kt0 = (kstart / kBN) * kBN;
   const int kend = causal ? min(S, q0 + kBM) : S;
   const uint8_t* mrow = kmask ? kmask + static_cast<int64_t>(b) * S : nullptr;
-  const bf16x8_t ones = as_bf16x8(make_uint4(0x3f803f80u, 0x3f803f80u, 0x3f803f80u, 0x3f803f80u));
+  const bf16x8_t ones = bf16_ones8();
 
   float m_run[2] = {-INFINITY, -INFINITY};
   f32x4_t lsum[2], o[2][4];
@@ -206,7 +180,7 @@ __global__ __launch_bounds__(256, 3) void attn_prefill_kernel(
 #pragma unroll
         for (int i = 0; i < 4; ++i) tmax = fmaxf(tmax, sc[j][nb][i]);
       tmax = max_over_groups(tmax);
-      const float mnew = fmaxf(m_run[j], tmax * kLog2eP);
+      const float mnew = fmaxf(m_run[j], tmax * kLog2eF);
       const float mb = (mnew == -INFINITY) ? 0.f : mnew;   // no visible key yet: p = 0
       const float alpha = __builtin_amdgcn_exp2f(m_run[j] - mb);
       m_run[j] = mnew;
@@ -217,13 +191,9 @@ __global__ __launch_bounds__(256, 3) void attn_prefill_kernel(
       for (int nb = 0; nb < 4; ++nb)
 #pragma unroll
         for (int i = 0; i < 4; ++i)
-          sc[j][nb][i] = __builtin_amdgcn_exp2f(fmaf(sc[j][nb][i], kLog2eP, -mb));
+          sc[j][nb][i] = __builtin_amdgcn_exp2f(fmaf(sc[j][nb][i], kLog2eF, -mb));
 #pragma unroll
-      for (int kk = 0; kk < 2; ++kk)
-        pb[j][kk] = bf16x8_t{(__bf16)sc[j][2 * kk][0], (__bf16)sc[j][2 * kk][1],
-                             (__bf16)sc[j][2 * kk][2], (__bf16)sc[j][2 * kk][3],
-                             (__bf16)sc[j][2 * kk + 1][0], (__bf16)sc[j][2 * kk + 1][1],
-                             (__bf16)sc[j][2 * kk + 1][2], (__bf16)sc[j][2 * kk + 1][3]};
+      for (int kk = 0; kk < 2; ++kk) pb[j][kk] = pt_operand(sc[j][2 * kk], sc[j][2 * kk + 1]);
     }
 
     // O^T += V^T P^T and the row sums, two k-steps of 32 keys
@@ -231,12 +201,7 @@ __global__ __launch_bounds__(256, 3) void attn_prefill_kernel(
     for (int kk = 0; kk < 2; ++kk) {
 #pragma unroll
       for (int db = 0; db < 4; ++db) {
-        const int r0 = 32 * kk + 4 * g + (c16 >> 2);
-        const int cc = 16 * db + 4 * (c16 & 3);
-        const s16x4_t lo4 = lds_read_tr16(&Vs[r0 * kLds + cc]);
-        const s16x4_t hi4 = lds_read_tr16(&Vs[(r0 + 16) * kLds + cc]);
-        const bf16x8_t a = __builtin_bit_cast(
-            bf16x8_t, __builtin_shufflevector(lo4, hi4, 0, 1, 2, 3, 4, 5, 6, 7));
+        const bf16x8_t a = vt_operand(Vs, kLds, kk, db, c16, g);
         o[0][db] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, pb[0][kk], o[0][db], 0, 0, 0);
         o[1][db] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, pb[1][kk], o[1][db], 0, 0, 0);
       }
