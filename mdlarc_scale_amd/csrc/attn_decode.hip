@@ -165,7 +165,10 @@ __global__ __launch_bounds__(256) void attn_decode_kernel(
           sc[nb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf16x8(kf[nb][kk]), qf[kk],
                                                            sc[nb], 0, 0, 0);
       }
-      // the previous tile's transposing reads of Vw are done before it is overwritten
+      // Vw is this wave's alone, and LDS operations of one wavefront execute in issue order, so
+      // program order is all that the tile hand-over needs: the wavefront-scope fences keep the
+      // compiler from moving the stores above the previous tile's transposing reads (here) or
+      // below this tile's (further down)
       __builtin_amdgcn_fence(__ATOMIC_ACQ_REL, "wavefront");
       __builtin_amdgcn_wave_barrier();
 #pragma unroll
@@ -203,7 +206,7 @@ __global__ __launch_bounds__(256) void attn_decode_kernel(
       bf16x8_t pb[NB / 2];
 #pragma unroll
       for (int kk = 0; kk < NB / 2; ++kk) pb[kk] = pt_operand(sc[2 * kk], sc[2 * kk + 1]);
-      // the staged V tile is visible to the whole wave
+      // the staged V tile is visible to the whole wave (program order, as above)
       __builtin_amdgcn_fence(__ATOMIC_ACQ_REL, "wavefront");
       __builtin_amdgcn_wave_barrier();
 #pragma unroll
