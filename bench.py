@@ -303,8 +303,8 @@ def main() -> int:
     args = _args()
     if args.gpus != 1:
         print("bench.py runs on exactly one GPU: this build measures the single-GPU hot path "
-              "(decode rows shard by batch with no exchange; see DESIGN.md). Use --gpus 1.",
-              file=sys.stderr)
+              "(decode rows would shard by batch across GPUs with no exchange, so one GPU's "
+              "throughput is the per-GPU figure). Use --gpus 1.", file=sys.stderr)
         return 2
     import torch
 
@@ -460,12 +460,12 @@ def main() -> int:
         "data": "synthetic",
         "config": {
             "workload": WORKLOADS[spec.name],
-            "model": spec.preset, "global_batch": B, "seq_len": S, "cache_slots": total,
+            "preset": spec.preset, "rows": B, "padded_prompt_slots": S, "cache_slots": total,
             "decode_steps_available": max_new - 1, "timed_cache_fill": [t_first,
                                                                         t_first + args.steps],
             "prompt_len_min": int(n_valid.min()), "prompt_len_mean": round(float(
                 n_valid.float().mean()), 1), "prompt_len_max": int(n_valid.max()),
-            "parallelism": "single GPU (rows shard by batch across GPUs, no exchange)",
+            "sharding": "one GPU (rows would shard by batch across GPUs, no exchange)",
             "graph": not args.eager, "workload_seed": spec.seed,
         },
         "roofline": {

@@ -5,7 +5,7 @@
  * The reference has no FFI: its boundary is the PyTorch module / function API of
  * src/transformer.py and src/inference.py.  Each entry point below replaces the reference ops
  * named in its comment (file:line in the reference checkout).  The host side
- * (mdlarc_scale_amd/, Python) binds these with ctypes; INTEGRATION.md shows the binding.
+ * (mdlarc_scale_amd/_lib.py, Python) binds these with ctypes.
  *
  * Conventions
  *   - bf16 tensors are passed as uint16_t* (raw bfloat16 bits), fp32 as float*.
