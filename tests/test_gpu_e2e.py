@@ -359,6 +359,49 @@ def test_forward_non_causal_vs_oracle():
     assert err <= 2e-2
 
 
+def test_autograd_forward_on_gpu():
+    """With autograd on -- test-time adaptation of the example embedding, src/eval.py:144-215 --
+    forward composes torch ops on the GPU instead of the kernels: its logits agree with the
+    kernel path to the parity bar, and the gradient reaches exactly the example-embedding rows
+    the batch uses."""
+    from mdlarc_scale_amd import create_tiny_model
+
+    torch.manual_seed(3)
+    m = create_tiny_model(dropout=0.0)
+    with torch.no_grad():                            # the kernels' GEMM operands are bf16
+        for p in m.parameters():
+            p.copy_(p.to(torch.bfloat16).float())
+    state = {k: v.clone() for k, v in m.state_dict().items()}
+    m = m.to(DEV).eval()
+    rng = np.random.default_rng(3)
+    prompts = _random_prompts(rng, 3, 2, 2, 5)
+    L = min(len(p) for p in prompts)
+    ids = torch.tensor([p[-L:] for p in prompts], dtype=torch.long)
+    pos = torch.stack([torch.from_numpy(odf.compute_positions_3d(p[-L:])) for p in prompts])
+    ids, pos = ids.to(DEV), pos.to(DEV)
+    ex = torch.tensor([4, 9, 4], device=DEV)
+    with torch.no_grad():
+        kern = m(ids, pos, ex, None, True).float()
+    m.zero_grad(set_to_none=True)
+    out = m(ids, pos, ex, None, True)
+    assert out.requires_grad
+    c = m.config
+    om = rp.OracleModel(rp.OracleConfig(c.d_model, c.n_heads, c.n_layers, c.d_ff,
+                                        c.num_examples, c.max_seq_len), state)
+    ref = om.forward(ids.cpu(), pos.cpu(), ex.cpu(), None, True)
+    e_kern = (kern.cpu() - ref).abs().max().item()
+    e_grad = (out.detach().float().cpu() - ref).abs().max().item()
+    print(f"logits max-abs vs the fp32 oracle: kernel path {e_kern:.3e}, autograd path "
+          f"{e_grad:.3e}")
+    assert e_kern <= 2e-2 and e_grad <= 2e-2
+    out.float().logsumexp(-1).mean().backward()
+    g = m.example_embed.weight.grad
+    used = torch.zeros(g.shape[0], dtype=torch.bool, device=DEV)
+    used[ex] = True
+    assert bool(torch.isfinite(g).all())
+    assert bool((g[used].abs().sum(1) > 0).all()) and bool((g[~used] == 0).all())
+
+
 @pytest.mark.parametrize("stop_on_end", [True, False])
 def test_graph_replay_matches_eager_launches(stop_on_end):
     """Greedy decode replayed from one captured HIP graph returns exactly the tokens of the
