@@ -193,6 +193,27 @@ int mdl_attn_prefill_packed(const uint16_t* q, const uint16_t* k_cache, const ui
                             const int32_t* q_offset, int causal, uint16_t* out, void* stream);
 
 /*
+ * K4c -- exact (fp32) causal attention for the lead queries of each row, after K4a.
+ * Replaces: the same SDPA call as mdl_attn_prefill (src/inference.py:409; src/transformer.py:
+ *           333-349 with is_causal=True) for the first 64 queries at or after kv_start[b]: those
+ *           see at most 64 keys, so K4a's bf16 roundings of q, K, V and the probabilities are
+ *           not averaged away there.
+ * qkv / rstd / pos: the projection GEMM's fp32 output and the inputs K2 consumed
+ *   (mdl_qkv_rope_cache, same layout and rope arguments; q_scale as there).  Token position i
+ *   of row b is row b*seq + i of them and of out, or, with q_offset (packed rows; kv_start then
+ *   required), row q_offset[b] + i - kv_start[b].
+ * Recomputes q, k, v of those tokens in fp32 (RMSNorm scale, 3D RoPE, softmax scale), applies
+ * the key mask as mdl_attn_prefill does and overwrites the split output rows of the first
+ * min(64, seq - kv_start[b]) queries; every other row of out is left as it is.
+ */
+int mdl_attn_prefill_lead(const float* qkv, int64_t qkv_ld, const float* rstd,
+                          const int64_t* pos, const float* rope_tab, int max_x, int max_y,
+                          int max_z, int px, int py, int pz, float q_scale, int batch, int seq,
+                          int n_heads, int head_dim, const uint8_t* key_mask,
+                          const int32_t* kv_start, const int32_t* q_offset, uint16_t* out,
+                          void* stream);
+
+/*
  * K4b -- decode attention over the static cache (split-K flash decoding on bf16 MFMA: QK^T with
  * K straight from HBM as the A operand, PV with V staged through LDS; the probabilities enter
  * the PV product rounded to bf16).

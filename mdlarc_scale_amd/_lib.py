@@ -49,6 +49,9 @@ SIGNATURES: dict[str, tuple[object, list]] = {
     "mdl_attn_prefill": (c_int, [P, P, P, c_int, c_int, c_int, c_int, c_int, P, P, c_int, P, P]),
     "mdl_attn_prefill_packed": (c_int, [P, P, P, c_int, c_int, c_int, c_int, c_int, P, P, P,
                                         c_int, P, P]),
+    "mdl_attn_prefill_lead": (c_int, [P, c_int64, P, P, P, c_int, c_int, c_int, c_int, c_int,
+                                      c_int, c_float, c_int, c_int, c_int, c_int, P, P, P, P,
+                                      P]),
     "mdl_attn_decode_workspace_bytes": (c_int64, [c_int, c_int, c_int, c_int]),
     "mdl_attn_decode": (c_int, [P, P, P, c_int, c_int, c_int, c_int, P, c_int, P, P, P, c_int,
                                 P, P, c_int64, c_int, P, P]),

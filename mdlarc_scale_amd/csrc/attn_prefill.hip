@@ -31,6 +31,7 @@
 // different lengths spread evenly.  Within a head the latest (most expensive) query tile runs
 // first.
 #include "mfma.h"
+#include "rope.h"
 
 namespace mdl {
 
@@ -232,6 +233,135 @@ __global__ __launch_bounds__(256, 3) void attn_prefill_kernel(
   }
 }
 
+// K4c -- exact attention for the lead queries of each row.
+//
+// The first queries of a row attend to few keys: query kv_start + r sees at most r + 1 of them,
+// so the bf16 roundings of q, K, V and of the probabilities in K4a are not averaged away (at the
+// first query the output is one bf16-rounded V row).  This pass recomputes, for each (b, h), the
+// outputs of the kLead queries from kv_start on in fp32 from the projection GEMM's fp32 output:
+// the same RMSNorm scale, 3D RoPE and softmax scale K2 applies, then exact masked softmax and PV.
+// Those queries see only keys among the same kLead tokens (causal), so one block holds them all
+// in LDS.  Later queries average over more than kLead keys and keep K4a's output.
+//
+// Block = one (b, h), 256 threads: thread t owns query t/4 and dims 16 (t%4) .. +15.  It first
+// rotates those dims of its own token's q (kept in registers) and k (to LDS) -- RoPE pairs
+// 8 (t%4) .. +7 -- and scales its v dims (to LDS).  Then, with K and V rows read as float4, a
+// first pass over the visible keys finds the score maximum and a second one accumulates
+// exp(s - max) and P V; each dot product is summed over the query's 4 threads with 2 xor
+// shuffles.  A wave's loop stops at the wave's last query (keys after it are in every query's
+// future).
+constexpr int kLead = 64;
+constexpr int kLeadLd = kHeadDim + 4;   // LDS row stride (floats): 16-byte aligned rows
+
+__global__ __launch_bounds__(256) void attn_lead_kernel(
+    const float* __restrict__ qkv, int64_t ld, const float* __restrict__ rstd,
+    const int64_t* __restrict__ pos, const float* __restrict__ tab, RopeArgs ra, float q_scale,
+    int S, int H, const uint8_t* __restrict__ kmask, const int32_t* __restrict__ kv_start,
+    const int32_t* __restrict__ q_offset, uint16_t* __restrict__ out) {
+  const int bh = blockIdx.x;
+  const int b = bh / H, h = bh - b * H;
+  const int kstart = kv_start ? min(max(kv_start[b], 0), S) : 0;
+  const int n = min(kLead, S - kstart);
+  if (n <= 0) return;
+  // token row of position kstart + r in qkv / rstd / pos and out (packed or [batch, seq])
+  const int64_t row0 = (q_offset ? static_cast<int64_t>(q_offset[b]) - kstart
+                                 : static_cast<int64_t>(b) * S) + kstart;
+  const int64_t d = static_cast<int64_t>(H) * kHeadDim;
+  __shared__ __attribute__((aligned(16))) float ks[kLead * kLeadLd];
+  __shared__ __attribute__((aligned(16))) float vs[kLead * kLeadLd];
+  __shared__ uint8_t ok[kLead];
+  const int t = threadIdx.x;
+  const int r = t >> 2, part = t & 3;
+  float q[16];
+  if (r < n) {
+    const int64_t row = row0 + r;
+    const float rs = rstd[row];
+    const float* src = qkv + row * ld + h * kHeadDim + 16 * part;
+    float qa[16], ka[16], va[16];
+#pragma unroll
+    for (int c = 0; c < 4; ++c) {
+      *reinterpret_cast<float4*>(qa + 4 * c) = *reinterpret_cast<const float4*>(src + 4 * c);
+      *reinterpret_cast<float4*>(ka + 4 * c) = *reinterpret_cast<const float4*>(src + d + 4 * c);
+      *reinterpret_cast<float4*>(va + 4 * c) =
+          *reinterpret_cast<const float4*>(src + 2 * d + 4 * c);
+    }
+    float kr[16];
+#pragma unroll
+    for (int pp = 0; pp < 8; ++pp) {
+      float cs, sn;
+      rope_cos_sin(part * 8 + pp, pos + row * 3, tab, ra, cs, sn);
+      const float q0 = qa[2 * pp] * rs, q1 = qa[2 * pp + 1] * rs;
+      const float k0 = ka[2 * pp] * rs, k1 = ka[2 * pp + 1] * rs;
+      q[2 * pp] = (q0 * cs - q1 * sn) * q_scale;
+      q[2 * pp + 1] = (q1 * cs + q0 * sn) * q_scale;
+      kr[2 * pp] = k0 * cs - k1 * sn;
+      kr[2 * pp + 1] = k1 * cs + k0 * sn;
+      va[2 * pp] *= rs;
+      va[2 * pp + 1] *= rs;
+    }
+#pragma unroll
+    for (int c = 0; c < 4; ++c) {
+      *reinterpret_cast<float4*>(ks + r * kLeadLd + 16 * part + 4 * c) =
+          *reinterpret_cast<const float4*>(kr + 4 * c);
+      *reinterpret_cast<float4*>(vs + r * kLeadLd + 16 * part + 4 * c) =
+          *reinterpret_cast<const float4*>(va + 4 * c);
+    }
+    if (part == 0) ok[r] = !kmask || kmask[static_cast<int64_t>(b) * S + kstart + r] != 0;
+  }
+  __syncthreads();
+  if (r >= n) return;   // no barrier follows; the rest of the 4-thread group returns with it
+  // queries of this wave: 16 (t / 64) .. +15; no key after the wave's last query is visible
+  const int jend = min(16 * (t >> 6) + 15, n - 1);
+
+  auto dot = [&](int j) {
+    const float4* kr = reinterpret_cast<const float4*>(ks + j * kLeadLd + 16 * part);
+    float a = 0.f;
+#pragma unroll
+    for (int c = 0; c < 4; ++c) {
+      const float4 k4 = kr[c];
+      a = fmaf(q[4 * c], k4.x, a);
+      a = fmaf(q[4 * c + 1], k4.y, a);
+      a = fmaf(q[4 * c + 2], k4.z, a);
+      a = fmaf(q[4 * c + 3], k4.w, a);
+    }
+    a += __shfl_xor(a, 1, kWave);
+    return a + __shfl_xor(a, 2, kWave);
+  };
+  float mx = -INFINITY;
+  for (int j = 0; j <= jend; ++j) {
+    const float s = dot(j);
+    if (j <= r && ok[j]) mx = fmaxf(mx, s);
+  }
+  float l = 0.f, o[16];
+#pragma unroll
+  for (int e = 0; e < 16; ++e) o[e] = 0.f;
+  for (int j = 0; j <= jend; ++j) {
+    const float s = dot(j);
+    if (j <= r && ok[j]) {
+      const float pj = expf(s - mx);
+      l += pj;
+      const float4* vr = reinterpret_cast<const float4*>(vs + j * kLeadLd + 16 * part);
+#pragma unroll
+      for (int c = 0; c < 4; ++c) {
+        const float4 v4 = vr[c];
+        o[4 * c] = fmaf(pj, v4.x, o[4 * c]);
+        o[4 * c + 1] = fmaf(pj, v4.y, o[4 * c + 1]);
+        o[4 * c + 2] = fmaf(pj, v4.z, o[4 * c + 2]);
+        o[4 * c + 3] = fmaf(pj, v4.w, o[4 * c + 3]);
+      }
+    }
+  }
+  const float inv = l > 0.f ? 1.f / l : 0.f;   // no visible key: 0, as in K4a
+  uint16_t* op = out + (row0 + r) * 2 * d + h * kHeadDim + 16 * part;
+#pragma unroll
+  for (int e = 0; e < 16; e += 2) {
+    uint32_t hi, lo;
+    split_bf2(o[e] * inv, o[e + 1] * inv, hi, lo);
+    *reinterpret_cast<uint32_t*>(op + e) = hi;
+    *reinterpret_cast<uint32_t*>(op + d + e) = lo;
+  }
+}
+
 }  // namespace mdl
 
 using namespace mdl;
@@ -281,4 +411,29 @@ extern "C" int mdl_attn_prefill_packed(const uint16_t* q, const uint16_t* k_cach
   return launch_prefill(q, k_cache, v_cache, batch, seq, n_heads, head_dim, cache_slots,
                         key_mask, kv_start, q_offset, causal, out,
                         static_cast<hipStream_t>(stream));
+}
+
+extern "C" int mdl_attn_prefill_lead(const float* qkv, int64_t qkv_ld, const float* rstd,
+                                     const int64_t* pos, const float* rope_tab, int max_x,
+                                     int max_y, int max_z, int px, int py, int pz, float q_scale,
+                                     int batch, int seq, int n_heads, int head_dim,
+                                     const uint8_t* key_mask, const int32_t* kv_start,
+                                     const int32_t* q_offset, uint16_t* out, void* stream) {
+  if (!qkv || !rstd || !pos || !rope_tab || !out) return MDL_ERR_NULL;
+  if (q_offset && !kv_start) return MDL_ERR_NULL;
+  if (head_dim != kHeadDim) return MDL_ERR_HEAD_DIM;
+  if (batch < 0 || seq < 0 || n_heads <= 0 || max_x <= 0 || max_y <= 0 || max_z <= 0 ||
+      px < 0 || py < 0 || pz < 0 || px + py + pz != kHeadDim / 2 ||
+      qkv_ld < 3 * static_cast<int64_t>(n_heads) * kHeadDim)
+    return MDL_ERR_SHAPE;
+  if (!aligned16(qkv) || qkv_ld % 4 != 0 || !aligned4(out) || !aligned4(rope_tab))
+    return MDL_ERR_ALIGN;
+  const int64_t blocks = static_cast<int64_t>(batch) * n_heads;
+  if (blocks == 0 || seq == 0) return MDL_OK;
+  if (blocks > 0x7fffffff) return MDL_ERR_SHAPE;
+  const RopeArgs ra{max_x, max_y, max_z, px, py, pz};
+  attn_lead_kernel<<<static_cast<unsigned>(blocks), 256, 0, static_cast<hipStream_t>(stream)>>>(
+      qkv, qkv_ld, rstd, pos, rope_tab, ra, q_scale, seq, n_heads, key_mask, kv_start, q_offset,
+      out);
+  return launch_status();
 }

@@ -6,6 +6,7 @@ Dataflow per layer (M token rows, d channels, F ffn width; fp32 residual stream 
     qkv = xs @ [W_qkv|W_qkv]^T       (hipBLASLt, bf16 x bf16 -> fp32)            [M, 3d] fp32
     K2: q = rope(rstd*q)/8 -> [M, d] bf16; k, v = rope(rstd*k), rstd*v -> bf16 cache slots
     attn = K4(q, cache)              (prefill: MFMA flash; decode: split-K)      [M, 2d] bf16
+           (prefill: the first 64 queries of each row recomputed exactly in fp32, K4c)
     delta = attn @ [W_out|W_out]^T                                              [M, d] fp32
     x += delta; xs = split(x * g2), rstd                           <- add_rmsnorm
     gu = xs @ [W_gu|W_gu]^T          (gate and up concatenated)                  [M, 2F] fp32
@@ -232,6 +233,9 @@ class HipEngine:
             K.qkv_rope_cache(sc.qkv, sc.rstd, pos, W.rope_tab, W.rope_geom, B, S, H, qs, sc.q,
                              kc, vc, slot0=0)
             K.attn_prefill(sc.q, kc, vc, B, S, H, key_mask, kv_start, causal, sc.attn)
+            if causal:
+                K.attn_prefill_lead(sc.qkv, sc.rstd, pos, W.rope_tab, W.rope_geom, qs, B, S, H,
+                                    key_mask, kv_start, None, B * S, sc.attn)
             self._mlp(W, li, sc)
 
     def run_packed(self, W: PackedWeights, ids: torch.Tensor, pos: torch.Tensor,
@@ -261,6 +265,8 @@ class HipEngine:
                                     pk.token_row, pk.token_slot, H, qs, sc.q, kc, vc)
             K.attn_prefill_packed(sc.q, kc, vc, B, S, H, key_mask, kv_start, pk.q_offset,
                                   pk.n_valid, True, sc.attn)
+            K.attn_prefill_lead(sc.qkv, sc.rstd, pos_p, W.rope_tab, W.rope_geom, qs, B, S, H,
+                                key_mask, kv_start, pk.q_offset, pk.n_tokens, sc.attn)
             self._mlp(W, li, sc)
 
     def _mlp(self, W: PackedWeights, li: int, sc: Scratch) -> None:
@@ -293,14 +299,20 @@ class HipEngine:
             ex_ids = ex_ids.to(device=dev, dtype=torch.int64).contiguous()
         self._validate_ids(ids, ex_ids)
         W = self.packed(dev)
-        mask = None
+        mask, kv_start = None, None
         if attention_mask is not None:
             mask = attention_mask.to(device=dev, dtype=torch.bool).to(torch.uint8).contiguous()
+            # each row's first valid position: the attention skips the keys before it and the
+            # lead-query pass starts there
+            first = mask.to(torch.int32).argmax(1)
+            kv_start = torch.where(mask.bool().any(1), first, torch.full_like(first, S)).to(
+                torch.int32).contiguous()
         H = cfg.n_heads
         kbuf = torch.empty(B, H, S, 64, dtype=torch.bfloat16, device=dev)
         vbuf = torch.empty_like(kbuf)
         sc = Scratch.alloc(B * S, cfg.d_model, cfg.d_ff, dev)
-        self.run_prompt(W, ids, pos, ex_ids, mask, None, is_causal, lambda li: (kbuf, vbuf), sc)
+        self.run_prompt(W, ids, pos, ex_ids, mask, kv_start, is_causal, lambda li: (kbuf, vbuf),
+                        sc)
         logits = torch.empty(B * S, cfg.vocab_size, dtype=torch.float32, device=dev)
         K.lm_head(sc.x, None, B * S, W.ln_f, W.eps, W.head, logits, None)
         return logits.view(B, S, cfg.vocab_size)

@@ -239,6 +239,35 @@ def attn_prefill_packed(q: torch.Tensor, k_cache: torch.Tensor, v_cache: torch.T
         "mdl_attn_prefill_packed")
 
 
+def attn_prefill_lead(qkv: torch.Tensor, rstd: torch.Tensor, pos: torch.Tensor,
+                      rope_tab: torch.Tensor, rope_geom: tuple[int, int, int, int, int, int],
+                      q_scale: float, batch: int, seq: int, n_heads: int,
+                      key_mask: torch.Tensor | None, kv_start: torch.Tensor | None,
+                      q_offset: torch.Tensor | None, n_rows: int, out: torch.Tensor) -> None:
+    """Exact fp32 causal attention for the first 64 queries at or after kv_start of each row,
+    overwriting those rows of ``out`` (after attn_prefill / attn_prefill_packed).  ``qkv`` /
+    ``rstd`` / ``pos`` hold the n_rows token rows K2 consumed; rows are [batch, seq] or, with
+    q_offset, packed."""
+    d = n_heads * HEAD_DIM
+    _need(qkv, "qkv", F32, n_rows * 3 * d)
+    if qkv.dim() != 2 or qkv.shape[1] != 3 * d:
+        raise ValueError(f"qkv must be [rows, {3 * d}]")
+    _need(rstd, "rstd", F32, n_rows)
+    _need(pos, "pos", I64, n_rows * 3)
+    _need(rope_tab, "rope_tab", F32)
+    _need(out, "out", BF16, n_rows * 2 * d)
+    _need(key_mask, "key_mask", U8, batch * seq, optional=True)
+    _need(kv_start, "kv_start", I32, batch, optional=q_offset is None)
+    _need(q_offset, "q_offset", I32, batch, optional=True)
+    if q_offset is None and n_rows < batch * seq:
+        raise ValueError("unpacked rows need batch * seq rows")
+    mx, my, mz, px, py, pz = rope_geom
+    _lib.check(_lib.lib().mdl_attn_prefill_lead(
+        _p(qkv), qkv.shape[1], _p(rstd), _p(pos), _p(rope_tab), mx, my, mz, px, py, pz, q_scale,
+        batch, seq, n_heads, HEAD_DIM, _p(key_mask), _p(kv_start), _p(q_offset), _p(out),
+        _stream()), "mdl_attn_prefill_lead")
+
+
 def attn_decode_workspace_bytes(batch: int, n_heads: int, slots: int, split_len: int) -> int:
     return int(_lib.lib().mdl_attn_decode_workspace_bytes(batch, n_heads, slots, split_len))
 

@@ -60,5 +60,12 @@ def test_argument_errors_are_reported_before_any_launch():
                                        32, 8, 10, 10, 12, 0.125, fake, fake, fake, 4, None) == -1
     assert L.mdl_qkv_rope_cache_packed(fake, 192, None, fake, fake, 4, fake, fake, 1, 1, 32, 32,
                                        32, 8, 10, 10, 12, 0.125, fake, fake, fake, 4, None) == -4
+    # exact lead attention: q_offset needs kv_start; head_dim 64 only; qkv rows 16-byte aligned
+    assert L.mdl_attn_prefill_lead(fake, 192, fake, fake, fake, 32, 32, 8, 10, 10, 12, 0.125, 1, 4,
+                                   1, 64, None, None, fake, fake, None) == -1
+    assert L.mdl_attn_prefill_lead(fake, 96, fake, fake, fake, 32, 32, 8, 10, 10, 12, 0.125, 1, 4,
+                                   1, 32, None, None, None, fake, None) == -4
+    assert L.mdl_attn_prefill_lead(fake, 194, fake, fake, fake, 32, 32, 8, 10, 10, 12, 0.125, 1, 4,
+                                   1, 64, None, None, None, fake, None) == -2
     with pytest.raises(RuntimeError, match="head_dim"):
         _lib.check(-4, "probe")

@@ -428,6 +428,81 @@ def test_attn_prefill_packed_equals_padded(causal):
     assert bool((out_pk[pk.n_valid:] == 3).all())
 
 
+@pytest.mark.parametrize("packed", [False, True])
+def test_attn_prefill_lead_exact(packed):
+    """K4c: the first 64 queries at or after kv_start of each row come out as exact causal
+    attention (fp64 reference from the same fp32 projection output: RMSNorm scale, 3D RoPE,
+    softmax scale 1/8, key mask with holes) to fp32 rounding; every other output row keeps K4a's
+    value bit for bit."""
+    from mdlarc_scale_amd.transformer import RotaryEmbedding3D
+
+    g = torch.Generator().manual_seed(5 + packed)
+    B, H, S, slots = 5, 3, 150, 160
+    d = 64 * H
+    cfg = _cfg(d, H)
+    kv = [0, 40, 149, 150, 100]
+    mask = torch.ones(B, S, dtype=torch.bool)
+    for b, k0 in enumerate(kv):
+        mask[b, :k0] = False
+    mask[0, 3:6] = False                       # holes among the lead keys
+    mask[4, 110:112] = False
+    qkv = torch.randn(B * S, 3 * d, generator=g)
+    rstd = 0.5 + torch.rand(B * S, generator=g)
+    pos = torch.randint(0, 31, (B * S, 3), generator=g)
+    rope = RotaryEmbedding3D(64, cfg.max_x, cfg.max_y, cfg.max_z)
+    tab = rope.device_table(DEV)
+    geom = (rope.max_x, rope.max_y, rope.max_z, rope.px, rope.py, rope.pz)
+    kv_dev = torch.tensor(kv, dtype=torch.int32, device=DEV)
+    mask8 = mask.to(torch.uint8).to(DEV)
+    kc = torch.zeros(B, H, slots, 64, device=DEV, dtype=torch.bfloat16)
+    vc = torch.zeros_like(kc)
+    if packed:
+        pk = _pack(kv, B, S)
+        gi = pk.gather.long().cpu()
+        rows = pk.n_tokens
+        qkv_r, rstd_r, pos_r = qkv[gi], rstd[gi], pos[gi]
+        q = torch.empty(rows, d, device=DEV, dtype=torch.bfloat16)
+        K().qkv_rope_cache_packed(qkv_r.to(DEV), rstd_r.to(DEV), pos_r.to(DEV), tab, geom,
+                                  pk.token_row, pk.token_slot, H, 0.125, q, kc, vc)
+        out = torch.full((rows, 2 * d), 5.0, device=DEV, dtype=torch.bfloat16)
+        K().attn_prefill_packed(q, kc, vc, B, S, H, mask8, kv_dev, pk.q_offset, pk.n_valid,
+                                True, out)
+        row_of = lambda b, i: int(pk.q_offset[b]) + i - kv[b]   # noqa: E731
+    else:
+        rows = B * S
+        qkv_r, rstd_r, pos_r = qkv, rstd, pos
+        q = torch.empty(rows, d, device=DEV, dtype=torch.bfloat16)
+        K().qkv_rope_cache(qkv.to(DEV), rstd.to(DEV), pos.to(DEV), tab, geom, B, S, H, 0.125, q,
+                           kc, vc)
+        out = torch.empty(rows, 2 * d, device=DEV, dtype=torch.bfloat16)
+        K().attn_prefill(q, kc, vc, B, S, H, mask8, kv_dev, True, out)
+        row_of = lambda b, i: b * S + i                            # noqa: E731
+    before = out.clone()
+    K().attn_prefill_lead(qkv_r.to(DEV), rstd_r.to(DEV), pos_r.to(DEV), tab, geom, 0.125, B, S,
+                          H, mask8, kv_dev, pk.q_offset if packed else None, rows, out)
+    torch.cuda.synchronize()
+    # fp64 reference over the padded batch
+    y = (qkv.double() * rstd.double()[:, None]).view(B, S, 3, H, 64)
+    tabs = rp.rope3d_tables(cfg)
+    p3 = pos.view(B, S, 3)
+    qr = rp.apply_rope3d(y[:, :, 0], p3, tabs, cfg).double()
+    kr = rp.apply_rope3d(y[:, :, 1], p3, tabs, cfg).double()
+    vis = mask.clone()
+    for b, k0 in enumerate(kv):
+        vis[b, :k0] = False
+    ref = rp.attention(qr.transpose(1, 2), kr.transpose(1, 2), y[:, :, 2].transpose(1, 2), vis,
+                       True).transpose(1, 2)                           # [B, S, H, 64]
+    got = unsplit(out).view(rows, H, 64)
+    lead = torch.zeros(rows, dtype=torch.bool)
+    for b, k0 in enumerate(kv):
+        for i in range(k0, min(k0 + 64, S)):
+            r = row_of(b, i)
+            lead[r] = True
+            err = (got[r].double() - ref[b, i]).abs()
+            assert bool((err <= 1e-5 + 1e-5 * ref[b, i].abs()).all()), (b, i, err.max().item())
+    assert torch.equal(out[~lead.to(DEV)], before[~lead.to(DEV)])
+
+
 # ---------------------------------------------------------------------------- K4b decode
 
 @pytest.mark.parametrize("split_len,slots,t", [(128, 700, 611), (256, 700, 611),
