@@ -397,7 +397,8 @@ def main() -> int:
             kc, vc = st.cache.layer(li)
             K.attn_decode_rope(st.sc.qkv, st.sc.rstd, st.pos, W.rope_tab, W.rope_geom, qs, kc,
                                vc, B, H, st.pmask, S, st.kv_start, t, None, st.ws, st.split_len,
-                               st.sc.attn, row_holes=st.holes, row_order=st.order)
+                               st.sc.attn, row_holes=st.holes, row_order=st.order,
+                               tiled=st.sc.tiled)
         ta.stop()
         attn_ms = ta.ms() / len(ts)
         attn_bytes = sum(decode_attention_bytes(B, H, t, kv_start_h, S, holes_h)

@@ -19,6 +19,12 @@
  *     weight packed as [W | W] ([N, 2K] bf16) a bf16 GEMM with fp32 accumulation returns
  *     (hi + lo) . w, i.e. the fp32 activation against the bf16 weight.  GEMM outputs are
  *     consumed in fp32.
+ *   - MDL_LAYOUT_TILES stores a [rows, C] bf16 matrix (C a multiple of 32; the split
+ *     activation has C = 2K) as 16 x 32 blocks of 1 KB, block (r / 16, c / 32) at element
+ *     512 * ((r / 16) * (C / 32) + c / 32); inside a block, row r % 16, columns 8 q .. 8 q + 7
+ *     (q = (c / 8) % 4) are the 16 bytes at element 8 * (16 q + r % 16).  Each block is then one
+ *     v_mfma_f32_16x16x32_bf16 operand in lane order and a wave loads it as one contiguous
+ *     kilobyte.  Buffers hold ceil(rows / 16) * 16 rows; rows past `rows` are never written.
  *   - KV cache layout is the reference StaticKVCache layout (src/inference.py:73-77):
  *     one layer's K (or V) is [batch, n_heads, cache_slots, 64] bf16, slot-major rows of 128 B.
  */
@@ -42,6 +48,10 @@ extern "C" {
 
 #define MDL_DTYPE_F32 0
 #define MDL_DTYPE_BF16 1
+
+/* Layout of a split activation written by a producer entry point (its *_layout argument). */
+#define MDL_LAYOUT_ROWS 0          /* row-major [rows, 2K]: hi in columns [0, K), lo in [K, 2K) */
+#define MDL_LAYOUT_TILES 1         /* the same matrix in MFMA tiles (see the conventions) */
 
 /*
  * Soft decoding constraints on a row's logits, applied before the argmax in the order of
@@ -79,12 +89,13 @@ const char* mdl_error_string(int code);
  *   rstd[m]  = 1 / sqrt(mean(x[m]^2) + eps)
  *   xs[m]    = split(x[m] * gamma)       bf16 [rows, 2d] (GEMM input; rstd is applied after
  *                                        the GEMM).  xs_out may be NULL.
+ * xs_layout: MDL_LAYOUT_ROWS, or MDL_LAYOUT_TILES (d a multiple of 16) for mdl_gemm_split.
  * Tables are fp32 or bf16 (table_dtype); ids are clamped into range (callers validate first).
  */
 int mdl_embed_rmsnorm(const int64_t* ids, const int64_t* example_ids, const void* tok_table,
                       const void* ex_table, int table_dtype, int vocab, int n_examples, int rows,
                       int row_len, int d, const float* gamma, float eps, float* x_out,
-                      uint16_t* xs_out, float* rstd_out, void* stream);
+                      uint16_t* xs_out, float* rstd_out, int xs_layout, void* stream);
 
 /*
  * Decode-step entry: grid position of the token each row just emitted, then K1 on that token.
@@ -92,13 +103,15 @@ int mdl_embed_rmsnorm(const int64_t* ids, const int64_t* example_ids, const void
  *           blocks[0].ln1 of _decode_step (src/inference.py:433-437).
  * Per row b: pos_out[b] = position of token[b] from the state (gx, gy, in_out), the state
  * advances past it (the rule of mdl_grid_step), then x / xs / rstd as mdl_embed_rmsnorm with
- * row_len = 1.  counters (int32[2], may be NULL) are incremented by one, as by mdl_grid_step.
+ * row_len = 1 and xs_layout as there.  counters (int32[2], may be NULL) are incremented by one,
+ * as by mdl_grid_step.
  */
 int mdl_decode_embed(const int64_t* token, const int64_t* example_ids, const void* tok_table,
                      const void* ex_table, int table_dtype, int vocab, int n_examples, int batch,
                      int d, const float* gamma, float eps, int32_t* gx, int32_t* gy,
                      uint8_t* in_out, int max_x, int max_y, int64_t* pos_out, int32_t* counters,
-                     float* x_out, uint16_t* xs_out, float* rstd_out, void* stream);
+                     float* x_out, uint16_t* xs_out, float* rstd_out, int xs_layout,
+                     void* stream);
 
 /*
  * Residual add fused with the next RMSNorm's reduction.
@@ -107,11 +120,12 @@ int mdl_decode_embed(const int64_t* token, const int64_t* example_ids, const voi
  *           (src/transformer.py:443), and the reduction of the following ln2 / ln1 / ln_f.
  *   x[m]    += delta[m] (+ bias)           delta fp32 [rows, d] (may be NULL), bias fp32 [d] or NULL
  *   rstd[m]  = 1 / sqrt(mean(x[m]^2) + eps)
- *   xs[m]    = split(x[m] * gamma)         bf16 [rows, 2d] (skipped when xs_out is NULL)
+ *   xs[m]    = split(x[m] * gamma)         bf16 [rows, 2d] (skipped when xs_out is NULL), in
+ *                                          xs_layout as for mdl_embed_rmsnorm
  */
 int mdl_add_rmsnorm(float* x, const float* delta, const float* bias, int rows, int d,
                     const float* gamma, float eps, uint16_t* xs_out, float* rstd_out,
-                    void* stream);
+                    int xs_layout, void* stream);
 
 /*
  * K2 -- RMSNorm scale + Q/K/V split + 3D RoPE + static-cache write.
@@ -155,11 +169,42 @@ int mdl_qkv_rope_cache_packed(const float* qkv, int64_t qkv_ld, const float* rst
  * Replaces: FeedForward.forward's silu(fc_gate(x)) * fc_up(x) (src/transformer.py:441-449).
  * gate_up: fp32 [rows, 2*d_ff] (row stride ld) = (x*gamma2) @ [W_gate; W_up]^T.
  *   h[m, j] = silu(rstd[m]*g[m,j] + bias_gate[j]) * (rstd[m]*u[m,j] + bias_up[j])
- * h_out: split bf16 [rows, 2*d_ff].  rstd / biases may be NULL (treated as 1 / 0).  d_ff must
- * be a multiple of 8.
+ * h_out: split bf16 [rows, 2*d_ff] in h_layout (MDL_LAYOUT_TILES needs d_ff % 16 == 0).
+ * rstd / biases may be NULL (treated as 1 / 0).  d_ff must be a multiple of 8.
  */
 int mdl_swiglu(const float* gate_up, int64_t ld, const float* rstd, const float* bias_gate,
-               const float* bias_up, int rows, int d_ff, uint16_t* h_out, void* stream);
+               const float* bias_up, int rows, int d_ff, uint16_t* h_out, int h_layout,
+               void* stream);
+
+/*
+ * K5 -- decode projection GEMM on split activations (bf16 MFMA, fp32 accumulation).
+ * Replaces: the nn.Linear projections of one decode step -- qkv_proj (src/inference.py:439),
+ *           out_proj (:453), fc_gate / fc_up and fc_down (FeedForward.forward,
+ *           src/transformer.py:441-449) -- at decode-sized row counts.
+ *   out[i, j] (fp32, row stride ldo) = sum_{k < K} (a[i, k] + a[i, K + k]) * w[j, k]
+ * a: split bf16 activation [m, 2K] (hi in columns [0, K), lo in [K, 2K)) in a_layout; w: bf16
+ * [n, K] in nn.Linear orientation in w_layout.  A row-major operand has row stride lda / ldw
+ * (the left half of a [W | W] operand serves, ldw = 2K); a tiled one (MDL_LAYOUT_TILES, from the
+ * producers' *_layout argument or mdl_tile_matrix) ignores its ld.  Both tiled is the fast form
+ * (contiguous kilobyte loads).  k must be a positive multiple of 32 and n a multiple of 4;
+ * pointers 16-byte aligned, row-major lda / ldw multiples of 8, ldo a multiple of 4.
+ * tile = 0 picks the block shape from (m, n, k) (mdl_gemm_split_pick); 1 .. mdl_gemm_split_tiles()
+ * forces one.  A given tile gives bit-identical results run to run and across layouts; tiles
+ * differ at fp32 rounding.
+ */
+int mdl_gemm_split(const uint16_t* a, int64_t lda, int a_layout, const uint16_t* w, int64_t ldw,
+                   int w_layout, float* out, int64_t ldo, int m, int n, int k, int tile,
+                   void* stream);
+/* Number of compiled block shapes, and the automatic choice for (m, n, k) (host only). */
+int mdl_gemm_split_tiles(void);
+int mdl_gemm_split_pick(int m, int n, int k);
+/*
+ * dst = src ([rows, cols] bf16, row stride ld) in MDL_LAYOUT_TILES, rows padded to a multiple
+ * of 16 with zeros (dst holds ceil(rows / 16) * 16 * cols elements).  cols a multiple of 32.
+ * Packs the decode weights once per model version (no reference counterpart: a layout step).
+ */
+int mdl_tile_matrix(const uint16_t* src, int64_t ld, int rows, int cols, uint16_t* dst,
+                    void* stream);
 
 /*
  * K4a -- prefill / full-sequence attention on bf16 MFMA (flash style, online softmax).
@@ -219,7 +264,8 @@ int mdl_attn_prefill_lead(const float* qkv, int64_t qkv_ld, const float* rstd,
  * the PV product rounded to bf16).
  * Replaces: F.scaled_dot_product_attention in _decode_step (src/inference.py:452) with the
  *           mask rebuilt from full_attention_mask (src/inference.py:446-450, :557-558, :626).
- * q: bf16 [batch, n_heads, 64] (pre-scaled); out: split bf16 [batch, 2*n_heads*64].
+ * q: bf16 [batch, n_heads, 64] (pre-scaled); out: split bf16 [batch, 2*n_heads*64] in
+ * out_layout (MDL_LAYOUT_ROWS or MDL_LAYOUT_TILES).
  * The query of row b sees slot j iff
  *   kv_start[b] <= j <= t, t = (seq_dev ? *seq_dev : seq_pos), and
  *   (j >= prompt_len || prompt_mask[b*prompt_len + j] != 0)   (prompt_mask may be NULL).
@@ -237,7 +283,7 @@ int mdl_attn_decode(const uint16_t* q, const uint16_t* k_cache, const uint16_t* 
                     const int32_t* kv_start, const int32_t* row_order, int seq_pos,
                     const int32_t* seq_dev,
                     float* workspace, int64_t workspace_bytes, int split_len, uint16_t* out,
-                    void* stream);
+                    int out_layout, void* stream);
 
 /*
  * K2 + K4b fused for the decode step: mdl_qkv_rope_cache (seq = 1, slot t) followed by
@@ -254,7 +300,7 @@ int mdl_attn_decode_rope(const float* qkv, int64_t qkv_ld, const float* rstd, co
                          int prompt_len, const uint8_t* row_holes, const int32_t* kv_start,
                          const int32_t* row_order, int seq_pos, const int32_t* seq_dev,
                          float* workspace, int64_t workspace_bytes, int split_len, uint16_t* out,
-                         void* stream);
+                         int out_layout, void* stream);
 
 /*
  * Final RMSNorm + LM head + greedy argmax.

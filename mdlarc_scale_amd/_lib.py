@@ -35,17 +35,22 @@ SIGNATURES: dict[str, tuple[object, list]] = {
     "mdl_version": (c_int, []),
     "mdl_error_string": (ctypes.c_char_p, [c_int]),
     "mdl_embed_rmsnorm": (c_int, [P, P, P, P, c_int, c_int, c_int, c_int, c_int, c_int, P,
-                                  c_float, P, P, P, P]),
+                                  c_float, P, P, P, c_int, P]),
     "mdl_decode_embed": (c_int, [P, P, P, P, c_int, c_int, c_int, c_int, c_int, P, c_float, P,
-                                 P, P, c_int, c_int, P, P, P, P, P, P]),
-    "mdl_add_rmsnorm": (c_int, [P, P, P, c_int, c_int, P, c_float, P, P, P]),
+                                 P, P, c_int, c_int, P, P, P, P, P, c_int, P]),
+    "mdl_add_rmsnorm": (c_int, [P, P, P, c_int, c_int, P, c_float, P, P, c_int, P]),
     "mdl_qkv_rope_cache": (c_int, [P, c_int64, P, P, P, c_int, c_int, c_int, c_int, c_int, c_int,
                                    c_int, c_int, c_int, c_int, c_float, P, P, P, c_int, c_int, P,
                                    P]),
     "mdl_qkv_rope_cache_packed": (c_int, [P, c_int64, P, P, P, c_int64, P, P, c_int, c_int, c_int,
                                           c_int, c_int, c_int, c_int, c_int, c_int, c_float, P, P,
                                           P, c_int, P]),
-    "mdl_swiglu": (c_int, [P, c_int64, P, P, P, c_int, c_int, P, P]),
+    "mdl_swiglu": (c_int, [P, c_int64, P, P, P, c_int, c_int, P, c_int, P]),
+    "mdl_gemm_split": (c_int, [P, c_int64, c_int, P, c_int64, c_int, P, c_int64, c_int, c_int,
+                               c_int, c_int, P]),
+    "mdl_gemm_split_tiles": (c_int, []),
+    "mdl_gemm_split_pick": (c_int, [c_int, c_int, c_int]),
+    "mdl_tile_matrix": (c_int, [P, c_int64, c_int, c_int, P, P]),
     "mdl_attn_prefill": (c_int, [P, P, P, c_int, c_int, c_int, c_int, c_int, P, P, c_int, P, P]),
     "mdl_attn_prefill_packed": (c_int, [P, P, P, c_int, c_int, c_int, c_int, c_int, P, P, P,
                                         c_int, P, P]),
@@ -54,10 +59,10 @@ SIGNATURES: dict[str, tuple[object, list]] = {
                                       P]),
     "mdl_attn_decode_workspace_bytes": (c_int64, [c_int, c_int, c_int, c_int]),
     "mdl_attn_decode": (c_int, [P, P, P, c_int, c_int, c_int, c_int, P, c_int, P, P, P, c_int,
-                                P, P, c_int64, c_int, P, P]),
+                                P, P, c_int64, c_int, P, c_int, P]),
     "mdl_attn_decode_rope": (c_int, [P, c_int64, P, P, P, c_int, c_int, c_int, c_int, c_int,
                                      c_int, c_float, P, P, c_int, c_int, c_int, c_int, P, c_int,
-                                     P, P, P, c_int, P, P, c_int64, c_int, P, P]),
+                                     P, P, P, c_int, P, P, c_int64, c_int, P, c_int, P]),
     "mdl_lm_head": (c_int, [P, P, c_int, c_int, P, c_float, P, c_int, P, P, CONS, P]),
     "mdl_decode_head": (c_int, [P, c_int, c_int, P, c_float, P, c_int, P, P, P, c_int64, c_int,
                                 P, P, c_int, c_int, CONS, P]),

@@ -31,6 +31,7 @@ SOURCES = [
     "attn_prefill.hip",
     "head_state.hip",
     "prompt_build.hip",
+    "split_gemm.hip",
 ]
 
 FLAGS = [

@@ -29,15 +29,23 @@ namespace mdl {
 constexpr int kPart = 2 + kHeadDim;   // m, l, acc[64] per split
 
 // Channel `lane` of head h = bh % n_heads of batch row b = bh / n_heads into the out-projection
-// GEMM input: row b holds 2*n_heads*64 bf16, hi of every head then lo of every head.
+// GEMM input: row b holds 2*n_heads*64 bf16, hi of every head then lo of every head (row-major,
+// or MFMA tiles when `tiled`).
 __device__ __forceinline__ void store_split(uint16_t* out, int bh, int n_heads, int lane,
-                                            float o) {
+                                            float o, int tiled) {
   const int b = bh / n_heads, h = bh - b * n_heads;
-  const int64_t d = static_cast<int64_t>(n_heads) * kHeadDim;
-  uint16_t* p = out + static_cast<int64_t>(b) * 2 * d + h * kHeadDim + lane;
+  const int d = n_heads * kHeadDim;
+  const int j = h * kHeadDim + lane;
   const uint32_t hi = f2bf(o);
-  p[0] = static_cast<uint16_t>(hi);
-  p[d] = static_cast<uint16_t>(f2bf(o - bf2f(hi)));
+  const uint16_t lo = static_cast<uint16_t>(f2bf(o - bf2f(hi)));
+  if (tiled) {
+    out[tile_off(b, j, 2 * d)] = static_cast<uint16_t>(hi);
+    out[tile_off(b, d + j, 2 * d)] = lo;
+  } else {
+    uint16_t* p = out + static_cast<int64_t>(b) * 2 * d + j;
+    p[0] = static_cast<uint16_t>(hi);
+    p[d] = lo;
+  }
 }
 
 // K2 inputs for the fused variant: the fp32 qkv GEMM output of the decode token of each row.
@@ -66,7 +74,7 @@ __global__ __launch_bounds__(256) void attn_decode_kernel(
     const uint8_t* __restrict__ row_holes, const int32_t* __restrict__ kv_start,
     const int32_t* __restrict__ row_order, int seq_pos, const int32_t* __restrict__ seq_dev,
     int n_split, int split_len, float* __restrict__ ws, uint16_t* __restrict__ out,
-    RopeIn rin) {
+    int out_tiled, RopeIn rin) {
   const int ri = blockIdx.x / n_heads;
   const int n_rows = gridDim.x / n_heads;
   const int b = row_order ? min(max(row_order[ri], 0), n_rows - 1) : ri;
@@ -245,7 +253,7 @@ __global__ __launch_bounds__(256) void attn_decode_kernel(
       O += red[w][2 + lane] * sc;
     }
     if (n_split == 1) {
-      store_split(out, bh, n_heads, lane, L > 0.f ? O / L : 0.f);
+      store_split(out, bh, n_heads, lane, L > 0.f ? O / L : 0.f, out_tiled);
     } else {
       float* p = ws + (static_cast<int64_t>(bh) * n_split + split) * kPart;
       if (lane == 0) {
@@ -261,7 +269,8 @@ __global__ __launch_bounds__(256) void attn_decode_kernel(
 __global__ __launch_bounds__(256) void attn_decode_combine_kernel(const float* __restrict__ ws,
                                                                   int n_bh, int n_heads,
                                                                   int n_split,
-                                                                  uint16_t* __restrict__ out) {
+                                                                  uint16_t* __restrict__ out,
+                                                                  int out_tiled) {
   const int bh = blockIdx.x * 4 + (threadIdx.x >> 6);
   const int lane = threadIdx.x & 63;
   if (bh >= n_bh) return;
@@ -275,7 +284,7 @@ __global__ __launch_bounds__(256) void attn_decode_combine_kernel(const float* _
     L += p[s * kPart + 1] * sc;
     O += p[s * kPart + 2 + lane] * sc;
   }
-  store_split(out, bh, n_heads, lane, L > 0.f ? O / L : 0.f);
+  store_split(out, bh, n_heads, lane, L > 0.f ? O / L : 0.f, out_tiled);
 }
 
 constexpr int kSlotsPerIter = 128;   // split_len granularity
@@ -307,12 +316,13 @@ static int decode_impl(bool fused, const RopeIn& rin, const uint16_t* q, uint16_
                        const uint8_t* prompt_mask, int prompt_len, const uint8_t* row_holes,
                        const int32_t* kv_start, const int32_t* row_order, int seq_pos,
                        const int32_t* seq_dev, float* workspace, int64_t workspace_bytes,
-                       int split_len, uint16_t* out, void* stream) {
+                       int split_len, uint16_t* out, int out_layout, void* stream) {
   if ((!fused && !q) || !k_cache || !v_cache || !out) return MDL_ERR_NULL;
   if (head_dim != kHeadDim) return MDL_ERR_HEAD_DIM;
   if (batch < 0 || n_heads <= 0 || cache_slots <= 0 || prompt_len < 0 ||
       (prompt_mask && prompt_len == 0) || split_len < kSlotsPerIter ||
-      split_len % kSlotsPerIter != 0)
+      split_len % kSlotsPerIter != 0 ||
+      (out_layout != MDL_LAYOUT_ROWS && out_layout != MDL_LAYOUT_TILES))
     return MDL_ERR_SHAPE;
   if (!seq_dev && (seq_pos < 0 || seq_pos >= cache_slots)) return MDL_ERR_CACHE;
   if ((!fused && !aligned16(q)) || !aligned16(k_cache) || !aligned16(v_cache) || !aligned4(out))
@@ -328,7 +338,7 @@ static int decode_impl(bool fused, const RopeIn& rin, const uint16_t* q, uint16_
 #define MDL_DECODE(FUSED, NB)                                                                  \
   attn_decode_kernel<FUSED, NB><<<grid, 256, 0, s>>>(                                          \
       q, k_cache, v_cache, n_heads, cache_slots, prompt_mask, prompt_len, row_holes, kv_start, \
-      row_order, seq_pos, seq_dev, ns, split_len, workspace, out, rin)
+      row_order, seq_pos, seq_dev, ns, split_len, workspace, out, out_layout, rin)
   if (fused) {
     if (long_items) MDL_DECODE(true, 4);
     else MDL_DECODE(true, 2);
@@ -339,7 +349,7 @@ static int decode_impl(bool fused, const RopeIn& rin, const uint16_t* q, uint16_
 #undef MDL_DECODE
   if (ns > 1)
     attn_decode_combine_kernel<<<dim3((n_bh + 3) / 4), 256, 0, s>>>(workspace, n_bh, n_heads,
-                                                                     ns, out);
+                                                                     ns, out, out_layout);
   return launch_status();
 }
 
@@ -352,12 +362,12 @@ extern "C" int mdl_attn_decode(const uint16_t* q, const uint16_t* k_cache,
                                const int32_t* row_order, int seq_pos,
                                const int32_t* seq_dev, float* workspace,
                                int64_t workspace_bytes, int split_len, uint16_t* out,
-                               void* stream) {
+                               int out_layout, void* stream) {
   const RopeIn none{};
   return decode_impl(false, none, q, const_cast<uint16_t*>(k_cache),
                      const_cast<uint16_t*>(v_cache), batch, n_heads, head_dim, cache_slots,
                      prompt_mask, prompt_len, row_holes, kv_start, row_order, seq_pos, seq_dev,
-                     workspace, workspace_bytes, split_len, out, stream);
+                     workspace, workspace_bytes, split_len, out, out_layout, stream);
 }
 
 extern "C" int mdl_attn_decode_rope(const float* qkv, int64_t qkv_ld, const float* rstd,
@@ -370,7 +380,7 @@ extern "C" int mdl_attn_decode_rope(const float* qkv, int64_t qkv_ld, const floa
                                     const int32_t* row_order, int seq_pos,
                                     const int32_t* seq_dev, float* workspace,
                                     int64_t workspace_bytes, int split_len, uint16_t* out,
-                                    void* stream) {
+                                    int out_layout, void* stream) {
   if (!qkv || !rstd || !pos || !rope_tab) return MDL_ERR_NULL;
   if (max_x <= 0 || max_y <= 0 || max_z <= 0 || px < 0 || py < 0 || pz < 0 ||
       px + py + pz != kHeadDim / 2 || n_heads <= 0 || qkv_ld < 3 * int64_t(n_heads) * kHeadDim)
@@ -380,5 +390,6 @@ extern "C" int mdl_attn_decode_rope(const float* qkv, int64_t qkv_ld, const floa
                    q_scale};
   return decode_impl(true, rin, nullptr, k_cache, v_cache, batch, n_heads, head_dim,
                      cache_slots, prompt_mask, prompt_len, row_holes, kv_start, row_order,
-                     seq_pos, seq_dev, workspace, workspace_bytes, split_len, out, stream);
+                     seq_pos, seq_dev, workspace, workspace_bytes, split_len, out, out_layout,
+                     stream);
 }

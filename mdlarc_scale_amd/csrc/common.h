@@ -47,7 +47,11 @@ __device__ __forceinline__ uint4 pack8(const float* f) {
 // lo = bf16(v - hi) in [K, 2K) (v - hi is exact in fp32).  Against a weight packed as [W | W]
 // the bf16 GEMM then returns (hi + lo) . w, i.e. v to about 2^-17 relative instead of the 2^-9
 // of a single bf16 rounding; the same buffer read as [2M, K] gives hi.w and lo.w as row pairs.
+// v is the rounded fp32 value: contraction is off here, so a product feeding v is never fused
+// into v - hi (the compiler otherwise fuses it in some instantiations of a kernel and not in
+// others, and the same activation then splits differently in different kernels).
 __device__ __forceinline__ void split_bf2(float a, float b, uint32_t& hi, uint32_t& lo) {
+#pragma clang fp contract(off)
   const bf16x2_t h = {static_cast<__bf16>(a), static_cast<__bf16>(b)};
   hi = __builtin_bit_cast(uint32_t, h);
   lo = pack_bf2(a - static_cast<float>(h[0]), b - static_cast<float>(h[1]));
@@ -141,6 +145,13 @@ __device__ __forceinline__ float wave_max(float v) {
 #pragma unroll
   for (int o = 32; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o, kWave));
   return v;
+}
+
+// Element offset of (row m, column j) of a [rows, cols] bf16 matrix in the MFMA tile layout
+// (MDL_LAYOUT_TILES; cols a multiple of 32).  Columns j .. j + 7 with j % 8 == 0 are contiguous.
+__device__ __forceinline__ int64_t tile_off(int64_t m, int j, int cols) {
+  return 512 * ((m >> 4) * (cols >> 5) + (j >> 5)) + 8 * (16 * ((j >> 3) & 3) + (m & 15)) +
+         (j & 7);
 }
 
 // ---- host-side launch checking ---------------------------------------------------------------

@@ -55,11 +55,13 @@ __device__ __forceinline__ void load_gamma(const float* gamma, int lane, int d, 
   }
 }
 
-// rstd of the row held in v, then x (fp32) and split(x * gamma) stores (non-temporal if NT).
+// rstd of the row held in v, then x (fp32) and split(x * gamma) stores (non-temporal if NT)
+// into row m of xs (row-major [rows, 2d], or MFMA tiles when `tiled`).
 template <int NC, bool TAIL, bool HAS_XS, bool NT>
 __device__ __forceinline__ void finish_row(int lane, int d, float eps, const float (*v)[4],
                                            const float (*g)[4], float ss, float* xo,
-                                           uint16_t* xs, float* rstd_out) {
+                                           uint16_t* xs, int64_t m, int tiled,
+                                           float* rstd_out) {
   ss = wave_sum(ss);
   const float r = rsqrtf(ss / static_cast<float>(d) + eps);
 #pragma unroll
@@ -72,8 +74,13 @@ __device__ __forceinline__ void finish_row(int lane, int d, float eps, const flo
                             v[i][3] * g[i][3]};
         uint2 hi, lo;
         split4(t, hi, lo);
-        st_u2<NT>(xs + e, hi);
-        st_u2<NT>(xs + d + e, lo);
+        if (tiled) {
+          st_u2<NT>(xs + tile_off(m, e, 2 * d), hi);
+          st_u2<NT>(xs + tile_off(m, d + e, 2 * d), lo);
+        } else {
+          st_u2<NT>(xs + m * 2 * d + e, hi);
+          st_u2<NT>(xs + m * 2 * d + d + e, lo);
+        }
       }
     }
   }
@@ -112,7 +119,7 @@ __global__ __launch_bounds__(256) void embed_rmsnorm_kernel(
     const int64_t* __restrict__ ids, const int64_t* __restrict__ ex_ids,
     const TT* __restrict__ tok, const TT* __restrict__ ex, int vocab, int n_ex, int rows,
     int row_len, int d, const float* __restrict__ gamma, float eps, float* __restrict__ x_out,
-    uint16_t* __restrict__ xs_out, float* __restrict__ rstd_out) {
+    uint16_t* __restrict__ xs_out, float* __restrict__ rstd_out, int xs_tiled) {
   const int lane = threadIdx.x & 63;
   const int64_t m = static_cast<int64_t>(blockIdx.x) * 4 + (threadIdx.x >> 6);
   if (m >= rows) return;
@@ -121,8 +128,8 @@ __global__ __launch_bounds__(256) void embed_rmsnorm_kernel(
   const TT* trow = tok + clamp_id(ids[m], vocab) * d;
   const TT* erow = HAS_EX ? ex + clamp_id(ex_ids[m / row_len], n_ex) * d : nullptr;
   const float ss = gather_row<NC, TAIL, TT, HAS_EX>(trow, erow, lane, d, v);
-  finish_row<NC, TAIL, HAS_XS, false>(lane, d, eps, v, g, ss, x_out + m * d,
-                                      HAS_XS ? xs_out + m * 2 * d : nullptr, rstd_out + m);
+  finish_row<NC, TAIL, HAS_XS, false>(lane, d, eps, v, g, ss, x_out + m * d, xs_out, m, xs_tiled,
+                                      rstd_out + m);
 }
 
 // Decode step entry: lane 0 of each row's wave turns the token the row just emitted into its 3D
@@ -134,7 +141,7 @@ __global__ __launch_bounds__(256) void decode_embed_kernel(
     const float* __restrict__ gamma, float eps, int32_t* __restrict__ gx,
     int32_t* __restrict__ gy, uint8_t* __restrict__ gio, int max_x, int max_y,
     int64_t* __restrict__ pos_out, int32_t* __restrict__ counters, float* __restrict__ x_out,
-    uint16_t* __restrict__ xs_out, float* __restrict__ rstd_out) {
+    uint16_t* __restrict__ xs_out, float* __restrict__ rstd_out, int xs_tiled) {
   const int lane = threadIdx.x & 63;
   if (counters && blockIdx.x == 0 && threadIdx.x == 0) {
     counters[0] = counters[0] + 1;
@@ -156,7 +163,7 @@ __global__ __launch_bounds__(256) void decode_embed_kernel(
   const TT* trow = tok + clamp_id(t, vocab) * d;
   const TT* erow = HAS_EX ? ex + clamp_id(ex_ids[m], n_ex) * d : nullptr;
   const float ss = gather_row<NC, TAIL, TT, HAS_EX>(trow, erow, lane, d, v);
-  finish_row<NC, TAIL, true, false>(lane, d, eps, v, g, ss, x_out + m * d, xs_out + m * 2 * d,
+  finish_row<NC, TAIL, true, false>(lane, d, eps, v, g, ss, x_out + m * d, xs_out, m, xs_tiled,
                                     rstd_out + m);
 }
 
@@ -164,7 +171,7 @@ template <int NC, bool TAIL, bool HAS_DELTA, bool HAS_BIAS, bool HAS_XS, bool NT
 __global__ __launch_bounds__(256) void add_rmsnorm_kernel(
     float* __restrict__ x, const float* __restrict__ delta, const float* __restrict__ bias,
     int rows, int d, const float* __restrict__ gamma, float eps, uint16_t* __restrict__ xs_out,
-    float* __restrict__ rstd_out) {
+    float* __restrict__ rstd_out, int xs_tiled) {
   const int lane = threadIdx.x & 63;
   const int64_t m = static_cast<int64_t>(blockIdx.x) * 4 + (threadIdx.x >> 6);
   if (m >= rows) return;
@@ -193,8 +200,8 @@ __global__ __launch_bounds__(256) void add_rmsnorm_kernel(
       for (int j = 0; j < 4; ++j) ss += v[i][j] * v[i][j];
     }
   }
-  finish_row<NC, TAIL, HAS_XS, NT>(lane, d, eps, v, g, ss, xr,
-                                   HAS_XS ? xs_out + m * 2 * d : nullptr, rstd_out + m);
+  finish_row<NC, TAIL, HAS_XS, NT>(lane, d, eps, v, g, ss, xr, xs_out, m, xs_tiled,
+                                   rstd_out + m);
 }
 
 constexpr int kMaxChunks = 8;  // d <= 2048
@@ -222,10 +229,10 @@ struct LaunchEmbed {
   static void run(dim3 grid, hipStream_t s, bool has_ex, bool has_xs, const int64_t* ids,
                   const int64_t* ex_ids, const TT* tok, const TT* ex, int vocab, int n_ex,
                   int rows, int row_len, int d, const float* gamma, float eps, float* x,
-                  uint16_t* xs, float* r) {
+                  uint16_t* xs, float* r, int tiled) {
 #define MDL_EMB(E, X)                                                                         \
   embed_rmsnorm_kernel<NC, TAIL, TT, E, X><<<grid, 256, 0, s>>>(                              \
-      ids, ex_ids, tok, ex, vocab, n_ex, rows, row_len, d, gamma, eps, x, xs, r)
+      ids, ex_ids, tok, ex, vocab, n_ex, rows, row_len, d, gamma, eps, x, xs, r, tiled)
     if (has_ex && has_xs) MDL_EMB(true, true);
     else if (has_ex) MDL_EMB(true, false);
     else if (has_xs) MDL_EMB(false, true);
@@ -241,15 +248,15 @@ struct LaunchDecodeEmbed {
                   const int64_t* ex_ids, const TT* tok, const TT* ex, int vocab, int n_ex,
                   int batch, int d, const float* gamma, float eps, int32_t* gx, int32_t* gy,
                   uint8_t* gio, int max_x, int max_y, int64_t* pos, int32_t* counters, float* x,
-                  uint16_t* xs, float* r) {
+                  uint16_t* xs, float* r, int tiled) {
     if (has_ex)
       decode_embed_kernel<NC, TAIL, TT, true><<<grid, 256, 0, s>>>(
           token, ex_ids, tok, ex, vocab, n_ex, batch, d, gamma, eps, gx, gy, gio, max_x, max_y,
-          pos, counters, x, xs, r);
+          pos, counters, x, xs, r, tiled);
     else
       decode_embed_kernel<NC, TAIL, TT, false><<<grid, 256, 0, s>>>(
           token, ex_ids, tok, ex, vocab, n_ex, batch, d, gamma, eps, gx, gy, gio, max_x, max_y,
-          pos, counters, x, xs, r);
+          pos, counters, x, xs, r, tiled);
   }
 };
 
@@ -257,18 +264,19 @@ template <int NC, bool TAIL>
 struct LaunchAdd {
   static void run(dim3 grid, hipStream_t s, bool nt, float* x, const float* delta,
                   const float* bias, int rows, int d, const float* gamma, float eps, uint16_t* xs,
-                  float* r) {
-    if (nt) go<true>(grid, s, x, delta, bias, rows, d, gamma, eps, xs, r);
-    else go<false>(grid, s, x, delta, bias, rows, d, gamma, eps, xs, r);
+                  float* r, int tiled) {
+    if (nt) go<true>(grid, s, x, delta, bias, rows, d, gamma, eps, xs, r, tiled);
+    else go<false>(grid, s, x, delta, bias, rows, d, gamma, eps, xs, r, tiled);
   }
 
   template <bool NT>
   static void go(dim3 grid, hipStream_t s, float* x, const float* delta, const float* bias,
-                 int rows, int d, const float* gamma, float eps, uint16_t* xs, float* r) {
+                 int rows, int d, const float* gamma, float eps, uint16_t* xs, float* r,
+                 int tiled) {
     const int key = (delta ? 4 : 0) | (bias ? 2 : 0) | (xs ? 1 : 0);
 #define MDL_ADD(D, B, X)                                                                     \
   add_rmsnorm_kernel<NC, TAIL, D, B, X, NT><<<grid, 256, 0, s>>>(x, delta, bias, rows, d, gamma, \
-                                                                 eps, xs, r)
+                                                                 eps, xs, r, tiled)
     switch (key) {
       case 7: MDL_ADD(true, true, true); break;
       case 6: MDL_ADD(true, true, false); break;
@@ -282,6 +290,11 @@ struct LaunchAdd {
 #undef MDL_ADD
   }
 };
+
+// a split output of 2d columns in `layout` (MDL_LAYOUT_TILES needs 2d % 32 == 0)
+inline bool layout_ok(int layout, int d) {
+  return layout == MDL_LAYOUT_ROWS || (layout == MDL_LAYOUT_TILES && d % 16 == 0);
+}
 
 // host-side checks shared by the two embedding entry points
 inline int check_tables(const void* tok_table, const void* ex_table, bool use_ex, int table_dtype,
@@ -306,12 +319,12 @@ extern "C" int mdl_embed_rmsnorm(const int64_t* ids, const int64_t* example_ids,
                                  const void* tok_table, const void* ex_table, int table_dtype,
                                  int vocab, int n_examples, int rows, int row_len, int d,
                                  const float* gamma, float eps, float* x_out, uint16_t* xs_out,
-                                 float* rstd_out, void* stream) {
+                                 float* rstd_out, int xs_layout, void* stream) {
   if (!ids || !gamma || !x_out || !rstd_out) return MDL_ERR_NULL;
   const bool use_ex = example_ids != nullptr;
   const int tc = check_tables(tok_table, ex_table, use_ex, table_dtype, vocab, n_examples, d);
   if (tc != MDL_OK) return tc;
-  if (rows < 0 || row_len <= 0) return MDL_ERR_SHAPE;
+  if (rows < 0 || row_len <= 0 || !layout_ok(xs_layout, d)) return MDL_ERR_SHAPE;
   if (!aligned16(x_out) || !aligned16(gamma) || (xs_out && !aligned8(xs_out)))
     return MDL_ERR_ALIGN;
   if (rows == 0) return MDL_OK;
@@ -321,12 +334,12 @@ extern "C" int mdl_embed_rmsnorm(const int64_t* ids, const int64_t* example_ids,
     dispatch_nc<LaunchEmbed>(d, grid, s, use_ex, xs_out != nullptr, ids, example_ids,
                              static_cast<const float*>(tok_table),
                              static_cast<const float*>(ex_table), vocab, n_examples, rows,
-                             row_len, d, gamma, eps, x_out, xs_out, rstd_out);
+                             row_len, d, gamma, eps, x_out, xs_out, rstd_out, xs_layout);
   else
     dispatch_nc<LaunchEmbed>(d, grid, s, use_ex, xs_out != nullptr, ids, example_ids,
                              static_cast<const uint16_t*>(tok_table),
                              static_cast<const uint16_t*>(ex_table), vocab, n_examples, rows,
-                             row_len, d, gamma, eps, x_out, xs_out, rstd_out);
+                             row_len, d, gamma, eps, x_out, xs_out, rstd_out, xs_layout);
   return launch_status();
 }
 
@@ -335,13 +348,14 @@ extern "C" int mdl_decode_embed(const int64_t* token, const int64_t* example_ids
                                 int vocab, int n_examples, int batch, int d, const float* gamma,
                                 float eps, int32_t* gx, int32_t* gy, uint8_t* in_out, int max_x,
                                 int max_y, int64_t* pos_out, int32_t* counters, float* x_out,
-                                uint16_t* xs_out, float* rstd_out, void* stream) {
+                                uint16_t* xs_out, float* rstd_out, int xs_layout,
+                                void* stream) {
   if (!token || !gamma || !gx || !gy || !in_out || !pos_out || !x_out || !xs_out || !rstd_out)
     return MDL_ERR_NULL;
   const bool use_ex = example_ids != nullptr;
   const int tc = check_tables(tok_table, ex_table, use_ex, table_dtype, vocab, n_examples, d);
   if (tc != MDL_OK) return tc;
-  if (batch < 0 || max_x < 0 || max_y < 0) return MDL_ERR_SHAPE;
+  if (batch < 0 || max_x < 0 || max_y < 0 || !layout_ok(xs_layout, d)) return MDL_ERR_SHAPE;
   if (!aligned16(x_out) || !aligned16(gamma) || !aligned8(xs_out)) return MDL_ERR_ALIGN;
   if (batch == 0) return MDL_OK;
   const dim3 grid((batch + 3) / 4);
@@ -351,21 +365,22 @@ extern "C" int mdl_decode_embed(const int64_t* token, const int64_t* example_ids
                                    static_cast<const float*>(tok_table),
                                    static_cast<const float*>(ex_table), vocab, n_examples, batch,
                                    d, gamma, eps, gx, gy, in_out, max_x, max_y, pos_out, counters,
-                                   x_out, xs_out, rstd_out);
+                                   x_out, xs_out, rstd_out, xs_layout);
   else
     dispatch_nc<LaunchDecodeEmbed>(d, grid, s, use_ex, token, example_ids,
                                    static_cast<const uint16_t*>(tok_table),
                                    static_cast<const uint16_t*>(ex_table), vocab, n_examples,
                                    batch, d, gamma, eps, gx, gy, in_out, max_x, max_y, pos_out,
-                                   counters, x_out, xs_out, rstd_out);
+                                   counters, x_out, xs_out, rstd_out, xs_layout);
   return launch_status();
 }
 
 extern "C" int mdl_add_rmsnorm(float* x, const float* delta, const float* bias, int rows,
                                int d, const float* gamma, float eps, uint16_t* xs_out,
-                               float* rstd_out, void* stream) {
+                               float* rstd_out, int xs_layout, void* stream) {
   if (!x || !gamma || !rstd_out) return MDL_ERR_NULL;
-  if (rows < 0 || d <= 0 || d % 4 != 0 || d > 4 * 64 * kMaxChunks) return MDL_ERR_SHAPE;
+  if (rows < 0 || d <= 0 || d % 4 != 0 || d > 4 * 64 * kMaxChunks || !layout_ok(xs_layout, d))
+    return MDL_ERR_SHAPE;
   if (!aligned16(x) || !aligned16(gamma) || (delta && !aligned16(delta)) ||
       (bias && !aligned16(bias)) || (xs_out && !aligned8(xs_out)))
     return MDL_ERR_ALIGN;
@@ -373,6 +388,6 @@ extern "C" int mdl_add_rmsnorm(float* x, const float* delta, const float* bias, 
   const bool nt = static_cast<int64_t>(rows) * d * (8 + (delta ? 4 : 0) + (xs_out ? 4 : 0)) >=
                   kStreamBytes;
   dispatch_nc<LaunchAdd>(d, dim3((rows + 3) / 4), static_cast<hipStream_t>(stream), nt,
-                         x, delta, bias, rows, d, gamma, eps, xs_out, rstd_out);
+                         x, delta, bias, rows, d, gamma, eps, xs_out, rstd_out, xs_layout);
   return launch_status();
 }

@@ -16,7 +16,8 @@ __global__ __launch_bounds__(256) void swiglu_kernel(const float* __restrict__ g
                                                      const float* __restrict__ rstd,
                                                      const float* __restrict__ bg,
                                                      const float* __restrict__ bu, int64_t rows,
-                                                     int d_ff, uint16_t* __restrict__ h) {
+                                                     int d_ff, uint16_t* __restrict__ h,
+                                                     int tiled) {
   const int per_row = d_ff >> 3;
   const int64_t idx = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
   if (idx >= rows * per_row) return;
@@ -50,9 +51,14 @@ __global__ __launch_bounds__(256) void swiglu_kernel(const float* __restrict__ g
   }
   uint4 hi, lo;
   split8(o, hi, lo);
-  uint16_t* hr = h + m * 2 * d_ff + c;
-  st_u4<NT>(hr, hi);
-  st_u4<NT>(hr + d_ff, lo);
+  if (tiled) {
+    st_u4<NT>(h + tile_off(m, c, 2 * d_ff), hi);
+    st_u4<NT>(h + tile_off(m, d_ff + c, 2 * d_ff), lo);
+  } else {
+    uint16_t* hr = h + m * 2 * d_ff + c;
+    st_u4<NT>(hr, hi);
+    st_u4<NT>(hr + d_ff, lo);
+  }
 }
 
 }  // namespace mdl
@@ -61,9 +67,11 @@ using namespace mdl;
 
 extern "C" int mdl_swiglu(const float* gate_up, int64_t ld, const float* rstd,
                           const float* bias_gate, const float* bias_up, int rows, int d_ff,
-                          uint16_t* h_out, void* stream) {
+                          uint16_t* h_out, int h_layout, void* stream) {
   if (!gate_up || !h_out) return MDL_ERR_NULL;
   if (rows < 0 || d_ff <= 0 || d_ff % 8 != 0 || ld < 2 * static_cast<int64_t>(d_ff))
+    return MDL_ERR_SHAPE;
+  if (h_layout != MDL_LAYOUT_ROWS && !(h_layout == MDL_LAYOUT_TILES && d_ff % 16 == 0))
     return MDL_ERR_SHAPE;
   if (!aligned16(gate_up) || ld % 4 != 0 || !aligned16(h_out) ||
       (bias_gate && !aligned16(bias_gate)) || (bias_up && !aligned16(bias_up)))
@@ -74,9 +82,9 @@ extern "C" int mdl_swiglu(const float* gate_up, int64_t ld, const float* rstd,
   const hipStream_t st = static_cast<hipStream_t>(stream);
   if (static_cast<int64_t>(rows) * d_ff * 12 >= kStreamBytes)
     swiglu_kernel<true><<<grid, 256, 0, st>>>(gate_up, ld, rstd, bias_gate, bias_up, rows, d_ff,
-                                              h_out);
+                                              h_out, h_layout);
   else
     swiglu_kernel<false><<<grid, 256, 0, st>>>(gate_up, ld, rstd, bias_gate, bias_up, rows, d_ff,
-                                               h_out);
+                                               h_out, h_layout);
   return launch_status();
 }

@@ -15,6 +15,10 @@ Dataflow per layer (M token rows, d channels, F ffn width; fp32 residual stream 
     x += delta + b_down; xs = split(x * g1_next), rstd              <- add_rmsnorm
   final: logits = lm_head(ln_f(x)) and greedy argmax                <- lm_head kernel
 
+At decode (M = batch rows) the projections run on K5 instead of hipBLASLt: the producers write
+xs / attn / h in the MFMA tile layout and K5 multiplies them with tiled copies of W (read once,
+not as [W | W]); see ``project``.
+
 "split" stores a GEMM input as a hi|lo pair of bf16 (hi = bf16(v), lo = bf16(v - hi)); against a
 weight packed as [W | W] the bf16 MFMA GEMM then sees the activation to ~2^-17 instead of 2^-9.
 Rounding every GEMM operand and output to a single bf16 puts the final logits 3e-2 away from the
@@ -47,6 +51,22 @@ def gemm_f32(a: torch.Tensor, w2: torch.Tensor, out: torch.Tensor) -> torch.Tens
     return torch.ops.aten.mm.dtype_out(a, w2.t(), torch.float32, out=out)
 
 
+def tiles_supported(d_model: int, d_ff: int) -> bool:
+    """K5 with tiled operands needs every projection's K (d_model, d_ff) to be a multiple of 32;
+    all reference presets are."""
+    return d_model % 32 == 0 and d_ff % 32 == 0
+
+
+def project(sc: "Scratch", a: torch.Tensor, w2: torch.Tensor, wt: torch.Tensor | None,
+            out: torch.Tensor) -> None:
+    """One projection out = a @ W^T: on K5 with tiled activations and weights when ``sc`` is a
+    decode scratch in the tile layout, else on hipBLASLt against the [W | W] operand."""
+    if sc.tiled:
+        K.gemm_split(a, wt, out, w2.shape[1] // 2, a_tiled=True, w_tiled=True)
+    else:
+        gemm_f32(a, w2, out)
+
+
 def pack_split_weight(w: torch.Tensor, device: torch.device) -> torch.Tensor:
     """bf16 [W | W] ([N, 2K]) for a split-activation GEMM input (see gemm_f32)."""
     wb = w.detach().to(device=device, dtype=torch.bfloat16)
@@ -72,6 +92,13 @@ class PackedWeights:
             self.b_gate.append(f32(blk.ffn.fc_gate.bias))
             self.b_up.append(f32(blk.ffn.fc_up.bias))
             self.b_down.append(f32(blk.ffn.fc_down.bias))
+        # decode (K5): each weight once, in the MFMA tile layout (the left half of [W | W])
+        self.tiles_ok = tiles_supported(cfg.d_model, cfg.d_ff)
+        tile = lambda w2: K.tile_matrix(w2, w2.shape[1] // 2)  # noqa: E731
+        self.qkv_t = [tile(w) for w in self.qkv] if self.tiles_ok else None
+        self.out_t = [tile(w) for w in self.out] if self.tiles_ok else None
+        self.gu_t = [tile(w) for w in self.gu] if self.tiles_ok else None
+        self.down_t = [tile(w) for w in self.down] if self.tiles_ok else None
         self.ln_f = f32(model.ln_f.weight)
         self.head = f32(model.lm_head.weight)
         rope = model.blocks[0].attn.rope
@@ -83,7 +110,8 @@ class PackedWeights:
 @dataclass
 class Scratch:
     """Activation buffers for M rows (reused across layers).  xs / attn / h are split bf16 GEMM
-    inputs (2x the channel count); qkv / delta / gu are fp32 GEMM outputs."""
+    inputs (2x the channel count; in the MFMA tile layout, whole 16-row blocks, when ``tiled``);
+    qkv / delta / gu are fp32 GEMM outputs."""
 
     x: torch.Tensor
     xs: torch.Tensor
@@ -94,14 +122,18 @@ class Scratch:
     delta: torch.Tensor
     gu: torch.Tensor
     h: torch.Tensor
+    tiled: bool = False
 
     @staticmethod
-    def alloc(rows: int, d: int, d_ff: int, device: torch.device) -> "Scratch":
+    def alloc(rows: int, d: int, d_ff: int, device: torch.device,
+              tiled: bool = False) -> "Scratch":
         e = lambda *s, dt=torch.bfloat16: torch.empty(*s, dtype=dt, device=device)  # noqa: E731
         f = torch.float32
-        return Scratch(x=e(rows, d, dt=f), xs=e(rows, 2 * d), rstd=e(rows, dt=f),
-                       qkv=e(rows, 3 * d, dt=f), q=e(rows, d), attn=e(rows, 2 * d),
-                       delta=e(rows, d, dt=f), gu=e(rows, 2 * d_ff, dt=f), h=e(rows, 2 * d_ff))
+        sr = K.tile_rows(rows) if tiled else rows       # rows of the split activations
+        return Scratch(x=e(rows, d, dt=f), xs=e(sr, 2 * d), rstd=e(rows, dt=f),
+                       qkv=e(rows, 3 * d, dt=f), q=e(rows, d), attn=e(sr, 2 * d),
+                       delta=e(rows, d, dt=f), gu=e(rows, 2 * d_ff, dt=f), h=e(sr, 2 * d_ff),
+                       tiled=tiled)
 
 
 @dataclass
@@ -272,14 +304,15 @@ class HipEngine:
     def _mlp(self, W: PackedWeights, li: int, sc: Scratch) -> None:
         """out_proj + residual, ln2, SwiGLU MLP + residual, next norm (shared by both phases)."""
         cfg = self.cfg
-        gemm_f32(sc.attn, W.out[li], sc.delta)
-        K.add_rmsnorm(sc.x, sc.delta, None, W.ln2[li], W.eps, sc.xs, sc.rstd)
-        gemm_f32(sc.xs, W.gu[li], sc.gu)
-        K.swiglu(sc.gu, sc.rstd, W.b_gate[li], W.b_up[li], sc.h)
-        gemm_f32(sc.h, W.down[li], sc.delta)
+        t = sc.tiled
+        project(sc, sc.attn, W.out[li], W.out_t[li] if t else None, sc.delta)
+        K.add_rmsnorm(sc.x, sc.delta, None, W.ln2[li], W.eps, sc.xs, sc.rstd, tiled=t)
+        project(sc, sc.xs, W.gu[li], W.gu_t[li] if t else None, sc.gu)
+        K.swiglu(sc.gu, sc.rstd, W.b_gate[li], W.b_up[li], sc.h, tiled=t)
+        project(sc, sc.h, W.down[li], W.down_t[li] if t else None, sc.delta)
         last = li + 1 == cfg.n_layers
         K.add_rmsnorm(sc.x, sc.delta, W.b_down[li], W.ln_f if last else W.ln1[li + 1], W.eps,
-                      None if last else sc.xs, sc.rstd)
+                      None if last else sc.xs, sc.rstd, tiled=t)
 
     @torch.no_grad()
     def forward(self, ids: torch.Tensor, pos: torch.Tensor, ex_ids: torch.Tensor | None,

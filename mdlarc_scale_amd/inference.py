@@ -38,7 +38,7 @@ from .data import (
 )
 from .engine import GRID_MAX_X, GRID_MAX_Y, HipEngine, PackedWeights, Scratch, choose_split_len
 from .engine import pack_prompt
-from .engine import engine_for, gemm_f32
+from .engine import engine_for, project, tiles_supported
 from .transformer import TinyTransformer, softmax_scale
 
 SYNC_EVERY = 8
@@ -55,6 +55,10 @@ USE_GRAPHS = True
 # layer over the whole padded [B, S] batch.  Logits and cache contents agree to fp32 rounding (the
 # GEMMs see a different row count).
 PACKED_PREFILL = True
+# Decode steps run their projections on K5 (mdl_gemm_split) over activations and weights in the
+# MFMA tile layout; False keeps them on hipBLASLt with row-major activations.  Logits agree to
+# fp32 rounding.
+DECODE_TILED = True
 
 
 # =============================================================================================
@@ -301,7 +305,9 @@ class Generator:
             counters=torch.tensor([S - 1, S], dtype=torch.int32, device=dev),
             out_ids=out_ids, finish=torch.full((B,), -1, dtype=torch.int32, device=dev),
             logits=torch.empty(B, cfg.vocab_size, dtype=torch.float32, device=dev),
-            cache=cache, sc=Scratch.alloc(B, cfg.d_model, cfg.d_ff, dev), ws=ws,
+            cache=cache, ws=ws,
+            sc=Scratch.alloc(B, cfg.d_model, cfg.d_ff, dev,
+                             tiled=DECODE_TILED and tiles_supported(cfg.d_model, cfg.d_ff)),
             split_len=split)
 
     def prefill(self, st: DecodeState, W: PackedWeights, input_ids, positions_3d,
@@ -343,11 +349,11 @@ class Generator:
         slot = st.counters[0:1]
         for li in range(cfg.n_layers):
             kc, vc = st.cache.layer(li)
-            gemm_f32(sc.xs, W.qkv[li], sc.qkv)
+            project(sc, sc.xs, W.qkv[li], W.qkv_t[li] if sc.tiled else None, sc.qkv)
             # RMSNorm scale + split + 3D RoPE + cache write fused into the attention launch
             K.attn_decode_rope(sc.qkv, sc.rstd, st.pos, W.rope_tab, W.rope_geom, qs, kc, vc, B,
                                H, st.pmask, st.S, st.kv_start, 0, slot, st.ws, st.split_len,
-                               sc.attn, row_holes=st.holes, row_order=st.order)
+                               sc.attn, row_holes=st.holes, row_order=st.order, tiled=sc.tiled)
             self.eng._mlp(W, li, sc)
 
     def decode_layers(self, st: DecodeState, W: PackedWeights, want_logits: bool) -> None:
@@ -357,7 +363,7 @@ class Generator:
         sc = st.sc
         tok_tab, ex_tab, use_ex = self._embed_inputs(st)
         K.embed_rmsnorm(st.tok, use_ex, tok_tab, ex_tab, 1, W.ln1[0], W.eps, sc.x, sc.xs,
-                        sc.rstd)
+                        sc.rstd, tiled=sc.tiled)
         self._layers(st, W)
         K.lm_head(sc.x, None, st.B, W.ln_f, W.eps, W.head, st.logits if want_logits else None,
                   st.tok)
@@ -369,7 +375,7 @@ class Generator:
         sc = st.sc
         tok_tab, ex_tab, use_ex = self._embed_inputs(st)
         K.decode_embed(st.tok, use_ex, tok_tab, ex_tab, W.ln1[0], W.eps, st.gx, st.gy, st.gio,
-                       st.pos, st.counters, sc.x, sc.xs, sc.rstd)
+                       st.pos, st.counters, sc.x, sc.xs, sc.rstd, tiled=sc.tiled)
         self._layers(st, W)
         K.decode_head(sc.x, W.ln_f, W.eps, W.head, None, st.tok, st.out_ids, 0, st.counters,
                       st.finish if stop_on_end else None, st.S, END_TOKEN_ID, cons)

@@ -42,6 +42,23 @@ def _need(t: torch.Tensor | None, name: str, dtype: torch.dtype, numel: int | No
         raise ValueError(f"{name} has {t.numel()} elements, needs {numel}")
 
 
+LAYOUT_ROWS, LAYOUT_TILES = 0, 1      # MDL_LAYOUT_* of include/mdlarc_hip.h
+
+
+def _layout(tiled: bool) -> int:
+    return LAYOUT_TILES if tiled else LAYOUT_ROWS
+
+
+def tile_rows(rows: int) -> int:
+    """Rows a buffer in the MFMA tile layout holds for ``rows`` rows (whole 16-row blocks)."""
+    return (rows + 15) // 16 * 16
+
+
+def split_numel(rows: int, k: int, tiled: bool) -> int:
+    """Elements of a split activation of k channels ([rows, 2k] bf16) in either layout."""
+    return (tile_rows(rows) if tiled else rows) * 2 * k
+
+
 def table_dtype_code(t: torch.Tensor) -> int:
     if t.dtype == F32:
         return 0
@@ -53,8 +70,9 @@ def table_dtype_code(t: torch.Tensor) -> int:
 def embed_rmsnorm(ids: torch.Tensor, example_ids: torch.Tensor | None, tok_table: torch.Tensor,
                   ex_table: torch.Tensor | None, row_len: int, gamma: torch.Tensor, eps: float,
                   x_out: torch.Tensor, xs_out: torch.Tensor | None,
-                  rstd_out: torch.Tensor) -> None:
-    """x = tok[ids] + ex[example_ids], rstd, xs = split(x * gamma) as [rows, 2d] bf16."""
+                  rstd_out: torch.Tensor, tiled: bool = False) -> None:
+    """x = tok[ids] + ex[example_ids], rstd, xs = split(x * gamma) as [rows, 2d] bf16
+    (row-major, or in MFMA tiles for gemm_split when ``tiled``)."""
     rows = ids.numel()
     vocab, d = tok_table.shape
     _need(ids, "ids", I64)
@@ -68,20 +86,21 @@ def embed_rmsnorm(ids: torch.Tensor, example_ids: torch.Tensor | None, tok_table
             raise ValueError("example_ids shorter than the number of batch rows")
     _need(gamma, "gamma", F32, d)
     _need(x_out, "x_out", F32, rows * d)
-    _need(xs_out, "xs_out", BF16, rows * 2 * d, optional=True)
+    _need(xs_out, "xs_out", BF16, split_numel(rows, d, tiled), optional=True)
     _need(rstd_out, "rstd_out", F32, rows)
     n_ex = ex_table.shape[0] if ex_table is not None else 0
     _lib.check(_lib.lib().mdl_embed_rmsnorm(
         _p(ids), _p(example_ids), _p(tok_table), _p(ex_table), table_dtype_code(tok_table),
         vocab, n_ex, rows, row_len, d, _p(gamma), eps, _p(x_out), _p(xs_out), _p(rstd_out),
-        _stream()), "mdl_embed_rmsnorm")
+        _layout(tiled), _stream()), "mdl_embed_rmsnorm")
 
 
 def decode_embed(token: torch.Tensor, example_ids: torch.Tensor | None, tok_table: torch.Tensor,
                  ex_table: torch.Tensor | None, gamma: torch.Tensor, eps: float,
                  gx: torch.Tensor, gy: torch.Tensor, in_out: torch.Tensor, pos_out: torch.Tensor,
                  counters: torch.Tensor | None, x_out: torch.Tensor, xs_out: torch.Tensor,
-                 rstd_out: torch.Tensor, max_x: int = 30, max_y: int = 29) -> None:
+                 rstd_out: torch.Tensor, max_x: int = 30, max_y: int = 29,
+                 tiled: bool = False) -> None:
     """Grid position of each row's emitted token (state advanced), then K1 on that token."""
     batch = token.numel()
     vocab, d = tok_table.shape
@@ -98,30 +117,31 @@ def decode_embed(token: torch.Tensor, example_ids: torch.Tensor | None, tok_tabl
     _need(counters, "counters", I32, 2, optional=True)
     _need(gamma, "gamma", F32, d)
     _need(x_out, "x_out", F32, batch * d)
-    _need(xs_out, "xs_out", BF16, batch * 2 * d)
+    _need(xs_out, "xs_out", BF16, split_numel(batch, d, tiled))
     _need(rstd_out, "rstd_out", F32, batch)
     n_ex = ex_table.shape[0] if ex_table is not None else 0
     _lib.check(_lib.lib().mdl_decode_embed(
         _p(token), _p(example_ids), _p(tok_table), _p(ex_table), table_dtype_code(tok_table),
         vocab, n_ex, batch, d, _p(gamma), eps, _p(gx), _p(gy), _p(in_out), max_x, max_y,
-        _p(pos_out), _p(counters), _p(x_out), _p(xs_out), _p(rstd_out), _stream()),
-        "mdl_decode_embed")
+        _p(pos_out), _p(counters), _p(x_out), _p(xs_out), _p(rstd_out), _layout(tiled),
+        _stream()), "mdl_decode_embed")
 
 
 def add_rmsnorm(x: torch.Tensor, delta: torch.Tensor | None, bias: torch.Tensor | None,
                 gamma: torch.Tensor, eps: float, xs_out: torch.Tensor | None,
-                rstd_out: torch.Tensor) -> None:
-    """x += delta (+ bias) in place (fp32), rstd, xs = split(x * gamma) as [rows, 2d] bf16."""
+                rstd_out: torch.Tensor, tiled: bool = False) -> None:
+    """x += delta (+ bias) in place (fp32), rstd, xs = split(x * gamma) as [rows, 2d] bf16
+    (row-major, or in MFMA tiles when ``tiled``)."""
     rows, d = x.shape
     _need(x, "x", F32)
     _need(delta, "delta", F32, rows * d, optional=True)
     _need(bias, "bias", F32, d, optional=True)
     _need(gamma, "gamma", F32, d)
-    _need(xs_out, "xs_out", BF16, rows * 2 * d, optional=True)
+    _need(xs_out, "xs_out", BF16, split_numel(rows, d, tiled), optional=True)
     _need(rstd_out, "rstd_out", F32, rows)
     _lib.check(_lib.lib().mdl_add_rmsnorm(
         _p(x), _p(delta), _p(bias), rows, d, _p(gamma), eps, _p(xs_out), _p(rstd_out),
-        _stream()), "mdl_add_rmsnorm")
+        _layout(tiled), _stream()), "mdl_add_rmsnorm")
 
 
 def qkv_rope_cache(qkv: torch.Tensor, rstd: torch.Tensor | None, pos: torch.Tensor,
@@ -183,18 +203,71 @@ def qkv_rope_cache_packed(qkv: torch.Tensor, rstd: torch.Tensor | None, pos: tor
 
 
 def swiglu(gate_up: torch.Tensor, rstd: torch.Tensor | None, bias_gate: torch.Tensor | None,
-           bias_up: torch.Tensor | None, h_out: torch.Tensor) -> None:
-    """h = silu(rstd*g + b_g) * (rstd*u + b_u) from fp32 gate|up, written as split [rows, 2F]."""
+           bias_up: torch.Tensor | None, h_out: torch.Tensor, tiled: bool = False) -> None:
+    """h = silu(rstd*g + b_g) * (rstd*u + b_u) from fp32 gate|up, written as split [rows, 2F]
+    (row-major, or in MFMA tiles when ``tiled``)."""
     rows, two_f = gate_up.shape
     f = two_f // 2
     _need(gate_up, "gate_up", F32)
     _need(rstd, "rstd", F32, rows, optional=True)
     _need(bias_gate, "bias_gate", F32, f, optional=True)
     _need(bias_up, "bias_up", F32, f, optional=True)
-    _need(h_out, "h_out", BF16, rows * 2 * f)
+    _need(h_out, "h_out", BF16, split_numel(rows, f, tiled))
     _lib.check(_lib.lib().mdl_swiglu(
         _p(gate_up), two_f, _p(rstd), _p(bias_gate), _p(bias_up), rows, f, _p(h_out),
-        _stream()), "mdl_swiglu")
+        _layout(tiled), _stream()), "mdl_swiglu")
+
+
+def gemm_split(a: torch.Tensor, w: torch.Tensor, out: torch.Tensor, k: int,
+               a_tiled: bool = False, w_tiled: bool = False, tile: int = 0) -> None:
+    """out[m, n] (fp32) = (a_hi + a_lo) @ w[:, :k]^T on the decode GEMM kernel (K5); m, n from
+    ``out``.  A row-major ``a`` is [m, >= 2k] (hi | lo), a row-major ``w`` [n, >= k] -- the
+    [W | W] operand of gemm_f32 serves, its left half is read.  Tiled operands (MFMA tile
+    layout) hold tile_rows(m) * 2k and tile_rows(n) * k elements."""
+    _need(a, "a", BF16)
+    _need(w, "w", BF16)
+    _need(out, "out", F32)
+    if out.dim() != 2:
+        raise ValueError("out must be [m, n]")
+    m, n = out.shape
+    lda = ldw = 0
+    if a_tiled:
+        _need(a, "a", BF16, tile_rows(m) * 2 * k)
+    else:
+        if a.dim() != 2 or a.shape[0] != m or a.shape[1] < 2 * k:
+            raise ValueError(f"a must be [{m}, >= {2 * k}] (got {tuple(a.shape)})")
+        lda = a.shape[1]
+    if w_tiled:
+        _need(w, "w", BF16, tile_rows(n) * k)
+    else:
+        if w.dim() != 2 or w.shape[0] != n or w.shape[1] < k:
+            raise ValueError(f"w must be [{n}, >= {k}] (got {tuple(w.shape)})")
+        ldw = w.shape[1]
+    _lib.check(_lib.lib().mdl_gemm_split(
+        _p(a), lda, _layout(a_tiled), _p(w), ldw, _layout(w_tiled), _p(out), n, m, n, k, tile,
+        _stream()), "mdl_gemm_split")
+
+
+def gemm_split_tiles() -> int:
+    return _lib.lib().mdl_gemm_split_tiles()
+
+
+def gemm_split_pick(m: int, n: int, k: int) -> int:
+    return _lib.lib().mdl_gemm_split_pick(m, n, k)
+
+
+def tile_matrix(src: torch.Tensor, cols: int | None = None) -> torch.Tensor:
+    """Columns [0, cols) of the 2-D bf16 ``src`` in the MFMA tile layout (a new flat tensor of
+    tile_rows(rows) * cols elements; padding rows zero)."""
+    _need(src, "src", BF16)
+    if src.dim() != 2:
+        raise ValueError("src must be 2-D")
+    rows = src.shape[0]
+    cols = src.shape[1] if cols is None else cols
+    dst = torch.empty(tile_rows(rows) * cols, dtype=BF16, device=src.device)
+    _lib.check(_lib.lib().mdl_tile_matrix(_p(src), src.shape[1], rows, cols, _p(dst),
+                                          _stream()), "mdl_tile_matrix")
+    return dst
 
 
 def attn_prefill(q: torch.Tensor, k_cache: torch.Tensor, v_cache: torch.Tensor, batch: int,
@@ -277,13 +350,14 @@ def attn_decode(q: torch.Tensor, k_cache: torch.Tensor, v_cache: torch.Tensor, b
                 kv_start: torch.Tensor | None, seq_pos: int, seq_dev: torch.Tensor | None,
                 workspace: torch.Tensor | None, split_len: int, out: torch.Tensor,
                 row_holes: torch.Tensor | None = None,
-                row_order: torch.Tensor | None = None) -> None:
-    """out: split [batch, 2*n_heads*64] bf16.  row_holes (uint8 [batch], from grid_init):
-    rows marked 0 skip the prompt-mask reads.  row_order (int32 [batch]): permutation giving
-    the dispatch order of the rows (longest first)."""
+                row_order: torch.Tensor | None = None, tiled: bool = False) -> None:
+    """out: split [batch, 2*n_heads*64] bf16 (row-major, or MFMA tiles when ``tiled``).
+    row_holes (uint8 [batch], from grid_init): rows marked 0 skip the prompt-mask reads.
+    row_order (int32 [batch]): permutation giving the dispatch order of the rows (longest
+    first)."""
     n = batch * n_heads * HEAD_DIM
     _need(q, "q", BF16, n)
-    _need(out, "out", BF16, 2 * n)
+    _need(out, "out", BF16, split_numel(batch, n_heads * HEAD_DIM, tiled))
     for name, c in (("k_cache", k_cache), ("v_cache", v_cache)):
         _need(c, name, BF16)
         if c.dim() != 4 or c.shape[0] != batch or c.shape[1] != n_heads or c.shape[3] != 64:
@@ -299,7 +373,8 @@ def attn_decode(q: torch.Tensor, k_cache: torch.Tensor, v_cache: torch.Tensor, b
         _p(q), _p(k_cache), _p(v_cache), batch, n_heads, HEAD_DIM, k_cache.shape[2],
         _p(prompt_mask), prompt_len, _p(row_holes), _p(kv_start), _p(row_order), seq_pos,
         _p(seq_dev),
-        _p(workspace), ws_bytes, split_len, _p(out), _stream()), "mdl_attn_decode")
+        _p(workspace), ws_bytes, split_len, _p(out), _layout(tiled), _stream()),
+        "mdl_attn_decode")
 
 
 def attn_decode_rope(qkv: torch.Tensor, rstd: torch.Tensor, pos: torch.Tensor,
@@ -309,7 +384,7 @@ def attn_decode_rope(qkv: torch.Tensor, rstd: torch.Tensor, pos: torch.Tensor,
                      kv_start: torch.Tensor | None, seq_pos: int, seq_dev: torch.Tensor | None,
                      workspace: torch.Tensor | None, split_len: int, out: torch.Tensor,
                      row_holes: torch.Tensor | None = None,
-                     row_order: torch.Tensor | None = None) -> None:
+                     row_order: torch.Tensor | None = None, tiled: bool = False) -> None:
     """qkv_rope_cache (one token per row, slot t) + attn_decode in one launch."""
     d = n_heads * HEAD_DIM
     _need(qkv, "qkv", F32, batch * 3 * d)
@@ -318,7 +393,7 @@ def attn_decode_rope(qkv: torch.Tensor, rstd: torch.Tensor, pos: torch.Tensor,
     _need(rstd, "rstd", F32, batch)
     _need(pos, "pos", I64, batch * 3)
     _need(rope_tab, "rope_tab", F32)
-    _need(out, "out", BF16, 2 * batch * d)
+    _need(out, "out", BF16, split_numel(batch, d, tiled))
     for name, c in (("k_cache", k_cache), ("v_cache", v_cache)):
         _need(c, name, BF16)
         if c.dim() != 4 or c.shape[0] != batch or c.shape[1] != n_heads or c.shape[3] != 64:
@@ -335,7 +410,8 @@ def attn_decode_rope(qkv: torch.Tensor, rstd: torch.Tensor, pos: torch.Tensor,
         _p(qkv), qkv.shape[1], _p(rstd), _p(pos), _p(rope_tab), mx, my, mz, px, py, pz, q_scale,
         _p(k_cache), _p(v_cache), batch, n_heads, HEAD_DIM, k_cache.shape[2], _p(prompt_mask),
         prompt_len, _p(row_holes), _p(kv_start), _p(row_order), seq_pos, _p(seq_dev),
-        _p(workspace), ws_bytes, split_len, _p(out), _stream()), "mdl_attn_decode_rope")
+        _p(workspace), ws_bytes, split_len, _p(out), _layout(tiled), _stream()),
+        "mdl_attn_decode_rope")
 
 
 class HeadConstraints:

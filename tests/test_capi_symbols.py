@@ -44,13 +44,27 @@ def test_argument_errors_are_reported_before_any_launch():
     L = _lib.lib()
     fake = 1 << 20                                  # never dereferenced: rejected first
     assert L.mdl_attn_prefill(fake, fake, fake, 1, 4, 1, 32, 4, None, None, 1, fake, None) == -4
-    assert L.mdl_swiglu(None, 16, None, None, None, 1, 8, fake, None) == -1
-    assert L.mdl_swiglu(fake, 16, None, None, None, 1, 12, fake, None) == -3
-    assert L.mdl_swiglu(fake + 2, 16, None, None, None, 1, 8, fake, None) == -2
+    assert L.mdl_swiglu(None, 16, None, None, None, 1, 8, fake, 0, None) == -1
+    assert L.mdl_swiglu(fake, 16, None, None, None, 1, 12, fake, 0, None) == -3
+    assert L.mdl_swiglu(fake + 2, 16, None, None, None, 1, 8, fake, 0, None) == -2
+    # the tile layout needs whole 32-column blocks of the split row; layout codes are 0 / 1
+    assert L.mdl_swiglu(fake, 16, None, None, None, 1, 8, fake, 1, None) == -3
+    assert L.mdl_swiglu(fake, 32, None, None, None, 1, 16, fake, 2, None) == -3
+    assert L.mdl_add_rmsnorm(fake, None, None, 1, 8, fake, 1e-5, fake, fake, 1, None) == -3
     assert L.mdl_qkv_rope_cache(fake, 192, None, fake, fake, 1, 4, 1, 64, 32, 32, 8, 10, 10, 12,
                                 0.125, fake, fake, fake, 4, 1, None, None) == -5
     assert L.mdl_attn_decode(fake, fake, fake, 1, 1, 64, 1024, None, 0, None, None, None, 5,
-                             None, None, 0, 128, fake, None) == -6
+                             None, None, 0, 128, fake, 0, None) == -6
+    # K5: k a multiple of 32, n of 4, layout codes 0 / 1, row-major lda >= 2k
+    assert L.mdl_gemm_split(fake, 64, 0, fake, 32, 0, fake, 8, 4, 8, 48, 0, None) == -3
+    assert L.mdl_gemm_split(fake, 64, 0, fake, 32, 0, fake, 8, 4, 6, 32, 0, None) == -3
+    assert L.mdl_gemm_split(fake, 64, 2, fake, 32, 0, fake, 8, 4, 8, 32, 0, None) == -3
+    assert L.mdl_gemm_split(fake, 32, 0, fake, 32, 0, fake, 8, 4, 8, 32, 0, None) == -3
+    assert L.mdl_gemm_split(fake + 8, 64, 0, fake, 32, 0, fake, 8, 4, 8, 32, 0, None) == -2
+    assert L.mdl_gemm_split(None, 0, 1, fake, 0, 1, fake, 8, 4, 8, 32, 0, None) == -1
+    assert L.mdl_tile_matrix(fake, 40, 4, 40, fake, None) == -3
+    assert L.mdl_gemm_split_tiles() >= 1
+    assert 1 <= L.mdl_gemm_split_pick(256, 2304, 768) <= L.mdl_gemm_split_tiles()
     # packed prefill: the per-row starts / offsets and the per-token rows / slots are required
     assert L.mdl_attn_prefill_packed(fake, fake, fake, 1, 4, 1, 64, 4, None, None, fake, 1, fake,
                                      None) == -1

@@ -887,9 +887,130 @@ def test_capi_rejects_bad_arguments_before_launch():
                                 32, 32, 8, 10, 10, 12, 0.125, x.data_ptr(), x.data_ptr(),
                                 x.data_ptr(), 4, 1, None, None) == -5
     # misaligned pointer
-    assert L.mdl_swiglu(x.data_ptr() + 2, 16, None, None, None, 1, 8, x.data_ptr(), None) == -2
+    assert L.mdl_swiglu(x.data_ptr() + 2, 16, None, None, None, 1, 8, x.data_ptr(), 0,
+                        None) == -2
     # workspace too small for a multi-split decode
     assert L.mdl_attn_decode(x.data_ptr(), x.data_ptr(), x.data_ptr(), 1, 1, 64, 1024, None, 0,
-                             None, None, None, 5, None, None, 0, 128, x.data_ptr(), None) == -6
+                             None, None, None, 5, None, None, 0, 128, x.data_ptr(), 0,
+                             None) == -6
     with pytest.raises(RuntimeError, match="head_dim"):
         _lib.check(-4, "probe")
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("m,n,k", [(256, 2304, 768), (256, 768, 2048), (128, 5504, 1024),
+                                   (64, 1280, 3392), (3, 80, 64), (17, 1408, 704),
+                                   (100, 256, 96)])
+def test_gemm_split(m, n, k):
+    """K5, every compiled block shape and the automatic choice, against an fp64 CPU product of
+    the same bf16 operands: (hi + lo) @ w^T to fp32 accumulation error (bound: 1e-5 of the sum
+    of |products|, a few ulps per term at these K), rows and columns past the tiles included.
+    For one block shape the four operand layouts (row-major / MFMA tiles, each operand) give
+    identical bits, and so do two calls; the row-major weight may be the left half of the
+    [W | W] prefill operand; the hipBLASLt [W | W] GEMM of the prefill agrees to the bound."""
+    from mdlarc_scale_amd.engine import gemm_f32
+
+    g = torch.Generator().manual_seed(m * 7 + n + k)
+    x = torch.randn(m, k, generator=g) * 2.0
+    hi = x.to(torch.bfloat16)
+    lo = (x - hi.float()).to(torch.bfloat16)
+    w = (torch.randn(n, k, generator=g) * 0.05).to(torch.bfloat16)
+    ref = (hi.double() + lo.double()) @ w.double().T
+    bound = 1e-5 * ((hi.double().abs() + lo.double().abs()) @ w.double().abs().T) + 1e-30
+    a = torch.cat([hi, lo], 1).to(DEV)
+    w2 = torch.cat([w, w], 1).to(DEV)
+    wd = w.to(DEV)
+    at, wt = K().tile_matrix(a), K().tile_matrix(wd)
+
+    def run(tile, a_op, a_tiled, w_op, w_tiled):
+        out = torch.full((m, n), float("nan"), device=DEV)
+        K().gemm_split(a_op, w_op, out, k, a_tiled=a_tiled, w_tiled=w_tiled, tile=tile)
+        return out
+
+    for t in list(range(1, K().gemm_split_tiles() + 1)) + [0]:
+        out = run(t, at, True, wt, True)
+        torch.cuda.synchronize()
+        err = (out.cpu().double() - ref).abs()
+        assert bool((err <= bound).all()), f"tile {t}: max err {err.max().item():.3e}"
+        for a_op, a_t, w_op, w_t in ((at, True, wt, True), (a, False, w2, False),
+                                     (a, False, wd, False), (at, True, w2, False),
+                                     (a, False, wt, True)):
+            assert torch.equal(run(t, a_op, a_t, w_op, w_t), out), f"tile {t} layouts"
+    blas = torch.empty(m, n, device=DEV)
+    gemm_f32(a, w2, blas)
+    assert bool(((blas.cpu().double() - ref).abs() <= bound).all())
+
+
+def test_tile_matrix_layout():
+    """mdl_tile_matrix against the layout's definition: element (r, c) of a [rows, cols] matrix
+    sits at 512 (r/16 * cols/32 + c/32) + 8 (16 ((c/8) % 4) + r % 16) + c % 8; padding rows 0."""
+    rows, cols = 37, 96
+    src = torch.arange(rows * cols, dtype=torch.float32).view(rows, cols)
+    src_b = (src % 251).to(torch.bfloat16)
+    got = K().tile_matrix(src_b.to(DEV)).cpu()
+    r = torch.arange(48).view(48, 1).expand(48, cols)
+    c = torch.arange(cols).view(1, cols).expand(48, cols)
+    off = 512 * ((r // 16) * (cols // 32) + c // 32) + 8 * (16 * ((c // 8) % 4) + r % 16) + c % 8
+    want = torch.zeros(48, cols, dtype=torch.bfloat16)
+    want[:rows] = src_b
+    assert got.numel() == 48 * cols
+    assert torch.equal(got[off.reshape(-1)].view(48, cols), want)
+
+
+def test_producers_write_the_tile_layout():
+    """Every producer of a decode GEMM input writes, with the tile layout selected, exactly
+    mdl_tile_matrix of its row-major output (padding rows left untouched)."""
+    g = torch.Generator().manual_seed(11)
+    B, d, F, H = 37, 256, 704, 4
+
+    def both(fn, numel_rows, cols):
+        outs = []
+        for tiled in (False, True):
+            buf = torch.zeros((K().tile_rows(numel_rows) if tiled else numel_rows) * cols,
+                              device=DEV, dtype=torch.bfloat16)
+            fn(buf, tiled)
+            outs.append(buf)
+        torch.cuda.synchronize()
+        assert torch.equal(K().tile_matrix(outs[0].view(numel_rows, cols)), outs[1])
+
+    tok = torch.randn(14, d, generator=g).to(DEV)
+    ex = torch.randn(5, d, generator=g).to(DEV)
+    gamma = (1 + 0.1 * torch.randn(d, generator=g)).to(DEV)
+    ids = torch.randint(0, 14, (B,), generator=g).to(DEV)
+    exi = torch.randint(0, 5, (B,), generator=g).to(DEV)
+    x = torch.empty(B, d, device=DEV)
+    r = torch.empty(B, device=DEV)
+    both(lambda buf, t: K().embed_rmsnorm(ids, exi, tok, ex, 1, gamma, 1e-5, x, buf, r,
+                                          tiled=t), B, 2 * d)
+    state = (torch.randint(0, 30, (B,), generator=g).to(torch.int32),
+             torch.randint(0, 29, (B,), generator=g).to(torch.int32),
+             torch.randint(0, 2, (B,), generator=g).to(torch.uint8))
+    pos = torch.empty(B, 3, dtype=torch.int64, device=DEV)
+    both(lambda buf, t: K().decode_embed(ids, exi, tok, ex, gamma, 1e-5,
+                                         *(s.clone().to(DEV) for s in state), pos, None, x, buf,
+                                         r, tiled=t), B, 2 * d)
+    x0 = torch.randn(B, d, generator=g).to(DEV)
+    delta = torch.randn(B, d, generator=g).to(DEV)
+    both(lambda buf, t: K().add_rmsnorm(x0.clone(), delta, None, gamma, 1e-5, buf, r, tiled=t),
+         B, 2 * d)
+    gu = torch.randn(B, 2 * F, generator=g).to(DEV)
+    both(lambda buf, t: K().swiglu(gu, r, None, None, buf, tiled=t), B, 2 * F)
+    # decode attention, unfused and fused with K2, single split and split-K (combine kernel)
+    from mdlarc_scale_amd.transformer import RotaryEmbedding3D
+    rope = RotaryEmbedding3D(64, 32, 32, 8)
+    tab, geom = rope.device_table(DEV), (32, 32, 8, rope.px, rope.py, rope.pz)
+    slots, t_pos = 300, 250
+    kc = bf(torch.randn(B, H, slots, 64, generator=g)).to(DEV)
+    vc = bf(torch.randn(B, H, slots, 64, generator=g)).to(DEV)
+    q = bf(torch.randn(B, H * 64, generator=g) / 8).to(DEV)
+    qkv = torch.randn(B, 3 * H * 64, generator=g).to(DEV)
+    rstd = (0.5 + torch.rand(B, generator=g)).to(DEV)
+    posr = torch.randint(0, 30, (B, 3), generator=g).to(DEV)
+    for split_len in (128, 384):
+        ws_n = K().attn_decode_workspace_bytes(B, H, slots, split_len) // 4
+        ws = torch.empty(max(ws_n, 1), device=DEV)
+        both(lambda buf, t: K().attn_decode(q, kc, vc, B, H, None, 0, None, t_pos, None, ws,
+                                            split_len, buf, tiled=t), B, 2 * H * 64)
+        both(lambda buf, t: K().attn_decode_rope(qkv, rstd, posr, tab, geom, 0.125, kc.clone(),
+                                                 vc.clone(), B, H, None, 0, None, t_pos, None,
+                                                 ws, split_len, buf, tiled=t), B, 2 * H * 64)
