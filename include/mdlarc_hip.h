@@ -195,6 +195,21 @@ int mdl_swiglu(const float* gate_up, int64_t ld, const float* rstd, const float*
 int mdl_gemm_split(const uint16_t* a, int64_t lda, int a_layout, const uint16_t* w, int64_t ldw,
                    int w_layout, float* out, int64_t ldo, int m, int n, int k, int tile,
                    void* stream);
+/*
+ * K5 with the SwiGLU gate (K3) fused into its epilogue, for the decode step:
+ *   h[i, c] = silu(rstd[i] g + bias_gate[c]) * (rstd[i] u + bias_up[c]),
+ *   g, u = the fc_gate / fc_up rows c of w_gu against a, as mdl_gemm_split computes them,
+ * written as the split h of mdl_swiglu ([m, 2 d_ff], MDL_LAYOUT_TILES) with no fp32 gate / up
+ * round trip; the result equals mdl_gemm_split + mdl_swiglu bit for bit for the same tile.
+ * Replaces: FeedForward.forward's silu(fc_gate(x)) * fc_up(x) (src/transformer.py:441-449).
+ * a: split activation [m, 2k] in MDL_LAYOUT_TILES.  w_gu: [W_gate; W_up] ([2 d_ff, k]) with
+ * their 16-row blocks interleaved (row block 2 b = W_gate rows 16 b .. 16 b + 15, row block
+ * 2 b + 1 = W_up rows 16 b ..), in MDL_LAYOUT_TILES.  rstd / biases may be NULL (1 / 0).
+ * d_ff a multiple of 16, k of 32; tile as for mdl_gemm_split (chosen for n = 2 d_ff).
+ */
+int mdl_gemm_split_swiglu(const uint16_t* a, const uint16_t* w_gu, const float* rstd,
+                          const float* bias_gate, const float* bias_up, uint16_t* h_out, int m,
+                          int d_ff, int k, int tile, void* stream);
 /* Number of compiled block shapes, and the automatic choice for (m, n, k) (host only). */
 int mdl_gemm_split_tiles(void);
 int mdl_gemm_split_pick(int m, int n, int k);

@@ -48,6 +48,7 @@ SIGNATURES: dict[str, tuple[object, list]] = {
     "mdl_swiglu": (c_int, [P, c_int64, P, P, P, c_int, c_int, P, c_int, P]),
     "mdl_gemm_split": (c_int, [P, c_int64, c_int, P, c_int64, c_int, P, c_int64, c_int, c_int,
                                c_int, c_int, P]),
+    "mdl_gemm_split_swiglu": (c_int, [P, P, P, P, P, P, c_int, c_int, c_int, c_int, P]),
     "mdl_gemm_split_tiles": (c_int, []),
     "mdl_gemm_split_pick": (c_int, [c_int, c_int, c_int]),
     "mdl_tile_matrix": (c_int, [P, c_int64, c_int, c_int, P, P]),

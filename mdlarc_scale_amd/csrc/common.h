@@ -42,6 +42,12 @@ __device__ __forceinline__ uint4 pack8(const float* f) {
   return v;
 }
 
+// silu(a) * b, the SwiGLU gate, in the one form every kernel that computes it uses (K3 and the
+// fused epilogue of K5 then agree bit for bit)
+__device__ __forceinline__ float silu_mul(float a, float b) {
+  return a / (1.f + __expf(-a)) * b;
+}
+
 // ---- split activations -----------------------------------------------------------------------
 // A GEMM input row of width K is stored as 2K bf16: hi = bf16(v) in columns [0, K) and
 // lo = bf16(v - hi) in [K, 2K) (v - hi is exact in fp32).  Against a weight packed as [W | W]

@@ -55,11 +55,23 @@ __device__ __forceinline__ int64_t frag_step(int s) {
   return TILED ? static_cast<int64_t>(512) * s : static_cast<int64_t>(32) * s;
 }
 
-template <int TN, int TM, bool WT, bool AT>
+// SwiGLU epilogue (the gate / up projection with the MLP gate fused): w holds [W_gate; W_up]
+// with their 16-row blocks interleaved (block 2 b = gate rows 16 b .., block 2 b + 1 = up rows
+// 16 b ..), so output fragments 2 p and 2 p + 1 of a block are the gate and the up value of the
+// same 16 channels.
+struct SwigluEpi {
+  const float* rstd;       // [M] or NULL (1)
+  const float* bias_gate;  // [F] or NULL (0)
+  const float* bias_up;    // [F] or NULL (0)
+  uint16_t* h;             // split bf16 [M, 2F] in the tile layout
+  int d_ff;
+};
+
+template <int TN, int TM, bool WT, bool AT, bool SWIGLU = false>
 __global__ __launch_bounds__(64 * kGemmWaves) void split_gemm_kernel(
     const uint16_t* __restrict__ a, int64_t lda, const uint16_t* __restrict__ w, int64_t ldw,
     float* __restrict__ out, int64_t ldo, int M, int N, int K, int n_tiles, int m_tiles,
-    int per_xcd) {
+    int per_xcd, SwigluEpi epi = {}) {
   constexpr int FN = TN / 16, FM = TM / 16, NW = kGemmWaves;
   static_assert(TN % 16 == 0 && TM % 16 == 0, "tile must be a multiple of 16");
   // logical tile of this block: tiles per_xcd * x .. per_xcd * (x + 1) - 1 run on XCD x
@@ -128,17 +140,51 @@ __global__ __launch_bounds__(64 * kGemmWaves) void split_gemm_kernel(
 #pragma unroll
     for (int j = 0; j < FM; ++j) red[wave][i * FM + j][lane] = acc[i][j];
   __syncthreads();
-  for (int q = threadIdx.x; q < FN * FM * 64; q += 64 * NW) {
-    const int t = q >> 6, ln = q & 63;
-    f32x4_t v = red[0][t][ln];
+  if constexpr (SWIGLU) {
+    static_assert(FN % 2 == 0, "the SwiGLU epilogue pairs gate and up fragments");
+    // q = (channel block p, row block j, lane): gate fragment 2 p, up fragment 2 p + 1
+    for (int q = threadIdx.x; q < (FN / 2) * FM * 64; q += 64 * NW) {
+      const int pj = q >> 6, ln = q & 63;
+      const int p = pj / FM, j = pj - p * FM;
+      const int tg = (2 * p) * FM + j, tu = (2 * p + 1) * FM + j;
+      f32x4_t gv = red[0][tg][ln], uv = red[0][tu][ln];
 #pragma unroll
-    for (int wv = 1; wv < NW; ++wv) v += red[wv][t][ln];
-    const int i = t / FM, j = t - i * FM;
-    const int m = m0 + 16 * j + (ln & 15);
-    const int n = n0 + 16 * i + 4 * (ln >> 4);
-    if (m < M && n < N)
-      *reinterpret_cast<float4*>(out + static_cast<int64_t>(m) * ldo + n) =
-          make_float4(v[0], v[1], v[2], v[3]);
+      for (int wv = 1; wv < NW; ++wv) {
+        gv += red[wv][tg][ln];
+        uv += red[wv][tu][ln];
+      }
+      const int m = m0 + 16 * j + (ln & 15);
+      const int ch = 16 * (n0 / 32 + p) + 4 * (ln >> 4);   // gate / up channel of element 0
+      if (m < M && 2 * ch < N) {
+        const float r = epi.rstd ? epi.rstd[m] : 1.f;
+        const float4 bg = epi.bias_gate ? *reinterpret_cast<const float4*>(epi.bias_gate + ch)
+                                        : make_float4(0.f, 0.f, 0.f, 0.f);
+        const float4 bu = epi.bias_up ? *reinterpret_cast<const float4*>(epi.bias_up + ch)
+                                      : make_float4(0.f, 0.f, 0.f, 0.f);
+        // the arithmetic of K3 (swiglu.hip), so fused and unfused agree bit for bit
+        const float o[4] = {silu_mul(fmaf(r, gv[0], bg.x), fmaf(r, uv[0], bu.x)),
+                            silu_mul(fmaf(r, gv[1], bg.y), fmaf(r, uv[1], bu.y)),
+                            silu_mul(fmaf(r, gv[2], bg.z), fmaf(r, uv[2], bu.z)),
+                            silu_mul(fmaf(r, gv[3], bg.w), fmaf(r, uv[3], bu.w))};
+        uint2 hi, lo;
+        split4(o, hi, lo);
+        *reinterpret_cast<uint2*>(epi.h + tile_off(m, ch, 2 * epi.d_ff)) = hi;
+        *reinterpret_cast<uint2*>(epi.h + tile_off(m, epi.d_ff + ch, 2 * epi.d_ff)) = lo;
+      }
+    }
+  } else {
+    for (int q = threadIdx.x; q < FN * FM * 64; q += 64 * NW) {
+      const int t = q >> 6, ln = q & 63;
+      f32x4_t v = red[0][t][ln];
+#pragma unroll
+      for (int wv = 1; wv < NW; ++wv) v += red[wv][t][ln];
+      const int i = t / FM, j = t - i * FM;
+      const int m = m0 + 16 * j + (ln & 15);
+      const int n = n0 + 16 * i + 4 * (ln >> 4);
+      if (m < M && n < N)
+        *reinterpret_cast<float4*>(out + static_cast<int64_t>(m) * ldo + n) =
+            make_float4(v[0], v[1], v[2], v[3]);
+    }
   }
 }
 
@@ -173,17 +219,17 @@ int pick_tile(int M, int N, int K) {
   return best + 1;
 }
 
-template <int TN, int TM, bool WT, bool AT>
+template <int TN, int TM, bool WT, bool AT, bool SWIGLU = false>
 int launch_tile(const uint16_t* a, int64_t lda, const uint16_t* w, int64_t ldw, float* out,
-                int64_t ldo, int M, int N, int K, hipStream_t st) {
+                int64_t ldo, int M, int N, int K, hipStream_t st, SwigluEpi epi = {}) {
   const int n_tiles = (N + TN - 1) / TN, m_tiles = (M + TM - 1) / TM;
   const int64_t tiles = static_cast<int64_t>(n_tiles) * m_tiles;
   const int64_t per_xcd = (tiles + 7) / 8;
   if (8 * per_xcd > 0x7fffffff) return MDL_ERR_SHAPE;
-  hipLaunchKernelGGL((split_gemm_kernel<TN, TM, WT, AT>),
+  hipLaunchKernelGGL((split_gemm_kernel<TN, TM, WT, AT, SWIGLU>),
                      dim3(static_cast<unsigned>(8 * per_xcd)), dim3(64 * kGemmWaves), 0, st, a,
                      lda, w, ldw, out, ldo, M, N, K, n_tiles, m_tiles,
-                     static_cast<int>(per_xcd));
+                     static_cast<int>(per_xcd), epi);
   return launch_status();
 }
 
@@ -197,6 +243,19 @@ int launch_layouts(int tile, const uint16_t* a, int64_t lda, const uint16_t* w, 
     case 4: return launch_tile<32, 32, WT, AT>(a, lda, w, ldw, out, ldo, M, N, K, st);
     case 5: return launch_tile<64, 16, WT, AT>(a, lda, w, ldw, out, ldo, M, N, K, st);
     case 6: return launch_tile<32, 16, WT, AT>(a, lda, w, ldw, out, ldo, M, N, K, st);
+    default: return MDL_ERR_SHAPE;
+  }
+}
+
+int launch_swiglu(int tile, const uint16_t* a, const uint16_t* w, int M, int N, int K,
+                  hipStream_t st, const SwigluEpi& epi) {
+  switch (tile) {
+    case 1: return launch_tile<64, 64, true, true, true>(a, 0, w, 0, nullptr, 0, M, N, K, st, epi);
+    case 2: return launch_tile<128, 32, true, true, true>(a, 0, w, 0, nullptr, 0, M, N, K, st, epi);
+    case 3: return launch_tile<64, 32, true, true, true>(a, 0, w, 0, nullptr, 0, M, N, K, st, epi);
+    case 4: return launch_tile<32, 32, true, true, true>(a, 0, w, 0, nullptr, 0, M, N, K, st, epi);
+    case 5: return launch_tile<64, 16, true, true, true>(a, 0, w, 0, nullptr, 0, M, N, K, st, epi);
+    case 6: return launch_tile<32, 16, true, true, true>(a, 0, w, 0, nullptr, 0, M, N, K, st, epi);
     default: return MDL_ERR_SHAPE;
   }
 }
@@ -263,4 +322,22 @@ extern "C" int mdl_tile_matrix(const uint16_t* src, int64_t ld, int rows, int co
   hipLaunchKernelGGL(tile_matrix_kernel, dim3(static_cast<unsigned>(blocks)), dim3(256), 0,
                      static_cast<hipStream_t>(stream), src, ld, rows, cols, chunks, dst);
   return launch_status();
+}
+
+extern "C" int mdl_gemm_split_swiglu(const uint16_t* a, const uint16_t* w_gu, const float* rstd,
+                                     const float* bias_gate, const float* bias_up,
+                                     uint16_t* h_out, int m, int d_ff, int k, int tile,
+                                     void* stream) {
+  if (!a || !w_gu || !h_out) return MDL_ERR_NULL;
+  if (m < 0 || d_ff <= 0 || d_ff % 16 != 0 || k <= 0 || k % 32 != 0 || tile < 0 ||
+      tile > kNumTiles)
+    return MDL_ERR_SHAPE;
+  if (!aligned16(a) || !aligned16(w_gu) || !aligned8(h_out) ||
+      (bias_gate && !aligned16(bias_gate)) || (bias_up && !aligned16(bias_up)))
+    return MDL_ERR_ALIGN;
+  if (m == 0) return MDL_OK;
+  const int n = 2 * d_ff;
+  const SwigluEpi epi{rstd, bias_gate, bias_up, h_out, d_ff};
+  return launch_swiglu(tile ? tile : pick_tile(m, n, k), a, w_gu, m, n, k,
+                       static_cast<hipStream_t>(stream), epi);
 }

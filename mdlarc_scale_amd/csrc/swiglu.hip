@@ -45,9 +45,9 @@ __global__ __launch_bounds__(256) void swiglu_kernel(const float* __restrict__ g
   float o[8];
 #pragma unroll
   for (int i = 0; i < 8; ++i) {
-    const float a = r * g[i] + b1[i];
-    const float b = r * u[i] + b2[i];
-    o[i] = a / (1.f + __expf(-a)) * b;
+    const float a = fmaf(r, g[i], b1[i]);   // explicit: the fused K5 epilogue computes the same
+    const float b = fmaf(r, u[i], b2[i]);
+    o[i] = silu_mul(a, b);
   }
   uint4 hi, lo;
   split8(o, hi, lo);

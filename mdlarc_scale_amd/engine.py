@@ -17,7 +17,8 @@ Dataflow per layer (M token rows, d channels, F ffn width; fp32 residual stream 
 
 At decode (M = batch rows) the projections run on K5 instead of hipBLASLt: the producers write
 xs / attn / h in the MFMA tile layout and K5 multiplies them with tiled copies of W (read once,
-not as [W | W]); see ``project``.
+not as [W | W]); see ``project``.  The gate / up GEMM there carries the SwiGLU in its epilogue
+and writes h directly (no gu round trip, no K3 launch).
 
 "split" stores a GEMM input as a hi|lo pair of bf16 (hi = bf16(v), lo = bf16(v - hi)); against a
 weight packed as [W | W] the bf16 MFMA GEMM then sees the activation to ~2^-17 instead of 2^-9.
@@ -97,7 +98,9 @@ class PackedWeights:
         tile = lambda w2: K.tile_matrix(w2, w2.shape[1] // 2)  # noqa: E731
         self.qkv_t = [tile(w) for w in self.qkv] if self.tiles_ok else None
         self.out_t = [tile(w) for w in self.out] if self.tiles_ok else None
-        self.gu_t = [tile(w) for w in self.gu] if self.tiles_ok else None
+        # gate / up with 16-row blocks interleaved: the SwiGLU runs in that GEMM's epilogue
+        self.gu_t = [K.tile_matrix(K.interleave_gate_up(*w[:, :w.shape[1] // 2].chunk(2, 0)))
+                     for w in self.gu] if self.tiles_ok else None
         self.down_t = [tile(w) for w in self.down] if self.tiles_ok else None
         self.ln_f = f32(model.ln_f.weight)
         self.head = f32(model.lm_head.weight)
@@ -307,8 +310,12 @@ class HipEngine:
         t = sc.tiled
         project(sc, sc.attn, W.out[li], W.out_t[li] if t else None, sc.delta)
         K.add_rmsnorm(sc.x, sc.delta, None, W.ln2[li], W.eps, sc.xs, sc.rstd, tiled=t)
-        project(sc, sc.xs, W.gu[li], W.gu_t[li] if t else None, sc.gu)
-        K.swiglu(sc.gu, sc.rstd, W.b_gate[li], W.b_up[li], sc.h, tiled=t)
+        if t:      # decode: gate / up GEMM with the SwiGLU fused (K5 epilogue)
+            K.gemm_split_swiglu(sc.xs, W.gu_t[li], sc.rstd, W.b_gate[li], W.b_up[li], sc.h,
+                                sc.x.shape[0], cfg.d_ff, cfg.d_model)
+        else:
+            gemm_f32(sc.xs, W.gu[li], sc.gu)
+            K.swiglu(sc.gu, sc.rstd, W.b_gate[li], W.b_up[li], sc.h)
         project(sc, sc.h, W.down[li], W.down_t[li] if t else None, sc.delta)
         last = li + 1 == cfg.n_layers
         K.add_rmsnorm(sc.x, sc.delta, W.b_down[li], W.ln_f if last else W.ln1[li + 1], W.eps,

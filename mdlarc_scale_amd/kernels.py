@@ -248,6 +248,33 @@ def gemm_split(a: torch.Tensor, w: torch.Tensor, out: torch.Tensor, k: int,
         _stream()), "mdl_gemm_split")
 
 
+def gemm_split_swiglu(a: torch.Tensor, w_gu: torch.Tensor, rstd: torch.Tensor | None,
+                      bias_gate: torch.Tensor | None, bias_up: torch.Tensor | None,
+                      h_out: torch.Tensor, m: int, d_ff: int, k: int, tile: int = 0) -> None:
+    """h = silu(rstd*g + b_g) * (rstd*u + b_u) straight from the gate / up GEMM (K5 with the
+    SwiGLU epilogue): ``a`` tiled split [m, 2k], ``w_gu`` the tiled interleave_gate_up weight,
+    ``h_out`` tiled split [m, 2 d_ff]."""
+    _need(a, "a", BF16, tile_rows(m) * 2 * k)
+    _need(w_gu, "w_gu", BF16, 2 * d_ff * k)
+    _need(rstd, "rstd", F32, m, optional=True)
+    _need(bias_gate, "bias_gate", F32, d_ff, optional=True)
+    _need(bias_up, "bias_up", F32, d_ff, optional=True)
+    _need(h_out, "h_out", BF16, split_numel(m, d_ff, True))
+    _lib.check(_lib.lib().mdl_gemm_split_swiglu(
+        _p(a), _p(w_gu), _p(rstd), _p(bias_gate), _p(bias_up), _p(h_out), m, d_ff, k, tile,
+        _stream()), "mdl_gemm_split_swiglu")
+
+
+def interleave_gate_up(w_gate: torch.Tensor, w_up: torch.Tensor) -> torch.Tensor:
+    """[W_gate; W_up] with their 16-row blocks interleaved (the weight order of
+    gemm_split_swiglu): row block 2b = W_gate rows 16b.., row block 2b+1 = W_up rows 16b.."""
+    f, k = w_gate.shape
+    if tuple(w_up.shape) != (f, k) or f % 16:
+        raise ValueError("gate and up weights must be [d_ff, k] with d_ff a multiple of 16")
+    return torch.stack([w_gate.reshape(f // 16, 16, k), w_up.reshape(f // 16, 16, k)],
+                       1).reshape(2 * f, k).contiguous()
+
+
 def gemm_split_tiles() -> int:
     return _lib.lib().mdl_gemm_split_tiles()
 

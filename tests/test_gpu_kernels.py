@@ -1014,3 +1014,32 @@ def test_producers_write_the_tile_layout():
         both(lambda buf, t: K().attn_decode_rope(qkv, rstd, posr, tab, geom, 0.125, kc.clone(),
                                                  vc.clone(), B, H, None, 0, None, t_pos, None,
                                                  ws, split_len, buf, tiled=t), B, 2 * H * 64)
+
+
+@pytest.mark.parametrize("m,f,k", [(256, 2048, 768), (37, 704, 256), (64, 3392, 1280)])
+def test_gemm_split_swiglu_equals_gemm_then_swiglu(m, f, k):
+    """K5 with the SwiGLU epilogue (gate / up weights with 16-row blocks interleaved) writes the
+    same split h, bit for bit, as K5 on [W_gate; W_up] followed by K3 (mdl_swiglu), for every
+    block shape and the automatic choice, with and without rstd and biases."""
+    g = torch.Generator().manual_seed(m + f + k)
+    x = torch.randn(m, k, generator=g) * 2.0
+    hi = x.to(torch.bfloat16)
+    lo = (x - hi.float()).to(torch.bfloat16)
+    at = K().tile_matrix(torch.cat([hi, lo], 1).to(DEV))
+    wg = (torch.randn(f, k, generator=g) * 0.05).to(torch.bfloat16).to(DEV)
+    wu = (torch.randn(f, k, generator=g) * 0.05).to(torch.bfloat16).to(DEV)
+    w_il = K().tile_matrix(K().interleave_gate_up(wg, wu))
+    w_cat = K().tile_matrix(torch.cat([wg, wu], 0))
+    rstd = (0.5 + torch.rand(m, generator=g)).to(DEV)
+    bg = (0.1 * torch.randn(f, generator=g)).to(DEV)
+    bu = (0.1 * torch.randn(f, generator=g)).to(DEV)
+    for t in list(range(1, K().gemm_split_tiles() + 1)) + [0]:
+        for r, b1, b2 in ((rstd, bg, bu), (None, None, None)):
+            fused = torch.zeros(K().split_numel(m, f, True), device=DEV, dtype=torch.bfloat16)
+            K().gemm_split_swiglu(at, w_il, r, b1, b2, fused, m, f, k, tile=t)
+            gu = torch.empty(m, 2 * f, device=DEV)
+            K().gemm_split(at, w_cat, gu, k, a_tiled=True, w_tiled=True, tile=t)
+            ref = torch.zeros_like(fused)
+            K().swiglu(gu, r, b1, b2, ref, tiled=True)
+            torch.cuda.synchronize()
+            assert torch.equal(fused, ref), f"tile {t}"
