@@ -76,6 +76,10 @@ def _args():
     ap.add_argument("--no-micro", action="store_true", help="skip the config-1 microbench")
     ap.add_argument("--eager", action="store_true",
                     help="launch every kernel from the host instead of replaying a HIP graph")
+    ap.add_argument("--gemm-compare", action="store_true",
+                    help="also time the decode projections at this workload's shapes (M = rows): "
+                         "K5 (mdl_gemm_split, tiled operands; gate/up with the SwiGLU fused) "
+                         "against hipBLASLt on [W | W], each replayed 50x from a HIP graph")
     ap.add_argument("--augment", action="store_true",
                     help="also time predict_with_augmentations on one task of the workload: "
                          "8 dihedral x 8 colour variants in one fused generation against the "
@@ -220,6 +224,71 @@ def microbench(dev):
         v["frac_of_peak"] = round(v["gbs"] / HBM_PEAK_GBS, 4)
         v["ms"] = round(v["ms"], 5)
         v["gbs"] = round(v["gbs"], 1)
+    return res
+
+
+def graph_time_us(fn, reps=50, replays=10):
+    """Average duration of ``fn``'s launches replayed from a HIP graph of ``reps`` calls
+    (back to back, no host launch gaps)."""
+    import torch
+
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        for _ in range(3):
+            fn()
+    torch.cuda.current_stream().wait_stream(side)
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        for _ in range(reps):
+            fn()
+    g.replay()
+    t = Timer()
+    t.start()
+    for _ in range(replays):
+        g.replay()
+    t.stop()
+    return t.ms() * 1e3 / (reps * replays)
+
+
+def decode_gemm_compare(cfg, B, dev):
+    """The four decode projections of one layer at M = B rows on random bf16 weights: K5 with
+    tiled operands (the decode step's form) against hipBLASLt on the [W | W] operand (the form
+    before K5), plus the gate / up projection with the SwiGLU fused against K5 + K3."""
+    import torch
+
+    from mdlarc_scale_amd import kernels as K
+    from mdlarc_scale_amd.engine import gemm_f32
+
+    d, F = cfg.d_model, cfg.d_ff
+    g = torch.Generator(device="cpu").manual_seed(3)
+    res = {}
+    for name, N, k in (("qkv", 3 * d, d), ("out", d, d), ("gate_up", 2 * F, d), ("down", d, F)):
+        a = torch.randn(B, 2 * k, generator=g).to(dev, torch.bfloat16)
+        w2 = (0.05 * torch.randn(N, 2 * k, generator=g)).to(dev, torch.bfloat16)
+        at, wt = K.tile_matrix(a), K.tile_matrix(w2, k)
+        out = torch.empty(B, N, device=dev)
+        t_blas = graph_time_us(lambda: gemm_f32(a, w2, out))
+        t_k5 = graph_time_us(lambda: K.gemm_split(at, wt, out, k, a_tiled=True, w_tiled=True))
+        nbytes = N * k * 2 + B * 2 * k * 2 + B * N * 4     # W once, split A, fp32 out
+        res[name] = dict(n=N, k=k, tile=K.gemm_split_pick(B, N, k), hipblaslt_us=round(t_blas, 2),
+                         k5_us=round(t_k5, 2), bytes=nbytes,
+                         k5_gbs=round(nbytes / t_k5 / 1e3, 1))
+        if name == "gate_up":
+            rstd = (0.5 + torch.rand(B, generator=g)).to(dev)
+            bg = (0.1 * torch.randn(F, generator=g)).to(dev)
+            bu = (0.1 * torch.randn(F, generator=g)).to(dev)
+            h = torch.empty(K.split_numel(B, F, True), device=dev, dtype=torch.bfloat16)
+            w_il = K.tile_matrix(K.interleave_gate_up(w2[:F, :k], w2[F:, :k]))
+            t_sw = graph_time_us(lambda: K.swiglu(out, rstd, bg, bu, h, tiled=True))
+            t_f = graph_time_us(lambda: K.gemm_split_swiglu(at, w_il, rstd, bg, bu, h, B, F, k))
+            res[name].update(swiglu_us=round(t_sw, 2), fused_swiglu_us=round(t_f, 2))
+    res["per_layer_us"] = dict(
+        hipblaslt_plus_swiglu=round(sum(res[n]["hipblaslt_us"] for n in
+                                        ("qkv", "out", "gate_up", "down")) +
+                                    res["gate_up"]["swiglu_us"], 2),
+        k5_fused=round(res["qkv"]["k5_us"] + res["out"]["k5_us"] + res["down"]["k5_us"] +
+                       res["gate_up"]["fused_swiglu_us"], 2))
     return res
 
 
@@ -436,6 +505,7 @@ def main() -> int:
         del qp, op
 
         micro = None if (args.no_micro or not headline) else microbench(dev)
+        gemm_cmp = decode_gemm_compare(cfg, B, dev) if args.gemm_compare else None
         augment = augmentation_bench(model, dev, spec) if args.augment else None
 
         cpu = None
@@ -494,6 +564,7 @@ def main() -> int:
         },
         "microbench": micro,
         **({"augmentation": augment} if augment is not None else {}),
+        **({"decode_gemm": gemm_cmp} if gemm_cmp is not None else {}),
         "wall_s_timed": round(wall_s, 4),
         "host_prompt_build_s": round(host_build_s, 3),
     }
