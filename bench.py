@@ -283,12 +283,44 @@ def decode_gemm_compare(cfg, B, dev):
             t_sw = graph_time_us(lambda: K.swiglu(out, rstd, bg, bu, h, tiled=True))
             t_f = graph_time_us(lambda: K.gemm_split_swiglu(at, w_il, rstd, bg, bu, h, B, F, k))
             res[name].update(swiglu_us=round(t_sw, 2), fused_swiglu_us=round(t_f, 2))
+    # the decode step's forms: RMSNorm in the qkv / gate-up prologues (x in the fp32 tile
+    # layout), residual adds in the out / down epilogues, against the separate add+RMSNorm
+    x = torch.randn(B, d, generator=g).to(dev)
+    xt = K.tile_f32(x)
+    gam = (1 + 0.1 * torch.randn(d, generator=g)).to(dev)
+    rstd = torch.empty(B, device=dev)
+    delta = torch.randn(B, d, generator=g).to(dev)
+    xs = torch.empty(K.split_numel(B, d, True), device=dev, dtype=torch.bfloat16)
+    res["add_rmsnorm_us"] = round(graph_time_us(
+        lambda: K.add_rmsnorm(x, delta, None, gam, 1e-5, xs, rstd, tiled=True)), 2)
+    for name, N, k in (("qkv", 3 * d, d), ("out", d, d), ("gate_up", 2 * F, d), ("down", d, F)):
+        a = K.tile_matrix(torch.randn(B, 2 * k, generator=g).to(dev, torch.bfloat16))
+        wt = K.tile_matrix((0.05 * torch.randn(N, k, generator=g)).to(dev, torch.bfloat16))
+        if name == "qkv":
+            out = torch.empty(B, N, device=dev)
+            res[name]["k5_norm_us"] = round(graph_time_us(
+                lambda: K.gemm_norm(xt, gam, 1e-5, wt, out, rstd, k)), 2)
+        elif name == "gate_up":
+            h = torch.empty(K.split_numel(B, F, True), device=dev, dtype=torch.bfloat16)
+            res[name]["k5_norm_swiglu_us"] = round(graph_time_us(
+                lambda: K.gemm_norm_swiglu(xt, gam, 1e-5, wt, None, None, h, B, F, k)), 2)
+        else:
+            xr = K.tile_f32(torch.zeros(B, N, device=dev))
+            res[name]["k5_residual_us"] = round(graph_time_us(
+                lambda: K.gemm_split_residual(a, wt, xr, None, B, N, k)), 2)
     res["per_layer_us"] = dict(
         hipblaslt_plus_swiglu=round(sum(res[n]["hipblaslt_us"] for n in
                                         ("qkv", "out", "gate_up", "down")) +
                                     res["gate_up"]["swiglu_us"], 2),
         k5_fused=round(res["qkv"]["k5_us"] + res["out"]["k5_us"] + res["down"]["k5_us"] +
-                       res["gate_up"]["fused_swiglu_us"], 2))
+                       res["gate_up"]["fused_swiglu_us"], 2),
+        k5_fused_plus_2_add_rmsnorm=round(res["qkv"]["k5_us"] + res["out"]["k5_us"] +
+                                          res["down"]["k5_us"] +
+                                          res["gate_up"]["fused_swiglu_us"] +
+                                          2 * res["add_rmsnorm_us"], 2),
+        k5_norm_fused=round(res["qkv"]["k5_norm_us"] + res["out"]["k5_residual_us"] +
+                            res["gate_up"]["k5_norm_swiglu_us"] +
+                            res["down"]["k5_residual_us"], 2))
     return res
 
 

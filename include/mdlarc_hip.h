@@ -25,6 +25,10 @@
  *     (q = (c / 8) % 4) are the 16 bytes at element 8 * (16 q + r % 16).  Each block is then one
  *     v_mfma_f32_16x16x32_bf16 operand in lane order and a wave loads it as one contiguous
  *     kilobyte.  Buffers hold ceil(rows / 16) * 16 rows; rows past `rows` are never written.
+ *     For an fp32 [rows, C] matrix (the decode residual stream x) the blocks are 16 x 32 floats
+ *     (2 KB) in the same order, lane l = 16 q + r % 16 owning row r, columns 8 q .. 8 q + 7, its
+ *     columns 0..3 at float 4 l and 4..7 at float 256 + 4 l of the block (two contiguous
+ *     kilobytes per wave load).
  *   - KV cache layout is the reference StaticKVCache layout (src/inference.py:73-77):
  *     one layer's K (or V) is [batch, n_heads, cache_slots, 64] bf16, slot-major rows of 128 B.
  */
@@ -89,13 +93,14 @@ const char* mdl_error_string(int code);
  *   rstd[m]  = 1 / sqrt(mean(x[m]^2) + eps)
  *   xs[m]    = split(x[m] * gamma)       bf16 [rows, 2d] (GEMM input; rstd is applied after
  *                                        the GEMM).  xs_out may be NULL.
- * xs_layout: MDL_LAYOUT_ROWS, or MDL_LAYOUT_TILES (d a multiple of 16) for mdl_gemm_split.
+ * layout: MDL_LAYOUT_ROWS, or MDL_LAYOUT_TILES (d a multiple of 32): x in the fp32 tile layout
+ * and xs in the bf16 one, for the K5 decode entries.  xs_out and rstd_out may be NULL.
  * Tables are fp32 or bf16 (table_dtype); ids are clamped into range (callers validate first).
  */
 int mdl_embed_rmsnorm(const int64_t* ids, const int64_t* example_ids, const void* tok_table,
                       const void* ex_table, int table_dtype, int vocab, int n_examples, int rows,
                       int row_len, int d, const float* gamma, float eps, float* x_out,
-                      uint16_t* xs_out, float* rstd_out, int xs_layout, void* stream);
+                      uint16_t* xs_out, float* rstd_out, int layout, void* stream);
 
 /*
  * Decode-step entry: grid position of the token each row just emitted, then K1 on that token.
@@ -103,14 +108,14 @@ int mdl_embed_rmsnorm(const int64_t* ids, const int64_t* example_ids, const void
  *           blocks[0].ln1 of _decode_step (src/inference.py:433-437).
  * Per row b: pos_out[b] = position of token[b] from the state (gx, gy, in_out), the state
  * advances past it (the rule of mdl_grid_step), then x / xs / rstd as mdl_embed_rmsnorm with
- * row_len = 1 and xs_layout as there.  counters (int32[2], may be NULL) are incremented by one,
- * as by mdl_grid_step.
+ * row_len = 1 and layout as there (xs_out / rstd_out may be NULL).  counters (int32[2], may be
+ * NULL) are incremented by one, as by mdl_grid_step.
  */
 int mdl_decode_embed(const int64_t* token, const int64_t* example_ids, const void* tok_table,
                      const void* ex_table, int table_dtype, int vocab, int n_examples, int batch,
                      int d, const float* gamma, float eps, int32_t* gx, int32_t* gy,
                      uint8_t* in_out, int max_x, int max_y, int64_t* pos_out, int32_t* counters,
-                     float* x_out, uint16_t* xs_out, float* rstd_out, int xs_layout,
+                     float* x_out, uint16_t* xs_out, float* rstd_out, int layout,
                      void* stream);
 
 /*
@@ -210,7 +215,40 @@ int mdl_gemm_split(const uint16_t* a, int64_t lda, int a_layout, const uint16_t*
 int mdl_gemm_split_swiglu(const uint16_t* a, const uint16_t* w_gu, const float* rstd,
                           const float* bias_gate, const float* bias_up, uint16_t* h_out, int m,
                           int d_ff, int k, int tile, void* stream);
-/* Number of compiled block shapes, and the automatic choice for (m, n, k) (host only). */
+/*
+ * K5 with the RMSNorm of the projection's input fused into its prologue (decode step):
+ *   out[i, j] = sum_k split(x[i, k] * gamma[k]) * w[j, k]       (fp32, row stride ldo)
+ *   rstd_out[i] = 1 / sqrt(mean_k(x[i, k]^2) + eps)              (may be NULL)
+ * x: the fp32 residual stream [m, k] in MDL_LAYOUT_TILES (written by mdl_decode_embed /
+ * mdl_embed_rmsnorm with that layout and updated by mdl_gemm_split_residual); w tiled [n, k].
+ * split(x * gamma) and rstd are what mdl_add_rmsnorm would write (rstd to fp32 rounding: the
+ * sum of squares is taken in another order), so this replaces that launch and the split
+ * activation buffer.  k a positive multiple of 32, n of 16.
+ * Replaces: qkv_proj(ln1(x)) (src/inference.py:438-439; RMSNorm.forward
+ *           src/transformer.py:45-48).
+ */
+int mdl_gemm_norm(const float* x, const float* gamma, float eps, const uint16_t* w, float* out,
+                  int64_t ldo, float* rstd_out, int m, int n, int k, int tile, void* stream);
+/*
+ * mdl_gemm_norm feeding the SwiGLU epilogue of mdl_gemm_split_swiglu (rstd from the prologue):
+ * h = split(silu(rstd g + bias_gate) * (rstd u + bias_up)) with g / u the gate / up rows of
+ * w_gu against split(x * gamma).  Replaces ffn(ln2(x))'s gate (src/transformer.py:441-449,
+ * :494-496).
+ */
+int mdl_gemm_norm_swiglu(const float* x, const float* gamma, float eps, const uint16_t* w_gu,
+                         const float* bias_gate, const float* bias_up, uint16_t* h_out, int m,
+                         int d_ff, int k, int tile, void* stream);
+/*
+ * K5 with the residual add in its epilogue (decode step): x[i, j] += sum_k (a_hi + a_lo)[i, k]
+ * w[j, k] (+ bias[j]), in place on the fp32 residual stream x [m, n] in MDL_LAYOUT_TILES; a the
+ * tiled split activation [m, 2k], w tiled [n, k], bias [n] or NULL.  n a multiple of 32.
+ * Replaces: the residual adds x + out_proj(...) and x + fc_down(...) (+ its bias) of
+ *           _decode_step (src/inference.py:453-456; src/transformer.py:443, :494-496).
+ */
+int mdl_gemm_split_residual(const uint16_t* a, const uint16_t* w, float* x, const float* bias,
+                            int m, int n, int k, int tile, void* stream);
+/* Number of compiled block shapes, and the automatic choice for (m, n, k) of the split forms
+ * (host only; the norm forms weight the activation rows twice, see csrc/split_gemm.hip). */
 int mdl_gemm_split_tiles(void);
 int mdl_gemm_split_pick(int m, int n, int k);
 /*
@@ -325,11 +363,12 @@ int mdl_attn_decode_rope(const float* qkv, int64_t qkv_ld, const float* rstd, co
  * Row r uses x[row_index ? row_index[r] : r].  logits_out fp32 [rows, vocab] and token_out
  * int64 [rows] may each be NULL.  w_head fp32 [vocab, d], gamma fp32 [d].  vocab <= 32.
  * constraints (may be NULL) are applied to row r's logits before the argmax; logits_out then
- * holds the constrained logits.
+ * holds the constrained logits.  x_layout: MDL_LAYOUT_ROWS, or MDL_LAYOUT_TILES (the fp32 tile
+ * layout of the decode residual stream; d a multiple of 32).
  */
 int mdl_lm_head(const float* x, const int32_t* row_index, int rows, int d, const float* gamma,
                 float eps, const float* w_head, int vocab, float* logits_out, int64_t* token_out,
-                const mdl_logit_constraints* constraints, void* stream);
+                const mdl_logit_constraints* constraints, int x_layout, void* stream);
 
 /*
  * Decode-step tail: final RMSNorm + LM head + greedy argmax + token commit in one launch.
@@ -339,13 +378,15 @@ int mdl_lm_head(const float* x, const int32_t* row_index, int rows, int d, const
  * token_out[b] = argmax; out_ids[b*out_ld + c] = token_out[b] with c = (counters ? counters[1]
  * : col); finish_step[b] (may be NULL) = c - gen_base at the first END.  logits_out may be NULL.
  * constraints (may be NULL) as for mdl_lm_head, with the grid state the step's mdl_decode_embed
- * advanced (so constrained greedy decoding replays from a captured graph too).
+ * advanced (so constrained greedy decoding replays from a captured graph too).  x_layout as
+ * for mdl_lm_head.
  */
 int mdl_decode_head(const float* x, int batch, int d, const float* gamma, float eps,
                     const float* w_head, int vocab, float* logits_out, int64_t* token_out,
                     int64_t* out_ids, int64_t out_ld, int col, const int32_t* counters,
                     int32_t* finish_step, int gen_base, int end_id,
-                    const mdl_logit_constraints* constraints, void* stream);
+                    const mdl_logit_constraints* constraints, int x_layout,
+                    void* stream);
 
 /*
  * Grid-state initialisation from the prompt.

@@ -49,6 +49,9 @@ SIGNATURES: dict[str, tuple[object, list]] = {
     "mdl_gemm_split": (c_int, [P, c_int64, c_int, P, c_int64, c_int, P, c_int64, c_int, c_int,
                                c_int, c_int, P]),
     "mdl_gemm_split_swiglu": (c_int, [P, P, P, P, P, P, c_int, c_int, c_int, c_int, P]),
+    "mdl_gemm_norm": (c_int, [P, P, c_float, P, P, c_int64, P, c_int, c_int, c_int, c_int, P]),
+    "mdl_gemm_norm_swiglu": (c_int, [P, P, c_float, P, P, P, P, c_int, c_int, c_int, c_int, P]),
+    "mdl_gemm_split_residual": (c_int, [P, P, P, P, c_int, c_int, c_int, c_int, P]),
     "mdl_gemm_split_tiles": (c_int, []),
     "mdl_gemm_split_pick": (c_int, [c_int, c_int, c_int]),
     "mdl_tile_matrix": (c_int, [P, c_int64, c_int, c_int, P, P]),
@@ -64,9 +67,9 @@ SIGNATURES: dict[str, tuple[object, list]] = {
     "mdl_attn_decode_rope": (c_int, [P, c_int64, P, P, P, c_int, c_int, c_int, c_int, c_int,
                                      c_int, c_float, P, P, c_int, c_int, c_int, c_int, P, c_int,
                                      P, P, P, c_int, P, P, c_int64, c_int, P, c_int, P]),
-    "mdl_lm_head": (c_int, [P, P, c_int, c_int, P, c_float, P, c_int, P, P, CONS, P]),
+    "mdl_lm_head": (c_int, [P, P, c_int, c_int, P, c_float, P, c_int, P, P, CONS, c_int, P]),
     "mdl_decode_head": (c_int, [P, c_int, c_int, P, c_float, P, c_int, P, P, P, c_int64, c_int,
-                                P, P, c_int, c_int, CONS, P]),
+                                P, P, c_int, c_int, CONS, c_int, P]),
     "mdl_grid_init": (c_int, [P, P, P, P, c_int, c_int, c_int, c_int, P, P, P, P, P, P, P]),
     "mdl_build_prompts": (c_int, [P, c_int64, P, c_int, P, c_int, P, c_int, P, c_int, P, P, P,
                                   P]),

@@ -160,6 +160,16 @@ __device__ __forceinline__ int64_t tile_off(int64_t m, int j, int cols) {
          (j & 7);
 }
 
+// Element offset of (row m, column j) of a [rows, cols] fp32 matrix in the fp32 tile layout
+// (MDL_LAYOUT_TILES for fp32; cols a multiple of 32): 16 x 32 blocks of 512 floats in the order
+// of the bf16 layout; inside a block, row m % 16, columns 8 q .. 8 q + 7 (q = (j / 8) % 4) belong
+// to lane l = 16 q + m % 16, whose elements 0..3 sit at 4 l and 4..7 at 256 + 4 l, so a wave
+// reads a block as two contiguous kilobytes.  Columns j .. j + 3 with j % 4 == 0 are contiguous.
+__device__ __forceinline__ int64_t tile_off32(int64_t m, int j, int cols) {
+  return 512 * ((m >> 4) * (cols >> 5) + (j >> 5)) + 256 * ((j >> 2) & 1) +
+         4 * (16 * ((j >> 3) & 3) + (m & 15)) + (j & 3);
+}
+
 // ---- host-side launch checking ---------------------------------------------------------------
 inline int launch_status() {
   hipError_t e = hipGetLastError();

@@ -59,7 +59,7 @@ __global__ __launch_bounds__(256) void head_kernel(
     const float* __restrict__ gamma, float eps, const float* __restrict__ w, int vocab,
     float* __restrict__ logits, int64_t* __restrict__ token, int64_t* __restrict__ out_ids,
     int64_t ld, int col, const int32_t* __restrict__ counters, int32_t* __restrict__ finish,
-    int gen_base, int64_t end_id, HeadCons cons) {
+    int gen_base, int64_t end_id, HeadCons cons, int x_tiled) {
   constexpr int KW = NV / 4;                       // vocab slots per wave
   constexpr int LOG_KW = KW == 4 ? 2 : 3;
   __shared__ float lg[NV];
@@ -67,14 +67,15 @@ __global__ __launch_bounds__(256) void head_kernel(
   const int r = blockIdx.x;
   if (r >= rows) return;
   const int64_t m = row_index ? row_index[r] : r;
-  const float* xr = x + m * d;
+  const float* xr = x + m * d;   // row-major; x_tiled: the fp32 tile layout (tile_off32)
   float v[NC][4];
   float ss = 0.f;
 #pragma unroll
   for (int i = 0; i < NC; ++i) {
     const int e = 4 * (lane + 64 * i);
     if (i < NC - 1 || e < d) {
-      const float4 a = *reinterpret_cast<const float4*>(xr + e);
+      const float4 a = *reinterpret_cast<const float4*>(x_tiled ? x + tile_off32(m, e, d)
+                                                                 : xr + e);
       const float4 gm = *reinterpret_cast<const float4*>(gamma + e);
       ss += a.x * a.x + a.y * a.y + a.z * a.z + a.w * a.w;
       v[i][0] = a.x * gm.x; v[i][1] = a.y * gm.y; v[i][2] = a.z * gm.z; v[i][3] = a.w * gm.w;
@@ -244,22 +245,28 @@ struct LaunchHead {
                   int rows, int d, const float* gamma, float eps, const float* w, int vocab,
                   float* logits, int64_t* token, int64_t* out_ids, int64_t ld, int col,
                   const int32_t* counters, int32_t* finish, int gen_base, int64_t end_id,
-                  const HeadCons& cons) {
+                  const HeadCons& cons, int x_tiled) {
     if (nv == 16)
       head_kernel<NC, 16><<<grid, 256, 0, s>>>(x, row_index, rows, d, gamma, eps, w, vocab,
                                                logits, token, out_ids, ld, col, counters, finish,
-                                               gen_base, end_id, cons);
+                                               gen_base, end_id, cons, x_tiled);
     else
       head_kernel<NC, 32><<<grid, 256, 0, s>>>(x, row_index, rows, d, gamma, eps, w, vocab,
                                                logits, token, out_ids, ld, col, counters, finish,
-                                               gen_base, end_id, cons);
+                                               gen_base, end_id, cons, x_tiled);
   }
 };
+
+// x in `layout`: the fp32 tile layout needs whole 32-column blocks
+inline bool x_layout_ok(int layout, int d) {
+  return layout == MDL_LAYOUT_ROWS || (layout == MDL_LAYOUT_TILES && d % 32 == 0);
+}
 
 int launch_head(const float* x, const int32_t* row_index, int rows, int d, const float* gamma,
                 float eps, const float* w, int vocab, float* logits, int64_t* token,
                 int64_t* out_ids, int64_t ld, int col, const int32_t* counters, int32_t* finish,
-                int gen_base, int64_t end_id, const mdl_logit_constraints* c, hipStream_t s) {
+                int gen_base, int64_t end_id, const mdl_logit_constraints* c, int x_tiled,
+                hipStream_t s) {
   HeadCons cons{0u, nullptr, 0.f, nullptr, nullptr, nullptr, 0.f};
   if (c) {
     if (c->target_shape && (!c->grid_x || !c->grid_y)) return MDL_ERR_NULL;
@@ -271,7 +278,7 @@ int launch_head(const float* x, const int32_t* row_index, int rows, int d, const
 #define MDL_HEAD(N)                                                                            \
   case N:                                                                                      \
     LaunchHead<N>::run(nv, grid, s, x, row_index, rows, d, gamma, eps, w, vocab, logits, token, \
-                       out_ids, ld, col, counters, finish, gen_base, end_id, cons);            \
+                       out_ids, ld, col, counters, finish, gen_base, end_id, cons, x_tiled);   \
     break;
   switch ((d + 255) / 256) { MDL_HEAD(1) MDL_HEAD(2) MDL_HEAD(3) MDL_HEAD(4) MDL_HEAD(5)
                              MDL_HEAD(6) MDL_HEAD(7) MDL_HEAD(8) }
@@ -302,14 +309,16 @@ extern "C" const char* mdl_error_string(int code) {
 extern "C" int mdl_lm_head(const float* x, const int32_t* row_index, int rows, int d,
                            const float* gamma, float eps, const float* w_head, int vocab,
                            float* logits_out, int64_t* token_out,
-                           const mdl_logit_constraints* constraints, void* stream) {
+                           const mdl_logit_constraints* constraints, int x_layout,
+                           void* stream) {
   if (!x || !gamma || !w_head) return MDL_ERR_NULL;
-  if (rows < 0 || d <= 0 || d % 4 != 0 || d > 2048 || vocab <= 0 || vocab > kVmax)
+  if (rows < 0 || d <= 0 || d % 4 != 0 || d > 2048 || vocab <= 0 || vocab > kVmax ||
+      !x_layout_ok(x_layout, d))
     return MDL_ERR_SHAPE;
   if (!aligned16(x) || !aligned16(gamma) || !aligned16(w_head)) return MDL_ERR_ALIGN;
   if (rows == 0) return MDL_OK;
   return launch_head(x, row_index, rows, d, gamma, eps, w_head, vocab, logits_out, token_out,
-                     nullptr, 0, 0, nullptr, nullptr, 0, 0, constraints,
+                     nullptr, 0, 0, nullptr, nullptr, 0, 0, constraints, x_layout,
                      static_cast<hipStream_t>(stream));
 }
 
@@ -318,16 +327,16 @@ extern "C" int mdl_decode_head(const float* x, int batch, int d, const float* ga
                                int64_t* token_out, int64_t* out_ids, int64_t out_ld, int col,
                                const int32_t* counters, int32_t* finish_step, int gen_base,
                                int end_id, const mdl_logit_constraints* constraints,
-                               void* stream) {
+                               int x_layout, void* stream) {
   if (!x || !gamma || !w_head || !token_out || !out_ids) return MDL_ERR_NULL;
   if (batch < 0 || d <= 0 || d % 4 != 0 || d > 2048 || vocab <= 0 || vocab > kVmax ||
-      out_ld <= 0 || (!counters && (col < 0 || col >= out_ld)))
+      out_ld <= 0 || (!counters && (col < 0 || col >= out_ld)) || !x_layout_ok(x_layout, d))
     return MDL_ERR_SHAPE;
   if (!aligned16(x) || !aligned16(gamma) || !aligned16(w_head)) return MDL_ERR_ALIGN;
   if (batch == 0) return MDL_OK;
   return launch_head(x, nullptr, batch, d, gamma, eps, w_head, vocab, logits_out, token_out,
                      out_ids, out_ld, col, counters, finish_step, gen_base, end_id, constraints,
-                     static_cast<hipStream_t>(stream));
+                     x_layout, static_cast<hipStream_t>(stream));
 }
 
 extern "C" int mdl_grid_init(const int64_t* ids, const int64_t* pos, const uint8_t* mask,

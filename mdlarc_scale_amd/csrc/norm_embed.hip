@@ -55,11 +55,13 @@ __device__ __forceinline__ void load_gamma(const float* gamma, int lane, int d, 
   }
 }
 
-// rstd of the row held in v, then x (fp32) and split(x * gamma) stores (non-temporal if NT)
-// into row m of xs (row-major [rows, 2d], or MFMA tiles when `tiled`).
+// rstd of the row held in v (stored when rstd_out is not NULL), then x (fp32) and
+// split(x * gamma) stores (non-temporal if NT) into row m of x ([rows, d]: row-major, or the
+// fp32 tile layout when `x_tiled`) and xs ([rows, 2d]: row-major, or MFMA tiles when
+// `tiled`).
 template <int NC, bool TAIL, bool HAS_XS, bool NT>
 __device__ __forceinline__ void finish_row(int lane, int d, float eps, const float (*v)[4],
-                                           const float (*g)[4], float ss, float* xo,
+                                           const float (*g)[4], float ss, float* x, int x_tiled,
                                            uint16_t* xs, int64_t m, int tiled,
                                            float* rstd_out) {
   ss = wave_sum(ss);
@@ -68,7 +70,8 @@ __device__ __forceinline__ void finish_row(int lane, int d, float eps, const flo
   for (int i = 0; i < NC; ++i) {
     const int e = 4 * (lane + 64 * i);
     if (in_row<NC, TAIL>(i, e, d)) {
-      st_f4<NT>(xo + e, make_float4(v[i][0], v[i][1], v[i][2], v[i][3]));
+      st_f4<NT>(x + (x_tiled ? tile_off32(m, e, d) : m * d + e),
+                make_float4(v[i][0], v[i][1], v[i][2], v[i][3]));
       if (HAS_XS) {
         const float t[4] = {v[i][0] * g[i][0], v[i][1] * g[i][1], v[i][2] * g[i][2],
                             v[i][3] * g[i][3]};
@@ -84,7 +87,7 @@ __device__ __forceinline__ void finish_row(int lane, int d, float eps, const flo
       }
     }
   }
-  if (lane == 0) *rstd_out = r;
+  if (lane == 0 && rstd_out) *rstd_out = r;
 }
 
 // x = tok[t] (+ ex[e]) for one row into v; returns the row's partial sum of squares.
@@ -119,7 +122,7 @@ __global__ __launch_bounds__(256) void embed_rmsnorm_kernel(
     const int64_t* __restrict__ ids, const int64_t* __restrict__ ex_ids,
     const TT* __restrict__ tok, const TT* __restrict__ ex, int vocab, int n_ex, int rows,
     int row_len, int d, const float* __restrict__ gamma, float eps, float* __restrict__ x_out,
-    uint16_t* __restrict__ xs_out, float* __restrict__ rstd_out, int xs_tiled) {
+    uint16_t* __restrict__ xs_out, float* __restrict__ rstd_out, int tiled) {
   const int lane = threadIdx.x & 63;
   const int64_t m = static_cast<int64_t>(blockIdx.x) * 4 + (threadIdx.x >> 6);
   if (m >= rows) return;
@@ -128,20 +131,20 @@ __global__ __launch_bounds__(256) void embed_rmsnorm_kernel(
   const TT* trow = tok + clamp_id(ids[m], vocab) * d;
   const TT* erow = HAS_EX ? ex + clamp_id(ex_ids[m / row_len], n_ex) * d : nullptr;
   const float ss = gather_row<NC, TAIL, TT, HAS_EX>(trow, erow, lane, d, v);
-  finish_row<NC, TAIL, HAS_XS, false>(lane, d, eps, v, g, ss, x_out + m * d, xs_out, m, xs_tiled,
-                                      rstd_out + m);
+  finish_row<NC, TAIL, HAS_XS, false>(lane, d, eps, v, g, ss, x_out, tiled, xs_out, m, tiled,
+                                      rstd_out ? rstd_out + m : nullptr);
 }
 
 // Decode step entry: lane 0 of each row's wave turns the token the row just emitted into its 3D
 // position (grid.h) and advances the row's grid state, then the wave embeds the token as K1.
-template <int NC, bool TAIL, typename TT, bool HAS_EX>
+template <int NC, bool TAIL, typename TT, bool HAS_EX, bool HAS_XS>
 __global__ __launch_bounds__(256) void decode_embed_kernel(
     const int64_t* __restrict__ token, const int64_t* __restrict__ ex_ids,
     const TT* __restrict__ tok, const TT* __restrict__ ex, int vocab, int n_ex, int batch, int d,
     const float* __restrict__ gamma, float eps, int32_t* __restrict__ gx,
     int32_t* __restrict__ gy, uint8_t* __restrict__ gio, int max_x, int max_y,
     int64_t* __restrict__ pos_out, int32_t* __restrict__ counters, float* __restrict__ x_out,
-    uint16_t* __restrict__ xs_out, float* __restrict__ rstd_out, int xs_tiled) {
+    uint16_t* __restrict__ xs_out, float* __restrict__ rstd_out, int tiled) {
   const int lane = threadIdx.x & 63;
   if (counters && blockIdx.x == 0 && threadIdx.x == 0) {
     counters[0] = counters[0] + 1;
@@ -150,7 +153,7 @@ __global__ __launch_bounds__(256) void decode_embed_kernel(
   const int64_t m = static_cast<int64_t>(blockIdx.x) * 4 + (threadIdx.x >> 6);
   if (m >= batch) return;
   float g[NC][4], v[NC][4];
-  load_gamma<NC, TAIL>(gamma, lane, d, g);
+  if (HAS_XS) load_gamma<NC, TAIL>(gamma, lane, d, g);
   const int64_t t = token[m];
   if (lane == 0) {
     int32_t x = gx[m], y = gy[m];
@@ -163,8 +166,8 @@ __global__ __launch_bounds__(256) void decode_embed_kernel(
   const TT* trow = tok + clamp_id(t, vocab) * d;
   const TT* erow = HAS_EX ? ex + clamp_id(ex_ids[m], n_ex) * d : nullptr;
   const float ss = gather_row<NC, TAIL, TT, HAS_EX>(trow, erow, lane, d, v);
-  finish_row<NC, TAIL, true, false>(lane, d, eps, v, g, ss, x_out + m * d, xs_out, m, xs_tiled,
-                                    rstd_out + m);
+  finish_row<NC, TAIL, HAS_XS, false>(lane, d, eps, v, g, ss, x_out, tiled, xs_out, m, tiled,
+                                      rstd_out ? rstd_out + m : nullptr);
 }
 
 template <int NC, bool TAIL, bool HAS_DELTA, bool HAS_BIAS, bool HAS_XS, bool NT>
@@ -200,7 +203,7 @@ __global__ __launch_bounds__(256) void add_rmsnorm_kernel(
       for (int j = 0; j < 4; ++j) ss += v[i][j] * v[i][j];
     }
   }
-  finish_row<NC, TAIL, HAS_XS, NT>(lane, d, eps, v, g, ss, xr, xs_out, m, xs_tiled,
+  finish_row<NC, TAIL, HAS_XS, NT>(lane, d, eps, v, g, ss, x, 0, xs_out, m, xs_tiled,
                                    rstd_out + m);
 }
 
@@ -249,14 +252,15 @@ struct LaunchDecodeEmbed {
                   int batch, int d, const float* gamma, float eps, int32_t* gx, int32_t* gy,
                   uint8_t* gio, int max_x, int max_y, int64_t* pos, int32_t* counters, float* x,
                   uint16_t* xs, float* r, int tiled) {
-    if (has_ex)
-      decode_embed_kernel<NC, TAIL, TT, true><<<grid, 256, 0, s>>>(
-          token, ex_ids, tok, ex, vocab, n_ex, batch, d, gamma, eps, gx, gy, gio, max_x, max_y,
-          pos, counters, x, xs, r, tiled);
-    else
-      decode_embed_kernel<NC, TAIL, TT, false><<<grid, 256, 0, s>>>(
-          token, ex_ids, tok, ex, vocab, n_ex, batch, d, gamma, eps, gx, gy, gio, max_x, max_y,
-          pos, counters, x, xs, r, tiled);
+#define MDL_DEC(E, X)                                                                        \
+  decode_embed_kernel<NC, TAIL, TT, E, X><<<grid, 256, 0, s>>>(                              \
+      token, ex_ids, tok, ex, vocab, n_ex, batch, d, gamma, eps, gx, gy, gio, max_x, max_y,  \
+      pos, counters, x, xs, r, tiled)
+    if (has_ex && xs) MDL_DEC(true, true);
+    else if (has_ex) MDL_DEC(true, false);
+    else if (xs) MDL_DEC(false, true);
+    else MDL_DEC(false, false);
+#undef MDL_DEC
   }
 };
 
@@ -291,9 +295,11 @@ struct LaunchAdd {
   }
 };
 
-// a split output of 2d columns in `layout` (MDL_LAYOUT_TILES needs 2d % 32 == 0)
-inline bool layout_ok(int layout, int d) {
-  return layout == MDL_LAYOUT_ROWS || (layout == MDL_LAYOUT_TILES && d % 16 == 0);
+// a split output of 2d columns in `layout` (MDL_LAYOUT_TILES needs 2d % 32 == 0), and with
+// `with_x` the fp32 x of d columns as well (d % 32 == 0)
+inline bool layout_ok(int layout, int d, bool with_x = false) {
+  return layout == MDL_LAYOUT_ROWS ||
+         (layout == MDL_LAYOUT_TILES && d % (with_x ? 32 : 16) == 0);
 }
 
 // host-side checks shared by the two embedding entry points
@@ -319,12 +325,12 @@ extern "C" int mdl_embed_rmsnorm(const int64_t* ids, const int64_t* example_ids,
                                  const void* tok_table, const void* ex_table, int table_dtype,
                                  int vocab, int n_examples, int rows, int row_len, int d,
                                  const float* gamma, float eps, float* x_out, uint16_t* xs_out,
-                                 float* rstd_out, int xs_layout, void* stream) {
-  if (!ids || !gamma || !x_out || !rstd_out) return MDL_ERR_NULL;
+                                 float* rstd_out, int layout, void* stream) {
+  if (!ids || !gamma || !x_out) return MDL_ERR_NULL;
   const bool use_ex = example_ids != nullptr;
   const int tc = check_tables(tok_table, ex_table, use_ex, table_dtype, vocab, n_examples, d);
   if (tc != MDL_OK) return tc;
-  if (rows < 0 || row_len <= 0 || !layout_ok(xs_layout, d)) return MDL_ERR_SHAPE;
+  if (rows < 0 || row_len <= 0 || !layout_ok(layout, d, true)) return MDL_ERR_SHAPE;
   if (!aligned16(x_out) || !aligned16(gamma) || (xs_out && !aligned8(xs_out)))
     return MDL_ERR_ALIGN;
   if (rows == 0) return MDL_OK;
@@ -334,12 +340,12 @@ extern "C" int mdl_embed_rmsnorm(const int64_t* ids, const int64_t* example_ids,
     dispatch_nc<LaunchEmbed>(d, grid, s, use_ex, xs_out != nullptr, ids, example_ids,
                              static_cast<const float*>(tok_table),
                              static_cast<const float*>(ex_table), vocab, n_examples, rows,
-                             row_len, d, gamma, eps, x_out, xs_out, rstd_out, xs_layout);
+                             row_len, d, gamma, eps, x_out, xs_out, rstd_out, layout);
   else
     dispatch_nc<LaunchEmbed>(d, grid, s, use_ex, xs_out != nullptr, ids, example_ids,
                              static_cast<const uint16_t*>(tok_table),
                              static_cast<const uint16_t*>(ex_table), vocab, n_examples, rows,
-                             row_len, d, gamma, eps, x_out, xs_out, rstd_out, xs_layout);
+                             row_len, d, gamma, eps, x_out, xs_out, rstd_out, layout);
   return launch_status();
 }
 
@@ -348,15 +354,15 @@ extern "C" int mdl_decode_embed(const int64_t* token, const int64_t* example_ids
                                 int vocab, int n_examples, int batch, int d, const float* gamma,
                                 float eps, int32_t* gx, int32_t* gy, uint8_t* in_out, int max_x,
                                 int max_y, int64_t* pos_out, int32_t* counters, float* x_out,
-                                uint16_t* xs_out, float* rstd_out, int xs_layout,
+                                uint16_t* xs_out, float* rstd_out, int layout,
                                 void* stream) {
-  if (!token || !gamma || !gx || !gy || !in_out || !pos_out || !x_out || !xs_out || !rstd_out)
-    return MDL_ERR_NULL;
+  if (!token || !gamma || !gx || !gy || !in_out || !pos_out || !x_out) return MDL_ERR_NULL;
   const bool use_ex = example_ids != nullptr;
   const int tc = check_tables(tok_table, ex_table, use_ex, table_dtype, vocab, n_examples, d);
   if (tc != MDL_OK) return tc;
-  if (batch < 0 || max_x < 0 || max_y < 0 || !layout_ok(xs_layout, d)) return MDL_ERR_SHAPE;
-  if (!aligned16(x_out) || !aligned16(gamma) || !aligned8(xs_out)) return MDL_ERR_ALIGN;
+  if (batch < 0 || max_x < 0 || max_y < 0 || !layout_ok(layout, d, true)) return MDL_ERR_SHAPE;
+  if (!aligned16(x_out) || !aligned16(gamma) || (xs_out && !aligned8(xs_out)))
+    return MDL_ERR_ALIGN;
   if (batch == 0) return MDL_OK;
   const dim3 grid((batch + 3) / 4);
   hipStream_t s = static_cast<hipStream_t>(stream);
@@ -365,13 +371,13 @@ extern "C" int mdl_decode_embed(const int64_t* token, const int64_t* example_ids
                                    static_cast<const float*>(tok_table),
                                    static_cast<const float*>(ex_table), vocab, n_examples, batch,
                                    d, gamma, eps, gx, gy, in_out, max_x, max_y, pos_out, counters,
-                                   x_out, xs_out, rstd_out, xs_layout);
+                                   x_out, xs_out, rstd_out, layout);
   else
     dispatch_nc<LaunchDecodeEmbed>(d, grid, s, use_ex, token, example_ids,
                                    static_cast<const uint16_t*>(tok_table),
                                    static_cast<const uint16_t*>(ex_table), vocab, n_examples,
                                    batch, d, gamma, eps, gx, gy, in_out, max_x, max_y, pos_out,
-                                   counters, x_out, xs_out, rstd_out, xs_layout);
+                                   counters, x_out, xs_out, rstd_out, layout);
   return launch_status();
 }
 

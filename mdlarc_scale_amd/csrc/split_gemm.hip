@@ -1,11 +1,21 @@
 // K5: split-activation GEMM for decode-sized row counts on bf16 MFMA (gfx950).
 //
-//   out[m, n] (fp32) = sum_k (a[m, k] + a[m, K + k]) * w[n, k],   k < K
+//   acc[m, n] (fp32) = sum_k (a_hi[m, k] + a_lo[m, k]) * w[n, k],   k < K
 //
-// a is a split activation (hi in columns [0, K), lo in [K, 2K)), w a bf16 weight in nn.Linear
-// orientation ([N, K]); either may be row-major or in the MFMA tile layout of mdl_tile_matrix
-// (MDL_LAYOUT_TILES).  A row-major w may be the left half of the [W | W] operand the prefill
-// GEMMs take (ldw = 2K).
+// w is a bf16 weight in nn.Linear orientation ([N, K]); a is the split activation (hi = bf16(v),
+// lo = bf16(v - hi)) of v[m, k], taken from one of three sources (AMODE):
+//   A_ROWS   a split [M, 2K] row-major (hi in columns [0, K), lo in [K, 2K));
+//   A_TILES  the same matrix in the MFMA tile layout (MDL_LAYOUT_TILES);
+//   A_NORM   v = x * gamma from the fp32 residual stream x [M, K] in the fp32 tile layout: the
+//            RMSNorm of the next projection done in the GEMM's prologue.  A block sees whole
+//            rows (its waves cover all of K), so it also sums x^2 and has rstd of its rows.
+// and acc goes to one of three epilogues (EPI):
+//   E_STORE     out[m, n] = acc (fp32, row-major); with A_NORM the n-tile-0 blocks also store
+//               rstd[m] (the decode attention applies it to q / k / v);
+//   E_SWIGLU    h = split(silu(rstd g + b_g) * (rstd u + b_u)) from the gate / up pair of
+//               fragments (weights with 16-row gate / up blocks interleaved), tiled;
+//   E_RESIDUAL  x[m, n] += acc (+ bias[n]) in place on the fp32 tile-layout residual stream
+//               (each element has one owner block, so the update needs no synchronisation).
 //
 // Why not the library GEMM at decode: at M <= 256 rows hipBLASLt runs 64x64 or 32x32 tiles over
 // the doubled K of [W | W] (each weight byte read twice) on at most 144 workgroups for the small
@@ -15,16 +25,17 @@
 //     of 32 and issues the loads of 4 of them before its first MFMA;
 //   - the row tiles sharing one weight tile run on one XCD (block i runs on XCD i mod 8), so the
 //     weight tile comes from HBM once and from that XCD's L2 after that;
-//   - with both operands tiled, each wave load is one contiguous kilobyte.  A row-major operand
+//   - with tiled operands each wave load is one contiguous kilobyte.  A row-major operand
 //     fragment spans 16 rows of 64 bytes and four consecutive lanes touch four cache lines; at
 //     these sizes that costs 1.5x (weight) and 2x (both) in time (measured at the model shapes).
 //
 // MFMA formulation: D^T = W . A^T with v_mfma_f32_16x16x32_bf16 (layouts in mfma.h).  The A
 // operand is 16 weight rows, the B operand 16 activation rows; lane (c, g) holds row c at
-// k = 32 s + 8 g .. + 7 (the tile layout stores exactly these 16 bytes at lane order).  The
-// accumulator of lane (c, g) holds out[m0 + c][n0 + 4 g .. + 3]: one float4 per lane.
+// k = 32 s + 8 g .. + 7 (the tile layouts store exactly these elements at lane order).  The
+// accumulator of lane (c, g) holds acc[m0 + c][n0 + 4 g .. + 3]: one float4 per lane.
 // Summation order is fixed (each wave's k-steps in order, hi before lo, waves summed 0..7 in the
-// reduction), so a given tile shape is bit-reproducible; layouts do not change the result.
+// reduction), so a given tile shape is bit-reproducible; the A source and the layouts do not
+// change the result.
 #include "common.h"
 #include "mfma.h"
 
@@ -33,9 +44,32 @@ namespace mdl {
 namespace {
 
 constexpr int kGemmWaves = 8;
-constexpr int kU = 4;   // k-steps whose loads are in flight together
+constexpr int kU = 4;   // k-steps whose loads are in flight together (A_NORM, large tiles: 2)
 
-// Pointer to lane (c, g)'s 16 bytes of row block `rb` (rows 16 rb + c) at k-step 0 of an
+enum AMode { A_ROWS = 0, A_TILES = 1, A_NORM = 2 };
+enum Epi { E_STORE = 0, E_SWIGLU = 1, E_RESIDUAL = 2 };
+
+struct GemmArgs {
+  const uint16_t* a;       // A_ROWS / A_TILES: split activation
+  int64_t lda;             // A_ROWS row stride (elements)
+  const float* x;          // A_NORM: fp32 residual stream, tile layout, [M, K]
+  const float* gamma;      // A_NORM: RMSNorm gain [K]
+  float eps;
+  const uint16_t* w;
+  int64_t ldw;             // row-major w row stride (elements)
+  float* out;              // E_STORE: [M, N] fp32, row stride ldo
+  int64_t ldo;
+  float* rstd_out;         // E_STORE with A_NORM: [M] (may be NULL)
+  const float* rstd_in;    // E_SWIGLU with a split A: [M] or NULL (1)
+  const float* bias_a;     // E_SWIGLU: gate bias [F]; E_RESIDUAL: bias [N] (may be NULL)
+  const float* bias_b;     // E_SWIGLU: up bias [F] (may be NULL)
+  uint16_t* h;             // E_SWIGLU: split [M, 2F], tile layout
+  float* x_res;            // E_RESIDUAL: fp32 residual stream [M, N], tile layout
+  int d_ff;
+  int M, N, K, n_tiles, m_tiles, per_xcd;
+};
+
+// Pointer to lane (c, g)'s 16 bytes of row block `rb` (rows 16 rb + c) at k-step 0 of a bf16
 // operand with `cols` columns: row-major (row stride ld, rows clamped to n_rows - 1) or tiled
 // (row blocks clamped to the last one; its padding rows exist in a tiled buffer).
 template <bool TILED>
@@ -49,74 +83,109 @@ __device__ __forceinline__ const uint16_t* frag_base(const uint16_t* p, int64_t 
            8 * (lane >> 4);
   }
 }
-// element step from k-step 0 to k-step s (k = 32 s)
+// element step from k-step 0 to k-step s (k = 32 s) of a bf16 operand
 template <bool TILED>
 __device__ __forceinline__ int64_t frag_step(int s) {
   return TILED ? static_cast<int64_t>(512) * s : static_cast<int64_t>(32) * s;
 }
 
-// SwiGLU epilogue (the gate / up projection with the MLP gate fused): w holds [W_gate; W_up]
-// with their 16-row blocks interleaved (block 2 b = gate rows 16 b .., block 2 b + 1 = up rows
-// 16 b ..), so output fragments 2 p and 2 p + 1 of a block are the gate and the up value of the
-// same 16 channels.
-struct SwigluEpi {
-  const float* rstd;       // [M] or NULL (1)
-  const float* bias_gate;  // [F] or NULL (0)
-  const float* bias_up;    // [F] or NULL (0)
-  uint16_t* h;             // split bf16 [M, 2F] in the tile layout
-  int d_ff;
-};
-
-template <int TN, int TM, bool WT, bool AT, bool SWIGLU = false>
-__global__ __launch_bounds__(64 * kGemmWaves) void split_gemm_kernel(
-    const uint16_t* __restrict__ a, int64_t lda, const uint16_t* __restrict__ w, int64_t ldw,
-    float* __restrict__ out, int64_t ldo, int M, int N, int K, int n_tiles, int m_tiles,
-    int per_xcd, SwigluEpi epi = {}) {
+template <int TN, int TM, bool WT, int AMODE, int EPI>
+__global__ __launch_bounds__(64 * kGemmWaves) void split_gemm_kernel(const GemmArgs p) {
   constexpr int FN = TN / 16, FM = TM / 16, NW = kGemmWaves;
+  // k-steps in flight: the fp32 x and gamma fragments of A_NORM take twice the registers of a
+  // split operand, and 4 steps of the two largest tiles would spill
+  constexpr int U = (AMODE == A_NORM && FN * FM >= 16) ? 3 : kU;
   static_assert(TN % 16 == 0 && TM % 16 == 0, "tile must be a multiple of 16");
+  const int M = p.M, N = p.N, K = p.K;
   // logical tile of this block: tiles per_xcd * x .. per_xcd * (x + 1) - 1 run on XCD x
-  const int L = (blockIdx.x & 7) * per_xcd + (blockIdx.x >> 3);
-  if (L >= n_tiles * m_tiles) return;   // whole block, before any barrier
-  const int nt = L / m_tiles, mt = L - nt * m_tiles;
+  const int L = (blockIdx.x & 7) * p.per_xcd + (blockIdx.x >> 3);
+  if (L >= p.n_tiles * p.m_tiles) return;   // whole block, before any barrier
+  const int nt = L / p.m_tiles, mt = L - nt * p.m_tiles;
   const int n0 = nt * TN, m0 = mt * TM;
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int g = lane >> 4;
 
   // rows past M / N load a valid row (in bounds; their results are never stored)
   const uint16_t* wp[FN];
+#pragma unroll
+  for (int i = 0; i < FN; ++i) wp[i] = frag_base<WT>(p.w, p.ldw, n0 / 16 + i, N, K, lane);
   const uint16_t* ap[FM];
+  const float* xp[FM];
+  int64_t lo_off = 0;
+  if constexpr (AMODE == A_NORM) {
+    // fp32 tile layout: 16 x 32 blocks of 512 floats, lane l's elements 0..3 at 4 l and 4..7 at
+    // 256 + 4 l; padding rows of the last row block exist
+    const int last = (M + 15) / 16 - 1;
 #pragma unroll
-  for (int i = 0; i < FN; ++i) wp[i] = frag_base<WT>(w, ldw, n0 / 16 + i, N, K, lane);
+    for (int j = 0; j < FM; ++j)
+      xp[j] = p.x + static_cast<int64_t>(min(m0 / 16 + j, last)) * (K / 32) * 512 + 4 * lane;
+  } else {
 #pragma unroll
-  for (int j = 0; j < FM; ++j) ap[j] = frag_base<AT>(a, lda, m0 / 16 + j, M, 2 * K, lane);
-  const int64_t lo_off = frag_step<AT>(K / 32);   // hi k-step s -> lo k-step s + K / 32
+    for (int j = 0; j < FM; ++j)
+      ap[j] = frag_base<AMODE == A_TILES>(p.a, p.lda, m0 / 16 + j, M, 2 * K, lane);
+    lo_off = frag_step<AMODE == A_TILES>(K / 32);   // hi k-step s -> lo k-step s + K / 32
+  }
 
   f32x4_t acc[FN][FM];
 #pragma unroll
   for (int i = 0; i < FN; ++i)
 #pragma unroll
     for (int j = 0; j < FM; ++j) acc[i][j] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+  float ss[FM];   // A_NORM: this lane's part of sum(x^2) of row m0 + 16 j + c
+#pragma unroll
+  for (int j = 0; j < FM; ++j) ss[j] = 0.f;
 
   // k-steps of 32: wave w takes [nk w / NW, nk (w + 1) / NW), contiguous
   const int nk = K >> 5;
   const int s0 = (nk * wave) / NW, s1 = (nk * (wave + 1)) / NW;
-  for (int s = s0; s < s1; s += kU) {
-    uint4 wf[kU][FN], ah[kU][FM], al[kU][FM];
+  for (int s = s0; s < s1; s += U) {
+    uint4 wf[U][FN], ah[U][FM], al[U][FM];
+    float4 xv[U][FM][2], gv[U][2];
 #pragma unroll
-    for (int u = 0; u < kU; ++u) {
+    for (int u = 0; u < U; ++u) {
       // steps past s1 reload step s1 - 1 (same lines, in bounds) and are not multiplied
       const int su = min(s + u, s1 - 1);
 #pragma unroll
       for (int i = 0; i < FN; ++i)
         wf[u][i] = *reinterpret_cast<const uint4*>(wp[i] + frag_step<WT>(su));
+      if constexpr (AMODE == A_NORM) {
+        gv[u][0] = *reinterpret_cast<const float4*>(p.gamma + 32 * su + 8 * g);
+        gv[u][1] = *reinterpret_cast<const float4*>(p.gamma + 32 * su + 8 * g + 4);
 #pragma unroll
-      for (int j = 0; j < FM; ++j) {
-        ah[u][j] = *reinterpret_cast<const uint4*>(ap[j] + frag_step<AT>(su));
-        al[u][j] = *reinterpret_cast<const uint4*>(ap[j] + frag_step<AT>(su) + lo_off);
+        for (int j = 0; j < FM; ++j) {
+          xv[u][j][0] = *reinterpret_cast<const float4*>(xp[j] + 512 * static_cast<int64_t>(su));
+          xv[u][j][1] =
+              *reinterpret_cast<const float4*>(xp[j] + 512 * static_cast<int64_t>(su) + 256);
+        }
+      } else {
+#pragma unroll
+        for (int j = 0; j < FM; ++j) {
+          ah[u][j] = *reinterpret_cast<const uint4*>(ap[j] + frag_step<AMODE == A_TILES>(su));
+          al[u][j] =
+              *reinterpret_cast<const uint4*>(ap[j] + frag_step<AMODE == A_TILES>(su) + lo_off);
+        }
       }
     }
 #pragma unroll
-    for (int u = 0; u < kU; ++u) {
+    for (int u = 0; u < U; ++u) {
       if (s + u < s1) {
+        if constexpr (AMODE == A_NORM) {
+          // the split of x * gamma, as the norm kernels write it (t rounded, then split)
+#pragma unroll
+          for (int j = 0; j < FM; ++j) {
+            const float xe[8] = {xv[u][j][0].x, xv[u][j][0].y, xv[u][j][0].z, xv[u][j][0].w,
+                                 xv[u][j][1].x, xv[u][j][1].y, xv[u][j][1].z, xv[u][j][1].w};
+            const float ge[8] = {gv[u][0].x, gv[u][0].y, gv[u][0].z, gv[u][0].w,
+                                 gv[u][1].x, gv[u][1].y, gv[u][1].z, gv[u][1].w};
+            float t[8];
+#pragma unroll
+            for (int e = 0; e < 8; ++e) {
+              t[e] = xe[e] * ge[e];
+              ss[j] = fmaf(xe[e], xe[e], ss[j]);
+            }
+            split8(t, ah[u][j], al[u][j]);
+          }
+        }
 #pragma unroll
         for (int i = 0; i < FN; ++i)
 #pragma unroll
@@ -133,43 +202,67 @@ __global__ __launch_bounds__(64 * kGemmWaves) void split_gemm_kernel(
   }
 
   // cross-wave reduction: every wave parks its accumulators (16 bytes per lane, lane-major,
-  // conflict-free), then each thread sums one float4 over the waves in wave order and stores it
+  // conflict-free), then each thread sums one float4 over the waves in wave order
   __shared__ f32x4_t red[NW][FN * FM][64];
+  __shared__ float ss_red[NW][TM];
 #pragma unroll
   for (int i = 0; i < FN; ++i)
 #pragma unroll
     for (int j = 0; j < FM; ++j) red[wave][i * FM + j][lane] = acc[i][j];
+  if constexpr (AMODE == A_NORM) {
+    // the four lane groups of a row, then the waves (below): a fixed order
+#pragma unroll
+    for (int j = 0; j < FM; ++j) {
+      float v = ss[j];
+      v += __shfl_xor(v, 16, kWave);
+      v += __shfl_xor(v, 32, kWave);
+      if (g == 0) ss_red[wave][16 * j + (lane & 15)] = v;
+    }
+  }
   __syncthreads();
-  if constexpr (SWIGLU) {
+  // rstd of local row r (A_NORM), as the norm kernels compute it from the sum of squares
+  auto row_rstd = [&](int r) {
+    float tot = ss_red[0][r];
+#pragma unroll
+    for (int wv = 1; wv < NW; ++wv) tot += ss_red[wv][r];
+    return rsqrtf(tot / static_cast<float>(K) + p.eps);
+  };
+  if constexpr (AMODE == A_NORM && EPI == E_STORE) {
+    if (p.rstd_out && nt == 0 && threadIdx.x < TM && m0 + static_cast<int>(threadIdx.x) < M)
+      p.rstd_out[m0 + threadIdx.x] = row_rstd(threadIdx.x);
+  }
+  if constexpr (EPI == E_SWIGLU) {
     static_assert(FN % 2 == 0, "the SwiGLU epilogue pairs gate and up fragments");
-    // q = (channel block p, row block j, lane): gate fragment 2 p, up fragment 2 p + 1
+    // q = (channel block pb, row block j, lane): gate fragment 2 pb, up fragment 2 pb + 1
     for (int q = threadIdx.x; q < (FN / 2) * FM * 64; q += 64 * NW) {
       const int pj = q >> 6, ln = q & 63;
-      const int p = pj / FM, j = pj - p * FM;
-      const int tg = (2 * p) * FM + j, tu = (2 * p + 1) * FM + j;
-      f32x4_t gv = red[0][tg][ln], uv = red[0][tu][ln];
+      const int pb = pj / FM, j = pj - pb * FM;
+      const int tg = (2 * pb) * FM + j, tu = (2 * pb + 1) * FM + j;
+      f32x4_t gsum = red[0][tg][ln], usum = red[0][tu][ln];
 #pragma unroll
       for (int wv = 1; wv < NW; ++wv) {
-        gv += red[wv][tg][ln];
-        uv += red[wv][tu][ln];
+        gsum += red[wv][tg][ln];
+        usum += red[wv][tu][ln];
       }
       const int m = m0 + 16 * j + (ln & 15);
-      const int ch = 16 * (n0 / 32 + p) + 4 * (ln >> 4);   // gate / up channel of element 0
+      const int ch = 16 * (n0 / 32 + pb) + 4 * (ln >> 4);   // gate / up channel of element 0
       if (m < M && 2 * ch < N) {
-        const float r = epi.rstd ? epi.rstd[m] : 1.f;
-        const float4 bg = epi.bias_gate ? *reinterpret_cast<const float4*>(epi.bias_gate + ch)
-                                        : make_float4(0.f, 0.f, 0.f, 0.f);
-        const float4 bu = epi.bias_up ? *reinterpret_cast<const float4*>(epi.bias_up + ch)
-                                      : make_float4(0.f, 0.f, 0.f, 0.f);
+        float r = 1.f;
+        if constexpr (AMODE == A_NORM) r = row_rstd(16 * j + (ln & 15));
+        else if (p.rstd_in) r = p.rstd_in[m];
+        const float4 bg = p.bias_a ? *reinterpret_cast<const float4*>(p.bias_a + ch)
+                                   : make_float4(0.f, 0.f, 0.f, 0.f);
+        const float4 bu = p.bias_b ? *reinterpret_cast<const float4*>(p.bias_b + ch)
+                                   : make_float4(0.f, 0.f, 0.f, 0.f);
         // the arithmetic of K3 (swiglu.hip), so fused and unfused agree bit for bit
-        const float o[4] = {silu_mul(fmaf(r, gv[0], bg.x), fmaf(r, uv[0], bu.x)),
-                            silu_mul(fmaf(r, gv[1], bg.y), fmaf(r, uv[1], bu.y)),
-                            silu_mul(fmaf(r, gv[2], bg.z), fmaf(r, uv[2], bu.z)),
-                            silu_mul(fmaf(r, gv[3], bg.w), fmaf(r, uv[3], bu.w))};
+        const float o[4] = {silu_mul(fmaf(r, gsum[0], bg.x), fmaf(r, usum[0], bu.x)),
+                            silu_mul(fmaf(r, gsum[1], bg.y), fmaf(r, usum[1], bu.y)),
+                            silu_mul(fmaf(r, gsum[2], bg.z), fmaf(r, usum[2], bu.z)),
+                            silu_mul(fmaf(r, gsum[3], bg.w), fmaf(r, usum[3], bu.w))};
         uint2 hi, lo;
         split4(o, hi, lo);
-        *reinterpret_cast<uint2*>(epi.h + tile_off(m, ch, 2 * epi.d_ff)) = hi;
-        *reinterpret_cast<uint2*>(epi.h + tile_off(m, epi.d_ff + ch, 2 * epi.d_ff)) = lo;
+        *reinterpret_cast<uint2*>(p.h + tile_off(m, ch, 2 * p.d_ff)) = hi;
+        *reinterpret_cast<uint2*>(p.h + tile_off(m, p.d_ff + ch, 2 * p.d_ff)) = lo;
       }
     }
   } else {
@@ -181,9 +274,22 @@ __global__ __launch_bounds__(64 * kGemmWaves) void split_gemm_kernel(
       const int i = t / FM, j = t - i * FM;
       const int m = m0 + 16 * j + (ln & 15);
       const int n = n0 + 16 * i + 4 * (ln >> 4);
-      if (m < M && n < N)
-        *reinterpret_cast<float4*>(out + static_cast<int64_t>(m) * ldo + n) =
-            make_float4(v[0], v[1], v[2], v[3]);
+      if (m < M && n < N) {
+        if constexpr (EPI == E_RESIDUAL) {
+          // x + delta, then + bias: the order of the add+RMSNorm kernel it replaces
+          float4* xr = reinterpret_cast<float4*>(p.x_res + tile_off32(m, n, N));
+          float4 xv = *xr;
+          xv.x += v[0]; xv.y += v[1]; xv.z += v[2]; xv.w += v[3];
+          if (p.bias_a) {
+            const float4 b = *reinterpret_cast<const float4*>(p.bias_a + n);
+            xv.x += b.x; xv.y += b.y; xv.z += b.z; xv.w += b.w;
+          }
+          *xr = xv;
+        } else {
+          *reinterpret_cast<float4*>(p.out + static_cast<int64_t>(m) * p.ldo + n) =
+              make_float4(v[0], v[1], v[2], v[3]);
+        }
+      }
     }
   }
 }
@@ -200,14 +306,17 @@ constexpr int kNumTiles = sizeof(kTiles) / sizeof(kTiles[0]);
 // number of 256-block rounds, ties to the lower total traffic.  A block holds a CU's load path
 // for about a memory latency, so the critical path is one block's operand bytes per round.  At
 // the 12 decode shapes of the reference presets (M = 256 / 128 / 64) it picks the measured
-// fastest shape or one within 3% of it.
-int pick_tile(int M, int N, int K) {
+// fastest shape or one within 3% of it.  `a_bytes` is what one activation element costs a
+// block: 4 for a split operand (hi + lo), 8 for A_NORM, whose fp32 x also goes through the
+// norm and split arithmetic in every block sharing its rows (with 8 it picks the measured
+// fastest shape at the 6 norm-fused decode shapes).
+int pick_tile(int M, int N, int K, double a_bytes = 4.0) {
   int best = 0;
   double best_key = 1e300, best_total = 1e300;
   for (int t = 0; t < kNumTiles; ++t) {
     const double blocks = static_cast<double>((N + kTiles[t].tn - 1) / kTiles[t].tn) *
                           ((M + kTiles[t].tm - 1) / kTiles[t].tm);
-    const double per_block = (2.0 * kTiles[t].tn + 4.0 * kTiles[t].tm) * K;
+    const double per_block = (2.0 * kTiles[t].tn + a_bytes * kTiles[t].tm) * K;
     const double rounds = static_cast<double>((static_cast<int64_t>(blocks) + 255) / 256);
     const double key = per_block * rounds, total = per_block * blocks;
     if (key < best_key * 0.999 || (key < best_key * 1.001 && total < best_total)) {
@@ -219,48 +328,33 @@ int pick_tile(int M, int N, int K) {
   return best + 1;
 }
 
-template <int TN, int TM, bool WT, bool AT, bool SWIGLU = false>
-int launch_tile(const uint16_t* a, int64_t lda, const uint16_t* w, int64_t ldw, float* out,
-                int64_t ldo, int M, int N, int K, hipStream_t st, SwigluEpi epi = {}) {
-  const int n_tiles = (N + TN - 1) / TN, m_tiles = (M + TM - 1) / TM;
-  const int64_t tiles = static_cast<int64_t>(n_tiles) * m_tiles;
+template <int TN, int TM, bool WT, int AMODE, int EPI>
+int launch_tile(GemmArgs p, hipStream_t st) {
+  p.n_tiles = (p.N + TN - 1) / TN;
+  p.m_tiles = (p.M + TM - 1) / TM;
+  const int64_t tiles = static_cast<int64_t>(p.n_tiles) * p.m_tiles;
   const int64_t per_xcd = (tiles + 7) / 8;
   if (8 * per_xcd > 0x7fffffff) return MDL_ERR_SHAPE;
-  hipLaunchKernelGGL((split_gemm_kernel<TN, TM, WT, AT, SWIGLU>),
-                     dim3(static_cast<unsigned>(8 * per_xcd)), dim3(64 * kGemmWaves), 0, st, a,
-                     lda, w, ldw, out, ldo, M, N, K, n_tiles, m_tiles,
-                     static_cast<int>(per_xcd), epi);
+  p.per_xcd = static_cast<int>(per_xcd);
+  hipLaunchKernelGGL((split_gemm_kernel<TN, TM, WT, AMODE, EPI>),
+                     dim3(static_cast<unsigned>(8 * per_xcd)), dim3(64 * kGemmWaves), 0, st, p);
   return launch_status();
 }
 
-template <bool WT, bool AT>
-int launch_layouts(int tile, const uint16_t* a, int64_t lda, const uint16_t* w, int64_t ldw,
-                   float* out, int64_t ldo, int M, int N, int K, hipStream_t st) {
-  switch (tile) {
-    case 1: return launch_tile<64, 64, WT, AT>(a, lda, w, ldw, out, ldo, M, N, K, st);
-    case 2: return launch_tile<128, 32, WT, AT>(a, lda, w, ldw, out, ldo, M, N, K, st);
-    case 3: return launch_tile<64, 32, WT, AT>(a, lda, w, ldw, out, ldo, M, N, K, st);
-    case 4: return launch_tile<32, 32, WT, AT>(a, lda, w, ldw, out, ldo, M, N, K, st);
-    case 5: return launch_tile<64, 16, WT, AT>(a, lda, w, ldw, out, ldo, M, N, K, st);
-    case 6: return launch_tile<32, 16, WT, AT>(a, lda, w, ldw, out, ldo, M, N, K, st);
+template <bool WT, int AMODE, int EPI>
+int launch(int tile, const GemmArgs& p, hipStream_t st) {
+  switch (tile ? tile : pick_tile(p.M, p.N, p.K, AMODE == A_NORM ? 8.0 : 4.0)) {
+    case 1: return launch_tile<64, 64, WT, AMODE, EPI>(p, st);
+    case 2: return launch_tile<128, 32, WT, AMODE, EPI>(p, st);
+    case 3: return launch_tile<64, 32, WT, AMODE, EPI>(p, st);
+    case 4: return launch_tile<32, 32, WT, AMODE, EPI>(p, st);
+    case 5: return launch_tile<64, 16, WT, AMODE, EPI>(p, st);
+    case 6: return launch_tile<32, 16, WT, AMODE, EPI>(p, st);
     default: return MDL_ERR_SHAPE;
   }
 }
 
-int launch_swiglu(int tile, const uint16_t* a, const uint16_t* w, int M, int N, int K,
-                  hipStream_t st, const SwigluEpi& epi) {
-  switch (tile) {
-    case 1: return launch_tile<64, 64, true, true, true>(a, 0, w, 0, nullptr, 0, M, N, K, st, epi);
-    case 2: return launch_tile<128, 32, true, true, true>(a, 0, w, 0, nullptr, 0, M, N, K, st, epi);
-    case 3: return launch_tile<64, 32, true, true, true>(a, 0, w, 0, nullptr, 0, M, N, K, st, epi);
-    case 4: return launch_tile<32, 32, true, true, true>(a, 0, w, 0, nullptr, 0, M, N, K, st, epi);
-    case 5: return launch_tile<64, 16, true, true, true>(a, 0, w, 0, nullptr, 0, M, N, K, st, epi);
-    case 6: return launch_tile<32, 16, true, true, true>(a, 0, w, 0, nullptr, 0, M, N, K, st, epi);
-    default: return MDL_ERR_SHAPE;
-  }
-}
-
-// dst = src in the tile layout, rows padded to a multiple of 16 with zeros.  One thread per
+// dst = src in the bf16 tile layout, rows padded to a multiple of 16 with zeros.  One thread per
 // 16-byte lane chunk of dst.
 __global__ void tile_matrix_kernel(const uint16_t* __restrict__ src, int64_t ld, int rows,
                                    int cols, int64_t chunks, uint16_t* __restrict__ dst) {
@@ -273,6 +367,12 @@ __global__ void tile_matrix_kernel(const uint16_t* __restrict__ src, int64_t ld,
   uint4 v = make_uint4(0u, 0u, 0u, 0u);
   if (r < rows) v = *reinterpret_cast<const uint4*>(src + r * ld + 32 * cb + 8 * g);
   *reinterpret_cast<uint4*>(dst + 8 * q) = v;
+}
+
+// common host checks of the tiled decode entries: k a positive multiple of 32, n of 16
+inline bool decode_shape_ok(int m, int n, int k, int tile) {
+  return m >= 0 && n >= 0 && k > 0 && k % 32 == 0 && n % 16 == 0 && tile >= 0 &&
+         tile <= kNumTiles;
 }
 
 }  // namespace
@@ -295,12 +395,113 @@ extern "C" int mdl_gemm_split(const uint16_t* a, int64_t lda, int a_layout, cons
       (!wt && ldw % 8 != 0) || ldo % 4 != 0)
     return MDL_ERR_ALIGN;
   if (m == 0 || n == 0) return MDL_OK;
+  GemmArgs p{};
+  p.a = a;
+  p.lda = lda;
+  p.w = w;
+  p.ldw = ldw;
+  p.out = out;
+  p.ldo = ldo;
+  p.M = m;
+  p.N = n;
+  p.K = k;
   auto st = static_cast<hipStream_t>(stream);
-  const int t = tile ? tile : pick_tile(m, n, k);
-  if (wt && at) return launch_layouts<true, true>(t, a, lda, w, ldw, out, ldo, m, n, k, st);
-  if (wt) return launch_layouts<true, false>(t, a, lda, w, ldw, out, ldo, m, n, k, st);
-  if (at) return launch_layouts<false, true>(t, a, lda, w, ldw, out, ldo, m, n, k, st);
-  return launch_layouts<false, false>(t, a, lda, w, ldw, out, ldo, m, n, k, st);
+  if (wt && at) return launch<true, A_TILES, E_STORE>(tile, p, st);
+  if (wt) return launch<true, A_ROWS, E_STORE>(tile, p, st);
+  if (at) return launch<false, A_TILES, E_STORE>(tile, p, st);
+  return launch<false, A_ROWS, E_STORE>(tile, p, st);
+}
+
+extern "C" int mdl_gemm_split_swiglu(const uint16_t* a, const uint16_t* w_gu, const float* rstd,
+                                     const float* bias_gate, const float* bias_up,
+                                     uint16_t* h_out, int m, int d_ff, int k, int tile,
+                                     void* stream) {
+  if (!a || !w_gu || !h_out) return MDL_ERR_NULL;
+  if (d_ff <= 0 || d_ff % 16 != 0 || !decode_shape_ok(m, 2 * d_ff, k, tile))
+    return MDL_ERR_SHAPE;
+  if (!aligned16(a) || !aligned16(w_gu) || !aligned8(h_out) ||
+      (bias_gate && !aligned16(bias_gate)) || (bias_up && !aligned16(bias_up)))
+    return MDL_ERR_ALIGN;
+  if (m == 0) return MDL_OK;
+  GemmArgs p{};
+  p.a = a;
+  p.w = w_gu;
+  p.rstd_in = rstd;
+  p.bias_a = bias_gate;
+  p.bias_b = bias_up;
+  p.h = h_out;
+  p.d_ff = d_ff;
+  p.M = m;
+  p.N = 2 * d_ff;
+  p.K = k;
+  return launch<true, A_TILES, E_SWIGLU>(tile, p, static_cast<hipStream_t>(stream));
+}
+
+extern "C" int mdl_gemm_norm(const float* x, const float* gamma, float eps, const uint16_t* w,
+                             float* out, int64_t ldo, float* rstd_out, int m, int n, int k,
+                             int tile, void* stream) {
+  if (!x || !gamma || !w || !out) return MDL_ERR_NULL;
+  if (!decode_shape_ok(m, n, k, tile) || ldo < n) return MDL_ERR_SHAPE;
+  if (!aligned16(x) || !aligned16(gamma) || !aligned16(w) || !aligned16(out) || ldo % 4 != 0)
+    return MDL_ERR_ALIGN;
+  if (m == 0 || n == 0) return MDL_OK;
+  GemmArgs p{};
+  p.x = x;
+  p.gamma = gamma;
+  p.eps = eps;
+  p.w = w;
+  p.out = out;
+  p.ldo = ldo;
+  p.rstd_out = rstd_out;
+  p.M = m;
+  p.N = n;
+  p.K = k;
+  return launch<true, A_NORM, E_STORE>(tile, p, static_cast<hipStream_t>(stream));
+}
+
+extern "C" int mdl_gemm_norm_swiglu(const float* x, const float* gamma, float eps,
+                                    const uint16_t* w_gu, const float* bias_gate,
+                                    const float* bias_up, uint16_t* h_out, int m, int d_ff, int k,
+                                    int tile, void* stream) {
+  if (!x || !gamma || !w_gu || !h_out) return MDL_ERR_NULL;
+  if (d_ff <= 0 || d_ff % 16 != 0 || !decode_shape_ok(m, 2 * d_ff, k, tile))
+    return MDL_ERR_SHAPE;
+  if (!aligned16(x) || !aligned16(gamma) || !aligned16(w_gu) || !aligned8(h_out) ||
+      (bias_gate && !aligned16(bias_gate)) || (bias_up && !aligned16(bias_up)))
+    return MDL_ERR_ALIGN;
+  if (m == 0) return MDL_OK;
+  GemmArgs p{};
+  p.x = x;
+  p.gamma = gamma;
+  p.eps = eps;
+  p.w = w_gu;
+  p.bias_a = bias_gate;
+  p.bias_b = bias_up;
+  p.h = h_out;
+  p.d_ff = d_ff;
+  p.M = m;
+  p.N = 2 * d_ff;
+  p.K = k;
+  return launch<true, A_NORM, E_SWIGLU>(tile, p, static_cast<hipStream_t>(stream));
+}
+
+extern "C" int mdl_gemm_split_residual(const uint16_t* a, const uint16_t* w, float* x,
+                                       const float* bias, int m, int n, int k, int tile,
+                                       void* stream) {
+  if (!a || !w || !x) return MDL_ERR_NULL;
+  if (!decode_shape_ok(m, n, k, tile) || n % 32 != 0) return MDL_ERR_SHAPE;
+  if (!aligned16(a) || !aligned16(w) || !aligned16(x) || (bias && !aligned16(bias)))
+    return MDL_ERR_ALIGN;
+  if (m == 0 || n == 0) return MDL_OK;
+  GemmArgs p{};
+  p.a = a;
+  p.w = w;
+  p.x_res = x;
+  p.bias_a = bias;
+  p.M = m;
+  p.N = n;
+  p.K = k;
+  return launch<true, A_TILES, E_RESIDUAL>(tile, p, static_cast<hipStream_t>(stream));
 }
 
 extern "C" int mdl_gemm_split_tiles(void) { return kNumTiles; }
@@ -322,22 +523,4 @@ extern "C" int mdl_tile_matrix(const uint16_t* src, int64_t ld, int rows, int co
   hipLaunchKernelGGL(tile_matrix_kernel, dim3(static_cast<unsigned>(blocks)), dim3(256), 0,
                      static_cast<hipStream_t>(stream), src, ld, rows, cols, chunks, dst);
   return launch_status();
-}
-
-extern "C" int mdl_gemm_split_swiglu(const uint16_t* a, const uint16_t* w_gu, const float* rstd,
-                                     const float* bias_gate, const float* bias_up,
-                                     uint16_t* h_out, int m, int d_ff, int k, int tile,
-                                     void* stream) {
-  if (!a || !w_gu || !h_out) return MDL_ERR_NULL;
-  if (m < 0 || d_ff <= 0 || d_ff % 16 != 0 || k <= 0 || k % 32 != 0 || tile < 0 ||
-      tile > kNumTiles)
-    return MDL_ERR_SHAPE;
-  if (!aligned16(a) || !aligned16(w_gu) || !aligned8(h_out) ||
-      (bias_gate && !aligned16(bias_gate)) || (bias_up && !aligned16(bias_up)))
-    return MDL_ERR_ALIGN;
-  if (m == 0) return MDL_OK;
-  const int n = 2 * d_ff;
-  const SwigluEpi epi{rstd, bias_gate, bias_up, h_out, d_ff};
-  return launch_swiglu(tile ? tile : pick_tile(m, n, k), a, w_gu, m, n, k,
-                       static_cast<hipStream_t>(stream), epi);
 }

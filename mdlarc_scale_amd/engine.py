@@ -15,10 +15,18 @@ Dataflow per layer (M token rows, d channels, F ffn width; fp32 residual stream 
     x += delta + b_down; xs = split(x * g1_next), rstd              <- add_rmsnorm
   final: logits = lm_head(ln_f(x)) and greedy argmax                <- lm_head kernel
 
-At decode (M = batch rows) the projections run on K5 instead of hipBLASLt: the producers write
-xs / attn / h in the MFMA tile layout and K5 multiplies them with tiled copies of W (read once,
-not as [W | W]); see ``project``.  The gate / up GEMM there carries the SwiGLU in its epilogue
-and writes h directly (no gu round trip, no K3 launch).
+At decode (M = batch rows) the projections run on K5 instead of hipBLASLt, on activations and
+tiled copies of W (read once, not as [W | W]) in the MFMA tile layout, and the small kernels go
+into K5's prologues and epilogues: per layer
+
+    qkv = split(x * g1) @ Wqkv^T, rstd             <- gemm_norm (ln1 in the prologue)
+    attn = K4(...)                                 (tiled output)
+    x += attn @ Wo^T                                <- gemm_split_residual
+    h = split(silu(rstd*g + b_g) * (rstd*u + b_u)), g / u = split(x * g2) @ Wg^T / Wu^T
+                                                    <- gemm_norm_swiglu (ln2 in the prologue)
+    x += h @ Wd^T + b_down                          <- gemm_split_residual
+
+with x (fp32) in the fp32 tile layout; the head kernel takes ln_f itself.
 
 "split" stores a GEMM input as a hi|lo pair of bf16 (hi = bf16(v), lo = bf16(v - hi)); against a
 weight packed as [W | W] the bf16 MFMA GEMM then sees the activation to ~2^-17 instead of 2^-9.
@@ -56,16 +64,6 @@ def tiles_supported(d_model: int, d_ff: int) -> bool:
     """K5 with tiled operands needs every projection's K (d_model, d_ff) to be a multiple of 32;
     all reference presets are."""
     return d_model % 32 == 0 and d_ff % 32 == 0
-
-
-def project(sc: "Scratch", a: torch.Tensor, w2: torch.Tensor, wt: torch.Tensor | None,
-            out: torch.Tensor) -> None:
-    """One projection out = a @ W^T: on K5 with tiled activations and weights when ``sc`` is a
-    decode scratch in the tile layout, else on hipBLASLt against the [W | W] operand."""
-    if sc.tiled:
-        K.gemm_split(a, wt, out, w2.shape[1] // 2, a_tiled=True, w_tiled=True)
-    else:
-        gemm_f32(a, w2, out)
 
 
 def pack_split_weight(w: torch.Tensor, device: torch.device) -> torch.Tensor:
@@ -125,18 +123,21 @@ class Scratch:
     delta: torch.Tensor
     gu: torch.Tensor
     h: torch.Tensor
+    rows: int = 0
     tiled: bool = False
 
     @staticmethod
     def alloc(rows: int, d: int, d_ff: int, device: torch.device,
               tiled: bool = False) -> "Scratch":
+        """``tiled``: the decode form -- x in the fp32 tile layout and attn / h in the bf16 one
+        (whole 16-row blocks); the RMSNorms run inside the K5 launches (``HipEngine._mlp``)."""
         e = lambda *s, dt=torch.bfloat16: torch.empty(*s, dtype=dt, device=device)  # noqa: E731
         f = torch.float32
-        sr = K.tile_rows(rows) if tiled else rows       # rows of the split activations
-        return Scratch(x=e(rows, d, dt=f), xs=e(sr, 2 * d), rstd=e(rows, dt=f),
+        sr = K.tile_rows(rows) if tiled else rows       # rows of the tiled activations
+        return Scratch(x=e(sr, d, dt=f), xs=e(sr, 2 * d), rstd=e(rows, dt=f),
                        qkv=e(rows, 3 * d, dt=f), q=e(rows, d), attn=e(sr, 2 * d),
                        delta=e(rows, d, dt=f), gu=e(rows, 2 * d_ff, dt=f), h=e(sr, 2 * d_ff),
-                       tiled=tiled)
+                       rows=rows, tiled=tiled)
 
 
 @dataclass
@@ -307,19 +308,24 @@ class HipEngine:
     def _mlp(self, W: PackedWeights, li: int, sc: Scratch) -> None:
         """out_proj + residual, ln2, SwiGLU MLP + residual, next norm (shared by both phases)."""
         cfg = self.cfg
-        t = sc.tiled
-        project(sc, sc.attn, W.out[li], W.out_t[li] if t else None, sc.delta)
-        K.add_rmsnorm(sc.x, sc.delta, None, W.ln2[li], W.eps, sc.xs, sc.rstd, tiled=t)
-        if t:      # decode: gate / up GEMM with the SwiGLU fused (K5 epilogue)
-            K.gemm_split_swiglu(sc.xs, W.gu_t[li], sc.rstd, W.b_gate[li], W.b_up[li], sc.h,
-                                sc.x.shape[0], cfg.d_ff, cfg.d_model)
-        else:
-            gemm_f32(sc.xs, W.gu[li], sc.gu)
-            K.swiglu(sc.gu, sc.rstd, W.b_gate[li], W.b_up[li], sc.h)
-        project(sc, sc.h, W.down[li], W.down_t[li] if t else None, sc.delta)
+        d, F = cfg.d_model, cfg.d_ff
+        if sc.tiled:
+            # decode: three K5 launches, the residual adds in the epilogues and ln2 in the
+            # gate / up prologue; the next layer's ln1 runs in its qkv launch (gemm_norm) and
+            # ln_f in the head kernel
+            K.gemm_split_residual(sc.attn, W.out_t[li], sc.x, None, sc.rows, d, d)
+            K.gemm_norm_swiglu(sc.x, W.ln2[li], W.eps, W.gu_t[li], W.b_gate[li], W.b_up[li],
+                               sc.h, sc.rows, F, d)
+            K.gemm_split_residual(sc.h, W.down_t[li], sc.x, W.b_down[li], sc.rows, d, F)
+            return
+        gemm_f32(sc.attn, W.out[li], sc.delta)
+        K.add_rmsnorm(sc.x, sc.delta, None, W.ln2[li], W.eps, sc.xs, sc.rstd)
+        gemm_f32(sc.xs, W.gu[li], sc.gu)
+        K.swiglu(sc.gu, sc.rstd, W.b_gate[li], W.b_up[li], sc.h)
+        gemm_f32(sc.h, W.down[li], sc.delta)
         last = li + 1 == cfg.n_layers
         K.add_rmsnorm(sc.x, sc.delta, W.b_down[li], W.ln_f if last else W.ln1[li + 1], W.eps,
-                      None if last else sc.xs, sc.rstd, tiled=t)
+                      None if last else sc.xs, sc.rstd)
 
     @torch.no_grad()
     def forward(self, ids: torch.Tensor, pos: torch.Tensor, ex_ids: torch.Tensor | None,

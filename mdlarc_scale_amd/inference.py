@@ -38,7 +38,7 @@ from .data import (
 )
 from .engine import GRID_MAX_X, GRID_MAX_Y, HipEngine, PackedWeights, Scratch, choose_split_len
 from .engine import pack_prompt
-from .engine import engine_for, project, tiles_supported
+from .engine import engine_for, gemm_f32, tiles_supported
 from .transformer import TinyTransformer, softmax_scale
 
 SYNC_EVERY = 8
@@ -55,9 +55,10 @@ USE_GRAPHS = True
 # layer over the whole padded [B, S] batch.  Logits and cache contents agree to fp32 rounding (the
 # GEMMs see a different row count).
 PACKED_PREFILL = True
-# Decode steps run their projections on K5 (mdl_gemm_split) over activations and weights in the
-# MFMA tile layout; False keeps them on hipBLASLt with row-major activations.  Logits agree to
-# fp32 rounding.
+# Decode steps run their projections on K5 over activations and weights in the MFMA tile
+# layouts, with the RMSNorms, residual adds and SwiGLU inside those launches (five per layer);
+# False runs hipBLASLt and the separate norm / SwiGLU kernels on row-major activations.  Logits
+# agree to fp32 rounding.
 DECODE_TILED = True
 
 
@@ -349,7 +350,10 @@ class Generator:
         slot = st.counters[0:1]
         for li in range(cfg.n_layers):
             kc, vc = st.cache.layer(li)
-            project(sc, sc.xs, W.qkv[li], W.qkv_t[li] if sc.tiled else None, sc.qkv)
+            if sc.tiled:     # ln1 in the projection's prologue; rstd for the attention launch
+                K.gemm_norm(sc.x, W.ln1[li], W.eps, W.qkv_t[li], sc.qkv, sc.rstd, cfg.d_model)
+            else:
+                gemm_f32(sc.xs, W.qkv[li], sc.qkv)
             # RMSNorm scale + split + 3D RoPE + cache write fused into the attention launch
             K.attn_decode_rope(sc.qkv, sc.rstd, st.pos, W.rope_tab, W.rope_geom, qs, kc, vc, B,
                                H, st.pmask, st.S, st.kv_start, 0, slot, st.ws, st.split_len,
@@ -362,11 +366,12 @@ class Generator:
         (the host-launched path of sampling / constrained decoding)."""
         sc = st.sc
         tok_tab, ex_tab, use_ex = self._embed_inputs(st)
-        K.embed_rmsnorm(st.tok, use_ex, tok_tab, ex_tab, 1, W.ln1[0], W.eps, sc.x, sc.xs,
-                        sc.rstd, tiled=sc.tiled)
+        t = sc.tiled
+        K.embed_rmsnorm(st.tok, use_ex, tok_tab, ex_tab, 1, W.ln1[0], W.eps, sc.x,
+                        None if t else sc.xs, None if t else sc.rstd, tiled=t)
         self._layers(st, W)
         K.lm_head(sc.x, None, st.B, W.ln_f, W.eps, W.head, st.logits if want_logits else None,
-                  st.tok)
+                  st.tok, x_tiled=t)
 
     def greedy_step(self, st: DecodeState, W: PackedWeights, stop_on_end: bool,
                     cons: K.HeadConstraints | None = None) -> None:
@@ -374,11 +379,13 @@ class Generator:
         the layers, then LM head (+ logit constraints) + argmax + commit."""
         sc = st.sc
         tok_tab, ex_tab, use_ex = self._embed_inputs(st)
+        t = sc.tiled
         K.decode_embed(st.tok, use_ex, tok_tab, ex_tab, W.ln1[0], W.eps, st.gx, st.gy, st.gio,
-                       st.pos, st.counters, sc.x, sc.xs, sc.rstd, tiled=sc.tiled)
+                       st.pos, st.counters, sc.x, None if t else sc.xs, None if t else sc.rstd,
+                       tiled=t)
         self._layers(st, W)
         K.decode_head(sc.x, W.ln_f, W.eps, W.head, None, st.tok, st.out_ids, 0, st.counters,
-                      st.finish if stop_on_end else None, st.S, END_TOKEN_ID, cons)
+                      st.finish if stop_on_end else None, st.S, END_TOKEN_ID, cons, x_tiled=t)
 
     def capture_greedy(self, st: DecodeState, W: PackedWeights, stop_on_end: bool,
                        cons: K.HeadConstraints | None = None) -> torch.cuda.CUDAGraph:

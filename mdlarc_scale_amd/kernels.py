@@ -70,9 +70,10 @@ def table_dtype_code(t: torch.Tensor) -> int:
 def embed_rmsnorm(ids: torch.Tensor, example_ids: torch.Tensor | None, tok_table: torch.Tensor,
                   ex_table: torch.Tensor | None, row_len: int, gamma: torch.Tensor, eps: float,
                   x_out: torch.Tensor, xs_out: torch.Tensor | None,
-                  rstd_out: torch.Tensor, tiled: bool = False) -> None:
-    """x = tok[ids] + ex[example_ids], rstd, xs = split(x * gamma) as [rows, 2d] bf16
-    (row-major, or in MFMA tiles for gemm_split when ``tiled``)."""
+                  rstd_out: torch.Tensor | None, tiled: bool = False) -> None:
+    """x = tok[ids] + ex[example_ids], rstd, xs = split(x * gamma) as [rows, 2d] bf16; with
+    ``tiled`` x in the fp32 and xs in the bf16 MFMA tile layout (the K5 decode entries).
+    xs_out and rstd_out may be None."""
     rows = ids.numel()
     vocab, d = tok_table.shape
     _need(ids, "ids", I64)
@@ -85,9 +86,9 @@ def embed_rmsnorm(ids: torch.Tensor, example_ids: torch.Tensor | None, tok_table
         if example_ids.numel() * row_len < rows:
             raise ValueError("example_ids shorter than the number of batch rows")
     _need(gamma, "gamma", F32, d)
-    _need(x_out, "x_out", F32, rows * d)
+    _need(x_out, "x_out", F32, (tile_rows(rows) if tiled else rows) * d)
     _need(xs_out, "xs_out", BF16, split_numel(rows, d, tiled), optional=True)
-    _need(rstd_out, "rstd_out", F32, rows)
+    _need(rstd_out, "rstd_out", F32, rows, optional=True)
     n_ex = ex_table.shape[0] if ex_table is not None else 0
     _lib.check(_lib.lib().mdl_embed_rmsnorm(
         _p(ids), _p(example_ids), _p(tok_table), _p(ex_table), table_dtype_code(tok_table),
@@ -98,10 +99,11 @@ def embed_rmsnorm(ids: torch.Tensor, example_ids: torch.Tensor | None, tok_table
 def decode_embed(token: torch.Tensor, example_ids: torch.Tensor | None, tok_table: torch.Tensor,
                  ex_table: torch.Tensor | None, gamma: torch.Tensor, eps: float,
                  gx: torch.Tensor, gy: torch.Tensor, in_out: torch.Tensor, pos_out: torch.Tensor,
-                 counters: torch.Tensor | None, x_out: torch.Tensor, xs_out: torch.Tensor,
-                 rstd_out: torch.Tensor, max_x: int = 30, max_y: int = 29,
-                 tiled: bool = False) -> None:
-    """Grid position of each row's emitted token (state advanced), then K1 on that token."""
+                 counters: torch.Tensor | None, x_out: torch.Tensor,
+                 xs_out: torch.Tensor | None, rstd_out: torch.Tensor | None, max_x: int = 30,
+                 max_y: int = 29, tiled: bool = False) -> None:
+    """Grid position of each row's emitted token (state advanced), then K1 on that token
+    (``tiled`` and the optional outputs as for embed_rmsnorm)."""
     batch = token.numel()
     vocab, d = tok_table.shape
     _need(token, "token", I64)
@@ -116,9 +118,9 @@ def decode_embed(token: torch.Tensor, example_ids: torch.Tensor | None, tok_tabl
     _need(pos_out, "pos_out", I64, batch * 3)
     _need(counters, "counters", I32, 2, optional=True)
     _need(gamma, "gamma", F32, d)
-    _need(x_out, "x_out", F32, batch * d)
-    _need(xs_out, "xs_out", BF16, split_numel(batch, d, tiled))
-    _need(rstd_out, "rstd_out", F32, batch)
+    _need(x_out, "x_out", F32, (tile_rows(batch) if tiled else batch) * d)
+    _need(xs_out, "xs_out", BF16, split_numel(batch, d, tiled), optional=True)
+    _need(rstd_out, "rstd_out", F32, batch, optional=True)
     n_ex = ex_table.shape[0] if ex_table is not None else 0
     _lib.check(_lib.lib().mdl_decode_embed(
         _p(token), _p(example_ids), _p(tok_table), _p(ex_table), table_dtype_code(tok_table),
@@ -273,6 +275,68 @@ def interleave_gate_up(w_gate: torch.Tensor, w_up: torch.Tensor) -> torch.Tensor
         raise ValueError("gate and up weights must be [d_ff, k] with d_ff a multiple of 16")
     return torch.stack([w_gate.reshape(f // 16, 16, k), w_up.reshape(f // 16, 16, k)],
                        1).reshape(2 * f, k).contiguous()
+
+
+def gemm_norm(x: torch.Tensor, gamma: torch.Tensor, eps: float, w: torch.Tensor,
+              out: torch.Tensor, rstd_out: torch.Tensor | None, k: int, tile: int = 0) -> None:
+    """out[m, n] = split(x * gamma) @ W^T with the RMSNorm in K5's prologue; rstd of each row
+    into rstd_out (may be None).  x: fp32 tile layout [tile_rows(m), k]; w tiled [n, k]."""
+    _need(out, "out", F32)
+    m, n = out.shape
+    _need(x, "x", F32, tile_rows(m) * k)
+    _need(gamma, "gamma", F32, k)
+    _need(w, "w", BF16, tile_rows(n) * k)
+    _need(rstd_out, "rstd_out", F32, m, optional=True)
+    _lib.check(_lib.lib().mdl_gemm_norm(_p(x), _p(gamma), eps, _p(w), _p(out), n, _p(rstd_out),
+                                        m, n, k, tile, _stream()), "mdl_gemm_norm")
+
+
+def gemm_norm_swiglu(x: torch.Tensor, gamma: torch.Tensor, eps: float, w_gu: torch.Tensor,
+                     bias_gate: torch.Tensor | None, bias_up: torch.Tensor | None,
+                     h_out: torch.Tensor, m: int, d_ff: int, k: int, tile: int = 0) -> None:
+    """The gate / up projection of split(x * gamma) (RMSNorm in the prologue) with the SwiGLU
+    epilogue: h (tiled split [m, 2 d_ff]).  x: fp32 tile layout; w_gu: tiled
+    interleave_gate_up weight."""
+    _need(x, "x", F32, tile_rows(m) * k)
+    _need(gamma, "gamma", F32, k)
+    _need(w_gu, "w_gu", BF16, 2 * d_ff * k)
+    _need(bias_gate, "bias_gate", F32, d_ff, optional=True)
+    _need(bias_up, "bias_up", F32, d_ff, optional=True)
+    _need(h_out, "h_out", BF16, split_numel(m, d_ff, True))
+    _lib.check(_lib.lib().mdl_gemm_norm_swiglu(
+        _p(x), _p(gamma), eps, _p(w_gu), _p(bias_gate), _p(bias_up), _p(h_out), m, d_ff, k,
+        tile, _stream()), "mdl_gemm_norm_swiglu")
+
+
+def gemm_split_residual(a: torch.Tensor, w: torch.Tensor, x: torch.Tensor,
+                        bias: torch.Tensor | None, m: int, n: int, k: int,
+                        tile: int = 0) -> None:
+    """x += (a_hi + a_lo) @ W^T (+ bias) in place; a tiled split [m, 2k], w tiled [n, k], x the
+    fp32 tile-layout residual stream [tile_rows(m), n]."""
+    _need(a, "a", BF16, tile_rows(m) * 2 * k)
+    _need(w, "w", BF16, tile_rows(n) * k)
+    _need(x, "x", F32, tile_rows(m) * n)
+    _need(bias, "bias", F32, n, optional=True)
+    _lib.check(_lib.lib().mdl_gemm_split_residual(_p(a), _p(w), _p(x), _p(bias), m, n, k, tile,
+                                                  _stream()), "mdl_gemm_split_residual")
+
+
+def tile_f32(x: torch.Tensor) -> torch.Tensor:
+    """[rows, cols] fp32 (cols a multiple of 32) in the fp32 tile layout: a new flat tensor of
+    tile_rows(rows) * cols floats, padding rows zero (torch ops; for tests and set-up)."""
+    rows, cols = x.shape
+    if cols % 32:
+        raise ValueError("the fp32 tile layout needs a multiple of 32 columns")
+    xp = torch.zeros(tile_rows(rows), cols, dtype=x.dtype, device=x.device)
+    xp[:rows] = x
+    # [row block, r, col block, q, h, e] -> [row block, col block, h, q, r, e]
+    return xp.view(-1, 16, cols // 32, 4, 2, 4).permute(0, 2, 4, 3, 1, 5).reshape(-1)
+
+
+def untile_f32(t: torch.Tensor, rows: int, cols: int) -> torch.Tensor:
+    """The inverse of tile_f32: the [rows, cols] matrix."""
+    v = t[:tile_rows(rows) * cols].view(-1, cols // 32, 2, 4, 16, 4)
+    return v.permute(0, 4, 1, 3, 2, 5).reshape(-1, cols)[:rows]
 
 
 def gemm_split_tiles() -> int:
@@ -476,12 +540,14 @@ class HeadConstraints:
 
 def lm_head(x: torch.Tensor, row_index: torch.Tensor | None, rows: int, gamma: torch.Tensor,
             eps: float, w_head: torch.Tensor, logits_out: torch.Tensor | None,
-            token_out: torch.Tensor | None, constraints: HeadConstraints | None = None) -> None:
+            token_out: torch.Tensor | None, constraints: HeadConstraints | None = None,
+            x_tiled: bool = False) -> None:
+    """x: [rows, d] fp32, row-major or (``x_tiled``) in the fp32 tile layout."""
     d = x.shape[-1]
     vocab = w_head.shape[0]
     _need(x, "x", F32)
     _need(row_index, "row_index", I32, rows, optional=True)
-    if row_index is None and x.numel() < rows * d:
+    if row_index is None and x.numel() < (tile_rows(rows) if x_tiled else rows) * d:
         raise ValueError("x has fewer rows than requested")
     _need(gamma, "gamma", F32, d)
     _need(w_head, "w_head", F32, vocab * d)
@@ -489,19 +555,21 @@ def lm_head(x: torch.Tensor, row_index: torch.Tensor | None, rows: int, gamma: t
     _need(token_out, "token_out", I64, rows, optional=True)
     _lib.check(_lib.lib().mdl_lm_head(
         _p(x), _p(row_index), rows, d, _p(gamma), eps, _p(w_head), vocab, _p(logits_out),
-        _p(token_out), None if constraints is None else constraints.ref(rows), _stream()),
-        "mdl_lm_head")
+        _p(token_out), None if constraints is None else constraints.ref(rows), _layout(x_tiled),
+        _stream()), "mdl_lm_head")
 
 
 def decode_head(x: torch.Tensor, gamma: torch.Tensor, eps: float, w_head: torch.Tensor,
                 logits_out: torch.Tensor | None, token_out: torch.Tensor, out_ids: torch.Tensor,
                 col: int, counters: torch.Tensor | None, finish_step: torch.Tensor | None,
-                gen_base: int, end_id: int, constraints: HeadConstraints | None = None) -> None:
+                gen_base: int, end_id: int, constraints: HeadConstraints | None = None,
+                x_tiled: bool = False) -> None:
     """ln_f + LM head (+ constraints) + argmax into token_out, committed to
-    out_ids[:, counters[1] or col]."""
-    batch, d = x.shape
+    out_ids[:, counters[1] or col].  x: [batch, d] fp32, or (``x_tiled``) the fp32 tile layout
+    with tile_rows(batch) rows."""
+    batch, d = token_out.numel(), x.shape[-1]
     vocab = w_head.shape[0]
-    _need(x, "x", F32)
+    _need(x, "x", F32, (tile_rows(batch) if x_tiled else batch) * d)
     _need(gamma, "gamma", F32, d)
     _need(w_head, "w_head", F32, vocab * d)
     _need(logits_out, "logits_out", F32, batch * vocab, optional=True)
@@ -514,7 +582,8 @@ def decode_head(x: torch.Tensor, gamma: torch.Tensor, eps: float, w_head: torch.
     _lib.check(_lib.lib().mdl_decode_head(
         _p(x), batch, d, _p(gamma), eps, _p(w_head), vocab, _p(logits_out), _p(token_out),
         _p(out_ids), out_ids.shape[1], col, _p(counters), _p(finish_step), gen_base, end_id,
-        None if constraints is None else constraints.ref(batch), _stream()), "mdl_decode_head")
+        None if constraints is None else constraints.ref(batch), _layout(x_tiled), _stream()),
+        "mdl_decode_head")
 
 
 def grid_init(ids: torch.Tensor, pos: torch.Tensor, mask: torch.Tensor | None, gx: torch.Tensor,

@@ -63,6 +63,13 @@ def test_argument_errors_are_reported_before_any_launch():
     assert L.mdl_gemm_split(fake + 8, 64, 0, fake, 32, 0, fake, 8, 4, 8, 32, 0, None) == -2
     assert L.mdl_gemm_split(None, 0, 1, fake, 0, 1, fake, 8, 4, 8, 32, 0, None) == -1
     assert L.mdl_tile_matrix(fake, 40, 4, 40, fake, None) == -3
+    # fused K5 forms: n a multiple of 16 (32 for the residual form), d_ff of 16, x required
+    assert L.mdl_gemm_norm(fake, fake, 1e-5, fake, fake, 24, None, 4, 24, 32, 0, None) == -3
+    assert L.mdl_gemm_norm(None, fake, 1e-5, fake, fake, 32, None, 4, 32, 32, 0, None) == -1
+    assert L.mdl_gemm_norm_swiglu(fake, fake, 1e-5, fake, None, None, fake, 4, 24, 32, 0,
+                                  None) == -3
+    assert L.mdl_gemm_split_residual(fake, fake, fake, None, 4, 48, 32, 0, None) == -3
+    assert L.mdl_gemm_split_residual(fake, fake, fake + 4, None, 4, 64, 32, 0, None) == -2
     assert L.mdl_gemm_split_tiles() >= 1
     assert 1 <= L.mdl_gemm_split_pick(256, 2304, 768) <= L.mdl_gemm_split_tiles()
     # packed prefill: the per-row starts / offsets and the per-token rows / slots are required

@@ -978,17 +978,29 @@ def test_producers_write_the_tile_layout():
     gamma = (1 + 0.1 * torch.randn(d, generator=g)).to(DEV)
     ids = torch.randint(0, 14, (B,), generator=g).to(DEV)
     exi = torch.randint(0, 5, (B,), generator=g).to(DEV)
-    x = torch.empty(B, d, device=DEV)
     r = torch.empty(B, device=DEV)
-    both(lambda buf, t: K().embed_rmsnorm(ids, exi, tok, ex, 1, gamma, 1e-5, x, buf, r,
-                                          tiled=t), B, 2 * d)
     state = (torch.randint(0, 30, (B,), generator=g).to(torch.int32),
              torch.randint(0, 29, (B,), generator=g).to(torch.int32),
              torch.randint(0, 2, (B,), generator=g).to(torch.uint8))
     pos = torch.empty(B, 3, dtype=torch.int64, device=DEV)
-    both(lambda buf, t: K().decode_embed(ids, exi, tok, ex, gamma, 1e-5,
-                                         *(s.clone().to(DEV) for s in state), pos, None, x, buf,
-                                         r, tiled=t), B, 2 * d)
+    # the embedding entries write x (fp32 tile layout) and xs (bf16 tile layout) when tiled
+    for embed in (lambda xb, xsb, t: K().embed_rmsnorm(ids, exi, tok, ex, 1, gamma, 1e-5, xb,
+                                                       xsb, r, tiled=t),
+                  lambda xb, xsb, t: K().decode_embed(ids, exi, tok, ex, gamma, 1e-5,
+                                                      *(s.clone().to(DEV) for s in state), pos,
+                                                      None, xb, xsb, r, tiled=t)):
+        xr = torch.zeros(B, d, device=DEV)
+        xsr = torch.zeros(B * 2 * d, device=DEV, dtype=torch.bfloat16)
+        embed(xr, xsr, False)
+        xt = torch.zeros(K().tile_rows(B) * d, device=DEV)
+        xst = torch.zeros(K().tile_rows(B) * 2 * d, device=DEV, dtype=torch.bfloat16)
+        embed(xt, xst, True)
+        xt_only = torch.zeros_like(xt)
+        embed(xt_only, None, True)                   # xs optional
+        torch.cuda.synchronize()
+        assert torch.equal(K().tile_f32(xr), xt)
+        assert torch.equal(xt_only, xt)
+        assert torch.equal(K().tile_matrix(xsr.view(B, 2 * d)), xst)
     x0 = torch.randn(B, d, generator=g).to(DEV)
     delta = torch.randn(B, d, generator=g).to(DEV)
     both(lambda buf, t: K().add_rmsnorm(x0.clone(), delta, None, gamma, 1e-5, buf, r, tiled=t),
@@ -1043,3 +1055,106 @@ def test_gemm_split_swiglu_equals_gemm_then_swiglu(m, f, k):
             K().swiglu(gu, r, b1, b2, ref, tiled=True)
             torch.cuda.synchronize()
             assert torch.equal(fused, ref), f"tile {t}"
+
+
+
+@pytest.mark.parametrize("m,n,k", [(256, 2304, 768), (37, 768, 256), (64, 3840, 1280)])
+def test_gemm_norm_equals_add_rmsnorm_then_gemm(m, n, k):
+    """K5 with the RMSNorm prologue (x in the fp32 tile layout) gives the same bits as
+    mdl_add_rmsnorm (xs tiled) followed by K5 for every block shape, and the same rstd to fp32
+    rounding (the sum of squares is taken in another order); the head kernels read the tiled x
+    as they read the row-major one."""
+    g = torch.Generator().manual_seed(m + n + k)
+    x = (torch.randn(m, k, generator=g) * 1.5).to(DEV)
+    gamma = (1 + 0.1 * torch.randn(k, generator=g)).to(DEV)
+    w = (torch.randn(n, k, generator=g) * 0.05).to(torch.bfloat16).to(DEV)
+    wt = K().tile_matrix(w)
+    xs = torch.zeros(K().split_numel(m, k, True), device=DEV, dtype=torch.bfloat16)
+    rstd_ref = torch.empty(m, device=DEV)
+    K().add_rmsnorm(x.clone(), None, None, gamma, 1e-5, xs, rstd_ref, tiled=True)
+    xt = K().tile_f32(x)
+    for t in list(range(1, K().gemm_split_tiles() + 1)) + [0]:
+        ref = torch.empty(m, n, device=DEV)
+        K().gemm_split(xs, wt, ref, k, a_tiled=True, w_tiled=True, tile=t)
+        out = torch.full((m, n), float("nan"), device=DEV)
+        rstd = torch.full((m,), float("nan"), device=DEV)
+        K().gemm_norm(xt, gamma, 1e-5, wt, out, rstd, k, tile=t)
+        torch.cuda.synchronize()
+        assert torch.equal(out, ref), f"tile {t}"
+        assert torch.allclose(rstd, rstd_ref, rtol=2e-6, atol=0), f"tile {t}"
+    # the head kernels on the tiled x
+    V = 14
+    wh = (torch.randn(V, k, generator=g) / math.sqrt(k)).to(DEV)
+    lr, lt = torch.empty(m, V, device=DEV), torch.empty(m, V, device=DEV)
+    K().lm_head(x, None, m, gamma, 1e-5, wh, lr, None)
+    K().lm_head(xt.view(-1, k), None, m, gamma, 1e-5, wh, lt, None, x_tiled=True)
+    torch.cuda.synchronize()
+    assert torch.equal(lr, lt)
+
+
+@pytest.mark.parametrize("m,f,k", [(256, 2048, 768), (37, 704, 256), (64, 3392, 1280)])
+def test_gemm_norm_swiglu_equals_unfused(m, f, k):
+    """The gate / up projection with the RMSNorm prologue and the SwiGLU epilogue against
+    mdl_add_rmsnorm + K5 + K3.  The fused rstd may differ from mdl_add_rmsnorm's in its last bit,
+    which can move the lo half of a split value by one ulp (hi + lo holds h to 2^-17 relative):
+    bound 3e-5 relative.  A missing rstd, bias or a wrong channel pairing is off by 1e-1."""
+    g = torch.Generator().manual_seed(m + f + k + 1)
+    x = (torch.randn(m, k, generator=g) * 1.5).to(DEV)
+    gamma = (1 + 0.1 * torch.randn(k, generator=g)).to(DEV)
+    wg = (torch.randn(f, k, generator=g) * 0.05).to(torch.bfloat16).to(DEV)
+    wu = (torch.randn(f, k, generator=g) * 0.05).to(torch.bfloat16).to(DEV)
+    bg = (0.1 * torch.randn(f, generator=g)).to(DEV)
+    bu = (0.1 * torch.randn(f, generator=g)).to(DEV)
+    w_il = K().tile_matrix(K().interleave_gate_up(wg, wu))
+    xs = torch.zeros(K().split_numel(m, k, True), device=DEV, dtype=torch.bfloat16)
+    rstd = torch.empty(m, device=DEV)
+    K().add_rmsnorm(x.clone(), None, None, gamma, 1e-5, xs, rstd, tiled=True)
+    xt = K().tile_f32(x)
+
+    def unsplit_tiled(h):
+        hb = h.view(-1)
+        r = torch.arange(K().tile_rows(m), device=DEV).view(-1, 1)
+        c = torch.arange(2 * f, device=DEV).view(1, -1)
+        off = (512 * ((r // 16) * (2 * f // 32) + c // 32) + 8 * (16 * ((c // 8) % 4) + r % 16)
+               + c % 8)
+        full = hb[off]
+        return full[:m, :f].float() + full[:m, f:].float()
+
+    for t in list(range(1, K().gemm_split_tiles() + 1)) + [0]:
+        ref = torch.zeros(K().split_numel(m, f, True), device=DEV, dtype=torch.bfloat16)
+        K().gemm_split_swiglu(xs, w_il, rstd, bg, bu, ref, m, f, k, tile=t)
+        got = torch.zeros_like(ref)
+        K().gemm_norm_swiglu(xt, gamma, 1e-5, w_il, bg, bu, got, m, f, k, tile=t)
+        torch.cuda.synchronize()
+        a, b = unsplit_tiled(got), unsplit_tiled(ref)
+        assert torch.allclose(a, b, rtol=3e-5, atol=1e-6), f"tile {t}"
+
+
+@pytest.mark.parametrize("m,n,k", [(256, 768, 768), (37, 256, 704), (64, 1280, 3392)])
+def test_gemm_split_residual(m, n, k):
+    """K5 with the residual epilogue: x (fp32 tile layout) += (hi + lo) @ W^T (+ bias) gives
+    exactly (x + K5's output) + bias, in place, for every block shape; rows past m untouched."""
+    g = torch.Generator().manual_seed(m + n + k + 2)
+    a = torch.randn(m, k, generator=g)
+    hi = a.to(torch.bfloat16)
+    lo = (a - hi.float()).to(torch.bfloat16)
+    at = K().tile_matrix(torch.cat([hi, lo], 1).to(DEV))
+    w = (torch.randn(n, k, generator=g) * 0.05).to(torch.bfloat16).to(DEV)
+    wt = K().tile_matrix(w)
+    x = torch.randn(m, n, generator=g).to(DEV)
+    bias = (0.1 * torch.randn(n, generator=g)).to(DEV)
+    for t in list(range(1, K().gemm_split_tiles() + 1)) + [0]:
+        for b in (bias, None):
+            out = torch.empty(m, n, device=DEV)
+            K().gemm_split(at, wt, out, k, a_tiled=True, w_tiled=True, tile=t)
+            want = x + out
+            if b is not None:
+                want = want + b
+            xt = K().tile_f32(x)
+            pad = xt.clone()
+            K().gemm_split_residual(at, wt, xt, b, m, n, k, tile=t)
+            torch.cuda.synchronize()
+            assert torch.equal(K().untile_f32(xt, m, n), want), f"tile {t}"
+            # padding rows of the last row block stay as they were
+            full = K().untile_f32(xt, K().tile_rows(m), n)
+            assert torch.equal(full[m:], K().untile_f32(pad, K().tile_rows(m), n)[m:])
