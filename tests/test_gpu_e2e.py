@@ -656,3 +656,43 @@ def test_packed_prefill_equals_padded(monkeypatch):
                 k0 = int(kv[r])
                 x, y = a[r, :, k0:S].float(), b[r, :, k0:S].float()
                 assert bool(((x - y).abs() <= 2 ** -7 * y.abs() + 1e-6).all())
+
+
+def test_decode_forms_agree(monkeypatch):
+    """The decode step on K5 with the norms, SwiGLU and residual adds fused (five launches per
+    layer, tiled x) against the separate-kernel form (hipBLASLt, add+RMSNorm, K3; row-major):
+    the same greedy tokens for a ragged batch whose size is not a multiple of 16 (the tile
+    layout's padding rows), and the logits of the first decode step equal to GEMM rounding
+    (generation replays a captured graph; the logits come from the host-launched step)."""
+    from mdlarc_scale_amd import create_model
+    from mdlarc_scale_amd import inference as inf
+    from mdlarc_scale_amd.transformer import MODEL_SIZES
+
+    torch.manual_seed(7)
+    m = create_model(**MODEL_SIZES["small"], dropout=0.0, max_seq_len=2048).to(DEV).eval()
+    rng = np.random.default_rng(77)
+    prompts = _random_prompts(rng, 9, 2, 2, 6) + _random_prompts(rng, 4, 1, 1, 3)
+    ids, pos, mask = _left_pad(prompts)
+    ids, pos, mask = ids.to(DEV), pos.to(DEV), mask.to(DEV)
+    B = ids.shape[0]
+    assert B % 16 != 0
+    ex = torch.arange(B, device=DEV)
+    out, logits = {}, {}
+    for tiled in (True, False):
+        monkeypatch.setattr(inf, "DECODE_TILED", tiled)
+        with torch.no_grad():
+            out[tiled] = inf.generate_output(m, ids, pos, ex, attention_mask=mask,
+                                             max_new_tokens=40, stop_on_end=False).cpu()
+            gen = inf.Generator(m)
+            W = gen.eng.packed(ids.device)
+            st = gen.prepare(ids, pos, ex, mask, ids.shape[1] + 4)
+            assert st.sc.tiled == tiled
+            gen.prefill(st, W, ids, pos)
+            gen.decode_layers(st, W, want_logits=True)
+            torch.cuda.synchronize()
+            logits[tiled] = st.logits.cpu()
+    err = (logits[True] - logits[False]).abs().max().item()
+    agree = (out[True] == out[False]).float().mean().item()
+    print(f"decode forms: first decode step logits max-abs {err:.3e}, token agreement {agree:.4f}")
+    assert err <= 1e-3
+    assert torch.equal(out[True], out[False])
