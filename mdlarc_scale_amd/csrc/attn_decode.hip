@@ -3,10 +3,13 @@
 // Split-K flash decoding.  Work item = (b*h, split): a 256-thread block attends over `split_len`
 // cache slots of one head; its 4 wavefronts take tiles of kT = 16 NB consecutive slots in turn
 // (NB = 2 or 4).  Per tile, on v_mfma_f32_16x16x32_bf16 (operand layouts in mfma.h):
-//   S^T = K q^T: the A operand is K itself -- lane (c, g) loads 16 bytes of slot row 16 nb + c at
-//     dims 32 kk + 8 g straight from HBM into registers, no staging needed; the B operand is q
-//     replicated over the 16 columns, so every lane ends up holding real scores (slots
-//     16 nb + 4 g + i) and the softmax needs no cross-lane gather beyond the 4-group max;
+//   S^T = K q^T: the A operand is K -- each wave loads its K tile with coalesced 16-byte loads
+//     (eight lanes per 128-byte slot row), stages it in its own LDS region and reads lane
+//     (c, g)'s 16 bytes of slot row 16 nb + c at dims 32 kk + 8 g back in the MFMA layout
+//     (loading that layout straight from HBM makes every load instruction touch 16 rows and
+//     measured 1-3% slower); the B operand is q replicated over the 16 columns, so every lane
+//     ends up holding real scores (slots 16 nb + 4 g + i) and the softmax needs no cross-lane
+//     gather beyond the 4-group max;
 //   O^T = V^T P^T: V is staged through the wave's own LDS tile (row-major, 144-byte rows) and read
 //     back transposed (ds_read_b64_tr_b16); P^T comes from the score accumulators, in the key
 //     order the transposing reads produce; the row sum is one more MFMA against ones, so it sums
@@ -23,6 +26,7 @@
 // starting at kv_start[b]; such rows skip the per-slot mask reads.
 #include "mfma.h"
 #include "rope.h"
+
 
 namespace mdl {
 
@@ -92,6 +96,7 @@ __global__ __launch_bounds__(256) void attn_decode_kernel(
   __shared__ __attribute__((aligned(16))) uint16_t q_lds[kHeadDim];
   constexpr int kT = 16 * NB;   // slots per wave tile
   __shared__ __attribute__((aligned(16))) uint16_t Vs[4][kT * kVld];
+  __shared__ __attribute__((aligned(16))) uint16_t Ks[4][kT * kVld];
 
   if (FUSED) {
     if (wave == 0) {
@@ -146,17 +151,15 @@ __global__ __launch_bounds__(256) void attn_decode_kernel(
     const bool dense = row_holes && row_holes[b] == 0;
     const uint8_t* pm = (pmask && !dense) ? pmask + static_cast<int64_t>(b) * plen : nullptr;
     uint16_t* Vw = Vs[wave];
+    uint16_t* Kw = Ks[wave];
 
     for (int base = lo + wave * kT; base < hi; base += 4 * kT) {
-      uint4 kf[NB][2], vr[2 * NB];
+      uint4 kf[NB][2], kr[2 * NB], vr[2 * NB];
 #pragma unroll
-      for (int nb = 0; nb < NB; ++nb) {
-        const int key = base + 16 * nb + c16;
-#pragma unroll
-        for (int kk = 0; kk < 2; ++kk)
-          kf[nb][kk] = key < hi ? load_nt16(K + static_cast<int64_t>(key) * kHeadDim + 32 * kk +
-                                            8 * g)
-                                : make_uint4(0, 0, 0, 0);
+      for (int r = 0; r < 2 * NB; ++r) {
+        const int key = base + 8 * r + (lane >> 3);
+        kr[r] = key < hi ? load_nt16(K + static_cast<int64_t>(key) * kHeadDim + 8 * (lane & 7))
+                         : make_uint4(0, 0, 0, 0);
       }
 #pragma unroll
       for (int r = 0; r < 2 * NB; ++r) {
@@ -164,6 +167,22 @@ __global__ __launch_bounds__(256) void attn_decode_kernel(
         vr[r] = key < hi ? load_nt16(V + static_cast<int64_t>(key) * kHeadDim + 8 * (lane & 7))
                          : make_uint4(0, 0, 0, 0);
       }
+      // the K tile through this wave's LDS region, read back in the MFMA A layout (same
+      // program-order hand-over as the V tile below; 144-byte rows keep the 16-byte reads of a
+      // lane group on distinct banks)
+      __builtin_amdgcn_fence(__ATOMIC_ACQ_REL, "wavefront");
+      __builtin_amdgcn_wave_barrier();
+#pragma unroll
+      for (int r = 0; r < 2 * NB; ++r)
+        *reinterpret_cast<uint4*>(Kw + (8 * r + (lane >> 3)) * kVld + 8 * (lane & 7)) = kr[r];
+      __builtin_amdgcn_fence(__ATOMIC_ACQ_REL, "wavefront");
+      __builtin_amdgcn_wave_barrier();
+#pragma unroll
+      for (int nb = 0; nb < NB; ++nb)
+#pragma unroll
+        for (int kk = 0; kk < 2; ++kk)
+          kf[nb][kk] = *reinterpret_cast<const uint4*>(Kw + (16 * nb + c16) * kVld + 32 * kk +
+                                                       8 * g);
       f32x4_t sc[NB];
 #pragma unroll
       for (int nb = 0; nb < NB; ++nb) {

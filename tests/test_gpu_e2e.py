@@ -666,6 +666,7 @@ def test_decode_forms_agree(monkeypatch):
     (generation replays a captured graph; the logits come from the host-launched step)."""
     from mdlarc_scale_amd import create_model
     from mdlarc_scale_amd import inference as inf
+    from mdlarc_scale_amd import kernels as K
     from mdlarc_scale_amd.transformer import MODEL_SIZES
 
     torch.manual_seed(7)
@@ -688,6 +689,8 @@ def test_decode_forms_agree(monkeypatch):
             st = gen.prepare(ids, pos, ex, mask, ids.shape[1] + 4)
             assert st.sc.tiled == tiled
             gen.prefill(st, W, ids, pos)
+            # the host-launched step: position of the prefill's token, then the layers
+            K.grid_step(st.tok, st.gx, st.gy, st.gio, st.pos, st.counters)
             gen.decode_layers(st, W, want_logits=True)
             torch.cuda.synchronize()
             logits[tiled] = st.logits.cpu()
