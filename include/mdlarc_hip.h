@@ -126,7 +126,8 @@ int mdl_decode_embed(const int64_t* token, const int64_t* example_ids, const voi
  *   x[m]    += delta[m] (+ bias)           delta fp32 [rows, d] (may be NULL), bias fp32 [d] or NULL
  *   rstd[m]  = 1 / sqrt(mean(x[m]^2) + eps)
  *   xs[m]    = split(x[m] * gamma)         bf16 [rows, 2d] (skipped when xs_out is NULL), in
- *                                          xs_layout as for mdl_embed_rmsnorm
+ *                                          xs_layout: MDL_LAYOUT_ROWS, or the bf16 tile layout
+ *                                          (d a multiple of 16); x itself is row-major here
  */
 int mdl_add_rmsnorm(float* x, const float* delta, const float* bias, int rows, int d,
                     const float* gamma, float eps, uint16_t* xs_out, float* rstd_out,
