@@ -22,7 +22,8 @@
 // model's projections, each waiting on a K loop of dependent loads.  Here:
 //   - every weight fragment is loaded once and feeds two MFMAs (the hi and the lo rows);
 //   - the 8 waves of a block split K and meet once, in LDS, at the end: a wave has 1-14 k-steps
-//     of 32 and issues the loads of 4 of them before its first MFMA;
+//     of 32 and issues the loads of 4 of them (3 in the two largest A_NORM tiles) before its
+//     first MFMA;
 //   - the row tiles sharing one weight tile run on one XCD (block i runs on XCD i mod 8), so the
 //     weight tile comes from HBM once and from that XCD's L2 after that;
 //   - with tiled operands each wave load is one contiguous kilobyte.  A row-major operand
