@@ -900,7 +900,7 @@ def test_capi_rejects_bad_arguments_before_launch():
 @pytest.mark.gpu
 @pytest.mark.parametrize("m,n,k", [(256, 2304, 768), (256, 768, 2048), (128, 5504, 1024),
                                    (64, 1280, 3392), (3, 80, 64), (17, 1408, 704),
-                                   (100, 256, 96)])
+                                   (100, 256, 96), (1000, 768, 256), (777, 2304, 768)])
 def test_gemm_split(m, n, k):
     """K5, every compiled block shape and the automatic choice, against an fp64 CPU product of
     the same bf16 operands: (hi + lo) @ w^T to fp32 accumulation error (bound: 1e-5 of the sum
