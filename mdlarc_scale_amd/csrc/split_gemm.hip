@@ -418,7 +418,7 @@ extern "C" int mdl_gemm_split_swiglu(const uint16_t* a, const uint16_t* w_gu, co
                                      uint16_t* h_out, int m, int d_ff, int k, int tile,
                                      void* stream) {
   if (!a || !w_gu || !h_out) return MDL_ERR_NULL;
-  if (d_ff <= 0 || d_ff % 16 != 0 || !decode_shape_ok(m, 2 * d_ff, k, tile))
+  if (d_ff <= 0 || d_ff % 16 != 0 || d_ff > (1 << 29) || !decode_shape_ok(m, 2 * d_ff, k, tile))
     return MDL_ERR_SHAPE;
   if (!aligned16(a) || !aligned16(w_gu) || !aligned8(h_out) ||
       (bias_gate && !aligned16(bias_gate)) || (bias_up && !aligned16(bias_up)))
@@ -465,7 +465,7 @@ extern "C" int mdl_gemm_norm_swiglu(const float* x, const float* gamma, float ep
                                     const float* bias_up, uint16_t* h_out, int m, int d_ff, int k,
                                     int tile, void* stream) {
   if (!x || !gamma || !w_gu || !h_out) return MDL_ERR_NULL;
-  if (d_ff <= 0 || d_ff % 16 != 0 || !decode_shape_ok(m, 2 * d_ff, k, tile))
+  if (d_ff <= 0 || d_ff % 16 != 0 || d_ff > (1 << 29) || !decode_shape_ok(m, 2 * d_ff, k, tile))
     return MDL_ERR_SHAPE;
   if (!aligned16(x) || !aligned16(gamma) || !aligned16(w_gu) || !aligned8(h_out) ||
       (bias_gate && !aligned16(bias_gate)) || (bias_up && !aligned16(bias_up)))

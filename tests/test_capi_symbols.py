@@ -68,6 +68,11 @@ def test_argument_errors_are_reported_before_any_launch():
     assert L.mdl_gemm_norm(None, fake, 1e-5, fake, fake, 32, None, 4, 32, 32, 0, None) == -1
     assert L.mdl_gemm_norm_swiglu(fake, fake, 1e-5, fake, None, None, fake, 4, 24, 32, 0,
                                   None) == -3
+    # d_ff above 2^29 is refused before 2 d_ff can overflow
+    assert L.mdl_gemm_norm_swiglu(fake, fake, 1e-5, fake, None, None, fake, 4, 1 << 30, 32, 0,
+                                  None) == -3
+    assert L.mdl_gemm_split_swiglu(fake, fake, None, None, None, fake, 4, 1 << 30, 32, 0,
+                                   None) == -3
     assert L.mdl_gemm_split_residual(fake, fake, fake, None, 4, 48, 32, 0, None) == -3
     assert L.mdl_gemm_split_residual(fake, fake, fake + 4, None, 4, 64, 32, 0, None) == -2
     assert L.mdl_gemm_split_tiles() >= 1
