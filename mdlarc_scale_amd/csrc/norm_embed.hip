@@ -55,39 +55,48 @@ __device__ __forceinline__ void load_gamma(const float* gamma, int lane, int d, 
   }
 }
 
-// rstd of the row held in v (stored when rstd_out is not NULL), then x (fp32) and
-// split(x * gamma) stores (non-temporal if NT) into row m of x ([rows, d]: row-major, or the
-// fp32 tile layout when `x_tiled`) and xs ([rows, 2d]: row-major, or MFMA tiles when
-// `tiled`).
+// x (fp32) and split(x * gamma) stores (non-temporal if NT) of the row held in v into row m of
+// x ([rows, d]: row-major, or the fp32 tile layout when `x_tiled`) and xs ([rows, 2d]:
+// row-major, or MFMA tiles when `tiled`), then the row's rstd (stored when rstd_out is not
+// NULL).
 template <int NC, bool TAIL, bool HAS_XS, bool NT>
 __device__ __forceinline__ void finish_row(int lane, int d, float eps, const float (*v)[4],
                                            const float (*g)[4], float ss, float* x, int x_tiled,
                                            uint16_t* xs, int64_t m, int tiled,
                                            float* rstd_out) {
-  ss = wave_sum(ss);
-  const float r = rsqrtf(ss / static_cast<float>(d) + eps);
+  // Chunk i of the lane covers columns 4 lane + 256 i: 8 whole 32-column blocks further on, so
+  // in either layout its offsets are chunk 0's plus i times one stride (row-major 256 elements,
+  // tiles 8 blocks of 512); the layout is chosen once per row, not per store.
+  const int e0 = 4 * lane;
+  float* xr = x + (x_tiled ? tile_off32(m, e0, d) : m * d + e0);
+  const int x_step = x_tiled ? 4096 : 256;
+  uint16_t* hr = nullptr;
+  int64_t lo_off = 0;
+  int xs_step = 0;
+  if (HAS_XS) {
+    hr = xs + (tiled ? tile_off(m, e0, 2 * d) : m * 2 * d + e0);
+    lo_off = tiled ? tile_off(m, d + e0, 2 * d) - tile_off(m, e0, 2 * d) : d;
+    xs_step = tiled ? 4096 : 256;
+  }
 #pragma unroll
   for (int i = 0; i < NC; ++i) {
-    const int e = 4 * (lane + 64 * i);
+    const int e = e0 + 256 * i;
     if (in_row<NC, TAIL>(i, e, d)) {
-      st_f4<NT>(x + (x_tiled ? tile_off32(m, e, d) : m * d + e),
-                make_float4(v[i][0], v[i][1], v[i][2], v[i][3]));
+      st_f4<NT>(xr + x_step * i, make_float4(v[i][0], v[i][1], v[i][2], v[i][3]));
       if (HAS_XS) {
         const float t[4] = {v[i][0] * g[i][0], v[i][1] * g[i][1], v[i][2] * g[i][2],
                             v[i][3] * g[i][3]};
         uint2 hi, lo;
         split4(t, hi, lo);
-        if (tiled) {
-          st_u2<NT>(xs + tile_off(m, e, 2 * d), hi);
-          st_u2<NT>(xs + tile_off(m, d + e, 2 * d), lo);
-        } else {
-          st_u2<NT>(xs + m * 2 * d + e, hi);
-          st_u2<NT>(xs + m * 2 * d + d + e, lo);
-        }
+        st_u2<NT>(hr + xs_step * i, hi);
+        st_u2<NT>(hr + xs_step * i + lo_off, lo);
       }
     }
   }
-  if (lane == 0 && rstd_out) *rstd_out = r;
+  // the row's reduction comes after the stores in program order: the layout choice above
+  // splits the code into blocks, and stores issued first overlap the reduction's latency
+  ss = wave_sum(ss);
+  if (lane == 0 && rstd_out) *rstd_out = rsqrtf(ss / static_cast<float>(d) + eps);
 }
 
 // x = tok[t] (+ ex[e]) for one row into v; returns the row's partial sum of squares.
