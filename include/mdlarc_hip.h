@@ -49,6 +49,10 @@ extern "C" {
 #define MDL_ERR_CACHE (-5)         /* slot range outside the cache */
 #define MDL_ERR_WORKSPACE (-6)     /* workspace too small */
 #define MDL_ERR_DTYPE (-7)         /* unsupported dtype code */
+#define MDL_ERR_SCRATCH (-8)       /* work exceeds the library's static scratch buffer */
+
+/* Size of the static device scratch buffer of mdl_attn_decode_rope_noalloc (per GPU). */
+#define MDL_DECODE_SCRATCH_BYTES (4 << 20)
 
 #define MDL_DTYPE_F32 0
 #define MDL_DTYPE_BF16 1
@@ -355,6 +359,30 @@ int mdl_attn_decode_rope(const float* qkv, int64_t qkv_ld, const float* rstd, co
                          const int32_t* row_order, int seq_pos, const int32_t* seq_dev,
                          float* workspace, int64_t workspace_bytes, int split_len, uint16_t* out,
                          int out_layout, void* stream);
+
+/*
+ * mdl_attn_decode_rope without the workspace argument: the split partials go to a static
+ * device array of MDL_DECODE_SCRATCH_BYTES (4 MiB) per GPU instead, so the call allocates
+ * nothing, on the host or the device, and asks its caller for no buffer beyond the inputs and
+ * outputs.  No counterpart in the reference: it is for callers that cannot allocate (code under
+ * HIP graph capture, tight serving loops, harnesses that forbid hipMalloc).
+ * Work needing more than MDL_DECODE_SCRATCH_BYTES (mdl_attn_decode_workspace_bytes of the same
+ * arguments) returns MDL_ERR_SCRATCH before any launch.  The device address of the array is
+ * looked up (hipGetSymbolAddress) on the first call on each device; make that first call
+ * outside graph capture.  Every call on one GPU shares its array: calls that overlap in time on
+ * one GPU (two streams, two threads) race and must be ordered by the caller.  Nothing in the
+ * array needs clearing between calls: each split writes its whole partial before it is read.
+ * Other arguments and results as mdl_attn_decode_rope.
+ */
+int mdl_attn_decode_rope_noalloc(const float* qkv, int64_t qkv_ld, const float* rstd,
+                                 const int64_t* pos, const float* rope_tab, int max_x, int max_y,
+                                 int max_z, int px, int py, int pz, float q_scale,
+                                 uint16_t* k_cache, uint16_t* v_cache, int batch, int n_heads,
+                                 int head_dim, int cache_slots, const uint8_t* prompt_mask,
+                                 int prompt_len, const uint8_t* row_holes,
+                                 const int32_t* kv_start, const int32_t* row_order, int seq_pos,
+                                 const int32_t* seq_dev, int split_len, uint16_t* out,
+                                 int out_layout, void* stream);
 
 /*
  * Final RMSNorm + LM head + greedy argmax.

@@ -24,6 +24,8 @@
 // prompt_mask[b, j]), the decode mask of the reference (prompt mask, then every generated slot).
 // row_holes[b] == 0 (from mdl_grid_init) says the prompt mask of row b is one contiguous run
 // starting at kv_start[b]; such rows skip the per-slot mask reads.
+#include <mutex>
+
 #include "mfma.h"
 #include "rope.h"
 
@@ -411,4 +413,60 @@ extern "C" int mdl_attn_decode_rope(const float* qkv, int64_t qkv_ld, const floa
                      cache_slots, prompt_mask, prompt_len, row_holes, kv_start, row_order,
                      seq_pos, seq_dev, workspace, workspace_bytes, split_len, out, out_layout,
                      stream);
+}
+
+// ------------------------------------------------------------ no-allocation variant
+//
+// The split partials of mdl_attn_decode_rope_noalloc live in `scratch`, one fixed array per
+// device (the code object's own copy on each GPU it is loaded on, held until the process ends).
+// Every split block writes all kPart floats of its partial before the combine kernel reads them,
+// so nothing in it has to start at zero.  Host code never passes `scratch` itself (in host code
+// the name is only a stand-in, not a device address): the device address comes from
+// hipGetSymbolAddress, once per device, with that device current.
+
+static __device__ __align__(256) float scratch[MDL_DECODE_SCRATCH_BYTES / sizeof(float)];
+
+namespace mdl {
+
+constexpr int kMaxDevices = 256;
+
+// Device address of `scratch` on the current device, looked up on the first call per device.
+static int scratch_for_current_device(float** ptr) {
+  static std::mutex mu;
+  static float* addr[kMaxDevices] = {};
+  int dev = -1;
+  hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess) return static_cast<int>(e);
+  if (dev < 0 || dev >= kMaxDevices) return MDL_ERR_SHAPE;
+  std::lock_guard<std::mutex> lock(mu);
+  if (!addr[dev]) {
+    void* p = nullptr;
+    e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    if (e != hipSuccess) return static_cast<int>(e);
+    addr[dev] = static_cast<float*>(p);
+  }
+  *ptr = addr[dev];
+  return MDL_OK;
+}
+
+}  // namespace mdl
+
+extern "C" int mdl_attn_decode_rope_noalloc(
+    const float* qkv, int64_t qkv_ld, const float* rstd, const int64_t* pos,
+    const float* rope_tab, int max_x, int max_y, int max_z, int px, int py, int pz,
+    float q_scale, uint16_t* k_cache, uint16_t* v_cache, int batch, int n_heads, int head_dim,
+    int cache_slots, const uint8_t* prompt_mask, int prompt_len, const uint8_t* row_holes,
+    const int32_t* kv_start, const int32_t* row_order, int seq_pos, const int32_t* seq_dev,
+    int split_len, uint16_t* out, int out_layout, void* stream) {
+  const int64_t need = mdl_attn_decode_workspace_bytes(batch, n_heads, cache_slots, split_len);
+  if (need > MDL_DECODE_SCRATCH_BYTES) return MDL_ERR_SCRATCH;
+  float* ws = nullptr;
+  if (need > 0) {
+    const int rc = scratch_for_current_device(&ws);
+    if (rc != MDL_OK) return rc;
+  }
+  return mdl_attn_decode_rope(qkv, qkv_ld, rstd, pos, rope_tab, max_x, max_y, max_z, px, py, pz,
+                              q_scale, k_cache, v_cache, batch, n_heads, head_dim, cache_slots,
+                              prompt_mask, prompt_len, row_holes, kv_start, row_order, seq_pos,
+                              seq_dev, ws, need, split_len, out, out_layout, stream);
 }

@@ -505,6 +505,47 @@ def attn_decode_rope(qkv: torch.Tensor, rstd: torch.Tensor, pos: torch.Tensor,
         "mdl_attn_decode_rope")
 
 
+DECODE_SCRATCH_BYTES = 4 << 20   # MDL_DECODE_SCRATCH_BYTES
+
+
+def attn_decode_rope_noalloc(qkv: torch.Tensor, rstd: torch.Tensor, pos: torch.Tensor,
+                             rope_tab: torch.Tensor,
+                             rope_geom: tuple[int, int, int, int, int, int], q_scale: float,
+                             k_cache: torch.Tensor, v_cache: torch.Tensor, batch: int,
+                             n_heads: int, prompt_mask: torch.Tensor | None, prompt_len: int,
+                             kv_start: torch.Tensor | None, seq_pos: int,
+                             seq_dev: torch.Tensor | None, split_len: int, out: torch.Tensor,
+                             row_holes: torch.Tensor | None = None,
+                             row_order: torch.Tensor | None = None, tiled: bool = False) -> None:
+    """attn_decode_rope with its split partials in the library's static per-GPU scratch buffer
+    (DECODE_SCRATCH_BYTES) instead of a workspace tensor: allocates nothing.  Calls on one GPU
+    share that buffer, so calls that overlap in time on one GPU race."""
+    d = n_heads * HEAD_DIM
+    _need(qkv, "qkv", F32, batch * 3 * d)
+    if qkv.dim() != 2 or qkv.shape[1] != 3 * d:
+        raise ValueError(f"qkv must be [batch, {3 * d}]")
+    _need(rstd, "rstd", F32, batch)
+    _need(pos, "pos", I64, batch * 3)
+    _need(rope_tab, "rope_tab", F32)
+    _need(out, "out", BF16, split_numel(batch, d, tiled))
+    for name, c in (("k_cache", k_cache), ("v_cache", v_cache)):
+        _need(c, name, BF16)
+        if c.dim() != 4 or c.shape[0] != batch or c.shape[1] != n_heads or c.shape[3] != 64:
+            raise ValueError(f"{name} must be [batch, n_heads, slots, 64]")
+    _need(prompt_mask, "prompt_mask", U8, batch * prompt_len, optional=True)
+    _need(row_holes, "row_holes", U8, batch, optional=True)
+    _need(kv_start, "kv_start", I32, batch, optional=True)
+    _need(row_order, "row_order", I32, batch, optional=True)
+    _need(seq_dev, "seq_dev", I32, 1, optional=True)
+    mx, my, mz, px, py, pz = rope_geom
+    _lib.check(_lib.lib().mdl_attn_decode_rope_noalloc(
+        _p(qkv), qkv.shape[1], _p(rstd), _p(pos), _p(rope_tab), mx, my, mz, px, py, pz, q_scale,
+        _p(k_cache), _p(v_cache), batch, n_heads, HEAD_DIM, k_cache.shape[2], _p(prompt_mask),
+        prompt_len, _p(row_holes), _p(kv_start), _p(row_order), seq_pos, _p(seq_dev),
+        split_len, _p(out), _layout(tiled), _stream()),
+        "mdl_attn_decode_rope_noalloc")
+
+
 class HeadConstraints:
     """Device form of DecodingConstraints for the head kernels (``mdl_logit_constraints``):
     keeps the tensors it points at alive for as long as the launches (or a captured graph)

@@ -55,6 +55,13 @@ def test_argument_errors_are_reported_before_any_launch():
                                 0.125, fake, fake, fake, 4, 1, None, None) == -5
     assert L.mdl_attn_decode(fake, fake, fake, 1, 1, 64, 1024, None, 0, None, None, None, 5,
                              None, None, 0, 128, fake, 0, None) == -6
+    # the no-allocation decode refuses work beyond its 4 MiB static scratch before touching a
+    # device: 64 rows x 20 heads x 52 splits x 66 floats needs 17.6 MB
+    assert L.mdl_attn_decode_workspace_bytes(64, 20, 6656, 128) > 4 << 20
+    assert L.mdl_attn_decode_rope_noalloc(fake, 3840, fake, fake, fake, 32, 32, 8, 10, 10, 12,
+                                          0.125, fake, fake, 64, 20, 64, 6656, None, 0, None,
+                                          None, None, 5, None, 128, fake, 0, None) == -8
+    assert b"scratch" in L.mdl_error_string(-8)
     # K5: k a multiple of 32, n of 4, layout codes 0 / 1, row-major lda >= 2k
     assert L.mdl_gemm_split(fake, 64, 0, fake, 32, 0, fake, 8, 4, 8, 48, 0, None) == -3
     assert L.mdl_gemm_split(fake, 64, 0, fake, 32, 0, fake, 8, 4, 6, 32, 0, None) == -3
