@@ -17,6 +17,8 @@ Contents
                     ``GridState`` and ``derive_initial_state``.
 ``data_format``     token format, 3D positions, dihedral transforms and colour permutations in
                     plain Python / numpy.
+``augment``         the augmentation caller ``predict_with_augmentations`` (batched chunk loop and
+                    sequential loop, greedy) on ``reference_path``.
 
 How each function is pinned (the tests that would catch a dropped term, wrong sign or index)
 ------------------------------------------------------------------------------------------------
@@ -34,6 +36,14 @@ How each function is pinned (the tests that would catch a dropped term, wrong si
                          golden vectors written by ``tests/golden/make_golden.py`` from the
                          reference itself (left-padded ragged batch, per-step logits, decode
                          positions, stop-on-END), plus incremental == teacher-forced forward.
+* ``apply_logit_constraints`` / ``generate_output(constraints=...)``
+                         bit-exact against the reference's own ``_apply_logit_constraints`` on
+                         nine cases covering every branch (tests/golden/constraints.npz, written
+                         by make_golden.py), and a planted mistake that the fixture catches.
+* ``augment.predict_with_augmentations``
+                         token for token against the reference's own runs
+                         (tests/golden/augment_micro.npz): chunk sizes 16 and 5, the sequential
+                         loop, constraints on and off, two micro models; decoded grids too.
 * ``GridState`` / ``derive_initial_state``
                          golden traces from the reference, and equality with
                          ``data_format.compute_positions_3d`` on whole token streams.

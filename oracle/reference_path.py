@@ -293,6 +293,75 @@ def derive_initial_state(ids: torch.Tensor, pos: torch.Tensor, mask: torch.Tenso
 
 
 # --------------------------------------------------------------------------------------------
+# decoding constraints
+# --------------------------------------------------------------------------------------------
+
+@dataclass(frozen=True)
+class OracleConstraints:
+    """Fields of ``DecodingConstraints`` (src/inference.py:36-43), same defaults."""
+
+    palette_mask: torch.Tensor | None = None     # bool [B or 1, 10]
+    target_shape: torch.Tensor | None = None     # long [B or 1, 2]; -1 = no shape
+    palette_penalty: float = 2.0
+    shape_penalty: float = 2.0
+    disallow_tokens: tuple[int, ...] = (START, IO_SEP)
+
+
+def _rows_of(t: torch.Tensor, batch: int, width: int) -> torch.Tensor | None:
+    """A constraint tensor as [batch, width]: reshaped to 2D, a single row broadcast, any other
+    batch mismatch -> None (the constraint is then skipped) (src/inference.py:305-311, :316-322)."""
+    if t.dim() != 2:
+        t = t.reshape(-1, t.shape[-1] if width == 10 else 2)
+    if t.shape[0] != batch:
+        return t.expand(batch, -1) if t.shape[0] == 1 else None
+    return t
+
+
+def apply_logit_constraints(logits: torch.Tensor, gx: torch.Tensor, gy: torch.Tensor,
+                            c: OracleConstraints | None) -> torch.Tensor:
+    """``_apply_logit_constraints`` (src/inference.py:285-364) on logits [B, V] (the reference's
+    [B, 1, V] without the middle axis), in place; (gx, gy) is the grid state after the current
+    token.  Order and rounding as the reference: disallowed tokens -> -inf (:296-297); colours
+    0-9 minus palette_penalty * (not allowed) (:299-312); with a target shape (h, w >= 0):
+    colours minus shape_penalty * (x >= w) (:347-350), NEWLINE minus shape_penalty * (x < w)
+    (:351-353), then colours and NEWLINE each minus shape_penalty * (y >= h) (:354-357), every
+    penalty a separate fp32 subtraction of (indicator * penalty).  A grid-state batch that
+    neither equals nor broadcasts the shape batch ends the rule early (:337-343)."""
+    if c is None:
+        return logits
+    B = logits.shape[0]
+    for tok in c.disallow_tokens:
+        logits[:, tok] = float("-inf")
+    if c.palette_mask is not None:
+        pm = _rows_of(c.palette_mask, B, 10)
+        if pm is not None:
+            logits[:, :10] = logits[:, :10] - (~pm).to(logits.dtype) * c.palette_penalty
+    if c.target_shape is not None:
+        ts = _rows_of(c.target_shape, B, 2)
+        if ts is not None:
+            th, tw = ts[:, 0].contiguous().view(-1), ts[:, 1].contiguous().view(-1)
+            has = (th >= 0) & (tw >= 0)
+            if bool(has.any()):
+                x, y = gx.contiguous().view(-1), gy.contiguous().view(-1)
+                if x.shape[0] != tw.shape[0]:
+                    if tw.shape[0] != 1:
+                        return logits
+                    th, tw, has = th.expand(x.shape[0]), tw.expand(x.shape[0]), has.expand(
+                        x.shape[0])
+                full, open_, past = has & (x >= tw), has & (x < tw), has & (y >= th)
+                pen = c.shape_penalty
+                if bool(full.any()):
+                    logits[:, :10] = logits[:, :10] - full.to(logits.dtype)[:, None] * pen
+                if bool(open_.any()):
+                    logits[:, NEWLINE] = logits[:, NEWLINE] - open_.to(logits.dtype) * pen
+                if bool(past.any()):
+                    p = past.to(logits.dtype) * pen
+                    logits[:, :10] = logits[:, :10] - p[:, None]
+                    logits[:, NEWLINE] = logits[:, NEWLINE] - p
+    return logits
+
+
+# --------------------------------------------------------------------------------------------
 # batched greedy generation
 # --------------------------------------------------------------------------------------------
 
@@ -301,19 +370,23 @@ class GenerateTrace:
     tokens: torch.Tensor                 # [B, S + g]
     step_logits: list[torch.Tensor]      # g entries of [B, V]; entry 0 from the prefill
     step_positions: list[torch.Tensor]   # g-1 entries of [B, 3] fed to the decode steps
+    raw_logits: list[torch.Tensor] = None  # g entries of [B, V] before the constraints
 
 
 def generate_output(model: OracleModel, ids: torch.Tensor, pos: torch.Tensor,
                     ex_ids: torch.Tensor | None = None,
                     attention_mask: torch.Tensor | None = None, max_new_tokens: int = 900,
-                    stop_on_end: bool = True) -> GenerateTrace:
-    """Greedy ``generate_output`` (src/inference.py:487-628), temperature <= 0, no constraints.
+                    stop_on_end: bool = True,
+                    constraints: OracleConstraints | None = None) -> GenerateTrace:
+    """Greedy ``generate_output`` (src/inference.py:487-628), temperature <= 0.
 
     Bug-compatible with the reference: example ids default to zeros (:524-525); the total length
     is capped at ``max_seq_len`` and an over-long prompt is returned unchanged (:534-537); the
     first token and the initial grid state come from index ``lengths-1``; rows that emitted END
     keep generating; the loop breaks before a step once every row has emitted END (:593-595);
-    argmax takes the first index on ties (:573-574, :610-611).
+    argmax takes the first index on ties (:573-574, :610-611).  ``constraints`` are applied
+    before every argmax (:572, :609), with the grid state after the prompt for the first token
+    and after the previous token for the others; ``step_logits`` holds the constrained logits.
     """
     B, S = ids.shape
     if ex_ids is None:
@@ -323,7 +396,7 @@ def generate_output(model: OracleModel, ids: torch.Tensor, pos: torch.Tensor,
     total = min(S + max_new_tokens, model.cfg.max_seq_len)
     max_new = total - S
     if max_new <= 0:
-        return GenerateTrace(ids.clone(), [], [])
+        return GenerateTrace(ids.clone(), [], [], [])
     cache = model.new_cache(B, total)
     gx, gy, gio = derive_initial_state(ids, pos, prompt_mask)
     grid = GridState(gx, gy, gio)
@@ -331,6 +404,8 @@ def generate_output(model: OracleModel, ids: torch.Tensor, pos: torch.Tensor,
     full_mask[:, :S] = prompt_mask
 
     logits = model.prefill(ids, pos, ex_ids, cache, prompt_mask)
+    raw = [logits.clone()]
+    logits = apply_logit_constraints(logits, grid.x, grid.y, constraints)
     nxt = logits.argmax(-1)
     out, lg, ps = [ids, nxt[:, None]], [logits], []
     finished = (nxt == END) if stop_on_end else torch.zeros(B, dtype=torch.bool)
@@ -342,10 +417,12 @@ def generate_output(model: OracleModel, ids: torch.Tensor, pos: torch.Tensor,
         ps.append(p)
         seq = S + step - 1
         logits = model.decode_step(nxt, p, ex_ids, cache, seq, full_mask[:, :seq + 1])
+        raw.append(logits.clone())
+        logits = apply_logit_constraints(logits, grid.x, grid.y, constraints)
         nxt = logits.argmax(-1)
         lg.append(logits)
         if stop_on_end:
             finished = finished | (nxt == END)
         out.append(nxt[:, None])
         full_mask[:, S + step] = True
-    return GenerateTrace(torch.cat(out, 1), lg, ps)
+    return GenerateTrace(torch.cat(out, 1), lg, ps, raw)

@@ -11,7 +11,15 @@ outputs of the functions whose behaviour no closed form pins:
   src/inference.py:127-168), and the stop-on-END break (src/inference.py:589-595);
 * ``TinyTransformer.forward`` (src/transformer.py:562-599) logits on the same padded batch;
 * ``GridStateUpdater`` traces and ``_derive_initial_state_from_prompt`` on ragged masks;
-* ``generate_color_permutations`` (src/data.py:257-278) under this container's numpy.
+* ``generate_color_permutations`` (src/data.py:257-278) under this container's numpy;
+* ``_apply_logit_constraints`` (src/inference.py:285-364) on random logits, grid states, palettes
+  and target shapes covering every branch (broadcast rows, mismatched batches, rows without a
+  shape, boundary x == w / y == h) -> ``constraints.npz``;
+* ``predict_with_augmentations`` (src/inference.py:697-1003) on a small task with the micro model
+  (weights rounded to bf16 so a bf16-weight GPU path runs the very same weights): the batched
+  chunk loop at chunk sizes 16 and 5 and the sequential loop, constraints on and off, recording
+  per variant the raw token stream the prediction is decoded from, the generated tokens and the
+  top-2 gap of the constrained logits at every step -> ``augment_micro.npz``.
 
 Weights are NOT the reference's random init: they are drawn here from a seeded numpy generator
 (perturbed norm gains and biases, so those code paths are exercised) and loaded into the
@@ -206,6 +214,9 @@ def main() -> None:
         init=np.stack([ix.numpy(), iy.numpy(), iio.numpy().astype(np.int64)], 1),
     )
 
+    _constraint_cases(rinf)
+    _augment_runs(rinf, cfg, TinyTransformer)
+
     np.savez_compressed(
         os.path.join(OUT, "color_perms.npz"),
         p8_42=rdata.generate_color_permutations(8, 42),
@@ -213,6 +224,166 @@ def main() -> None:
         p8_7=rdata.generate_color_permutations(8, 7),
     )
     print("wrote fixtures to", OUT)
+
+
+def _constraint_cases(rinf) -> None:
+    """Inputs and outputs of the reference's ``_apply_logit_constraints``."""
+    import torch
+
+    crng = np.random.default_rng(4242)
+    cases = []
+
+    def add(B, pal, shape, pp, sp, disallow=(10, 12), grid_b=None, x=None, y=None):
+        gb = B if grid_b is None else grid_b
+        lg = (3.0 * crng.standard_normal((B, 1, 14))).astype(np.float32)
+        gx = crng.integers(0, 31, size=gb) if x is None else np.asarray(x)
+        gy = crng.integers(0, 30, size=gb) if y is None else np.asarray(y)
+        cases.append(dict(B=B, logits=lg, gx=gx.astype(np.int64), gy=gy.astype(np.int64),
+                          pal=pal, shape=shape, pp=pp, sp=sp, disallow=tuple(disallow)))
+
+    B = 12
+    pal = crng.random((B, 10)) < 0.6
+    pal[3] = True                                            # a row with every colour allowed
+    shp = np.stack([crng.integers(1, 31, B), crng.integers(1, 31, B)], 1)
+    shp[[2, 7]] = -1                                         # rows without a target shape
+    shp[5, 0] = -1                                           # h < 0 alone also means "no shape"
+    x = crng.integers(0, 31, B)
+    y = crng.integers(0, 30, B)
+    x[0], y[0] = shp[0, 1], shp[0, 0]                        # boundary: x == w, y == h
+    x[1], y[1] = shp[1, 1] - 1, shp[1, 0] - 1                # just inside
+    add(B, pal, shp, 2.0, 2.0, x=x, y=y)
+    add(8, crng.random((1, 10)) < 0.5, np.array([[4, 6]]), 0.5, 3.25)          # 1-row broadcast
+    add(6, crng.random((3, 10)) < 0.5, None, 2.0, 2.0, disallow=(13,))         # mismatch: skip
+    add(6, None, np.stack([crng.integers(1, 9, 4), crng.integers(1, 9, 4)], 1), 2.0, 2.0)
+    add(5, None, np.full((5, 2), -1), 2.0, 2.0)                                 # no shape at all
+    add(4, np.ones((4, 10), bool), np.array([[3, 3]]), 1.0, 7.5, grid_b=1)      # early return
+    add(4, crng.random((4, 10)) < 0.5, np.array([[2, 9], [9, 2], [5, 5], [1, 1]]), 2.0, 2.0,
+        disallow=())
+    add(16, crng.random((16, 10)) < 0.3, np.stack([crng.integers(0, 31, 16),
+                                                    crng.integers(0, 31, 16)], 1), 2.0, 2.0)
+    add(3, np.zeros((3, 10), bool), None, 1e4, 2.0)                             # huge penalty
+
+    out = {}
+    for i, c in enumerate(cases):
+        upd = rinf.GridStateUpdater(len(c["gx"]), torch.device("cpu"))
+        upd.set_state(torch.from_numpy(c["gx"]), torch.from_numpy(c["gy"]),
+                      torch.zeros(len(c["gx"]), dtype=torch.bool))
+        cons = rinf.DecodingConstraints(
+            palette_mask=None if c["pal"] is None else torch.from_numpy(np.asarray(c["pal"])),
+            target_shape=None if c["shape"] is None else torch.from_numpy(
+                np.asarray(c["shape"], dtype=np.int64)),
+            palette_penalty=c["pp"], shape_penalty=c["sp"], disallow_tokens=c["disallow"])
+        res = rinf._apply_logit_constraints(torch.from_numpy(c["logits"].copy()), upd, cons)
+        k = f"c{i}_"
+        out[k + "logits"] = c["logits"]
+        out[k + "gx"], out[k + "gy"] = c["gx"], c["gy"]
+        if c["pal"] is not None:
+            out[k + "palette"] = np.asarray(c["pal"], dtype=bool)
+        if c["shape"] is not None:
+            out[k + "shape"] = np.asarray(c["shape"], dtype=np.int64)
+        out[k + "penalties"] = np.array([c["pp"], c["sp"]], dtype=np.float32)
+        out[k + "disallow"] = np.array(c["disallow"], dtype=np.int64)
+        out[k + "out"] = res.numpy()
+    out["n_cases"] = np.int64(len(cases))
+    np.savez_compressed(os.path.join(OUT, "constraints.npz"), **out)
+    print("constraints:", len(cases), "cases")
+
+
+AUG_TASK = {"train": [{"input": [[1, 2, 3, 4, 5, 6]], "output": [[6], [5], [4], [3], [2], [1]]},
+                      {"input": [[7, 0], [0, 7]], "output": [[0, 7], [7, 0]]}],
+            "test": [{"input": [[1, 0, 2, 0, 3]]}]}
+# (model, batched, max_batch_size, constrain_decoding); "stop" ends rows at many different steps,
+# "open" rarely emits END and runs into the max_seq_len budgets
+AUG_RUNS = [("stop", True, 16, False), ("stop", True, 5, False), ("stop", False, 1, False),
+            ("stop", True, 5, True), ("stop", False, 1, True), ("open", True, 16, False),
+            ("open", False, 1, True)]
+AUG_PERMS, AUG_MAX_NEW, AUG_EXAMPLE = 3, 130, 1
+
+
+def _augment_runs(rinf, cfg, TinyTransformer) -> None:
+    """Raw per-variant outputs of the reference's augmentation caller."""
+    import json
+
+    import torch
+
+    models = {}
+    for name, boost in (("stop", 2.2), ("open", 1.0)):
+        w = _weights(np.random.default_rng(7), boost)
+        m = TinyTransformer(cfg)
+        m.load_state_dict({k: torch.from_numpy(v).to(torch.bfloat16).float()
+                           for k, v in w.items()}, strict=True)
+        models[name] = m.eval()
+
+    out = {"task": np.array(json.dumps(AUG_TASK)),
+           "params": np.array([AUG_PERMS, AUG_MAX_NEW, AUG_EXAMPLE], dtype=np.int64),
+           "end_boost": np.array([2.2, 1.0], dtype=np.float64)}
+    orig_gen, orig_cons, orig_dec = (rinf.generate_output, rinf._apply_logit_constraints,
+                                     rinf.decode_output_grid)
+    for r, (mname, batched, chunk, constrain) in enumerate(AUG_RUNS):
+        calls, logs = [], []
+
+        def cons_rec(logits, grid_state, constraints):
+            res = orig_cons(logits, grid_state, constraints)
+            logs.append(res[:, 0].detach().clone())
+            return res
+
+        def gen_rec(model, input_ids, *a, **k):
+            start = len(logs)
+            res = orig_gen(model, input_ids, *a, **k)
+            calls.append((input_ids.shape[1], res.detach().clone(),
+                          torch.stack(logs[start:], 1) if len(logs) > start else None))
+            return res
+
+        rinf.generate_output, rinf._apply_logit_constraints = gen_rec, cons_rec
+        rinf.decode_output_grid = lambda toks: tuple(toks)
+        try:
+            with torch.no_grad():
+                if batched:
+                    base_palette = rinf._collect_palette(AUG_TASK, 0) if constrain else None
+                    base_shape = rinf._infer_output_shape(AUG_TASK) if constrain else None
+                    preds = rinf._predict_augmentations_batched(
+                        models[mname], AUG_TASK, 0, torch.device("cpu"), AUG_EXAMPLE, True,
+                        AUG_PERMS, AUG_MAX_NEW, 1, 0.0, None, constrain, base_palette,
+                        base_shape, 2.0, 2.0, False, max_batch_size=chunk)
+                else:
+                    preds = rinf.predict_with_augmentations(
+                        models[mname], AUG_TASK, 0, torch.device("cpu"), example_id=AUG_EXAMPLE,
+                        num_color_perms=AUG_PERMS, max_output_tokens=AUG_MAX_NEW,
+                        constrain_decoding=constrain, batched=False)
+        finally:
+            rinf.generate_output, rinf._apply_logit_constraints = orig_gen, orig_cons
+            rinf.decode_output_grid = orig_dec
+        gens, gaps = [], []
+        for L, res, lg in calls:
+            for i in range(res.shape[0]):
+                gens.append(res[i, L:].tolist())
+                top = lg[i].topk(2, dim=-1).values
+                gaps.append((top[:, 0] - top[:, 1]).tolist())
+        n, gmax = len(preds), max(len(g) for g in gens)
+        smax = max(len(p[0]) for p in preds)
+        streams = np.full((n, smax), -1, dtype=np.int64)
+        genarr = np.full((n, gmax), -1, dtype=np.int64)
+        gaparr = np.full((n, gmax), np.nan, dtype=np.float32)
+        for i, (p, g, gp) in enumerate(zip(preds, gens, gaps)):
+            streams[i, :len(p[0])] = p[0]
+            genarr[i, :len(g)] = g
+            gaparr[i, :len(gp)] = gp
+        k = f"r{r}_"
+        out[k + "run"] = np.array([mname == "stop", batched, chunk, constrain], dtype=np.int64)
+        out[k + "streams"], out[k + "gen"], out[k + "gaps"] = streams, genarr, gaparr
+        out[k + "aug"] = np.array([[p[1]] + (list(p[2]) if p[2] else [-1] * 10) for p in preds],
+                                  dtype=np.int64)
+        print(f"augment run {r} {AUG_RUNS[r]}: {n} variants, "
+              f"{len({len(g) for g in gens})} distinct generated lengths, "
+              f"min top-2 gap {np.nanmin(gaparr):.4f}")
+    # one run decoded to grids by the reference's own decode_output_grid
+    with torch.no_grad():
+        preds = rinf.predict_with_augmentations(
+            models["stop"], AUG_TASK, 0, torch.device("cpu"), example_id=AUG_EXAMPLE,
+            num_color_perms=AUG_PERMS, max_output_tokens=AUG_MAX_NEW)
+    out["grids_json"] = np.array(json.dumps([p[0] for p in preds]))
+    out["n_runs"] = np.int64(len(AUG_RUNS))
+    np.savez_compressed(os.path.join(OUT, "augment_micro.npz"), **out)
 
 
 if __name__ == "__main__":

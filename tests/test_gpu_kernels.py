@@ -778,14 +778,15 @@ def test_decode_head_equals_lm_head_plus_commit(d, V):
     assert not bool((tok.cpu() == V - 1).any())      # the tied duplicate of slot 2 never wins
 
 
-def test_head_constraints_equal_host_restatement():
-    """The head kernels with fused logit constraints equal the plain kernel's logits after the
-    host restatement of _apply_logit_constraints (src/inference.py:285-364): the same fp32
+def test_head_constraints_equal_oracle_rule():
+    """The head kernels with fused logit constraints return the plain kernel's logits after the
+    oracle's restatement of _apply_logit_constraints (src/inference.py:285-364), which the
+    reference's own outputs pin bit for bit (tests/golden/constraints.npz): the same fp32
     subtractions in the same order, so bit-identical logits and argmax.  The rows cover every
     branch: palette on / off, target shape on / off (-1), x below / at / past the width, y
     below / past the height, and the disallowed START / IO_SEP (which would otherwise win: their
-    weight rows are scaled up)."""
-    from mdlarc_scale_amd.inference import DecodingConstraints, apply_logit_constraints
+    weight rows are scaled up); the penalties are those of the reference fixture's cases."""
+    from tests.golden_io import constraint_cases
 
     g = torch.Generator().manual_seed(4)
     B, d, V = 64, 256, 14
@@ -795,37 +796,43 @@ def test_head_constraints_equal_host_restatement():
     w[10] *= 3
     w[12] *= 3
     w = w.to(DEV)
-    pal = torch.rand(B, 10, generator=g) < 0.5
-    pal[::5] = True                                           # rows without palette penalty
-    shape = torch.randint(1, 6, (B, 2), generator=g)
-    shape[::4] = -1                                           # rows without target shape
-    gx = torch.randint(0, 7, (B,), generator=g).to(torch.int32).to(DEV)
-    gy = torch.randint(0, 7, (B,), generator=g).to(torch.int32).to(DEV)
-    c = DecodingConstraints(palette_mask=pal.to(DEV), target_shape=shape.to(DEV),
-                            palette_penalty=2.5, shape_penalty=1.75)
-    hc = K().HeadConstraints(c.disallow_tokens, pal.to(DEV), 2.5, shape.to(DEV), gx, gy, 1.75)
     plain = torch.empty(B, V, device=DEV)
     K().lm_head(x, None, B, gamma, 1e-5, w, plain, None)
-    ref = apply_logit_constraints(plain.clone(), gx, gy, c)
-    got = torch.empty(B, V, device=DEV)
-    tok = torch.empty(B, dtype=torch.int64, device=DEV)
-    K().lm_head(x, None, B, gamma, 1e-5, w, got, tok, hc)
-    out = torch.full((B, 4), -1, dtype=torch.int64, device=DEV)
-    dlog = torch.empty(B, V, device=DEV)
-    dtok = torch.empty(B, dtype=torch.int64, device=DEV)
-    K().decode_head(x, gamma, 1e-5, w, dlog, dtok, out, 1, None, None, 0, 13, hc)
-    torch.cuda.synchronize()
-    assert torch.equal(got.cpu(), ref.cpu())
-    assert torch.equal(dlog.cpu(), ref.cpu())
-    assert torch.equal(tok.cpu(), ref.argmax(-1).cpu()) and torch.equal(dtok.cpu(), tok.cpu())
-    assert torch.equal(out[:, 1].cpu(), tok.cpu())
-    assert not bool(((tok == 10) | (tok == 12)).any())
-    assert not torch.equal(plain.argmax(-1).cpu(), tok.cpu())   # the constraints changed tokens
-    xs, ys, sh = gx.cpu(), gy.cpu(), shape
-    has = sh[:, 0] >= 0
-    for cond in (has & (xs >= sh[:, 1]), has & (xs < sh[:, 1]), has & (ys >= sh[:, 0]),
-                 has & (ys < sh[:, 0]), ~has):
-        assert bool(cond.any())                              # every branch is exercised
+    pens = sorted({(c["palette_penalty"], c["shape_penalty"]) for c in constraint_cases()})
+    assert len(pens) >= 3
+    for pp, sp in pens:
+        pal = torch.rand(B, 10, generator=g) < 0.5
+        pal[::5] = True                                       # rows without palette penalty
+        shape = torch.randint(1, 6, (B, 2), generator=g)
+        shape[::4] = -1                                       # rows without target shape
+        shape[1::8, 0] = -1                                   # h < 0 alone: no shape either
+        gx = torch.randint(0, 7, (B,), generator=g).to(torch.int32)
+        gy = torch.randint(0, 7, (B,), generator=g).to(torch.int32)
+        gx[2], gy[2] = shape[2, 1], shape[2, 0]               # exactly at the width / height
+        hc = K().HeadConstraints((10, 12), pal.to(DEV), pp, shape.to(DEV), gx.to(DEV),
+                                 gy.to(DEV), sp)
+        ref = rp.apply_logit_constraints(
+            plain.cpu().clone(), gx.long(), gy.long(),
+            rp.OracleConstraints(palette_mask=pal, target_shape=shape, palette_penalty=pp,
+                                 shape_penalty=sp, disallow_tokens=(10, 12)))
+        got = torch.empty(B, V, device=DEV)
+        tok = torch.empty(B, dtype=torch.int64, device=DEV)
+        K().lm_head(x, None, B, gamma, 1e-5, w, got, tok, hc)
+        out = torch.full((B, 4), -1, dtype=torch.int64, device=DEV)
+        dlog = torch.empty(B, V, device=DEV)
+        dtok = torch.empty(B, dtype=torch.int64, device=DEV)
+        K().decode_head(x, gamma, 1e-5, w, dlog, dtok, out, 1, None, None, 0, 13, hc)
+        torch.cuda.synchronize()
+        assert torch.equal(got.cpu(), ref), (pp, sp)
+        assert torch.equal(dlog.cpu(), ref), (pp, sp)
+        assert torch.equal(tok.cpu(), ref.argmax(-1)) and torch.equal(dtok.cpu(), tok.cpu())
+        assert torch.equal(out[:, 1].cpu(), tok.cpu())
+        assert not bool(((tok == 10) | (tok == 12)).any())
+        assert not torch.equal(plain.argmax(-1).cpu(), tok.cpu())  # the constraints changed tokens
+        has = (shape[:, 0] >= 0) & (shape[:, 1] >= 0)
+        for cond in (has & (gx >= shape[:, 1]), has & (gx < shape[:, 1]),
+                     has & (gy >= shape[:, 0]), has & (gy < shape[:, 0]), ~has):
+            assert bool(cond.any())                           # every branch is exercised
 
 
 def test_build_prompts_equals_host_tokeniser():

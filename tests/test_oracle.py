@@ -15,7 +15,7 @@ import torch
 
 from oracle import data_format as odf
 from oracle import reference_path as rp
-from tests.golden_io import load_e2e
+from tests.golden_io import augment_weights, constraint_cases, load_augment, load_e2e
 
 # ------------------------------------------------------------------ golden end-to-end vectors
 
@@ -61,6 +61,73 @@ def test_left_pad_quirk_is_exercised():
     assert (n - 1 < S - n).any()                           # quirk index inside the pad
     assert ((n - 1 >= S - n) & (n < S)).any()              # quirk index mid-prompt
     assert (n == S).any()
+
+
+def _oracle_constraints(c):
+    return rp.OracleConstraints(palette_mask=c["palette"], target_shape=c["shape"],
+                                palette_penalty=c["palette_penalty"],
+                                shape_penalty=c["shape_penalty"], disallow_tokens=c["disallow"])
+
+
+def test_constraints_match_reference_golden():
+    """The oracle's constraint rule returns the reference's logits bit for bit on every case
+    (broadcast rows, mismatched batches, rows without a shape, x == w / y == h, the early
+    return on a grid-state batch mismatch, a huge penalty)."""
+    cases = constraint_cases()
+    assert len(cases) >= 9
+    for i, c in enumerate(cases):
+        got = rp.apply_logit_constraints(c["logits"].clone(), c["gx"], c["gy"],
+                                         _oracle_constraints(c))
+        assert torch.equal(got, c["out"]), f"case {i}"
+    # the fixture exercises every branch: each penalty changes some logit somewhere
+    changed = [(c["out"] != c["logits"]) for c in cases]
+    assert any(ch[:, :10].any() for ch in changed)          # palette / shape on colours
+    assert any(ch[:, 11].any() for ch in changed)           # shape on NEWLINE
+    assert any(torch.equal(c["out"][:, :10], c["logits"][:, :10]) and c["palette"] is not None
+               for c in cases)                              # a skipped (mismatched) palette
+
+
+def test_constraint_rule_plants_fail():
+    """Plausible mistakes in the rule (here: the row-complete test inverted) change the result
+    on the fixture, so the bit-exact comparison above would catch them."""
+    c = constraint_cases()[0]
+    good = rp.apply_logit_constraints(c["logits"].clone(), c["gx"], c["gy"],
+                                      _oracle_constraints(c))
+    bad = rp.apply_logit_constraints(c["logits"].clone(), c["gx"] - 1, c["gy"],
+                                     _oracle_constraints(c))
+    assert not torch.equal(good, bad)
+
+
+@pytest.mark.parametrize("r", range(7))
+def test_augmentations_match_reference_golden(r):
+    """The oracle's augmentation caller reproduces the reference's runs: per variant the token
+    stream its prediction is decoded from, its generated tokens (the chunk's stop step) and the
+    dihedral / permutation labels."""
+    from oracle import augment as oa
+
+    fx = load_augment()
+    run = fx.runs[r]
+    cfg, w = augment_weights(run.stop_model)
+    m = rp.OracleModel(cfg, w)
+    tr = oa.predict_with_augmentations(
+        m, fx.task, 0, example_id=fx.example_id, num_color_perms=fx.num_color_perms,
+        max_output_tokens=fx.max_new, constrain_decoding=run.constrain, batched=run.batched,
+        max_batch_size=run.chunk, decode=lambda toks: tuple(toks))
+    assert [(p[1], p[2]) for p in tr.predictions] == run.aug
+    assert tr.generated == run.gen
+    assert [p[0] for p in tr.predictions] == run.streams
+
+
+def test_augmentation_grids_match_reference_golden():
+    from oracle import augment as oa
+
+    fx = load_augment()
+    cfg, w = augment_weights(True)
+    tr = oa.predict_with_augmentations(rp.OracleModel(cfg, w), fx.task, 0,
+                                       example_id=fx.example_id,
+                                       num_color_perms=fx.num_color_perms,
+                                       max_output_tokens=fx.max_new)
+    assert [p[0] for p in tr.predictions] == fx.grids
 
 
 def test_grid_state_matches_reference_golden():
