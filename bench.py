@@ -29,8 +29,17 @@ Also reported on the same JSON line:
   back to back; TFLOP/s of the valid causal (query, key) pairs against the 2.5 PFLOP/s dense
   bf16 MFMA peak.
 
-``--config medium_b128`` / ``large_b64`` run BASELINE configs 3 and 4 the same way (their own
-metric name; no microbench; the CPU baseline only with an explicit ``--cpu-seconds``).
+* ``configs``: BASELINE configs 3 (medium, B=128, 4,096-slot cache) and 4 (large, B=64, prompts
+  of 5,000-5,726 tokens) measured the same way over 32 graph-replayed steps each: decode
+  tokens/s, the decode attention's GB/s, the prefill and one layer's prefill-attention TFLOP/s
+  (``--no-side`` skips them).
+
+``roofline.traffic`` is the HBM bytes per launch the rocprofv3 FETCH_SIZE / WRITE_SIZE passes
+measured per algorithmic byte (profiles/pmc_traffic_small_b256.md) times this line's own
+algorithmic bytes per launch.
+
+``--config medium_b128`` / ``large_b64`` run BASELINE configs 3 and 4 as the headline workload
+(their own metric name; no microbench; the CPU baseline only with an explicit ``--cpu-seconds``).
 """
 
 from __future__ import annotations
@@ -74,6 +83,8 @@ def _args():
                     help="time bound of the CPU-baseline sample (0 disables it; default 15 s "
                          "for small_b256, off for the larger configs)")
     ap.add_argument("--no-micro", action="store_true", help="skip the config-1 microbench")
+    ap.add_argument("--no-side", action="store_true",
+                    help="skip the configs 3 and 4 sub-objects of the default (config 2) line")
     ap.add_argument("--eager", action="store_true",
                     help="launch every kernel from the host instead of replaying a HIP graph")
     ap.add_argument("--gemm-compare", action="store_true",
@@ -107,18 +118,19 @@ class Timer:
         return self.a.elapsed_time(self.b)
 
 
-def recorded_traffic(kernel: str, workload: str):
-    """HBM bytes per launch of ``kernel`` measured by the rocprofv3 FETCH_SIZE / WRITE_SIZE passes
-    (calibrated against a device copy) and recorded in profiles/pmc_traffic_<workload>.md, or
-    None when no such record exists."""
+def recorded_traffic_ratio(kernel: str, workload: str):
+    """HBM bytes per algorithmic byte of ``kernel`` at ``workload``: the rocprofv3 FETCH_SIZE /
+    WRITE_SIZE passes (calibrated against a device copy) over the same launches' algorithmic
+    bytes, recorded in profiles/pmc_traffic_<workload>.md; (None, None) without such a record.
+    The bench line's ``traffic`` is this ratio times its own launches' algorithmic bytes."""
     path = os.path.join(ROOT, "profiles", f"pmc_traffic_{workload}.md")
     if not os.path.exists(path):
         return None, None
-    key = f"traffic_bytes_per_launch {kernel} {workload}:"
+    key = f"traffic_per_algorithmic_byte {kernel} {workload}:"
     with open(path) as f:
         for line in f:
             if line.startswith(key):
-                return int(line[len(key):].strip()), os.path.relpath(path, ROOT)
+                return float(line[len(key):].strip()), os.path.relpath(path, ROOT)
     return None, None
 
 
@@ -220,8 +232,19 @@ def microbench(dev):
     nbytes = N * (d * 4 * 2 + d * 4 + d * 2 * 2 + 4)
     res["add_rmsnorm"] = dict(ms=ms, bytes=nbytes, gbs=nbytes / ms / 1e6)
     del x, delta, xs, rstd
-    for v in res.values():
+    # the bytes config 1 defines (bf16 activations in and out): K1 ids + x + normed x;
+    # K2 qkv + rstd/positions + q, k, v; K3 gate/up + h.  The kernels above move more: fp32
+    # residual / GEMM outputs and hi|lo split GEMM inputs (the parity design's formats)
+    algorithmic = {"k1_embed_rmsnorm": N * 8 + N * d * (2 + 2),
+                   "k2_qkv_rope_cache": N * (3 * d * 2 + 16 + 3 * d * 2),
+                   "k3_swiglu": N * 2 * F * 2 + N * F * 2}
+    for name, v in res.items():
         v["frac_of_peak"] = round(v["gbs"] / HBM_PEAK_GBS, 4)
+        if name in algorithmic:
+            a = algorithmic[name]
+            v["algorithmic_bytes"] = a
+            v["algorithmic_gbs"] = round(a / v["ms"] / 1e6, 1)
+            v["frac_of_algorithmic"] = round(a / v["ms"] / 1e6 / HBM_PEAK_GBS, 4)
         v["ms"] = round(v["ms"], 5)
         v["gbs"] = round(v["gbs"], 1)
     return res
@@ -400,32 +423,20 @@ def cpu_baseline(model_state, cfg, snap, t0, seconds):
                        f"os.cpu_count()={os.cpu_count()})")
 
 
-def main() -> int:
-    args = _args()
-    if args.gpus != 1:
-        print("bench.py runs on exactly one GPU: this build measures the single-GPU hot path "
-              "(decode rows would shard by batch across GPUs with no exchange, so one GPU's "
-              "throughput is the per-GPU figure). Use --gpus 1.", file=sys.stderr)
-        return 2
+def measure_workload(spec, steps, warmup, dev, eager=False, snapshot=False):
+    """Prefill and ``steps`` timed greedy decode steps of ``spec``'s batch (after ``warmup``
+    untimed ones), then the decode attention's timed launches re-issued under HIP events and one
+    layer's prefill-attention launch re-issued 10 times.  Returns the measurements, plus the
+    model and decode state when ``snapshot`` (the CPU baseline continues from them)."""
     import torch
 
-    from mdlarc_scale_amd import _lib
     from mdlarc_scale_amd import kernels as K
     from mdlarc_scale_amd import inference as I
     from mdlarc_scale_amd.data import END_TOKEN_ID
     from mdlarc_scale_amd.engine import engine_for, pack_prompt
     from mdlarc_scale_amd.transformer import MODEL_SIZES, create_model
-    from mdlarc_scale_amd.workload import SPECS, build_prompts, left_pad
+    from mdlarc_scale_amd.workload import build_prompts, left_pad
 
-    if not torch.cuda.is_available():
-        print("bench.py needs a ROCm GPU", file=sys.stderr)
-        return 1
-    _lib.lib()
-    dev = torch.device("cuda:0")
-    spec = SPECS[args.config]
-    headline = spec.name == "small_b256"
-    if args.cpu_seconds is None:
-        args.cpu_seconds = 15.0 if headline else 0.0
     t_build = time.perf_counter()
     prompts = build_prompts(spec)
     ids, pos, mask = left_pad(prompts)
@@ -437,20 +448,21 @@ def main() -> int:
     torch.manual_seed(0)
     model = create_model(**MODEL_SIZES[spec.preset], dropout=0.0, max_seq_len=spec.cache_slots)
     model = model.to(torch.bfloat16)                 # bf16 models
-    model_state = {k: v.float().clone() for k, v in model.state_dict().items()}
+    model_state = ({k: v.float().clone() for k, v in model.state_dict().items()}
+                   if snapshot else None)
     model = model.to(dev).eval()
     cfg = model.config
     total = min(S + spec.max_new, cfg.max_seq_len)
     max_new = total - S
-    need = args.warmup + args.steps
-    if need + 1 > max_new:
-        print(f"--warmup + --steps = {need} exceeds the {max_new - 1} decode steps the "
-              f"{cfg.max_seq_len}-slot cache leaves after the {S}-token prompts", file=sys.stderr)
-        return 2
+    if warmup + steps + 1 > max_new:
+        raise SystemExit(f"--warmup + --steps = {warmup + steps} exceeds the {max_new - 1} decode "
+                         f"steps the {cfg.max_seq_len}-slot cache leaves after the {S}-token "
+                         f"prompts of {spec.name}")
 
     eng = engine_for(model)
     gen = I.Generator(model)
     ids_d, pos_d, mask_d, ex_d = ids.to(dev), pos.to(dev), mask.to(dev), ex.to(dev)
+    res = {}
     with torch.no_grad():
         W = eng.packed(dev)
         st = gen.prepare(ids_d, pos_d, ex_d, mask_d, total)
@@ -464,15 +476,15 @@ def main() -> int:
         K.decode_commit(st.tok, st.out_ids, S, None, st.finish, S, END_TOKEN_ID)
         # warmup: one eager step, capture, replays
         gen.greedy_step(st, W, True)
-        graph = None if args.eager else gen.capture_greedy(st, W, True)
-        for _ in range(args.warmup - 1):
+        graph = None if eager else gen.capture_greedy(st, W, True)
+        for _ in range(warmup - 1):
             graph.replay() if graph is not None else gen.greedy_step(st, W, True)
         torch.cuda.synchronize()
-        t_first = S + args.warmup              # cache slot of the first timed step's token
+        t_first = S + warmup                   # cache slot of the first timed step's token
         tm = Timer()
         wall0 = time.perf_counter()
         tm.start()
-        for _ in range(args.steps):
+        for _ in range(steps):
             graph.replay() if graph is not None else gen.greedy_step(st, W, True)
         tm.stop()
         torch.cuda.synchronize()
@@ -481,7 +493,7 @@ def main() -> int:
 
         # the CPU baseline continues from this state; take it before the re-launches below
         # rewrite the slots they attend to
-        snap = snapshot_decode_state(st, ex_d) if args.cpu_seconds > 0 else None
+        snap = snapshot_decode_state(st, ex_d) if snapshot else None
 
         # decode attention (the fused mdl_attn_decode_rope the step runs): re-issue the timed
         # region's launches (every layer at every cache position t of the timed steps) back to
@@ -489,8 +501,8 @@ def main() -> int:
         # so the events time kernel execution only
         H = cfg.n_heads
         kv_start_h, holes_h = st.kv_start.cpu(), st.holes.cpu()
-        ts = [t_first + i for i in range(args.steps) for _ in range(cfg.n_layers)]
-        layers = [li for _ in range(args.steps) for li in range(cfg.n_layers)]
+        ts = [t_first + i for i in range(steps) for _ in range(cfg.n_layers)]
+        layers = [li for _ in range(steps) for li in range(cfg.n_layers)]
         qs = 1.0 / 8.0
         ta = Timer()
         ta.start()
@@ -504,8 +516,6 @@ def main() -> int:
         attn_ms = ta.ms() / len(ts)
         attn_bytes = sum(decode_attention_bytes(B, H, t, kv_start_h, S, holes_h)
                          for t in ts) / len(ts)
-        achieved = attn_bytes / attn_ms / 1e6
-        durs = ts
         # the launch's own choices (csrc/attn_decode.hip decode_impl): wave tiles of 64 slots
         # once a work item can exceed 2,048 slots, else 32; ceil(total / split_len) splits
         n_split = -(-total // st.split_len)
@@ -536,26 +546,129 @@ def main() -> int:
         pa_ms = tpa.ms() / reps
         del qp, op
 
+    res.update(
+        B=B, S=S, total=total, max_new=max_new, t_first=t_first, host_build_s=host_build_s,
+        prefill_ms=prefill_ms, timed_ms=timed_ms, wall_s=wall_s,
+        value=B * steps / (timed_ms / 1e3), attn_ms=attn_ms, attn_bytes=attn_bytes,
+        attn_launches=len(ts), n_split=n_split, decode_nb=decode_nb, n_valid=n_valid,
+        pa_ms=pa_ms, pa_flops=pa_flops, prefill_flops=cfg.n_layers * pa_flops, snap=snap,
+        model_state=model_state, cfg=cfg)
+    if snapshot:
+        res.update(model=model, st=st)
+    return res
+
+
+def roofline_of(r):
+    """The decode attention's roofline object: algorithmic bytes per launch over its average
+    launch duration against the 8 TB/s peak."""
+    achieved = r["attn_bytes"] / r["attn_ms"] / 1e6
+    return {
+        "kernel": f"attn_decode_kernel<true, {r['decode_nb']}> (mdl_attn_decode_rope: K2 + "
+                  f"decode attention on bf16 MFMA, {16 * r['decode_nb']}-slot wave tiles, "
+                  f"{r['n_split']} split(s) per (row, head))",
+        "bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS,
+        "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4),
+        "avg_launch_ms": round(r["attn_ms"], 5), "bytes_per_launch": int(r["attn_bytes"]),
+        "launches_timed": r["attn_launches"],
+    }
+
+
+def prefill_attention_of(r):
+    pa_ms, pa_flops = r["pa_ms"], r["pa_flops"]
+    return {
+        "kernel": "attn_prefill_kernel (mdl_attn_prefill_packed, bf16 MFMA)", "bound": "mfma",
+        "ms_per_layer": round(pa_ms, 4), "tflop_per_layer": round(pa_flops / 1e12, 4),
+        "achieved": round(pa_flops / pa_ms / 1e9, 1), "peak": BF16_PEAK_TFLOPS,
+        "unit": "TFLOP/s", "frac": round(pa_flops / pa_ms / 1e9 / BF16_PEAK_TFLOPS, 4),
+        "flops": "valid causal (query, key) pairs x 4 x 64 (QK^T and PV)",
+    }
+
+
+def prefill_of(r):
+    nv = int(r["n_valid"].sum())
+    return {"ms": round(r["prefill_ms"], 3), "tokens": nv, "padded_tokens": r["B"] * r["S"],
+            "tokens_per_s": round(nv / (r["prefill_ms"] / 1e3), 1),
+            "attention_causal_tflop": round(r["prefill_flops"] / 1e12, 3)}
+
+
+def side_config(name, dev, steps=32, warmup=4):
+    """BASELINE configs 3 and 4 on the default line: decode tokens/s over ``steps`` graph-replayed
+    steps, the decode attention's GB/s, the prefill and one layer's prefill-attention TFLOP/s."""
+    import torch
+
+    from mdlarc_scale_amd.workload import SPECS
+
+    r = measure_workload(SPECS[name], steps, warmup, dev)
+    out = {
+        "workload": WORKLOADS[name], "rows": r["B"], "padded_prompt_slots": r["S"],
+        "cache_slots": r["total"], "prompt_len_min": int(r["n_valid"].min()),
+        "prompt_len_max": int(r["n_valid"].max()), "steps": steps, "warmup": warmup,
+        "decode_tokens_per_s": round(r["value"], 1),
+        "ms_per_step": round(r["timed_ms"] / steps, 4),
+        "timed_cache_fill": [r["t_first"], r["t_first"] + steps],
+        "decode_attention": roofline_of(r), "prefill": prefill_of(r),
+        "prefill_attention": prefill_attention_of(r),
+    }
+    del r
+    torch.cuda.empty_cache()
+    return out
+
+
+def main() -> int:
+    args = _args()
+    if args.gpus != 1:
+        print("bench.py runs on exactly one GPU: this build measures the single-GPU hot path "
+              "(decode rows would shard by batch across GPUs with no exchange, so one GPU's "
+              "throughput is the per-GPU figure). Use --gpus 1.", file=sys.stderr)
+        return 2
+    import torch
+
+    from mdlarc_scale_amd import _lib
+    from mdlarc_scale_amd.workload import SPECS
+
+    if not torch.cuda.is_available():
+        print("bench.py needs a ROCm GPU", file=sys.stderr)
+        return 1
+    _lib.lib()
+    dev = torch.device("cuda:0")
+    spec = SPECS[args.config]
+    headline = spec.name == "small_b256"
+    if args.cpu_seconds is None:
+        args.cpu_seconds = 15.0 if headline else 0.0
+    r = measure_workload(spec, args.steps, args.warmup, dev, eager=args.eager,
+                         snapshot=args.cpu_seconds > 0 or args.augment or args.gemm_compare)
+    cfg, B, S = r["cfg"], r["B"], r["S"]
+    with torch.no_grad():
         micro = None if (args.no_micro or not headline) else microbench(dev)
         gemm_cmp = decode_gemm_compare(cfg, B, dev) if args.gemm_compare else None
-        augment = augmentation_bench(model, dev, spec) if args.augment else None
-
+        augment = augmentation_bench(r["model"], dev, spec) if args.augment else None
         cpu = None
-        if snap is not None:
-            cpu = cpu_baseline(model_state, cfg, snap, S + args.warmup + args.steps,
-                               args.cpu_seconds)
+        if args.cpu_seconds > 0:
+            cpu = cpu_baseline(r["model_state"], cfg, r["snap"],
+                               S + args.warmup + args.steps, args.cpu_seconds)
+    r.pop("snap", None)
+    r.pop("model", None)
+    r.pop("st", None)
+    torch.cuda.empty_cache()
+    sides = {}
+    if headline and not args.no_side:
+        for name in ("medium_b128", "large_b64"):
+            sides[name] = side_config(name, dev)
 
-    prefill_flops = cfg.n_layers * pa_flops
-    traffic, traffic_src = recorded_traffic("attn_decode_kernel", spec.name)
-    value = B * args.steps / (timed_ms / 1e3)
+    roof = roofline_of(r)
+    ratio, traffic_src = recorded_traffic_ratio("attn_decode_kernel", spec.name)
+    roof["traffic"] = None if ratio is None else int(round(ratio * roof["bytes_per_launch"]))
+    roof["traffic_per_algorithmic_byte"] = ratio
+    roof["traffic_source"] = traffic_src
+    n_valid = r["n_valid"]
     out = {
         "metric": METRIC if headline else f"greedy decode tokens/s at {spec.preset}, B={B}",
-        "value": round(value, 1),
+        "value": round(r["value"], 1),
         "unit": "tokens/s",
         "n_gpus": 1,
         "steps": args.steps,
         "warmup": args.warmup,
-        "ms_per_step": round(timed_ms / args.steps, 4),
+        "ms_per_step": round(r["timed_ms"] / args.steps, 4),
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
@@ -563,45 +676,27 @@ def main() -> int:
         "data": "synthetic",
         "config": {
             "workload": WORKLOADS[spec.name],
-            "preset": spec.preset, "rows": B, "padded_prompt_slots": S, "cache_slots": total,
-            "decode_steps_available": max_new - 1, "timed_cache_fill": [t_first,
-                                                                        t_first + args.steps],
+            "preset": spec.preset, "rows": B, "padded_prompt_slots": S,
+            "cache_slots": r["total"], "decode_steps_available": r["max_new"] - 1,
+            "timed_cache_fill": [r["t_first"], r["t_first"] + args.steps],
             "prompt_len_min": int(n_valid.min()), "prompt_len_mean": round(float(
                 n_valid.float().mean()), 1), "prompt_len_max": int(n_valid.max()),
             "sharding": "one GPU (rows would shard by batch across GPUs, no exchange)",
             "graph": not args.eager, "workload_seed": spec.seed,
         },
-        "roofline": {
-            "kernel": f"attn_decode_kernel<true, {decode_nb}> (mdl_attn_decode_rope: K2 + "
-                      f"decode attention on bf16 MFMA, {16 * decode_nb}-slot wave tiles, "
-                      f"{n_split} split(s) per (row, head))",
-            "bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS,
-            "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": traffic,
-            "traffic_source": traffic_src,
-            "avg_launch_ms": round(attn_ms, 5), "bytes_per_launch": int(attn_bytes),
-            "launches_timed": len(durs),
-        },
+        "roofline": roof,
         "cpu_baseline": cpu,
-        "prefill": {
-            "ms": round(prefill_ms, 3), "tokens": int(n_valid.sum()), "padded_tokens": B * S,
-            "tokens_per_s": round(int(n_valid.sum()) / (prefill_ms / 1e3), 1),
-            "attention_causal_tflop": round(prefill_flops / 1e12, 3),
-        },
-        "prefill_attention": {
-            "kernel": "attn_prefill_kernel (mdl_attn_prefill_packed, bf16 MFMA)", "bound": "mfma",
-            "ms_per_layer": round(pa_ms, 4), "tflop_per_layer": round(pa_flops / 1e12, 4),
-            "achieved": round(pa_flops / pa_ms / 1e9, 1), "peak": BF16_PEAK_TFLOPS,
-            "unit": "TFLOP/s", "frac": round(pa_flops / pa_ms / 1e9 / BF16_PEAK_TFLOPS, 4),
-            "flops": "valid causal (query, key) pairs x 4 x 64 (QK^T and PV)",
-        },
+        "prefill": prefill_of(r),
+        "prefill_attention": prefill_attention_of(r),
         "microbench": micro,
+        **({"configs": sides} if sides else {}),
         **({"augmentation": augment} if augment is not None else {}),
         **({"decode_gemm": gemm_cmp} if gemm_cmp is not None else {}),
-        "wall_s_timed": round(wall_s, 4),
-        "host_prompt_build_s": round(host_build_s, 3),
+        "wall_s_timed": round(r["wall_s"], 4),
+        "host_prompt_build_s": round(r["host_build_s"], 3),
     }
     if cpu:
-        out["vs_cpu"] = round(value / cpu["value"], 1)
+        out["vs_cpu"] = round(r["value"] / cpu["value"], 1)
     print(json.dumps(out), flush=True)
     return 0
 
