@@ -26,8 +26,8 @@ Also reported on the same JSON line:
   MALL cannot hold the working set).
 * ``prefill_attention``: the prefill attention kernel alone over one layer of the batch's cache
   (its real masks and left padding, packed query rows as the prefill launches it), re-launched
-  back to back; TFLOP/s of the valid causal (query, key) pairs against the 2.5 PFLOP/s dense
-  bf16 MFMA peak.
+  back to back (median of 5 rounds of 10 launches after 3 warm ones); TFLOP/s of the valid
+  causal (query, key) pairs against the 2.5 PFLOP/s dense bf16 MFMA peak.
 
 * ``configs``: BASELINE configs 3 (medium, B=128, 4,096-slot cache) and 4 (large, B=64, prompts
   of 5,000-5,726 tokens) measured the same way over 32 graph-replayed steps each: decode
@@ -536,14 +536,18 @@ def measure_workload(spec, steps, warmup, dev, eager=False, snapshot=False):
             K.attn_prefill_packed(qp, kc0, vc0, B, S, H, st.pmask, st.kv_start, pk.q_offset,
                                   pk.n_valid, True, op)
 
-        prefill_attention()
-        reps = 10
-        tpa = Timer()
-        tpa.start()
-        for _ in range(reps):
+        # steady state: 3 warm launches, then the median of 5 rounds of 10 back-to-back launches
+        for _ in range(3):
             prefill_attention()
-        tpa.stop()
-        pa_ms = tpa.ms() / reps
+        reps, rounds = 10, []
+        for _ in range(5):
+            tpa = Timer()
+            tpa.start()
+            for _ in range(reps):
+                prefill_attention()
+            tpa.stop()
+            rounds.append(tpa.ms() / reps)
+        pa_ms = sorted(rounds)[len(rounds) // 2]
         del qp, op
 
     res.update(
