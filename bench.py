@@ -23,7 +23,10 @@ Also reported on the same JSON line:
   from the same cache contents for a bounded number of steps on the host cores.
 * ``microbench``: BASELINE config 1 -- the fused norm / RoPE / SwiGLU kernels at N=65,536
   tokens, d=768, F=2048, GB/s against the 8 TB/s HBM peak (buffer sets rotated so the 256 MB
-  MALL cannot hold the working set).
+  MALL cannot hold the working set): the inference path's forms (fp32 GEMM outputs in, split
+  GEMM inputs out) and the ``*_bf16`` forms in config 1's own format (bf16 activations in and
+  out); ``frac_of_algorithmic`` divides config 1's algorithmic bytes (bf16 in and out) by the
+  kernel time.
 * ``prefill_attention``: the prefill attention kernel alone over one layer of the batch's cache
   (its real masks and left padding, packed query rows as the prefill launches it), re-launched
   back to back (median of 5 rounds of 10 launches after 3 warm ones); TFLOP/s of the valid
@@ -232,6 +235,33 @@ def microbench(dev):
     nbytes = N * (d * 4 * 2 + d * 4 + d * 2 * 2 + 4)
     res["add_rmsnorm"] = dict(ms=ms, bytes=nbytes, gbs=nbytes / ms / 1e6)
     del x, delta, xs, rstd
+
+    # the same three kernels in config 1's own format: bf16 activations in and out
+    ids = [torch.randint(0, 14, (N,), generator=g).to(dev) for _ in range(sets)]
+    xb = [torch.empty(N, d, device=dev, dtype=torch.bfloat16) for _ in range(sets)]
+    xn = [torch.empty(N, d, device=dev, dtype=torch.bfloat16) for _ in range(sets)]
+    ms = timeit(lambda i: K.embed_rmsnorm_bf16(ids[i], exi[i], tok, ex, T, gamma, 1e-5, xb[i],
+                                               xn[i]))
+    nbytes = N * 8 + N * d * 2 * 2
+    res["k1_embed_rmsnorm_bf16"] = dict(ms=ms, bytes=nbytes, gbs=nbytes / ms / 1e6)
+    del xb, xn
+    qkvb = [torch.randn(N, 3 * d, generator=g).to(dev, torch.bfloat16) for _ in range(sets)]
+    rstd = [(0.5 + torch.rand(N, generator=g)).to(dev) for _ in range(sets)]
+    q = [torch.empty(N, d, device=dev, dtype=torch.bfloat16) for _ in range(sets)]
+    kc = [torch.empty(Bm, H, T, 64, device=dev, dtype=torch.bfloat16) for _ in range(sets)]
+    vc = [torch.empty_like(kc[0]) for _ in range(sets)]
+    ms = timeit(lambda i: K.qkv_rope_cache_bf16(qkvb[i], rstd[i], pos, tab, geom, Bm, T, H, 0.125,
+                                                q[i], kc[i], vc[i], slot0=0))
+    nbytes = N * (3 * d * 2 + 4 + 24 + 3 * d * 2)     # positions as the reference's int64
+    res["k2_qkv_rope_cache_bf16"] = dict(ms=ms, bytes=nbytes, gbs=nbytes / ms / 1e6)
+    del qkvb, rstd, q, kc, vc
+    gub = [torch.randn(N, 2 * F, generator=g).to(dev, torch.bfloat16) for _ in range(sets)]
+    hb = [torch.empty(N, F, device=dev, dtype=torch.bfloat16) for _ in range(sets)]
+    ms = timeit(lambda i: K.swiglu_bf16(gub[i], None, bg, bu, hb[i]))
+    nbytes = N * (2 * F * 2 + F * 2)
+    res["k3_swiglu_bf16"] = dict(ms=ms, bytes=nbytes, gbs=nbytes / ms / 1e6)
+    del gub, hb
+
     # the bytes config 1 defines (bf16 activations in and out): K1 ids + x + normed x;
     # K2 qkv + rstd/positions + q, k, v; K3 gate/up + h.  The kernels above move more: fp32
     # residual / GEMM outputs and hi|lo split GEMM inputs (the parity design's formats)
@@ -240,8 +270,9 @@ def microbench(dev):
                    "k3_swiglu": N * 2 * F * 2 + N * F * 2}
     for name, v in res.items():
         v["frac_of_peak"] = round(v["gbs"] / HBM_PEAK_GBS, 4)
-        if name in algorithmic:
-            a = algorithmic[name]
+        base = name[:-5] if name.endswith("_bf16") else name
+        if base in algorithmic:
+            a = algorithmic[base]
             v["algorithmic_bytes"] = a
             v["algorithmic_gbs"] = round(a / v["ms"] / 1e6, 1)
             v["frac_of_algorithmic"] = round(a / v["ms"] / 1e6 / HBM_PEAK_GBS, 4)

@@ -187,6 +187,49 @@ int mdl_swiglu(const float* gate_up, int64_t ld, const float* rstd, const float*
                void* stream);
 
 /*
+ * The three fused kernels in the format of BASELINE's fused-kernel microbench (bf16
+ * activations in and out, no split outputs): the reference's bf16 model keeps its activations
+ * in bf16 (model.to(bfloat16), src/inference.py:522, :544).  The inference path above keeps
+ * fp32 GEMM outputs and split GEMM inputs instead (they hold the logits within the fp32
+ * reference's tolerance); these entries serve bf16-activation pipelines.
+ */
+
+/*
+ * K1, bf16 form.  Replaces: token_embed(ids) + example_embed(example_ids) and ln1
+ * (src/transformer.py:584-589, RMSNorm :37-48) for a bf16 model.
+ * tok_table / ex_table bf16 [vocab, d] / [n_examples, d]; example_ids as mdl_embed_rmsnorm
+ * (may be NULL).  x_out = bf16(tok + ex) and xn_out = bf16(x * rstd * gamma), rstd from the
+ * rounded x; both bf16 [rows, d] row-major.  d a multiple of 4, at most 2048.
+ */
+int mdl_embed_rmsnorm_bf16(const int64_t* ids, const int64_t* example_ids,
+                           const uint16_t* tok_table, const uint16_t* ex_table, int vocab,
+                           int n_examples, int rows, int row_len, int d, const float* gamma,
+                           float eps, uint16_t* x_out, uint16_t* xn_out, void* stream);
+
+/*
+ * K2, bf16 form: mdl_qkv_rope_cache on a bf16 qkv row (the output of a bf16 projection),
+ * rstd may be NULL (qkv already normed).  Same outputs, positions, cache slots and rounding.
+ * Replaces: the qkv split, RotaryEmbedding3D.apply_rotary and StaticKVCache.update
+ * (src/transformer.py:132-187, src/inference.py:84-92) for a bf16 model.  n_heads in
+ * {4, 12, 16, 20} (the reference presets).
+ */
+int mdl_qkv_rope_cache_bf16(const uint16_t* qkv, int64_t qkv_ld, const float* rstd,
+                            const int64_t* pos, const float* rope_tab, int batch, int seq,
+                            int n_heads, int head_dim, int max_x, int max_y, int max_z, int px,
+                            int py, int pz, float q_scale, uint16_t* q_out, uint16_t* k_cache,
+                            uint16_t* v_cache, int cache_slots, int slot0, void* stream);
+
+/*
+ * K3, bf16 form: gate_up bf16 [rows, 2*d_ff] (row stride ld, a multiple of 8) in, h_out bf16
+ * [rows, d_ff] = bf16(silu(rstd*g + b_g) * (rstd*u + b_u)) out.  rstd / biases may be NULL.
+ * Replaces: FeedForward.forward's silu(fc_gate(x)) * fc_up(x) (src/transformer.py:441-449)
+ * for a bf16 model.
+ */
+int mdl_swiglu_bf16(const uint16_t* gate_up, int64_t ld, const float* rstd,
+                    const float* bias_gate, const float* bias_up, int rows, int d_ff,
+                    uint16_t* h_out, void* stream);
+
+/*
  * K5 -- decode projection GEMM on split activations (bf16 MFMA, fp32 accumulation).
  * Replaces: the nn.Linear projections of one decode step -- qkv_proj (src/inference.py:439),
  *           out_proj (:453), fc_gate / fc_up and fc_down (FeedForward.forward,

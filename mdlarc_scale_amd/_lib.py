@@ -46,6 +46,12 @@ SIGNATURES: dict[str, tuple[object, list]] = {
                                           c_int, c_int, c_int, c_int, c_int, c_int, c_float, P, P,
                                           P, c_int, P]),
     "mdl_swiglu": (c_int, [P, c_int64, P, P, P, c_int, c_int, P, c_int, P]),
+    "mdl_embed_rmsnorm_bf16": (c_int, [P, P, P, P, c_int, c_int, c_int, c_int, c_int, P, c_float,
+                                       P, P, P]),
+    "mdl_qkv_rope_cache_bf16": (c_int, [P, c_int64, P, P, P, c_int, c_int, c_int, c_int, c_int,
+                                        c_int, c_int, c_int, c_int, c_int, c_float, P, P, P,
+                                        c_int, c_int, P]),
+    "mdl_swiglu_bf16": (c_int, [P, c_int64, P, P, P, c_int, c_int, P, P]),
     "mdl_gemm_split": (c_int, [P, c_int64, c_int, P, c_int64, c_int, P, c_int64, c_int, c_int,
                                c_int, c_int, P]),
     "mdl_gemm_split_swiglu": (c_int, [P, P, P, P, P, P, c_int, c_int, c_int, c_int, P]),

@@ -216,6 +216,62 @@ __global__ __launch_bounds__(256) void add_rmsnorm_kernel(
                                    rstd_out + m);
 }
 
+// Config-1 format of K1: bf16 activations in and out.  x = bf16(tok[t] + ex[e]) (the residual
+// a bf16 model holds) and xn = bf16(x * rstd * gamma) with rstd from the rounded x, both
+// [rows, d] row-major.  A half-wave owns a row and a lane 8 consecutive channels per pass of 256
+// (NP passes), so every load and store is 16 bytes and a half-wave instruction covers 512
+// contiguous bytes; the row's sum of squares is a 32-lane shuffle reduction.  The stores of x go
+// first; xn needs the row's rstd and follows the reduction.
+template <int NP, bool TAIL, bool HAS_EX>
+__global__ __launch_bounds__(256) void embed_rmsnorm_bf16_kernel(
+    const int64_t* __restrict__ ids, const int64_t* __restrict__ ex_ids,
+    const uint16_t* __restrict__ tok, const uint16_t* __restrict__ ex, int vocab, int n_ex,
+    int rows, int row_len, int d, const float* __restrict__ gamma, float eps,
+    uint16_t* __restrict__ x_out, uint16_t* __restrict__ xn_out) {
+  const int hl = threadIdx.x & 31;
+  const int64_t m = static_cast<int64_t>(blockIdx.x) * 8 + (threadIdx.x >> 5);
+  const bool live = m < rows;            // dead half-waves still take part in the shuffles
+  const int64_t mm = live ? m : 0;
+  float v[NP][8];
+  const uint16_t* trow = tok + clamp_id(ids[mm], vocab) * d;
+  const uint16_t* erow = HAS_EX ? ex + clamp_id(ex_ids[mm / row_len], n_ex) * d : nullptr;
+  float ss = 0.f;
+  uint16_t* xr = x_out + mm * d;
+#pragma unroll
+  for (int i = 0; i < NP; ++i) {
+    const int e = 8 * (hl + 32 * i);
+    if (!TAIL || e < d) {
+      unpack8(*reinterpret_cast<const uint4*>(trow + e), v[i]);
+      if (HAS_EX) {
+        float w[8];
+        unpack8(*reinterpret_cast<const uint4*>(erow + e), w);
+#pragma unroll
+        for (int j = 0; j < 8; ++j) v[i][j] += w[j];
+      }
+      const uint4 o = pack8(v[i]);
+      if (live) *reinterpret_cast<uint4*>(xr + e) = o;
+      unpack8(o, v[i]);                  // the norm sees the rounded residual
+#pragma unroll
+      for (int j = 0; j < 8; ++j) ss += v[i][j] * v[i][j];
+    }
+  }
+#pragma unroll
+  for (int o = 16; o > 0; o >>= 1) ss += __shfl_xor(ss, o, 32);
+  const float r = rsqrtf(ss / static_cast<float>(d) + eps);
+  uint16_t* nr = xn_out + mm * d;
+#pragma unroll
+  for (int i = 0; i < NP; ++i) {
+    const int e = 8 * (hl + 32 * i);
+    if ((!TAIL || e < d) && live) {
+      float g[8], t[8];
+      load8f(gamma + e, g);
+#pragma unroll
+      for (int j = 0; j < 8; ++j) t[j] = v[i][j] * r * g[j];
+      *reinterpret_cast<uint4*>(nr + e) = pack8(t);
+    }
+  }
+}
+
 constexpr int kMaxChunks = 8;  // d <= 2048
 
 // Instantiate F<NC, TAIL>::run for a row of d channels: NC = ceil(d / 256) chunks per lane,
@@ -250,6 +306,22 @@ struct LaunchEmbed {
     else if (has_xs) MDL_EMB(false, true);
     else MDL_EMB(false, false);
 #undef MDL_EMB
+  }
+};
+
+// NP = ceil(d / 256) passes of 32 lanes x 8 channels (the same count as dispatch_nc's chunks)
+template <int NP, bool TAIL>
+struct LaunchEmbedBf16 {
+  static void run(dim3 grid, hipStream_t s, bool has_ex, const int64_t* ids,
+                  const int64_t* ex_ids, const uint16_t* tok, const uint16_t* ex, int vocab,
+                  int n_ex, int rows, int row_len, int d, const float* gamma, float eps,
+                  uint16_t* x, uint16_t* xn) {
+    if (has_ex)
+      embed_rmsnorm_bf16_kernel<NP, TAIL, true><<<grid, 256, 0, s>>>(
+          ids, ex_ids, tok, ex, vocab, n_ex, rows, row_len, d, gamma, eps, x, xn);
+    else
+      embed_rmsnorm_bf16_kernel<NP, TAIL, false><<<grid, 256, 0, s>>>(
+          ids, ex_ids, tok, ex, vocab, n_ex, rows, row_len, d, gamma, eps, x, xn);
   }
 };
 
@@ -355,6 +427,26 @@ extern "C" int mdl_embed_rmsnorm(const int64_t* ids, const int64_t* example_ids,
                              static_cast<const uint16_t*>(tok_table),
                              static_cast<const uint16_t*>(ex_table), vocab, n_examples, rows,
                              row_len, d, gamma, eps, x_out, xs_out, rstd_out, layout);
+  return launch_status();
+}
+
+extern "C" int mdl_embed_rmsnorm_bf16(const int64_t* ids, const int64_t* example_ids,
+                                      const uint16_t* tok_table, const uint16_t* ex_table,
+                                      int vocab, int n_examples, int rows, int row_len, int d,
+                                      const float* gamma, float eps, uint16_t* x_out,
+                                      uint16_t* xn_out, void* stream) {
+  if (!ids || !gamma || !x_out || !xn_out) return MDL_ERR_NULL;
+  const bool use_ex = example_ids != nullptr;
+  const int tc = check_tables(tok_table, ex_table, use_ex, MDL_DTYPE_BF16, vocab, n_examples, d);
+  if (tc != MDL_OK) return tc;
+  if (rows < 0 || row_len <= 0 || d % 8 != 0) return MDL_ERR_SHAPE;
+  if (!aligned16(tok_table) || (use_ex && !aligned16(ex_table)) || !aligned16(x_out) ||
+      !aligned16(xn_out) || !aligned16(gamma))
+    return MDL_ERR_ALIGN;
+  if (rows == 0) return MDL_OK;
+  dispatch_nc<LaunchEmbedBf16>(d, dim3((rows + 7) / 8), static_cast<hipStream_t>(stream), use_ex,
+                               ids, example_ids, tok_table, ex_table, vocab, n_examples, rows,
+                               row_len, d, gamma, eps, x_out, xn_out);
   return launch_status();
 }
 

@@ -86,9 +86,27 @@ __global__ __launch_bounds__(256) void qkv_rope_cache_kernel(
 // chunk of the lane, so one cos/sin lookup pair per token serves all of them, and chunk i belongs
 // to q, k or v for i / (H/4) = 0, 1, 2.  All NCH loads are issued before the first store;
 // prompt-sized batches stream with the non-temporal hint (common.h, kStreamBytes).
-template <int NCH, bool NT>
+// 4 consecutive qkv channels as floats: an fp32 row (the GEMM output) or a bf16 one (the
+// config-1 format, 8 bytes per lane)
+template <bool NT>
+__device__ __forceinline__ float4 ld_qkv4(const float* p) {
+  return ld_f4<NT>(p);
+}
+template <bool NT>
+__device__ __forceinline__ float4 ld_qkv4(const uint16_t* p) {
+  uint2 u;
+  if constexpr (NT) {
+    const u32x2_t t = __builtin_nontemporal_load(reinterpret_cast<const u32x2_t*>(p));
+    u = make_uint2(t.x, t.y);
+  } else {
+    u = *reinterpret_cast<const uint2*>(p);
+  }
+  return make_float4(bf2f(u.x & 0xffffu), bf2f(u.x >> 16), bf2f(u.y & 0xffffu), bf2f(u.y >> 16));
+}
+
+template <int NCH, bool NT, typename TI = float>
 __global__ __launch_bounds__(256) void qkv_rope_cache_vec_kernel(
-    const float* __restrict__ qkv, int64_t ld, const float* __restrict__ rstd,
+    const TI* __restrict__ qkv, int64_t ld, const float* __restrict__ rstd,
     const int64_t* __restrict__ pos, const float* __restrict__ tab, RopeArgs ra, int64_t rows,
     int seq, float q_scale, uint16_t* __restrict__ q_out, uint16_t* __restrict__ kc,
     uint16_t* __restrict__ vc, int slots, int slot0, const int32_t* __restrict__ slot_dev,
@@ -97,11 +115,11 @@ __global__ __launch_bounds__(256) void qkv_rope_cache_vec_kernel(
   const int lane = threadIdx.x & 63;
   const int64_t m = static_cast<int64_t>(blockIdx.x) * 4 + (threadIdx.x >> 6);
   if (m >= rows) return;
-  const float* row = qkv + m * ld;
+  const TI* row = qkv + m * ld;
   float4 v[NCH];
 #pragma unroll
   for (int i = 0; i < NCH; ++i)
-    v[i] = ld_f4<NT>(row + 4 * (lane + 64 * i));
+    v[i] = ld_qkv4<NT>(row + 4 * (lane + 64 * i));
 
   float cs0, sn0, cs1, sn1;
   rope_cos_sin(2 * (lane & 15), pos + m * 3, tab, ra, cs0, sn0);
@@ -211,6 +229,48 @@ extern "C" int mdl_qkv_rope_cache(const float* qkv, int64_t qkv_ld, const float*
   return launch_k2(qkv, qkv_ld, rstd, pos, rope_tab, static_cast<int64_t>(batch) * seq, seq,
                    n_heads, ra, q_scale, q_out, k_cache, v_cache, cache_slots, slot0, slot_dev,
                    nullptr, nullptr, batch, static_cast<hipStream_t>(stream));
+}
+
+extern "C" int mdl_qkv_rope_cache_bf16(const uint16_t* qkv, int64_t qkv_ld, const float* rstd,
+                                       const int64_t* pos, const float* rope_tab, int batch,
+                                       int seq, int n_heads, int head_dim, int max_x, int max_y,
+                                       int max_z, int px, int py, int pz, float q_scale,
+                                       uint16_t* q_out, uint16_t* k_cache, uint16_t* v_cache,
+                                       int cache_slots, int slot0, void* stream) {
+  if (!qkv || !pos || !rope_tab || !q_out || !k_cache || !v_cache) return MDL_ERR_NULL;
+  if (head_dim != kHeadDim) return MDL_ERR_HEAD_DIM;
+  if (n_heads != 4 && n_heads != 12 && n_heads != 16 && n_heads != 20) return MDL_ERR_SHAPE;
+  if (max_x <= 0 || max_y <= 0 || max_z <= 0 || px < 0 || py < 0 || pz < 0 ||
+      px + py + pz != kHeadDim / 2 || qkv_ld < 3 * n_heads * 64 || batch < 0 || seq <= 0)
+    return MDL_ERR_SHAPE;
+  if (cache_slots <= 0 || slot0 < 0 || slot0 + seq > cache_slots) return MDL_ERR_CACHE;
+  if (!aligned8(qkv) || qkv_ld % 4 != 0 || !aligned16(q_out) || !aligned16(k_cache) ||
+      !aligned16(v_cache) || !aligned4(rope_tab))
+    return MDL_ERR_ALIGN;
+  const int64_t rows = static_cast<int64_t>(batch) * seq;
+  if (rows == 0) return MDL_OK;
+  if ((rows + 3) / 4 > 0x7fffffff) return MDL_ERR_SHAPE;
+  const RopeArgs ra{max_x, max_y, max_z, px, py, pz};
+  const dim3 grid(static_cast<unsigned>((rows + 3) / 4));
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  const bool nt = rows * n_heads * kHeadDim * 12 >= kStreamBytes;
+#define MDL_K2_BF(NCH)                                                                         \
+  if (nt)                                                                                     \
+    qkv_rope_cache_vec_kernel<NCH, true, uint16_t><<<grid, 256, 0, st>>>(                     \
+        qkv, qkv_ld, rstd, pos, rope_tab, ra, rows, seq, q_scale, q_out, k_cache, v_cache,    \
+        cache_slots, slot0, nullptr, nullptr, nullptr, batch);                                \
+  else                                                                                        \
+    qkv_rope_cache_vec_kernel<NCH, false, uint16_t><<<grid, 256, 0, st>>>(                    \
+        qkv, qkv_ld, rstd, pos, rope_tab, ra, rows, seq, q_scale, q_out, k_cache, v_cache,    \
+        cache_slots, slot0, nullptr, nullptr, nullptr, batch)
+  switch (n_heads) {
+    case 4: MDL_K2_BF(3); break;
+    case 12: MDL_K2_BF(9); break;
+    case 16: MDL_K2_BF(12); break;
+    default: MDL_K2_BF(15); break;
+  }
+#undef MDL_K2_BF
+  return launch_status();
 }
 
 extern "C" int mdl_qkv_rope_cache_packed(const float* qkv, int64_t qkv_ld, const float* rstd,

@@ -61,15 +61,77 @@ __global__ __launch_bounds__(256) void swiglu_kernel(const float* __restrict__ g
   }
 }
 
+// Config-1 format of K3: gate|up [rows, 2 d_ff] bf16 in, h [rows, d_ff] bf16 out (one rounding).
+// Block (y, x) covers channels 2048 y .. 2048 y + 2047 of row x, a thread 8 of them: one 16-byte
+// load from each half and one 16-byte store, no index division.
+template <bool NT>
+__global__ __launch_bounds__(256) void swiglu_bf16_kernel(const uint16_t* __restrict__ gu,
+                                                          int64_t ld,
+                                                          const float* __restrict__ rstd,
+                                                          const float* __restrict__ bg,
+                                                          const float* __restrict__ bu,
+                                                          int d_ff, uint16_t* __restrict__ h) {
+  const int64_t m = blockIdx.x;
+  const int c = 8 * (static_cast<int>(blockIdx.y) * 256 + static_cast<int>(threadIdx.x));
+  if (c >= d_ff) return;
+  const uint16_t* row = gu + m * ld;
+  float g[8], u[8], b1[8], b2[8];
+  // plain loads: as in K3, only the store takes the non-temporal hint
+  unpack8(*reinterpret_cast<const uint4*>(row + c), g);
+  unpack8(*reinterpret_cast<const uint4*>(row + d_ff + c), u);
+  if (bg) {
+    load8f(bg + c, b1);
+  } else {
+#pragma unroll
+    for (int i = 0; i < 8; ++i) b1[i] = 0.f;
+  }
+  if (bu) {
+    load8f(bu + c, b2);
+  } else {
+#pragma unroll
+    for (int i = 0; i < 8; ++i) b2[i] = 0.f;
+  }
+  const float r = rstd ? rstd[m] : 1.f;
+  float o[8];
+#pragma unroll
+  for (int i = 0; i < 8; ++i) o[i] = silu_mul(fmaf(r, g[i], b1[i]), fmaf(r, u[i], b2[i]));
+  st_u4<NT>(h + m * d_ff + c, pack8(o));
+}
+
 }  // namespace mdl
 
 using namespace mdl;
+
+extern "C" int mdl_swiglu_bf16(const uint16_t* gate_up, int64_t ld, const float* rstd,
+                               const float* bias_gate, const float* bias_up, int rows, int d_ff,
+                               uint16_t* h_out, void* stream) {
+  if (!gate_up || !h_out) return MDL_ERR_NULL;
+  // grid (rows, d_ff / 2048): at most 65535 column blocks
+  if (rows < 0 || d_ff <= 0 || d_ff % 8 != 0 || d_ff > 65535 * 2048 ||
+      ld < 2 * static_cast<int64_t>(d_ff))
+    return MDL_ERR_SHAPE;
+  if (!aligned16(gate_up) || ld % 8 != 0 || !aligned16(h_out) ||
+      (bias_gate && !aligned16(bias_gate)) || (bias_up && !aligned16(bias_up)))
+    return MDL_ERR_ALIGN;
+  if (rows == 0) return MDL_OK;
+  const dim3 grid(static_cast<unsigned>(rows), static_cast<unsigned>((d_ff + 2047) / 2048));
+  const hipStream_t st = static_cast<hipStream_t>(stream);
+  if (static_cast<int64_t>(rows) * d_ff * 6 >= kStreamBytes)
+    swiglu_bf16_kernel<true><<<grid, 256, 0, st>>>(gate_up, ld, rstd, bias_gate, bias_up, d_ff,
+                                                   h_out);
+  else
+    swiglu_bf16_kernel<false><<<grid, 256, 0, st>>>(gate_up, ld, rstd, bias_gate, bias_up, d_ff,
+                                                    h_out);
+  return launch_status();
+}
 
 extern "C" int mdl_swiglu(const float* gate_up, int64_t ld, const float* rstd,
                           const float* bias_gate, const float* bias_up, int rows, int d_ff,
                           uint16_t* h_out, int h_layout, void* stream) {
   if (!gate_up || !h_out) return MDL_ERR_NULL;
-  if (rows < 0 || d_ff <= 0 || d_ff % 8 != 0 || ld < 2 * static_cast<int64_t>(d_ff))
+  // the tiled store computes 2 * d_ff and d_ff + c in int: d_ff stays below 2^29
+  if (rows < 0 || d_ff <= 0 || d_ff % 8 != 0 || d_ff > (1 << 29) ||
+      ld < 2 * static_cast<int64_t>(d_ff))
     return MDL_ERR_SHAPE;
   if (h_layout != MDL_LAYOUT_ROWS && !(h_layout == MDL_LAYOUT_TILES && d_ff % 16 == 0))
     return MDL_ERR_SHAPE;
@@ -78,6 +140,7 @@ extern "C" int mdl_swiglu(const float* gate_up, int64_t ld, const float* rstd,
     return MDL_ERR_ALIGN;
   if (rows == 0) return MDL_OK;
   const int64_t items = static_cast<int64_t>(rows) * (d_ff / 8);
+  if ((items + 255) / 256 > 0x7fffffff) return MDL_ERR_SHAPE;
   const dim3 grid(static_cast<unsigned>((items + 255) / 256));
   const hipStream_t st = static_cast<hipStream_t>(stream);
   if (static_cast<int64_t>(rows) * d_ff * 12 >= kStreamBytes)

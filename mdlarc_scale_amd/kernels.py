@@ -220,6 +220,75 @@ def swiglu(gate_up: torch.Tensor, rstd: torch.Tensor | None, bias_gate: torch.Te
         _layout(tiled), _stream()), "mdl_swiglu")
 
 
+# --- config-1 format (bf16 activations in and out) ----------------------------------------------
+
+def embed_rmsnorm_bf16(ids: torch.Tensor, example_ids: torch.Tensor | None,
+                       tok_table: torch.Tensor, ex_table: torch.Tensor | None, row_len: int,
+                       gamma: torch.Tensor, eps: float, x_out: torch.Tensor,
+                       xn_out: torch.Tensor) -> None:
+    """x = bf16(tok[ids] + ex[example_ids]), xn = bf16(x * rstd * gamma), both [rows, d] bf16
+    (bf16 tables)."""
+    rows = ids.numel()
+    vocab, d = tok_table.shape
+    _need(ids, "ids", I64)
+    _need(example_ids, "example_ids", I64, optional=True)
+    _need(tok_table, "tok_table", BF16)
+    if example_ids is not None:
+        _need(ex_table, "ex_table", BF16)
+        if ex_table.shape[1] != d:
+            raise ValueError("example table width differs from token table width")
+        if example_ids.numel() * row_len < rows:
+            raise ValueError("example_ids shorter than the number of batch rows")
+    _need(gamma, "gamma", F32, d)
+    _need(x_out, "x_out", BF16, rows * d)
+    _need(xn_out, "xn_out", BF16, rows * d)
+    n_ex = ex_table.shape[0] if ex_table is not None else 0
+    _lib.check(_lib.lib().mdl_embed_rmsnorm_bf16(
+        _p(ids), _p(example_ids), _p(tok_table), _p(ex_table), vocab, n_ex, rows, row_len, d,
+        _p(gamma), eps, _p(x_out), _p(xn_out), _stream()), "mdl_embed_rmsnorm_bf16")
+
+
+def qkv_rope_cache_bf16(qkv: torch.Tensor, rstd: torch.Tensor | None, pos: torch.Tensor,
+                        rope_tab: torch.Tensor, rope_geom: tuple[int, int, int, int, int, int],
+                        batch: int, seq: int, n_heads: int, q_scale: float, q_out: torch.Tensor,
+                        k_cache: torch.Tensor, v_cache: torch.Tensor, slot0: int = 0) -> None:
+    """qkv_rope_cache on a bf16 qkv row [rows, 3d]."""
+    rows, d = batch * seq, n_heads * HEAD_DIM
+    _need(qkv, "qkv", BF16, rows * 3 * d)
+    if qkv.dim() != 2 or qkv.shape[1] != 3 * d:
+        raise ValueError(f"qkv must be [rows, {3 * d}]")
+    _need(rstd, "rstd", F32, rows, optional=True)
+    _need(pos, "pos", I64, rows * 3)
+    _need(rope_tab, "rope_tab", F32)
+    _need(q_out, "q_out", BF16, rows * d)
+    for name, c in (("k_cache", k_cache), ("v_cache", v_cache)):
+        _need(c, name, BF16)
+        if c.dim() != 4 or c.shape[0] != batch or c.shape[1] != n_heads or c.shape[3] != 64:
+            raise ValueError(f"{name} must be [batch, n_heads, slots, 64]")
+    mx, my, mz, px, py, pz = rope_geom
+    _lib.check(_lib.lib().mdl_qkv_rope_cache_bf16(
+        _p(qkv), qkv.shape[1], _p(rstd), _p(pos), _p(rope_tab), batch, seq, n_heads, HEAD_DIM,
+        mx, my, mz, px, py, pz, q_scale, _p(q_out), _p(k_cache), _p(v_cache), k_cache.shape[2],
+        slot0, _stream()), "mdl_qkv_rope_cache_bf16")
+
+
+def swiglu_bf16(gate_up: torch.Tensor, rstd: torch.Tensor | None,
+                bias_gate: torch.Tensor | None, bias_up: torch.Tensor | None,
+                h_out: torch.Tensor) -> None:
+    """h = bf16(silu(rstd*g + b_g) * (rstd*u + b_u)) from bf16 gate|up [rows, 2F] into
+    [rows, F] bf16."""
+    rows, two_f = gate_up.shape
+    f = two_f // 2
+    _need(gate_up, "gate_up", BF16)
+    _need(rstd, "rstd", F32, rows, optional=True)
+    _need(bias_gate, "bias_gate", F32, f, optional=True)
+    _need(bias_up, "bias_up", F32, f, optional=True)
+    _need(h_out, "h_out", BF16, rows * f)
+    _lib.check(_lib.lib().mdl_swiglu_bf16(
+        _p(gate_up), two_f, _p(rstd), _p(bias_gate), _p(bias_up), rows, f, _p(h_out),
+        _stream()), "mdl_swiglu_bf16")
+
+
 def gemm_split(a: torch.Tensor, w: torch.Tensor, out: torch.Tensor, k: int,
                a_tiled: bool = False, w_tiled: bool = False, tile: int = 0) -> None:
     """out[m, n] (fp32) = (a_hi + a_lo) @ w[:, :k]^T on the decode GEMM kernel (K5); m, n from

@@ -50,6 +50,17 @@ def test_argument_errors_are_reported_before_any_launch():
     # the tile layout needs whole 32-column blocks of the split row; layout codes are 0 / 1
     assert L.mdl_swiglu(fake, 16, None, None, None, 1, 8, fake, 1, None) == -3
     assert L.mdl_swiglu(fake, 32, None, None, None, 1, 16, fake, 2, None) == -3
+    # d_ff above 2^29 would overflow the tiled store's int column arithmetic; a grid above
+    # 2^31 - 1 blocks cannot be launched: both refused before any launch
+    assert L.mdl_swiglu(fake, 2 ** 31, None, None, None, 1, (1 << 29) + 8, fake, 0, None) == -3
+    assert L.mdl_swiglu(fake, 2 ** 29, None, None, None, 2 ** 31 - 1, 1 << 28, fake, 0,
+                        None) == -3
+    # the bf16 form: d_ff a multiple of 8, at most 65535 blocks of 2048 channels, ld % 8 == 0
+    assert L.mdl_swiglu_bf16(fake, 64, None, None, None, 1, 12, fake, None) == -3
+    assert L.mdl_swiglu_bf16(fake, 2 ** 30, None, None, None, 1, 65536 * 2048, fake, None) == -3
+    assert L.mdl_swiglu_bf16(fake, 36, None, None, None, 1, 16, fake, None) == -2
+    assert L.mdl_embed_rmsnorm_bf16(fake, None, fake, None, 14, 0, 1, 1, 36, fake, 1e-5, fake,
+                                    fake, None) == -3        # d % 8 != 0
     assert L.mdl_add_rmsnorm(fake, None, None, 1, 8, fake, 1e-5, fake, fake, 1, None) == -3
     assert L.mdl_qkv_rope_cache(fake, 192, None, fake, fake, 1, 4, 1, 64, 32, 32, 8, 10, 10, 12,
                                 0.125, fake, fake, fake, 4, 1, None, None) == -5

@@ -89,6 +89,33 @@ def test_embed_rmsnorm(d, table_dtype, with_ex):
     check_split(xs, x_ref.double() * gamma.double())
 
 
+@pytest.mark.parametrize("d", [128, 768, 800])
+@pytest.mark.parametrize("with_ex", [True, False])
+def test_embed_rmsnorm_bf16(d, with_ex):
+    """Config-1 format of K1: x is the bf16 rounding of the fp32 sum of the two bf16 rows
+    (exactly what a bf16 model's embedding add gives); xn = x * rstd * gamma from the rounded x,
+    against fp64 at bf16 resolution."""
+    g = torch.Generator().manual_seed(d + 1)
+    B, S, V, NE = 3, 37, 14, 5
+    tok = torch.randn(V, d, generator=g).to(torch.bfloat16)
+    ex = torch.randn(NE, d, generator=g).to(torch.bfloat16)
+    ids = torch.randint(0, V, (B, S), generator=g)
+    ex_ids = torch.randint(0, NE, (B,), generator=g)
+    gamma = 1 + 0.1 * torch.randn(d, generator=g)
+    x_ref = (tok.float()[ids] + (ex.float()[ex_ids][:, None] if with_ex else 0)).reshape(B * S, d)
+    x_ref = x_ref.to(torch.bfloat16)
+    xd = x_ref.double()
+    xn_ref = xd * torch.rsqrt((xd ** 2).mean(-1, keepdim=True) + 1e-5) * gamma.double()
+    x = torch.empty(B * S, d, device=DEV, dtype=torch.bfloat16)
+    xn = torch.empty_like(x)
+    K().embed_rmsnorm_bf16(ids.to(DEV).reshape(-1), ex_ids.to(DEV) if with_ex else None,
+                           tok.to(DEV), ex.to(DEV) if with_ex else None, S, gamma.to(DEV), 1e-5,
+                           x, xn)
+    torch.cuda.synchronize()
+    assert torch.equal(x.cpu(), x_ref)
+    close_bf16(xn, xn_ref.float(), atol=1e-6, rtol=8e-3)
+
+
 @pytest.mark.parametrize("d", [256, 768, 1024])
 def test_add_rmsnorm(d):
     g = torch.Generator().manual_seed(7)
@@ -149,6 +176,44 @@ def test_qkv_rope_cache(H, S, slot0):
     assert bool((vc[:, :, untouched.to(DEV)] == 7).all())
 
 
+@pytest.mark.parametrize("H,S,slot0,with_rstd", [(4, 33, 0, True), (12, 64, 10, True),
+                                                   (16, 5, 3, False), (20, 7, 100, True)])
+def test_qkv_rope_cache_bf16(H, S, slot0, with_rstd):
+    """Config-1 format of K2 (bf16 qkv in) against the oracle's 3D RoPE on the same bf16
+    values, at bf16 resolution; cache slots outside [slot0, slot0 + S) untouched."""
+    d = 64 * H
+    B, slots = 3, 200
+    cfg = _cfg(d, H)
+    g = torch.Generator().manual_seed(H * 100 + S + 1)
+    qkv = torch.randn(B * S, 3 * d, generator=g).to(torch.bfloat16)
+    rstd = 0.5 + torch.rand(B * S, generator=g)
+    pos = torch.randint(-3, 40, (B * S, 3), generator=g)
+    from mdlarc_scale_amd.transformer import RotaryEmbedding3D
+
+    rope = RotaryEmbedding3D(64, cfg.max_x, cfg.max_y, cfg.max_z)
+    tab = rope.device_table(DEV)
+    geom = (rope.max_x, rope.max_y, rope.max_z, rope.px, rope.py, rope.pz)
+    q = torch.empty(B * S, d, device=DEV, dtype=torch.bfloat16)
+    kc = torch.full((B, H, slots, 64), 7.0, device=DEV, dtype=torch.bfloat16)
+    vc = torch.full_like(kc, 7.0)
+    K().qkv_rope_cache_bf16(qkv.to(DEV), rstd.to(DEV) if with_rstd else None, pos.to(DEV), tab,
+                            geom, B, S, H, 0.125, q, kc, vc, slot0=slot0)
+    torch.cuda.synchronize()
+    r = rstd[:, None] if with_rstd else 1.0
+    y = (qkv.double() * r).view(B, S, 3, H, 64)
+    tabs = rp.rope3d_tables(cfg)
+    p3 = pos.view(B, S, 3)
+    q_ref = rp.apply_rope3d(y[:, :, 0], p3, tabs, cfg) * 0.125
+    k_ref = rp.apply_rope3d(y[:, :, 1], p3, tabs, cfg)
+    close_bf16(q.view(B, S, H, 64), q_ref.float())
+    close_bf16(kc[:, :, slot0:slot0 + S].permute(0, 2, 1, 3), k_ref.float())
+    close_bf16(vc[:, :, slot0:slot0 + S].permute(0, 2, 1, 3), y[:, :, 2].float())
+    untouched = torch.ones(slots, dtype=torch.bool)
+    untouched[slot0:slot0 + S] = False
+    assert bool((kc[:, :, untouched.to(DEV)] == 7).all())
+    assert bool((vc[:, :, untouched.to(DEV)] == 7).all())
+
+
 @pytest.mark.parametrize("H", [2, 4])       # generic kernel, whole-row kernel
 def test_qkv_rope_cache_device_slot(H):
     B, slots = 4, 50
@@ -198,6 +263,27 @@ def test_swiglu(F):
     K().swiglu(gu.to(DEV), None, None, None, h2)
     torch.cuda.synchronize()
     check_split(h2, rp.silu(gu[:, :F].double()) * gu[:, F:].double(), rtol=1e-5, atol=1e-6)
+
+
+@pytest.mark.parametrize("F,M", [(192, 77), (2048, 77), (3392, 5)])
+def test_swiglu_bf16(F, M):
+    """Config-1 format of K3: bf16 gate|up in, one bf16 h out, against the fp64 closed form at
+    bf16 resolution, with and without rstd and biases."""
+    g = torch.Generator().manual_seed(F + 2)
+    gu = (3 * torch.randn(M, 2 * F, generator=g)).to(torch.bfloat16)
+    r = 0.5 + torch.rand(M, generator=g)
+    bg = 0.1 * torch.randn(F, generator=g)
+    bu = 0.1 * torch.randn(F, generator=g)
+    h = torch.empty(M, F, device=DEV, dtype=torch.bfloat16)
+    K().swiglu_bf16(gu.to(DEV), r.to(DEV), bg.to(DEV), bu.to(DEV), h)
+    h2 = torch.empty_like(h)
+    K().swiglu_bf16(gu.to(DEV), None, None, None, h2)
+    torch.cuda.synchronize()
+    gd = gu.double()
+    a = gd[:, :F] * r[:, None].double() + bg.double()
+    b = gd[:, F:] * r[:, None].double() + bu.double()
+    close_bf16(h, (rp.silu(a) * b).float(), atol=1e-5, rtol=8e-3)
+    close_bf16(h2, (rp.silu(gd[:, :F]) * gd[:, F:]).float(), atol=1e-5, rtol=8e-3)
 
 
 # ---------------------------------------------------------------------------- streaming paths
@@ -964,11 +1050,14 @@ def test_tile_matrix_layout():
     assert torch.equal(got[off.reshape(-1)].view(48, cols), want)
 
 
-def test_producers_write_the_tile_layout():
+@pytest.mark.parametrize("d", [256, 768, 800])
+def test_producers_write_the_tile_layout(d):
     """Every producer of a decode GEMM input writes, with the tile layout selected, exactly
-    mdl_tile_matrix of its row-major output (padding rows left untouched)."""
-    g = torch.Generator().manual_seed(11)
-    B, d, F, H = 37, 256, 704, 4
+    mdl_tile_matrix of its row-major output (padding rows left untouched).  d = 256 is one
+    256-channel chunk per row, 768 three, 800 three and a tail (chunks after the first and the
+    tail are addressed from the first chunk's offsets)."""
+    g = torch.Generator().manual_seed(11 + d)
+    B, F, H = 37, 704, 4
 
     def both(fn, numel_rows, cols):
         outs = []
@@ -1014,6 +1103,8 @@ def test_producers_write_the_tile_layout():
          B, 2 * d)
     gu = torch.randn(B, 2 * F, generator=g).to(DEV)
     both(lambda buf, t: K().swiglu(gu, r, None, None, buf, tiled=t), B, 2 * F)
+    if d != 256:
+        return
     # decode attention, unfused and fused with K2, single split and split-K (combine kernel)
     from mdlarc_scale_amd.transformer import RotaryEmbedding3D
     rope = RotaryEmbedding3D(64, 32, 32, 8)
@@ -1033,6 +1124,27 @@ def test_producers_write_the_tile_layout():
         both(lambda buf, t: K().attn_decode_rope(qkv, rstd, posr, tab, geom, 0.125, kc.clone(),
                                                  vc.clone(), B, H, None, 0, None, t_pos, None,
                                                  ws, split_len, buf, tiled=t), B, 2 * H * 64)
+
+
+def test_add_rmsnorm_tiled_xs_half_block_width():
+    """mdl_add_rmsnorm's tiled split output at d = 784 (d = 16 mod 32): the lo half of a row
+    starts in the middle of a 32-column tile block, so its offsets are not the hi half's shifted
+    by whole blocks; exactly mdl_tile_matrix of the row-major output."""
+    g = torch.Generator().manual_seed(784)
+    B, d = 37, 784
+    gamma = (1 + 0.1 * torch.randn(d, generator=g)).to(DEV)
+    x0 = torch.randn(B, d, generator=g).to(DEV)
+    delta = torch.randn(B, d, generator=g).to(DEV)
+    r = torch.empty(B, device=DEV)
+    outs = []
+    for tiled in (False, True):
+        rows = K().tile_rows(B) if tiled else B
+        buf = torch.zeros(rows * 2 * d, device=DEV, dtype=torch.bfloat16)
+        x = x0.clone()
+        K().add_rmsnorm(x, delta, None, gamma, 1e-5, buf, r, tiled=tiled)
+        outs.append(buf)
+    torch.cuda.synchronize()
+    assert torch.equal(K().tile_matrix(outs[0].view(B, 2 * d)), outs[1])
 
 
 @pytest.mark.parametrize("m,f,k", [(256, 2048, 768), (37, 704, 256), (64, 3392, 1280)])
