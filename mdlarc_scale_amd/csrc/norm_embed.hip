@@ -221,8 +221,9 @@ __global__ __launch_bounds__(256) void add_rmsnorm_kernel(
 // [rows, d] row-major.  A half-wave owns a row and a lane 8 consecutive channels per pass of 256
 // (NP passes), so every load and store is 16 bytes and a half-wave instruction covers 512
 // contiguous bytes; the row's sum of squares is a 32-lane shuffle reduction.  The stores of x go
-// first; xn needs the row's rstd and follows the reduction.
-template <int NP, bool TAIL, bool HAS_EX>
+// first; xn needs the row's rstd and follows the reduction.  Prompt-sized outputs are stored
+// with the non-temporal hint (NT; measured at config 1: 4.6 -> 5.6 TB/s).
+template <int NP, bool TAIL, bool HAS_EX, bool NT>
 __global__ __launch_bounds__(256) void embed_rmsnorm_bf16_kernel(
     const int64_t* __restrict__ ids, const int64_t* __restrict__ ex_ids,
     const uint16_t* __restrict__ tok, const uint16_t* __restrict__ ex, int vocab, int n_ex,
@@ -249,7 +250,7 @@ __global__ __launch_bounds__(256) void embed_rmsnorm_bf16_kernel(
         for (int j = 0; j < 8; ++j) v[i][j] += w[j];
       }
       const uint4 o = pack8(v[i]);
-      if (live) *reinterpret_cast<uint4*>(xr + e) = o;
+      if (live) st_u4<NT>(xr + e, o);
       unpack8(o, v[i]);                  // the norm sees the rounded residual
 #pragma unroll
       for (int j = 0; j < 8; ++j) ss += v[i][j] * v[i][j];
@@ -267,7 +268,7 @@ __global__ __launch_bounds__(256) void embed_rmsnorm_bf16_kernel(
       load8f(gamma + e, g);
 #pragma unroll
       for (int j = 0; j < 8; ++j) t[j] = v[i][j] * r * g[j];
-      *reinterpret_cast<uint4*>(nr + e) = pack8(t);
+      st_u4<NT>(nr + e, pack8(t));
     }
   }
 }
@@ -316,11 +317,21 @@ struct LaunchEmbedBf16 {
                   const int64_t* ex_ids, const uint16_t* tok, const uint16_t* ex, int vocab,
                   int n_ex, int rows, int row_len, int d, const float* gamma, float eps,
                   uint16_t* x, uint16_t* xn) {
+    if (static_cast<int64_t>(rows) * d * 4 >= kStreamBytes) go<true>(grid, s, has_ex, ids,
+        ex_ids, tok, ex, vocab, n_ex, rows, row_len, d, gamma, eps, x, xn);
+    else go<false>(grid, s, has_ex, ids, ex_ids, tok, ex, vocab, n_ex, rows, row_len, d, gamma,
+                   eps, x, xn);
+  }
+  template <bool NT>
+  static void go(dim3 grid, hipStream_t s, bool has_ex, const int64_t* ids,
+                 const int64_t* ex_ids, const uint16_t* tok, const uint16_t* ex, int vocab,
+                 int n_ex, int rows, int row_len, int d, const float* gamma, float eps,
+                 uint16_t* x, uint16_t* xn) {
     if (has_ex)
-      embed_rmsnorm_bf16_kernel<NP, TAIL, true><<<grid, 256, 0, s>>>(
+      embed_rmsnorm_bf16_kernel<NP, TAIL, true, NT><<<grid, 256, 0, s>>>(
           ids, ex_ids, tok, ex, vocab, n_ex, rows, row_len, d, gamma, eps, x, xn);
     else
-      embed_rmsnorm_bf16_kernel<NP, TAIL, false><<<grid, 256, 0, s>>>(
+      embed_rmsnorm_bf16_kernel<NP, TAIL, false, NT><<<grid, 256, 0, s>>>(
           ids, ex_ids, tok, ex, vocab, n_ex, rows, row_len, d, gamma, eps, x, xn);
   }
 };

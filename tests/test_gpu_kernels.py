@@ -354,6 +354,35 @@ def test_streaming_paths_bit_identical():
         return q, kc[0].transpose(0, 1), vc[0].transpose(0, 1)
     both(k2)
 
+    # the config-1 (bf16 in and out) forms: K2 and K3 stream above 64 MiB at these sizes, K1's
+    # two bf16 outputs from 21,846 rows of 768 channels on
+    qkvb = qkv.to(torch.bfloat16)
+
+    def k2b(n):
+        q = torch.empty(n, d, device=DEV, dtype=torch.bfloat16)
+        kc = torch.zeros(1, H, n, 64, device=DEV, dtype=torch.bfloat16)
+        vc = torch.zeros_like(kc)
+        K().qkv_rope_cache_bf16(qkvb[:n], rs[:n], pos[:n], rope.device_table(DEV), geom, 1, n,
+                                H, 0.125, q, kc, vc, slot0=0)
+        return q, kc[0].transpose(0, 1), vc[0].transpose(0, 1)
+    both(k2b)
+    gub = gu.to(torch.bfloat16)
+
+    def k3b(n):
+        h = torch.empty(n, F, device=DEV, dtype=torch.bfloat16)
+        K().swiglu_bf16(gub[:n], rs[:n], bg, bg, h)
+        return (h,)
+    both(k3b)
+    big = 24_576
+    ids2 = torch.randint(0, V, (big,), device=DEV, generator=g)
+
+    def k1b(n):
+        x = torch.empty(n, d, device=DEV, dtype=torch.bfloat16)
+        xn = torch.empty_like(x)
+        K().embed_rmsnorm_bf16(ids2[:n], ex_ids[:1], tok, ex, n, gamma, 1e-5, x, xn)
+        return x, xn
+    both(k1b)
+
 
 # ---------------------------------------------------------------------------- K4a prefill
 
