@@ -300,6 +300,43 @@ int mdl_gemm_split_residual(const uint16_t* a, const uint16_t* w, float* x, cons
 int mdl_gemm_split_tiles(void);
 int mdl_gemm_split_pick(int m, int n, int k);
 /*
+ * K6 -- the projections of a prompt (prefill, forward): the K5 formulations at prompt-sized
+ * row counts, in 256 x 256 output tiles through LDS.  Weights are the tiled copies K5 uses
+ * (w: [n, k] MDL_LAYOUT_TILES; w_gu: interleaved gate / up, tiled).  Results are reproducible
+ * run to run; they differ from K5 and from hipBLASLt at fp32 rounding (another summation
+ * order).  k a positive multiple of 32, n (and 2 d_ff) of 16; pointers 16-byte aligned.
+ * Replaces: qkv_proj / out_proj (src/transformer.py:248-263) and fc_gate / fc_up / fc_down
+ *           (FeedForward.forward, :441-449) over a prompt (TinyTransformer.forward
+ *           :562-599, _prefill src/inference.py:383-424), with the RMSNorms (:45-48) and the
+ *           residual adds (TransformerBlock.forward :486-497) fused in.
+ *
+ * mdl_prefill_gemm_split:   out[i, j] = sum_k (a_hi + a_lo)[i, k] w[j, k] (fp32, row stride
+ *                           ldo); a split [m, 2k] in a_layout (row stride lda when row-major).
+ * mdl_prefill_gemm_norm:    out = split(x * gamma) . w^T and rstd_out[i] (may be NULL) =
+ *                           1 / sqrt(mean_k x[i, k]^2 + eps), x the fp32 residual stream [m, k]
+ *                           in MDL_LAYOUT_TILES: the ln1 + qkv_proj pair with rstd deferred to
+ *                           the consumer (as mdl_gemm_norm); k at most 2048.
+ * mdl_prefill_gemm_norm_swiglu: h = split(silu(rstd g + bias_gate) * (rstd u + bias_up)), g / u
+ *                           the gate / up rows of w_gu against split(x * gamma) (x as above);
+ *                           h_out tiled split [m, 2 d_ff] (ceil(m / 16) * 16 rows); biases may
+ *                           be NULL.
+ * mdl_prefill_gemm_split_residual: x[i, j] += sum_k (a_hi + a_lo)[i, k] w[j, k] (+ bias[j]) in
+ *                           place, x the fp32 residual stream [m, n] in MDL_LAYOUT_TILES (n a
+ *                           multiple of 32); bias may be NULL.
+ */
+int mdl_prefill_gemm_split(const uint16_t* a, int64_t lda, int a_layout, const uint16_t* w,
+                           float* out, int64_t ldo, int m, int n, int k, void* stream);
+int mdl_prefill_gemm_norm(const float* x, const float* gamma, float eps, const uint16_t* w,
+                          float* out, int64_t ldo, float* rstd_out, int m, int n, int k,
+                          void* stream);
+int mdl_prefill_gemm_norm_swiglu(const float* x, const float* gamma, float eps,
+                                 const uint16_t* w_gu, const float* bias_gate,
+                                 const float* bias_up, uint16_t* h_out, int m, int d_ff, int k,
+                                 void* stream);
+int mdl_prefill_gemm_split_residual(const uint16_t* a, int64_t lda, int a_layout,
+                                    const uint16_t* w, float* x, const float* bias, int m, int n,
+                                    int k, void* stream);
+/*
  * dst = src ([rows, cols] bf16, row stride ld) in MDL_LAYOUT_TILES, rows padded to a multiple
  * of 16 with zeros (dst holds ceil(rows / 16) * 16 * cols elements).  cols a multiple of 32.
  * Packs the decode weights once per model version (no reference counterpart: a layout step).
@@ -313,7 +350,8 @@ int mdl_tile_matrix(const uint16_t* src, int64_t ld, int rows, int cols, uint16_
  *           _build_sdpa_mask :372-380, is_causal=True) and in MultiHeadSelfAttention.forward
  *           (src/transformer.py:333-349, is_causal either way).
  * q: bf16 [batch, seq, n_heads, 64], already multiplied by the softmax scale.
- * out: split bf16 [batch*seq, 2*n_heads*64] (the out-projection GEMM input).
+ * out: split bf16 [batch*seq, 2*n_heads*64] (the out-projection GEMM input) in out_layout
+ *      (MDL_LAYOUT_ROWS, or MDL_LAYOUT_TILES with rows padded to a multiple of 16).
  * keys:    k_cache / v_cache slots [0, seq) of [batch, n_heads, cache_slots, 64].
  * Query i of row b sees key j iff j < seq, key_mask[b*seq + j] != 0 (key_mask may be NULL),
  * j >= kv_start[b] (kv_start may be NULL; it must not exclude a visible key) and, if causal,
@@ -322,12 +360,13 @@ int mdl_tile_matrix(const uint16_t* src, int64_t ld, int rows, int cols, uint16_
 int mdl_attn_prefill(const uint16_t* q, const uint16_t* k_cache, const uint16_t* v_cache,
                      int batch, int seq, int n_heads, int head_dim, int cache_slots,
                      const uint8_t* key_mask, const int32_t* kv_start, int causal,
-                     uint16_t* out, void* stream);
+                     uint16_t* out, int out_layout, void* stream);
 
 /*
  * K4a over packed query rows: as mdl_attn_prefill, for the queries i >= kv_start[b] of each row
  * only.  Query i of row b is row q_offset[b] + i - kv_start[b] of q (bf16 [rows, n_heads, 64])
- * and of out (split bf16 [rows, 2*n_heads*64]); no other row of out is written.  Keys are the
+ * and of out (split bf16 [rows, 2*n_heads*64], in out_layout); no other row of out is
+ * written.  Keys are the
  * cache slots as in mdl_attn_prefill; slots before kv_start[b] are never read into a product.
  * kv_start and q_offset are required; the caller sizes q / out to cover every row it names.
  * Replaces: the same SDPA call as mdl_attn_prefill (src/inference.py:409), without the padding
@@ -336,7 +375,8 @@ int mdl_attn_prefill(const uint16_t* q, const uint16_t* k_cache, const uint16_t*
 int mdl_attn_prefill_packed(const uint16_t* q, const uint16_t* k_cache, const uint16_t* v_cache,
                             int batch, int seq, int n_heads, int head_dim, int cache_slots,
                             const uint8_t* key_mask, const int32_t* kv_start,
-                            const int32_t* q_offset, int causal, uint16_t* out, void* stream);
+                            const int32_t* q_offset, int causal, uint16_t* out, int out_layout,
+                            void* stream);
 
 /*
  * K4c -- exact (fp32) causal attention for the lead queries of each row, after K4a.
@@ -350,14 +390,15 @@ int mdl_attn_prefill_packed(const uint16_t* q, const uint16_t* k_cache, const ui
  *   required), row q_offset[b] + i - kv_start[b].
  * Recomputes q, k, v of those tokens in fp32 (RMSNorm scale, 3D RoPE, softmax scale), applies
  * the key mask as mdl_attn_prefill does and overwrites the split output rows of the first
- * min(64, seq - kv_start[b]) queries; every other row of out is left as it is.
+ * min(64, seq - kv_start[b]) queries (out in out_layout, as K4a wrote it); every other row of
+ * out is left as it is.
  */
 int mdl_attn_prefill_lead(const float* qkv, int64_t qkv_ld, const float* rstd,
                           const int64_t* pos, const float* rope_tab, int max_x, int max_y,
                           int max_z, int px, int py, int pz, float q_scale, int batch, int seq,
                           int n_heads, int head_dim, const uint8_t* key_mask,
                           const int32_t* kv_start, const int32_t* q_offset, uint16_t* out,
-                          void* stream);
+                          int out_layout, void* stream);
 
 /*
  * K4b -- decode attention over the static cache (split-K flash decoding on bf16 MFMA: QK^T with

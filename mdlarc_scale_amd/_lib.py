@@ -60,13 +60,20 @@ SIGNATURES: dict[str, tuple[object, list]] = {
     "mdl_gemm_split_residual": (c_int, [P, P, P, P, c_int, c_int, c_int, c_int, P]),
     "mdl_gemm_split_tiles": (c_int, []),
     "mdl_gemm_split_pick": (c_int, [c_int, c_int, c_int]),
+    "mdl_prefill_gemm_split": (c_int, [P, c_int64, c_int, P, P, c_int64, c_int, c_int, c_int, P]),
+    "mdl_prefill_gemm_norm": (c_int, [P, P, c_float, P, P, c_int64, P, c_int, c_int, c_int, P]),
+    "mdl_prefill_gemm_norm_swiglu": (c_int, [P, P, c_float, P, P, P, P, c_int, c_int, c_int,
+                                             P]),
+    "mdl_prefill_gemm_split_residual": (c_int, [P, c_int64, c_int, P, P, P, c_int, c_int, c_int,
+                                                P]),
     "mdl_tile_matrix": (c_int, [P, c_int64, c_int, c_int, P, P]),
-    "mdl_attn_prefill": (c_int, [P, P, P, c_int, c_int, c_int, c_int, c_int, P, P, c_int, P, P]),
+    "mdl_attn_prefill": (c_int, [P, P, P, c_int, c_int, c_int, c_int, c_int, P, P, c_int, P,
+                                 c_int, P]),
     "mdl_attn_prefill_packed": (c_int, [P, P, P, c_int, c_int, c_int, c_int, c_int, P, P, P,
-                                        c_int, P, P]),
+                                        c_int, P, c_int, P]),
     "mdl_attn_prefill_lead": (c_int, [P, c_int64, P, P, P, c_int, c_int, c_int, c_int, c_int,
                                       c_int, c_float, c_int, c_int, c_int, c_int, P, P, P, P,
-                                      P]),
+                                      c_int, P]),
     "mdl_attn_decode_workspace_bytes": (c_int64, [c_int, c_int, c_int, c_int]),
     "mdl_attn_decode": (c_int, [P, P, P, c_int, c_int, c_int, c_int, P, c_int, P, P, P, c_int,
                                 P, P, c_int64, c_int, P, c_int, P]),

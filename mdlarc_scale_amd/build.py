@@ -32,6 +32,7 @@ SOURCES = [
     "head_state.hip",
     "prompt_build.hip",
     "split_gemm.hip",
+    "prefill_gemm.hip",
 ]
 
 FLAGS = [

@@ -45,7 +45,7 @@ __global__ __launch_bounds__(256, 3) void attn_prefill_kernel(
     const uint16_t* __restrict__ q, const uint16_t* __restrict__ kc,
     const uint16_t* __restrict__ vc, int S, int H, int slots, const uint8_t* __restrict__ kmask,
     const int32_t* __restrict__ kv_start, const int32_t* __restrict__ q_offset, int causal,
-    uint16_t* __restrict__ out, int nqt, int n_bh) {
+    uint16_t* __restrict__ out, int out_tiled, int nqt, int n_bh) {
   const int slot = blockIdx.x / kXcds;
   const int kq = slot / nqt;
   const int bh = blockIdx.x % kXcds + kXcds * kq;
@@ -211,24 +211,31 @@ __global__ __launch_bounds__(256, 3) void attn_prefill_kernel(
     }
   }
 
-  // output row (b, qi) holds 2*H*64 bf16: hi of every head, then lo of every head
+  // output row (b, qi) holds 2*H*64 bf16: hi of every head, then lo of every head (row-major,
+  // or in the bf16 MFMA tile layout, where each 4-column group stays contiguous)
   const int64_t d = static_cast<int64_t>(H) * kHeadDim;
 #pragma unroll
   for (int j = 0; j < 2; ++j) {
     if (qi[j] >= S || qi[j] < qlo) continue;
     const float l = lsum[j][0];     // every row of the ones product holds the query's sum
     const float inv = l > 0.f ? 1.f / l : 0.f;
-    uint16_t* op = out + (qbase + qi[j]) * 2 * d + h * kHeadDim;
+    const int64_t orow = qbase + qi[j];
 #pragma unroll
     for (int db = 0; db < 4; ++db) {
+      const int col = h * kHeadDim + 16 * db + 4 * g;
+      uint16_t* oh = out_tiled ? out + tile_off(orow, col, static_cast<int>(2 * d))
+                               : out + orow * 2 * d + col;
+      uint16_t* ol = out_tiled ? out + tile_off(orow, static_cast<int>(d) + col,
+                                                static_cast<int>(2 * d))
+                               : oh + d;
       const float t[4] = {o[j][db][0] * inv, o[j][db][1] * inv, o[j][db][2] * inv,
                           o[j][db][3] * inv};
       // v_cvt_pk_bf16_f32 rounds to nearest even, as f2bf does for every non-NaN value
       const bf16x4_t hv = {(__bf16)t[0], (__bf16)t[1], (__bf16)t[2], (__bf16)t[3]};
       const bf16x4_t lv = {(__bf16)(t[0] - (float)hv[0]), (__bf16)(t[1] - (float)hv[1]),
                            (__bf16)(t[2] - (float)hv[2]), (__bf16)(t[3] - (float)hv[3])};
-      *reinterpret_cast<bf16x4_t*>(op + 16 * db + 4 * g) = hv;
-      *reinterpret_cast<bf16x4_t*>(op + d + 16 * db + 4 * g) = lv;
+      *reinterpret_cast<bf16x4_t*>(oh) = hv;
+      *reinterpret_cast<bf16x4_t*>(ol) = lv;
     }
   }
 }
@@ -257,7 +264,7 @@ __global__ __launch_bounds__(256) void attn_lead_kernel(
     const float* __restrict__ qkv, int64_t ld, const float* __restrict__ rstd,
     const int64_t* __restrict__ pos, const float* __restrict__ tab, RopeArgs ra, float q_scale,
     int S, int H, const uint8_t* __restrict__ kmask, const int32_t* __restrict__ kv_start,
-    const int32_t* __restrict__ q_offset, uint16_t* __restrict__ out) {
+    const int32_t* __restrict__ q_offset, uint16_t* __restrict__ out, int out_tiled) {
   const int bh = blockIdx.x;
   const int b = bh / H, h = bh - b * H;
   const int kstart = kv_start ? min(max(kv_start[b], 0), S) : 0;
@@ -352,13 +359,19 @@ __global__ __launch_bounds__(256) void attn_lead_kernel(
     }
   }
   const float inv = l > 0.f ? 1.f / l : 0.f;   // no visible key: 0, as in K4a
-  uint16_t* op = out + (row0 + r) * 2 * d + h * kHeadDim + 16 * part;
+  const int64_t orow = row0 + r;
+  const int col0 = h * kHeadDim + 16 * part;
 #pragma unroll
   for (int e = 0; e < 16; e += 2) {
     uint32_t hi, lo;
     split_bf2(o[e] * inv, o[e + 1] * inv, hi, lo);
-    *reinterpret_cast<uint32_t*>(op + e) = hi;
-    *reinterpret_cast<uint32_t*>(op + d + e) = lo;
+    uint16_t* oh = out_tiled ? out + tile_off(orow, col0 + e, static_cast<int>(2 * d))
+                             : out + orow * 2 * d + col0 + e;
+    uint16_t* ol = out_tiled ? out + tile_off(orow, static_cast<int>(d) + col0 + e,
+                                              static_cast<int>(2 * d))
+                             : oh + d;
+    *reinterpret_cast<uint32_t*>(oh) = hi;
+    *reinterpret_cast<uint32_t*>(ol) = lo;
   }
 }
 
@@ -371,8 +384,9 @@ namespace mdl {
 int launch_prefill(const uint16_t* q, const uint16_t* k_cache, const uint16_t* v_cache,
                    int batch, int seq, int n_heads, int head_dim, int cache_slots,
                    const uint8_t* key_mask, const int32_t* kv_start, const int32_t* q_offset,
-                   int causal, uint16_t* out, hipStream_t st) {
+                   int causal, uint16_t* out, int out_layout, hipStream_t st) {
   if (!q || !k_cache || !v_cache || !out) return MDL_ERR_NULL;
+  if (out_layout != MDL_LAYOUT_ROWS && out_layout != MDL_LAYOUT_TILES) return MDL_ERR_SHAPE;
   if (head_dim != kHeadDim) return MDL_ERR_HEAD_DIM;
   if (batch < 0 || seq < 0 || n_heads <= 0 || n_heads > 65535 || batch > 65535)
     return MDL_ERR_SHAPE;
@@ -386,7 +400,8 @@ int launch_prefill(const uint16_t* q, const uint16_t* k_cache, const uint16_t* v
   if (blocks > 0x7fffffff) return MDL_ERR_SHAPE;
   attn_prefill_kernel<<<static_cast<unsigned>(blocks), 256, 0, st>>>(
       q, k_cache, v_cache, seq, n_heads, cache_slots, key_mask, kv_start, q_offset,
-      causal ? 1 : 0, out, static_cast<int>(nqt), static_cast<int>(heads));
+      causal ? 1 : 0, out, out_layout == MDL_LAYOUT_TILES ? 1 : 0, static_cast<int>(nqt),
+      static_cast<int>(heads));
   return launch_status();
 }
 
@@ -396,9 +411,9 @@ extern "C" int mdl_attn_prefill(const uint16_t* q, const uint16_t* k_cache,
                                 const uint16_t* v_cache, int batch, int seq, int n_heads,
                                 int head_dim, int cache_slots, const uint8_t* key_mask,
                                 const int32_t* kv_start, int causal, uint16_t* out,
-                                void* stream) {
+                                int out_layout, void* stream) {
   return launch_prefill(q, k_cache, v_cache, batch, seq, n_heads, head_dim, cache_slots,
-                        key_mask, kv_start, nullptr, causal, out,
+                        key_mask, kv_start, nullptr, causal, out, out_layout,
                         static_cast<hipStream_t>(stream));
 }
 
@@ -406,10 +421,11 @@ extern "C" int mdl_attn_prefill_packed(const uint16_t* q, const uint16_t* k_cach
                                        const uint16_t* v_cache, int batch, int seq, int n_heads,
                                        int head_dim, int cache_slots, const uint8_t* key_mask,
                                        const int32_t* kv_start, const int32_t* q_offset,
-                                       int causal, uint16_t* out, void* stream) {
+                                       int causal, uint16_t* out, int out_layout,
+                                       void* stream) {
   if (!kv_start || !q_offset) return MDL_ERR_NULL;
   return launch_prefill(q, k_cache, v_cache, batch, seq, n_heads, head_dim, cache_slots,
-                        key_mask, kv_start, q_offset, causal, out,
+                        key_mask, kv_start, q_offset, causal, out, out_layout,
                         static_cast<hipStream_t>(stream));
 }
 
@@ -418,8 +434,10 @@ extern "C" int mdl_attn_prefill_lead(const float* qkv, int64_t qkv_ld, const flo
                                      int max_y, int max_z, int px, int py, int pz, float q_scale,
                                      int batch, int seq, int n_heads, int head_dim,
                                      const uint8_t* key_mask, const int32_t* kv_start,
-                                     const int32_t* q_offset, uint16_t* out, void* stream) {
+                                     const int32_t* q_offset, uint16_t* out, int out_layout,
+                                     void* stream) {
   if (!qkv || !rstd || !pos || !rope_tab || !out) return MDL_ERR_NULL;
+  if (out_layout != MDL_LAYOUT_ROWS && out_layout != MDL_LAYOUT_TILES) return MDL_ERR_SHAPE;
   if (q_offset && !kv_start) return MDL_ERR_NULL;
   if (head_dim != kHeadDim) return MDL_ERR_HEAD_DIM;
   if (batch < 0 || seq < 0 || n_heads <= 0 || max_x <= 0 || max_y <= 0 || max_z <= 0 ||
@@ -434,6 +452,6 @@ extern "C" int mdl_attn_prefill_lead(const float* qkv, int64_t qkv_ld, const flo
   const RopeArgs ra{max_x, max_y, max_z, px, py, pz};
   attn_lead_kernel<<<static_cast<unsigned>(blocks), 256, 0, static_cast<hipStream_t>(stream)>>>(
       qkv, qkv_ld, rstd, pos, rope_tab, ra, q_scale, seq, n_heads, key_mask, kv_start, q_offset,
-      out);
+      out, out_layout == MDL_LAYOUT_TILES ? 1 : 0);
   return launch_status();
 }

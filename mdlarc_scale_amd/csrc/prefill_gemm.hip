@@ -1,0 +1,474 @@
+// K6: split-activation GEMM for prompt-sized row counts (prefill) on bf16 MFMA (gfx950), with
+// the RMSNorm of its input in the prologue and the SwiGLU gate or the residual add in the
+// epilogue, so a prefill layer needs no fp32 gate / up round trip and no add+RMSNorm pass.
+//
+//   acc[m, n] (fp32) = sum_k (a_hi[m, k] + a_lo[m, k]) * w[n, k],   k < K
+//
+// w: bf16 [N, K] in the MFMA tile layout (MDL_LAYOUT_TILES, the decode copies of the weights).
+// a (AMODE): A_ROWS  split [M, 2K] row-major (hi in [0, K), lo in [K, 2K)), row stride lda;
+//            A_TILES the same matrix in the tile layout;
+//            A_NORM  split(x * gamma) of the fp32 residual stream x [M, K] in the fp32 tile
+//                    layout, formed after the LDS read; the block sees whole rows, so it sums
+//                    x^2 and has rstd.
+// epilogue (EPI): E_STORE     out = acc (fp32 row-major; with A_NORM also rstd[m]);
+//                 E_SWIGLU    h = split(silu(rstd g + b_g) * (rstd u + b_u)) from the gate / up
+//                             accumulator pairs (weights with 16-row gate / up blocks
+//                             interleaved), h [M, 2F] in the tile layout;
+//                 E_RESIDUAL  x[m, n] += acc (+ bias[n]) in place, x [M, N] in the fp32 tile
+//                             layout.
+//
+// Block: a 256 x 256 output tile (activation rows x weight rows) on 8 waves, each owning 32 MFMA
+// tiles (128 fp32 accumulators per lane): 64 rows x 128 weight rows in a 4 x 2 wave grid for the
+// split forms, 32 rows x 256 weight rows (8 x 1) for A_NORM.  K advances 32 at a time through a ring of three LDS stages of
+// 48 KB.  A stage holds 16 weight fragments and 32 activation fragments of 1 KB in MFMA lane
+// order (bf16 {hi, lo} of 16 row blocks; for A_NORM the fp32 x of 16 row blocks in the fp32 tile
+// layout, split after the read), so every fragment read is one conflict-free 16-byte LDS read
+// per lane.  Global data goes straight to LDS (global_load_lds_dwordx4, 16 bytes per lane, one
+// kilobyte per wave instruction), issued two k-steps ahead; nothing is staged in registers, and
+// a step ends with one barrier after an exact vmcnt wait for the next stage's loads.  Blocks are
+// persistent (one per CU, each walking its tiles), and the load ring runs on across tile
+// boundaries, so a tile's epilogue overlaps the next tile's first loads.
+// Every weight fragment feeds two MFMAs (hi and lo rows), as in K5.
+// Blocks are numbered so that an XCD (block i runs on XCD i mod 8) takes a contiguous run of
+// tiles, row tile major: the N tiles of one row tile share its activation rows in one L2.
+// Summation order is fixed (k-steps in order, hi before lo), so results are reproducible.
+#include <algorithm>
+
+#include "common.h"
+#include "mfma.h"
+
+namespace mdl {
+
+namespace {
+
+constexpr int kBM = 256, kBN = 256;
+constexpr int kWaves = 8, kThreads = 64 * kWaves;
+constexpr int kAFrags = (kBM / 16) * 2;   // {hi, lo} fragments of 16 row blocks
+constexpr int kWFrags = kBN / 16;
+constexpr int kStage = (kAFrags + kWFrags) * 1024;   // bytes of one LDS stage
+constexpr int kRing = 3;                             // LDS stages (loads run 2 k-steps ahead)
+constexpr int kLoadsPerStage = 6;                    // DMA instructions per thread per stage
+constexpr int kMaxNormK = 2048;                      // A_NORM: gamma lives in LDS
+
+enum AMode { A_ROWS = 0, A_TILES = 1, A_NORM = 2 };
+enum Epi { E_STORE = 0, E_SWIGLU = 1, E_RESIDUAL = 2 };
+
+struct Args {
+  const uint16_t* a;   // A_ROWS / A_TILES
+  int64_t lda;
+  const float* x;      // A_NORM: [M, K] in the fp32 tile layout
+  const float* gamma;
+  float eps;
+  const uint16_t* w;   // tiled [N, K]
+  float* out;          // E_STORE
+  int64_t ldo;
+  float* rstd_out;     // E_STORE with A_NORM (may be NULL)
+  const float* bias_a; // E_SWIGLU gate bias / E_RESIDUAL bias (may be NULL)
+  const float* bias_b; // E_SWIGLU up bias (may be NULL)
+  uint16_t* h;         // E_SWIGLU: tiled split [M, 2 d_ff]
+  int d_ff;
+  float* x_res;        // E_RESIDUAL: [M, N] in the fp32 tile layout
+  int M, N, K, tiles_n, tiles, per_xcd;
+};
+
+// LDS byte address of a pointer into __shared__ memory
+__device__ __forceinline__ uint32_t lds_addr(const void* p) {
+  return static_cast<uint32_t>(
+      reinterpret_cast<uintptr_t>((const __attribute__((address_space(3))) void*)(p)));
+}
+
+// 16 bytes per lane from global memory straight into LDS: lane l's bytes land at
+// lds + 16 l (lds wave-uniform, through M0).  Issued as inline assembly so that the compiler
+// adds no waits of its own for it: the main loop counts these loads itself (vmcnt), and the
+// kernel issues no other global loads while any is in flight.
+__device__ __forceinline__ void dma16(const void* src, uint32_t lds) {
+  asm volatile("s_mov_b32 m0, %1\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, off"
+               :: "v"(src), "s"(lds) : "memory");
+}
+
+// Wait until at most N of this wave's global loads are in flight, then a block barrier that
+// also waits for this wave's LDS traffic; the memory clobbers keep the compiler from moving
+// LDS accesses across either.
+template <int N>
+__device__ __forceinline__ void stage_barrier() {
+  asm volatile("s_waitcnt vmcnt(%0)\n\ts_waitcnt lgkmcnt(0)\n\ts_barrier" :: "n"(N) : "memory");
+}
+
+template <int AMODE, int EPI>
+__global__ __launch_bounds__(kThreads, 1) void prefill_gemm_kernel(const Args p) {
+  constexpr int kGammaBytes = AMODE == A_NORM ? kMaxNormK * 4 : 0;
+  __shared__ __align__(16) uint8_t lds[kRing * kStage + kGammaBytes];
+  __shared__ float rstd_s[kBM];
+  // Persistent blocks: XCD x = blockIdx % 8 owns logical tiles [x per_xcd, (x + 1) per_xcd), row
+  // tile major; its bpx blocks take every bpx-th of them, so the XCD's CUs work on consecutive
+  // tiles at any time.
+  const int bpx = gridDim.x >> 3;
+  const int t_lo = (blockIdx.x & 7) * p.per_xcd;
+  const int t_hi = min(t_lo + p.per_xcd, p.tiles);
+  const int first = t_lo + (blockIdx.x >> 3);
+  if (first >= t_hi) return;   // whole block, before any barrier
+  const int M = p.M, N = p.N, K = p.K, nk = K >> 5;
+  const int total = (t_hi - first + bpx - 1) / bpx * nk;   // k-steps over this block's tiles
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  // wave grid WMW x WNW over the tile: wave (wm, wn) owns FM row blocks and FN weight fragments.
+  // The A_NORM forms split x * gamma in registers after the LDS read, so there every row block
+  // belongs to one wave (8 x 1) and is converted once; the split forms use 4 x 2 (8 activation
+  // and 8 weight fragment reads per wave and k-step).
+  constexpr int WMW = AMODE == A_NORM ? 8 : 4, WNW = kWaves / WMW;
+  constexpr int FM = kBM / 16 / WMW, FN = kBN / 16 / WNW;
+  const int wm = wave % WMW, wn = wave / WMW;
+  const int c = lane & 15, g = lane >> 4;
+  const int last_nb = (N + 15) / 16 - 1, last_mb = (M + 15) / 16 - 1;
+  const uint32_t lds0 = lds_addr(lds);
+
+  // The loads of k-step s of the tile at (m0, n0) into ring stage b.  Wave w copies weight
+  // fragments 8 j + w (j = 0, 1: row block n0 / 16 + 8 j + w) and activation fragments f = 8 j +
+  // w (j = 0..3): row block f / 2, part f % 2 (hi / lo; for A_NORM the first or second kilobyte of
+  // the fp32 16 x 32 block, lane l's columns 0..3 or 4..7).  Every copy is one contiguous
+  // kilobyte per wave, except row-major A.  Row blocks past M or N load valid memory (clamped to
+  // the last; tile-layout buffers hold its padding rows); their results are never stored.
+  auto issue = [&](int m0, int n0, int s, int b) {
+    const uint32_t base = lds0 + b * kStage;
+#pragma unroll
+    for (int j = 0; j < 2; ++j) {
+      const int nb = min(n0 / 16 + 8 * j + wave, last_nb);
+      dma16(p.w + (static_cast<int64_t>(nb) * nk + s) * 512 + 8 * lane,
+            __builtin_amdgcn_readfirstlane(base + (kAFrags + 8 * j + wave) * 1024));
+    }
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const int f = 8 * j + wave, rb = f >> 1, part = f & 1;
+      const void* src;
+      if constexpr (AMODE == A_NORM) {
+        const int64_t blk = static_cast<int64_t>(min(m0 / 16 + rb, last_mb)) * nk + s;
+        src = p.x + blk * 512 + 256 * part + 4 * lane;
+      } else if constexpr (AMODE == A_TILES) {
+        const int64_t blk = static_cast<int64_t>(min(m0 / 16 + rb, last_mb)) * 2 * nk;
+        src = p.a + (blk + part * nk + s) * 512 + 8 * lane;
+      } else {
+        const int row = min(m0 + 16 * rb + c, M - 1);
+        src = p.a + static_cast<int64_t>(row) * p.lda + part * K + 32 * s + 8 * g;
+      }
+      dma16(src, __builtin_amdgcn_readfirstlane(base + (8 * j + wave) * 1024));
+    }
+  };
+
+  const float* gam_s = reinterpret_cast<const float*>(lds + kRing * kStage);
+  if constexpr (AMODE == A_NORM) {
+    float* gw = reinterpret_cast<float*>(lds + kRing * kStage);
+    for (int i = tid; i < K; i += kThreads) gw[i] = p.gamma[i];
+    __syncthreads();   // before any stage load is in flight (it waits for every load)
+  }
+
+  f32x4_t acc[FN][FM];
+  float ss[FM];   // A_NORM: this lane's part of sum(x^2) of row 16 (FM wm + j) + c
+  auto reset = [&]() {
+#pragma unroll
+    for (int i = 0; i < FN; ++i)
+#pragma unroll
+      for (int j = 0; j < FM; ++j) acc[i][j] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int j = 0; j < FM; ++j) ss[j] = 0.f;
+  };
+
+  auto compute = [&](int s, int b) {
+    const uint8_t* base = lds + b * kStage;
+    bf16x8_t ah[FM], al[FM];
+    if constexpr (AMODE == A_NORM) {
+      // x of row 16 (FM wm + j) + c, columns 8 g .. 8 g + 7: the split of x * gamma, as the
+      // norm kernels write it (t rounded, then split)
+      const float4 g0 = *reinterpret_cast<const float4*>(gam_s + 32 * s + 8 * g);
+      const float4 g1 = *reinterpret_cast<const float4*>(gam_s + 32 * s + 8 * g + 4);
+      const float ge[8] = {g0.x, g0.y, g0.z, g0.w, g1.x, g1.y, g1.z, g1.w};
+#pragma unroll
+      for (int j = 0; j < FM; ++j) {
+        const float4 x0 =
+            *reinterpret_cast<const float4*>(base + (2 * (FM * wm + j)) * 1024 + 16 * lane);
+        const float4 x1 =
+            *reinterpret_cast<const float4*>(base + (2 * (FM * wm + j) + 1) * 1024 + 16 * lane);
+        const float xe[8] = {x0.x, x0.y, x0.z, x0.w, x1.x, x1.y, x1.z, x1.w};
+        float t[8];
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+          t[e] = xe[e] * ge[e];
+          ss[j] = fmaf(xe[e], xe[e], ss[j]);
+        }
+        uint4 hi, lo;
+        split8(t, hi, lo);
+        ah[j] = as_bf16x8(hi);
+        al[j] = as_bf16x8(lo);
+      }
+    } else {
+#pragma unroll
+      for (int j = 0; j < FM; ++j) {
+        ah[j] =
+            *reinterpret_cast<const bf16x8_t*>(base + (2 * (FM * wm + j)) * 1024 + 16 * lane);
+        al[j] = *reinterpret_cast<const bf16x8_t*>(base + (2 * (FM * wm + j) + 1) * 1024 +
+                                                   16 * lane);
+      }
+    }
+#pragma unroll
+    for (int i = 0; i < FN; ++i) {
+      const bf16x8_t wf = *reinterpret_cast<const bf16x8_t*>(
+          base + (kAFrags + FN * wn + i) * 1024 + 16 * lane);
+#pragma unroll
+      for (int j = 0; j < FM; ++j) {
+        acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(wf, ah[j], acc[i][j], 0, 0, 0);
+        acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(wf, al[j], acc[i][j], 0, 0, 0);
+      }
+    }
+  };
+
+  // the finished tile at (m0, n0): lane (c, g) of accumulator tile (i, j) holds
+  // acc[row 16 (FM wm + j) + c][weight rows 16 (FN wn + i) + 4 g ..]
+  auto epilogue = [&](int m0, int n0) {
+    if constexpr (AMODE == A_NORM) {
+      // the four lane groups of a row in a fixed order (one wave per row block: WNW = 1); the
+      // barrier waits for LDS only, so the next tile's loads stay in flight (rstd_s was last read
+      // in the previous tile's epilogue, nk >= 1 stage barriers ago)
+#pragma unroll
+      for (int j = 0; j < FM; ++j) {
+        float v = ss[j];
+        v += __shfl_xor(v, 16, kWave);
+        v += __shfl_xor(v, 32, kWave);
+        if (g == 0) rstd_s[16 * (FM * wm + j) + c] = rsqrtf(v / static_cast<float>(K) + p.eps);
+      }
+      asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
+      if constexpr (EPI == E_STORE) {
+        if (p.rstd_out && n0 == 0 && tid < kBM && m0 + tid < M) p.rstd_out[m0 + tid] = rstd_s[tid];
+      }
+    }
+    if constexpr (EPI == E_SWIGLU) {
+      const int F = p.d_ff;
+#pragma unroll
+      for (int pb = 0; pb < FN / 2; ++pb) {
+        // gate fragment 2 pb, up fragment 2 pb + 1: channels 16 (n0 / 32 + FN wn / 2 + pb) + 4 g
+        const int ch = 16 * (n0 / 32 + FN / 2 * wn + pb) + 4 * g;
+        if (2 * ch >= N) continue;
+        const float4 bg = p.bias_a ? *reinterpret_cast<const float4*>(p.bias_a + ch)
+                                   : make_float4(0.f, 0.f, 0.f, 0.f);
+        const float4 bu = p.bias_b ? *reinterpret_cast<const float4*>(p.bias_b + ch)
+                                   : make_float4(0.f, 0.f, 0.f, 0.f);
+#pragma unroll
+        for (int j = 0; j < FM; ++j) {
+          const int r = 16 * (FM * wm + j) + c;
+          const int m = m0 + r;
+          if (m >= M) continue;
+          const float rs = AMODE == A_NORM ? rstd_s[r] : 1.f;
+          const f32x4_t gs = acc[2 * pb][j], us = acc[2 * pb + 1][j];
+          // the arithmetic of K3 (swiglu.hip)
+          const float o[4] = {silu_mul(fmaf(rs, gs[0], bg.x), fmaf(rs, us[0], bu.x)),
+                              silu_mul(fmaf(rs, gs[1], bg.y), fmaf(rs, us[1], bu.y)),
+                              silu_mul(fmaf(rs, gs[2], bg.z), fmaf(rs, us[2], bu.z)),
+                              silu_mul(fmaf(rs, gs[3], bg.w), fmaf(rs, us[3], bu.w))};
+          uint2 hi, lo;
+          split4(o, hi, lo);
+          *reinterpret_cast<uint2*>(p.h + tile_off(m, ch, 2 * F)) = hi;
+          *reinterpret_cast<uint2*>(p.h + tile_off(m, F + ch, 2 * F)) = lo;
+        }
+      }
+    } else {
+#pragma unroll
+      for (int i = 0; i < FN; ++i) {
+        const int n = n0 + 16 * (FN * wn + i) + 4 * g;
+        if (n >= N) continue;
+        float4 bv = make_float4(0.f, 0.f, 0.f, 0.f);
+        if constexpr (EPI == E_RESIDUAL) {
+          if (p.bias_a) bv = *reinterpret_cast<const float4*>(p.bias_a + n);
+        }
+#pragma unroll
+        for (int j = 0; j < FM; ++j) {
+          const int m = m0 + 16 * (FM * wm + j) + c;
+          if (m >= M) continue;
+          const f32x4_t v = acc[i][j];
+          if constexpr (EPI == E_RESIDUAL) {
+            // x + delta, then + bias: the order of the add+RMSNorm kernel it replaces
+            float4* xr = reinterpret_cast<float4*>(p.x_res + tile_off32(m, n, N));
+            float4 xv = *xr;
+            xv.x += v[0]; xv.y += v[1]; xv.z += v[2]; xv.w += v[3];
+            if (p.bias_a) {
+              xv.x += bv.x; xv.y += bv.y; xv.z += bv.z; xv.w += bv.w;
+            }
+            *xr = xv;
+          } else {
+            *reinterpret_cast<float4*>(p.out + static_cast<int64_t>(m) * p.ldo + n) =
+                make_float4(v[0], v[1], v[2], v[3]);
+          }
+        }
+      }
+    }
+  };
+
+  // Step u (over all k-steps of this block's tiles, tile after tile) computes ring stage u % 3
+  // while steps u + 1 and u + 2 load -- across a tile boundary too, so the next tile's first
+  // stages are in flight during this tile's epilogue.  The stage step u overwrites,
+  // (u + 2) % 3, was last read in step u - 1, before that step's barrier.  Every wave runs the
+  // same steps (all counters are block-uniform), so every barrier is reached by all.
+  auto tile_origin = [&](int t, int& m0, int& n0) {
+    const int mt = t / p.tiles_n;
+    m0 = mt * kBM;
+    n0 = (t - mt * p.tiles_n) * kBN;
+  };
+  int it = first, is = 0, im0, in0;   // issue cursor: tile, k-step, tile origin
+  tile_origin(it, im0, in0);
+  auto advance_issue = [&]() {
+    if (++is == nk) {
+      is = 0;
+      it += bpx;
+      tile_origin(it, im0, in0);
+    }
+  };
+  issue(im0, in0, is, 0);
+  advance_issue();
+  if (total > 1) {
+    issue(im0, in0, is, 1);
+    advance_issue();
+    stage_barrier<kLoadsPerStage>();
+  } else {
+    stage_barrier<0>();
+  }
+  int ct = first, cs = 0, cm0, cn0;   // compute cursor
+  tile_origin(ct, cm0, cn0);
+  reset();
+  int b = 0;
+  for (int u = 0; u < total; ++u) {
+    const int b2 = b == 0 ? 2 : b - 1;   // (u + 2) % 3
+    if (u + 2 < total) {
+      issue(im0, in0, is, b2);
+      advance_issue();
+    }
+    compute(cs, b);
+    if (u + 2 < total) stage_barrier<kLoadsPerStage>();
+    else stage_barrier<0>();
+    b = b == 2 ? 0 : b + 1;
+    if (++cs == nk) {
+      epilogue(cm0, cn0);
+      reset();
+      cs = 0;
+      ct += bpx;
+      tile_origin(ct, cm0, cn0);
+    }
+  }
+}
+
+// CUs of the current device (hipDeviceAttributeMultiprocessorCount), cached per device
+int device_cus() {
+  static int cached[64] = {};
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
+  if (cached[dev] == 0) {
+    int n = 0;
+    if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess ||
+        n <= 0)
+      n = 256;
+    cached[dev] = n;
+  }
+  return cached[dev];
+}
+
+template <int AMODE, int EPI>
+int launch(Args p, hipStream_t st) {
+  const int64_t tm = (static_cast<int64_t>(p.M) + kBM - 1) / kBM;
+  const int64_t tn = (static_cast<int64_t>(p.N) + kBN - 1) / kBN;
+  const int64_t tiles = tm * tn;
+  if (tiles > 0x7fffffff - 8) return MDL_ERR_SHAPE;
+  const int64_t per_xcd = (tiles + 7) / 8;
+  // one block per CU (the LDS ring allows no second); blocks per XCD capped by its tiles
+  const int64_t bpx = std::min<int64_t>((device_cus() + 7) / 8, per_xcd);
+  p.tiles_n = static_cast<int>(tn);
+  p.tiles = static_cast<int>(tiles);
+  p.per_xcd = static_cast<int>(per_xcd);
+  prefill_gemm_kernel<AMODE, EPI><<<dim3(static_cast<unsigned>(8 * bpx)), kThreads, 0, st>>>(p);
+  return launch_status();
+}
+
+// shared argument checks: k a positive multiple of 32, n of 16, 16-byte aligned operands
+int check_common(const uint16_t* w, int m, int n, int k) {
+  if (!w) return MDL_ERR_NULL;
+  if (m < 0 || n <= 0 || k <= 0 || k % 32 != 0 || n % 16 != 0) return MDL_ERR_SHAPE;
+  if (!aligned16(w)) return MDL_ERR_ALIGN;
+  return MDL_OK;
+}
+
+int check_a(const uint16_t* a, int64_t lda, int a_layout, int k) {
+  if (!a) return MDL_ERR_NULL;
+  if (a_layout != MDL_LAYOUT_ROWS && a_layout != MDL_LAYOUT_TILES) return MDL_ERR_SHAPE;
+  if (a_layout == MDL_LAYOUT_ROWS && lda < 2 * static_cast<int64_t>(k)) return MDL_ERR_SHAPE;
+  if (!aligned16(a) || (a_layout == MDL_LAYOUT_ROWS && lda % 8 != 0)) return MDL_ERR_ALIGN;
+  return MDL_OK;
+}
+
+}  // namespace
+}  // namespace mdl
+
+using namespace mdl;
+
+extern "C" int mdl_prefill_gemm_split(const uint16_t* a, int64_t lda, int a_layout,
+                                      const uint16_t* w, float* out, int64_t ldo, int m, int n,
+                                      int k, void* stream) {
+  int rc = check_common(w, m, n, k);
+  if (rc == MDL_OK) rc = check_a(a, lda, a_layout, k);
+  if (rc != MDL_OK) return rc;
+  if (!out) return MDL_ERR_NULL;
+  if (ldo < n) return MDL_ERR_SHAPE;
+  if (!aligned16(out) || ldo % 4 != 0) return MDL_ERR_ALIGN;
+  if (m == 0) return MDL_OK;
+  Args p{};
+  p.a = a; p.lda = lda; p.w = w; p.out = out; p.ldo = ldo; p.M = m; p.N = n; p.K = k;
+  const hipStream_t st = static_cast<hipStream_t>(stream);
+  return a_layout == MDL_LAYOUT_TILES ? launch<A_TILES, E_STORE>(p, st)
+                                      : launch<A_ROWS, E_STORE>(p, st);
+}
+
+extern "C" int mdl_prefill_gemm_norm(const float* x, const float* gamma, float eps,
+                                     const uint16_t* w, float* out, int64_t ldo, float* rstd_out,
+                                     int m, int n, int k, void* stream) {
+  int rc = check_common(w, m, n, k);
+  if (rc != MDL_OK) return rc;
+  if (!x || !gamma || !out) return MDL_ERR_NULL;
+  if (ldo < n || k > kMaxNormK) return MDL_ERR_SHAPE;
+  if (!aligned16(x) || !aligned16(gamma) || !aligned16(out) || ldo % 4 != 0)
+    return MDL_ERR_ALIGN;
+  if (m == 0) return MDL_OK;
+  Args p{};
+  p.x = x; p.gamma = gamma; p.eps = eps; p.w = w; p.out = out; p.ldo = ldo;
+  p.rstd_out = rstd_out; p.M = m; p.N = n; p.K = k;
+  return launch<A_NORM, E_STORE>(p, static_cast<hipStream_t>(stream));
+}
+
+extern "C" int mdl_prefill_gemm_norm_swiglu(const float* x, const float* gamma, float eps,
+                                            const uint16_t* w_gu, const float* bias_gate,
+                                            const float* bias_up, uint16_t* h_out, int m,
+                                            int d_ff, int k, void* stream) {
+  if (d_ff <= 0 || d_ff % 16 != 0 || d_ff > (1 << 28)) return MDL_ERR_SHAPE;
+  int rc = check_common(w_gu, m, 2 * d_ff, k);
+  if (rc != MDL_OK) return rc;
+  if (!x || !gamma || !h_out) return MDL_ERR_NULL;
+  if (k > kMaxNormK) return MDL_ERR_SHAPE;
+  if (!aligned16(x) || !aligned16(gamma) || !aligned8(h_out) ||
+      (bias_gate && !aligned16(bias_gate)) || (bias_up && !aligned16(bias_up)))
+    return MDL_ERR_ALIGN;
+  if (m == 0) return MDL_OK;
+  Args p{};
+  p.x = x; p.gamma = gamma; p.eps = eps; p.w = w_gu; p.bias_a = bias_gate; p.bias_b = bias_up;
+  p.h = h_out; p.d_ff = d_ff; p.M = m; p.N = 2 * d_ff; p.K = k;
+  return launch<A_NORM, E_SWIGLU>(p, static_cast<hipStream_t>(stream));
+}
+
+extern "C" int mdl_prefill_gemm_split_residual(const uint16_t* a, int64_t lda, int a_layout,
+                                               const uint16_t* w, float* x, const float* bias,
+                                               int m, int n, int k, void* stream) {
+  int rc = check_common(w, m, n, k);
+  if (rc == MDL_OK) rc = check_a(a, lda, a_layout, k);
+  if (rc != MDL_OK) return rc;
+  if (!x) return MDL_ERR_NULL;
+  if (n % 32 != 0) return MDL_ERR_SHAPE;   // x in the fp32 tile layout: whole 32-column blocks
+  if (!aligned16(x) || (bias && !aligned16(bias))) return MDL_ERR_ALIGN;
+  if (m == 0) return MDL_OK;
+  Args p{};
+  p.a = a; p.lda = lda; p.w = w; p.x_res = x; p.bias_a = bias; p.M = m; p.N = n; p.K = k;
+  const hipStream_t st = static_cast<hipStream_t>(stream);
+  return a_layout == MDL_LAYOUT_TILES ? launch<A_TILES, E_RESIDUAL>(p, st)
+                                      : launch<A_ROWS, E_RESIDUAL>(p, st);
+}

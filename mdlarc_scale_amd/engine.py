@@ -66,6 +66,22 @@ def tiles_supported(d_model: int, d_ff: int) -> bool:
     return d_model % 32 == 0 and d_ff % 32 == 0
 
 
+def zero_tiled_rows(buf: torch.Tensor, r0: int, r1: int, cols: int) -> None:
+    """Zero rows [r0, r1) of a bf16 [rows, cols] matrix in the MFMA tile layout: each row is
+    cols / 8 chunks of 8 contiguous elements (tile_off of include/mdlarc_hip.h)."""
+    m = torch.arange(r0, r1, device=buf.device)[:, None]
+    q = torch.arange(cols // 8, device=buf.device)[None, :]
+    chunk = 64 * ((m >> 4) * (cols >> 5) + (q >> 2)) + 16 * (q & 3) + (m & 15)
+    buf.view(-1, 8)[chunk.reshape(-1)] = 0
+
+
+def prompt_gemms_fused(d_model: int, d_ff: int) -> bool:
+    """K6 runs a prompt's projections (RMSNorms and residual adds fused in) when the tiled
+    weights exist and the normed inputs fit its LDS copy of gamma; every reference preset does.
+    Otherwise the prompt path runs hipBLASLt on [W | W] with separate norm / SwiGLU passes."""
+    return tiles_supported(d_model, d_ff) and d_model <= K.PREFILL_NORM_MAX_K
+
+
 def pack_split_weight(w: torch.Tensor, device: torch.device) -> torch.Tensor:
     """bf16 [W | W] ([N, 2K]) for a split-activation GEMM input (see gemm_f32)."""
     wb = w.detach().to(device=device, dtype=torch.bfloat16)
@@ -112,7 +128,8 @@ class PackedWeights:
 class Scratch:
     """Activation buffers for M rows (reused across layers).  xs / attn / h are split bf16 GEMM
     inputs (2x the channel count; in the MFMA tile layout, whole 16-row blocks, when ``tiled``);
-    qkv / delta / gu are fp32 GEMM outputs."""
+    qkv / delta / gu are fp32 GEMM outputs.  The fused forms (``tiled`` decode on K5, ``fused``
+    prompts on K6) form xs inside the GEMMs and keep no delta / gu: those are empty there."""
 
     x: torch.Tensor
     xs: torch.Tensor
@@ -125,19 +142,24 @@ class Scratch:
     h: torch.Tensor
     rows: int = 0
     tiled: bool = False
+    fused: bool = False
 
     @staticmethod
     def alloc(rows: int, d: int, d_ff: int, device: torch.device,
-              tiled: bool = False) -> "Scratch":
+              tiled: bool = False, fused: bool = False) -> "Scratch":
         """``tiled``: the decode form -- x in the fp32 tile layout and attn / h in the bf16 one
-        (whole 16-row blocks); the RMSNorms run inside the K5 launches (``HipEngine._mlp``)."""
+        (whole 16-row blocks); the RMSNorms run inside the K5 launches (``HipEngine._mlp``).
+        ``fused``: the prompt form on K6 -- the same layouts; the RMSNorms run inside the K6
+        launches."""
         e = lambda *s, dt=torch.bfloat16: torch.empty(*s, dtype=dt, device=device)  # noqa: E731
         f = torch.float32
-        sr = K.tile_rows(rows) if tiled else rows       # rows of the tiled activations
-        return Scratch(x=e(sr, d, dt=f), xs=e(sr, 2 * d), rstd=e(rows, dt=f),
-                       qkv=e(rows, 3 * d, dt=f), q=e(rows, d), attn=e(sr, 2 * d),
-                       delta=e(rows, d, dt=f), gu=e(rows, 2 * d_ff, dt=f), h=e(sr, 2 * d_ff),
-                       rows=rows, tiled=tiled)
+        split_gemm = not (tiled or fused)               # hipBLASLt path: xs, delta, gu
+        sr = rows if split_gemm else K.tile_rows(rows)  # rows of the tiled activations
+        return Scratch(x=e(sr, d, dt=f), xs=e(sr if split_gemm else 0, 2 * d),
+                       rstd=e(rows, dt=f), qkv=e(rows, 3 * d, dt=f), q=e(rows, d),
+                       attn=e(sr, 2 * d), delta=e(rows if split_gemm else 0, d, dt=f),
+                       gu=e(rows if split_gemm else 0, 2 * d_ff, dt=f), h=e(sr, 2 * d_ff),
+                       rows=rows, tiled=tiled, fused=fused)
 
 
 @dataclass
@@ -260,18 +282,21 @@ class HipEngine:
         H, d = cfg.n_heads, cfg.d_model
         tok, ex = self._tables()
         use_ex = ex_ids if (ex_ids is not None and cfg.use_example_embedding) else None
+        fused = sc.fused   # K6: ln1 runs in the qkv launch, so the embedding writes x only
         K.embed_rmsnorm(ids.reshape(-1), use_ex, tok, ex if use_ex is not None else None, S,
-                        W.ln1[0], W.eps, sc.x, sc.xs, sc.rstd)
+                        W.ln1[0], W.eps, sc.x, None if fused else sc.xs,
+                        None if fused else sc.rstd, tiled=fused)
         qs = softmax_scale(d // H)
         for li in range(cfg.n_layers):
             kc, vc = kv_layers(li)
-            gemm_f32(sc.xs, W.qkv[li], sc.qkv)
+            self._qkv(W, li, sc)
             K.qkv_rope_cache(sc.qkv, sc.rstd, pos, W.rope_tab, W.rope_geom, B, S, H, qs, sc.q,
                              kc, vc, slot0=0)
-            K.attn_prefill(sc.q, kc, vc, B, S, H, key_mask, kv_start, causal, sc.attn)
+            K.attn_prefill(sc.q, kc, vc, B, S, H, key_mask, kv_start, causal, sc.attn,
+                           out_tiled=fused)
             if causal:
                 K.attn_prefill_lead(sc.qkv, sc.rstd, pos, W.rope_tab, W.rope_geom, qs, B, S, H,
-                                    key_mask, kv_start, None, B * S, sc.attn)
+                                    key_mask, kv_start, None, B * S, sc.attn, out_tiled=fused)
             self._mlp(W, li, sc)
 
     def run_packed(self, W: PackedWeights, ids: torch.Tensor, pos: torch.Tensor,
@@ -289,26 +314,50 @@ class HipEngine:
         ids_p = ids.reshape(-1).index_select(0, pk.gather)
         pos_p = pos.reshape(-1, 3).index_select(0, pk.gather)
         ex_p = ex_ids.reshape(-1).index_select(0, pk.token_row) if use_ex else None
+        fused = sc.fused
         K.embed_rmsnorm(ids_p, ex_p, tok, ex if use_ex else None, 1, W.ln1[0], W.eps, sc.x,
-                        sc.xs, sc.rstd)
-        if pk.n_tokens > pk.n_valid:
-            sc.attn[pk.n_valid:pk.n_tokens].zero_()   # padding queries: no visible key
+                        None if fused else sc.xs, None if fused else sc.rstd, tiled=fused)
+        if pk.n_tokens > pk.n_valid:   # padding queries: no visible key, attention output 0
+            if fused:
+                zero_tiled_rows(sc.attn, pk.n_valid, pk.n_tokens, 2 * d)
+            else:
+                sc.attn[pk.n_valid:pk.n_tokens].zero_()
         qs = softmax_scale(d // H)
         for li in range(cfg.n_layers):
             kc, vc = kv_layers(li)
-            gemm_f32(sc.xs, W.qkv[li], sc.qkv)
+            self._qkv(W, li, sc)
             K.qkv_rope_cache_packed(sc.qkv, sc.rstd, pos_p, W.rope_tab, W.rope_geom,
                                     pk.token_row, pk.token_slot, H, qs, sc.q, kc, vc)
             K.attn_prefill_packed(sc.q, kc, vc, B, S, H, key_mask, kv_start, pk.q_offset,
-                                  pk.n_valid, True, sc.attn)
+                                  pk.n_valid, True, sc.attn, out_tiled=fused)
             K.attn_prefill_lead(sc.qkv, sc.rstd, pos_p, W.rope_tab, W.rope_geom, qs, B, S, H,
-                                key_mask, kv_start, pk.q_offset, pk.n_tokens, sc.attn)
+                                key_mask, kv_start, pk.q_offset, pk.n_tokens, sc.attn,
+                                out_tiled=fused)
             self._mlp(W, li, sc)
+
+    def _qkv(self, W: PackedWeights, li: int, sc: Scratch) -> None:
+        """qkv_proj(ln1(x)) of a prompt: fp32 qkv and the rows' rstd (applied by the consumers)."""
+        if sc.fused:
+            K.prefill_gemm_norm(sc.x, W.ln1[li], W.eps, W.qkv_t[li], sc.qkv, sc.rstd,
+                                self.cfg.d_model)
+        else:
+            gemm_f32(sc.xs, W.qkv[li], sc.qkv)
 
     def _mlp(self, W: PackedWeights, li: int, sc: Scratch) -> None:
         """out_proj + residual, ln2, SwiGLU MLP + residual, next norm (shared by both phases)."""
         cfg = self.cfg
         d, F = cfg.d_model, cfg.d_ff
+        if sc.fused:
+            # prompt on K6: residual adds in the out / down epilogues, ln2 in the gate / up
+            # prologue with the SwiGLU in its epilogue; the next layer's ln1 runs in its qkv
+            # launch (_qkv) and ln_f in the head kernel
+            m = sc.rows
+            K.prefill_gemm_split_residual(sc.attn, W.out_t[li], sc.x, None, m, d, d, a_tiled=True)
+            K.prefill_gemm_norm_swiglu(sc.x, W.ln2[li], W.eps, W.gu_t[li], W.b_gate[li],
+                                       W.b_up[li], sc.h, m, F, d)
+            K.prefill_gemm_split_residual(sc.h, W.down_t[li], sc.x, W.b_down[li], m, d, F,
+                                          a_tiled=True)
+            return
         if sc.tiled:
             # decode: three K5 launches, the residual adds in the epilogues and ln2 in the
             # gate / up prologue; the next layer's ln1 runs in its qkv launch (gemm_norm) and
@@ -356,11 +405,12 @@ class HipEngine:
         H = cfg.n_heads
         kbuf = torch.empty(B, H, S, 64, dtype=torch.bfloat16, device=dev)
         vbuf = torch.empty_like(kbuf)
-        sc = Scratch.alloc(B * S, cfg.d_model, cfg.d_ff, dev)
+        sc = Scratch.alloc(B * S, cfg.d_model, cfg.d_ff, dev,
+                           fused=prompt_gemms_fused(cfg.d_model, cfg.d_ff))
         self.run_prompt(W, ids, pos, ex_ids, mask, kv_start, is_causal, lambda li: (kbuf, vbuf),
                         sc)
         logits = torch.empty(B * S, cfg.vocab_size, dtype=torch.float32, device=dev)
-        K.lm_head(sc.x, None, B * S, W.ln_f, W.eps, W.head, logits, None)
+        K.lm_head(sc.x, None, B * S, W.ln_f, W.eps, W.head, logits, None, x_tiled=sc.fused)
         return logits.view(B, S, cfg.vocab_size)
 
 

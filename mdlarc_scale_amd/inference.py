@@ -38,7 +38,7 @@ from .data import (
 )
 from .engine import GRID_MAX_X, GRID_MAX_Y, HipEngine, PackedWeights, Scratch, choose_split_len
 from .engine import pack_prompt
-from .engine import engine_for, gemm_f32, tiles_supported
+from .engine import engine_for, gemm_f32, prompt_gemms_fused, tiles_supported
 from .transformer import TinyTransformer, softmax_scale
 
 SYNC_EVERY = 8
@@ -322,16 +322,19 @@ class Generator:
             # one small device->host read of the row starts; the padding then costs nothing
             starts = torch.stack([st.kv_start, st.last_row]).cpu().numpy()
             pk = pack_prompt(starts[0], starts[1], st.B, st.S, dev)
-            sc = Scratch.alloc(pk.n_tokens, cfg.d_model, cfg.d_ff, dev)
+            sc = Scratch.alloc(pk.n_tokens, cfg.d_model, cfg.d_ff, dev,
+                               fused=prompt_gemms_fused(cfg.d_model, cfg.d_ff))
             self.eng.run_packed(W, input_ids, positions_3d, st.ex, st.pmask, st.kv_start, pk,
                                 st.cache.layer, sc)
             head_row = pk.head_row
         else:
-            sc = Scratch.alloc(st.B * st.S, cfg.d_model, cfg.d_ff, dev)
+            sc = Scratch.alloc(st.B * st.S, cfg.d_model, cfg.d_ff, dev,
+                               fused=prompt_gemms_fused(cfg.d_model, cfg.d_ff))
             self.eng.run_prompt(W, input_ids, positions_3d, st.ex, st.pmask, st.kv_start, True,
                                 st.cache.layer, sc)
             head_row = st.last_row
-        K.lm_head(sc.x, head_row, st.B, W.ln_f, W.eps, W.head, st.logits, st.tok, cons)
+        K.lm_head(sc.x, head_row, st.B, W.ln_f, W.eps, W.head, st.logits, st.tok, cons,
+                  x_tiled=sc.fused)
         st.cache.seq_len = st.S
 
     def _embed_inputs(self, st: DecodeState):

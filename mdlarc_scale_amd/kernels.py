@@ -390,6 +390,77 @@ def gemm_split_residual(a: torch.Tensor, w: torch.Tensor, x: torch.Tensor,
                                                   _stream()), "mdl_gemm_split_residual")
 
 
+PREFILL_NORM_MAX_K = 2048   # K6 norm forms: gamma is staged in LDS (kMaxNormK)
+
+
+def _split_a(a: torch.Tensor, m: int, k: int, tiled: bool) -> tuple[int, int]:
+    """(lda, layout) of a split activation [m, 2k] in either layout."""
+    if tiled:
+        _need(a, "a", BF16, tile_rows(m) * 2 * k)
+        return 2 * k, LAYOUT_TILES
+    _need(a, "a", BF16)
+    if a.dim() != 2 or a.shape[0] < m or a.shape[1] < 2 * k:
+        raise ValueError(f"a must be a row-major split activation [>= {m}, >= {2 * k}]")
+    return a.shape[1], LAYOUT_ROWS
+
+
+def prefill_gemm_split(a: torch.Tensor, w: torch.Tensor, out: torch.Tensor, k: int,
+                       a_tiled: bool = False) -> None:
+    """out[m, n] = (a_hi + a_lo) @ W^T on K6 (prompt-sized rows); w tiled [n, k]."""
+    _need(out, "out", F32)
+    m, n = out.shape
+    lda, lay = _split_a(a, m, k, a_tiled)
+    _need(w, "w", BF16, tile_rows(n) * k)
+    _lib.check(_lib.lib().mdl_prefill_gemm_split(_p(a), lda, lay, _p(w), _p(out), out.stride(0),
+                                                 m, n, k, _stream()), "mdl_prefill_gemm_split")
+
+
+def prefill_gemm_norm(x: torch.Tensor, gamma: torch.Tensor, eps: float, w: torch.Tensor,
+                      out: torch.Tensor, rstd_out: torch.Tensor | None, k: int) -> None:
+    """out[m, n] = split(x * gamma) @ W^T (RMSNorm in K6's prologue, rstd deferred) and rstd of
+    each row; x the fp32 tile-layout residual stream [tile_rows(m), k], w tiled [n, k]."""
+    _need(out, "out", F32)
+    m, n = out.shape
+    _need(x, "x", F32, tile_rows(m) * k)
+    _need(gamma, "gamma", F32, k)
+    _need(w, "w", BF16, tile_rows(n) * k)
+    _need(rstd_out, "rstd_out", F32, m, optional=True)
+    _lib.check(_lib.lib().mdl_prefill_gemm_norm(_p(x), _p(gamma), eps, _p(w), _p(out),
+                                                out.stride(0), _p(rstd_out), m, n, k,
+                                                _stream()), "mdl_prefill_gemm_norm")
+
+
+def prefill_gemm_norm_swiglu(x: torch.Tensor, gamma: torch.Tensor, eps: float,
+                             w_gu: torch.Tensor, bias_gate: torch.Tensor | None,
+                             bias_up: torch.Tensor | None, h_out: torch.Tensor, m: int,
+                             d_ff: int, k: int) -> None:
+    """h (tiled split [m, 2 d_ff]) = SwiGLU of the gate / up projection of split(x * gamma);
+    x the fp32 tile-layout residual stream, w_gu the tiled interleave_gate_up weight."""
+    _need(x, "x", F32, tile_rows(m) * k)
+    _need(gamma, "gamma", F32, k)
+    _need(w_gu, "w_gu", BF16, 2 * d_ff * k)
+    _need(bias_gate, "bias_gate", F32, d_ff, optional=True)
+    _need(bias_up, "bias_up", F32, d_ff, optional=True)
+    _need(h_out, "h_out", BF16, split_numel(m, d_ff, True))
+    _lib.check(_lib.lib().mdl_prefill_gemm_norm_swiglu(
+        _p(x), _p(gamma), eps, _p(w_gu), _p(bias_gate), _p(bias_up), _p(h_out), m, d_ff, k,
+        _stream()), "mdl_prefill_gemm_norm_swiglu")
+
+
+def prefill_gemm_split_residual(a: torch.Tensor, w: torch.Tensor, x: torch.Tensor,
+                                bias: torch.Tensor | None, m: int, n: int, k: int,
+                                a_tiled: bool = False) -> None:
+    """x += (a_hi + a_lo) @ W^T (+ bias) in place; x the fp32 tile-layout residual stream
+    [tile_rows(m), n], w tiled [n, k], a split [m, 2k] row-major or tiled."""
+    lda, lay = _split_a(a, m, k, a_tiled)
+    _need(x, "x", F32, tile_rows(m) * n)
+    _need(w, "w", BF16, tile_rows(n) * k)
+    _need(bias, "bias", F32, n, optional=True)
+    _lib.check(_lib.lib().mdl_prefill_gemm_split_residual(_p(a), lda, lay, _p(w), _p(x),
+                                                          _p(bias), m, n, k, _stream()),
+               "mdl_prefill_gemm_split_residual")
+
+
 def tile_f32(x: torch.Tensor) -> torch.Tensor:
     """[rows, cols] fp32 (cols a multiple of 32) in the fp32 tile layout: a new flat tensor of
     tile_rows(rows) * cols floats, padding rows zero (torch ops; for tests and set-up)."""
@@ -406,6 +477,13 @@ def untile_f32(t: torch.Tensor, rows: int, cols: int) -> torch.Tensor:
     """The inverse of tile_f32: the [rows, cols] matrix."""
     v = t[:tile_rows(rows) * cols].view(-1, cols // 32, 2, 4, 16, 4)
     return v.permute(0, 4, 1, 3, 2, 5).reshape(-1, cols)[:rows]
+
+
+def untile_matrix(t: torch.Tensor, rows: int, cols: int) -> torch.Tensor:
+    """The inverse of tile_matrix for a bf16 buffer: the [rows, cols] matrix (torch ops; for
+    tests and tools)."""
+    v = t.reshape(-1)[:tile_rows(rows) * cols].view(-1, cols // 32, 4, 16, 8)
+    return v.permute(0, 3, 1, 2, 4).reshape(-1, cols)[:rows]
 
 
 def gemm_split_tiles() -> int:
@@ -432,11 +510,12 @@ def tile_matrix(src: torch.Tensor, cols: int | None = None) -> torch.Tensor:
 
 def attn_prefill(q: torch.Tensor, k_cache: torch.Tensor, v_cache: torch.Tensor, batch: int,
                  seq: int, n_heads: int, key_mask: torch.Tensor | None,
-                 kv_start: torch.Tensor | None, causal: bool, out: torch.Tensor) -> None:
-    """out: split [batch*seq, 2*n_heads*64] bf16."""
+                 kv_start: torch.Tensor | None, causal: bool, out: torch.Tensor,
+                 out_tiled: bool = False) -> None:
+    """out: split [batch*seq, 2*n_heads*64] bf16 (row-major, or the MFMA tile layout)."""
     n = batch * seq * n_heads * HEAD_DIM
     _need(q, "q", BF16, n)
-    _need(out, "out", BF16, 2 * n)
+    _need(out, "out", BF16, split_numel(batch * seq, n_heads * HEAD_DIM, out_tiled))
     for name, c in (("k_cache", k_cache), ("v_cache", v_cache)):
         _need(c, name, BF16)
         if c.dim() != 4 or c.shape[0] != batch or c.shape[1] != n_heads or c.shape[3] != 64:
@@ -445,20 +524,20 @@ def attn_prefill(q: torch.Tensor, k_cache: torch.Tensor, v_cache: torch.Tensor, 
     _need(kv_start, "kv_start", I32, batch, optional=True)
     _lib.check(_lib.lib().mdl_attn_prefill(
         _p(q), _p(k_cache), _p(v_cache), batch, seq, n_heads, HEAD_DIM, k_cache.shape[2],
-        _p(key_mask), _p(kv_start), 1 if causal else 0, _p(out), _stream()),
+        _p(key_mask), _p(kv_start), 1 if causal else 0, _p(out), _layout(out_tiled), _stream()),
         "mdl_attn_prefill")
 
 
 def attn_prefill_packed(q: torch.Tensor, k_cache: torch.Tensor, v_cache: torch.Tensor,
                         batch: int, seq: int, n_heads: int, key_mask: torch.Tensor | None,
                         kv_start: torch.Tensor, q_offset: torch.Tensor, n_rows: int,
-                        causal: bool, out: torch.Tensor) -> None:
+                        causal: bool, out: torch.Tensor, out_tiled: bool = False) -> None:
     """Packed query rows: query i >= kv_start[b] of row b is row q_offset[b] + i - kv_start[b]
-    of q ([n_rows, n_heads*64]) and out (split [n_rows, 2*n_heads*64]).  The caller guarantees
-    q_offset[b] + seq - kv_start[b] <= n_rows for every row."""
+    of q ([n_rows, n_heads*64]) and out (split [n_rows, 2*n_heads*64], row-major or tiled).
+    The caller guarantees q_offset[b] + seq - kv_start[b] <= n_rows for every row."""
     n = n_rows * n_heads * HEAD_DIM
     _need(q, "q", BF16, n)
-    _need(out, "out", BF16, 2 * n)
+    _need(out, "out", BF16, split_numel(n_rows, n_heads * HEAD_DIM, out_tiled))
     for name, c in (("k_cache", k_cache), ("v_cache", v_cache)):
         _need(c, name, BF16)
         if c.dim() != 4 or c.shape[0] != batch or c.shape[1] != n_heads or c.shape[3] != 64:
@@ -468,15 +547,16 @@ def attn_prefill_packed(q: torch.Tensor, k_cache: torch.Tensor, v_cache: torch.T
     _need(q_offset, "q_offset", I32, batch)
     _lib.check(_lib.lib().mdl_attn_prefill_packed(
         _p(q), _p(k_cache), _p(v_cache), batch, seq, n_heads, HEAD_DIM, k_cache.shape[2],
-        _p(key_mask), _p(kv_start), _p(q_offset), 1 if causal else 0, _p(out), _stream()),
-        "mdl_attn_prefill_packed")
+        _p(key_mask), _p(kv_start), _p(q_offset), 1 if causal else 0, _p(out),
+        _layout(out_tiled), _stream()), "mdl_attn_prefill_packed")
 
 
 def attn_prefill_lead(qkv: torch.Tensor, rstd: torch.Tensor, pos: torch.Tensor,
                       rope_tab: torch.Tensor, rope_geom: tuple[int, int, int, int, int, int],
                       q_scale: float, batch: int, seq: int, n_heads: int,
                       key_mask: torch.Tensor | None, kv_start: torch.Tensor | None,
-                      q_offset: torch.Tensor | None, n_rows: int, out: torch.Tensor) -> None:
+                      q_offset: torch.Tensor | None, n_rows: int, out: torch.Tensor,
+                      out_tiled: bool = False) -> None:
     """Exact fp32 causal attention for the first 64 queries at or after kv_start of each row,
     overwriting those rows of ``out`` (after attn_prefill / attn_prefill_packed).  ``qkv`` /
     ``rstd`` / ``pos`` hold the n_rows token rows K2 consumed; rows are [batch, seq] or, with
@@ -488,7 +568,7 @@ def attn_prefill_lead(qkv: torch.Tensor, rstd: torch.Tensor, pos: torch.Tensor,
     _need(rstd, "rstd", F32, n_rows)
     _need(pos, "pos", I64, n_rows * 3)
     _need(rope_tab, "rope_tab", F32)
-    _need(out, "out", BF16, n_rows * 2 * d)
+    _need(out, "out", BF16, split_numel(n_rows, d, out_tiled))
     _need(key_mask, "key_mask", U8, batch * seq, optional=True)
     _need(kv_start, "kv_start", I32, batch, optional=q_offset is None)
     _need(q_offset, "q_offset", I32, batch, optional=True)
@@ -498,7 +578,7 @@ def attn_prefill_lead(qkv: torch.Tensor, rstd: torch.Tensor, pos: torch.Tensor,
     _lib.check(_lib.lib().mdl_attn_prefill_lead(
         _p(qkv), qkv.shape[1], _p(rstd), _p(pos), _p(rope_tab), mx, my, mz, px, py, pz, q_scale,
         batch, seq, n_heads, HEAD_DIM, _p(key_mask), _p(kv_start), _p(q_offset), _p(out),
-        _stream()), "mdl_attn_prefill_lead")
+        _layout(out_tiled), _stream()), "mdl_attn_prefill_lead")
 
 
 def attn_decode_workspace_bytes(batch: int, n_heads: int, slots: int, split_len: int) -> int:

@@ -43,7 +43,11 @@ def test_argument_errors_are_reported_before_any_launch():
     _require_lib()
     L = _lib.lib()
     fake = 1 << 20                                  # never dereferenced: rejected first
-    assert L.mdl_attn_prefill(fake, fake, fake, 1, 4, 1, 32, 4, None, None, 1, fake, None) == -4
+    assert L.mdl_attn_prefill(fake, fake, fake, 1, 4, 1, 32, 4, None, None, 1, fake, 0,
+                              None) == -4
+    # output layout codes are 0 / 1
+    assert L.mdl_attn_prefill(fake, fake, fake, 1, 4, 1, 64, 4, None, None, 1, fake, 2,
+                              None) == -3
     assert L.mdl_swiglu(None, 16, None, None, None, 1, 8, fake, 0, None) == -1
     assert L.mdl_swiglu(fake, 16, None, None, None, 1, 12, fake, 0, None) == -3
     assert L.mdl_swiglu(fake + 2, 16, None, None, None, 1, 8, fake, 0, None) == -2
@@ -97,19 +101,21 @@ def test_argument_errors_are_reported_before_any_launch():
     assert 1 <= L.mdl_gemm_split_pick(256, 2304, 768) <= L.mdl_gemm_split_tiles()
     # packed prefill: the per-row starts / offsets and the per-token rows / slots are required
     assert L.mdl_attn_prefill_packed(fake, fake, fake, 1, 4, 1, 64, 4, None, None, fake, 1, fake,
-                                     None) == -1
+                                     0, None) == -1
     assert L.mdl_attn_prefill_packed(fake, fake, fake, 1, 4, 1, 32, 4, None, fake, fake, 1, fake,
-                                     None) == -4
+                                     1, None) == -4
     assert L.mdl_qkv_rope_cache_packed(fake, 192, None, fake, fake, 4, None, fake, 1, 1, 64, 32,
                                        32, 8, 10, 10, 12, 0.125, fake, fake, fake, 4, None) == -1
     assert L.mdl_qkv_rope_cache_packed(fake, 192, None, fake, fake, 4, fake, fake, 1, 1, 32, 32,
                                        32, 8, 10, 10, 12, 0.125, fake, fake, fake, 4, None) == -4
     # exact lead attention: q_offset needs kv_start; head_dim 64 only; qkv rows 16-byte aligned
     assert L.mdl_attn_prefill_lead(fake, 192, fake, fake, fake, 32, 32, 8, 10, 10, 12, 0.125, 1, 4,
-                                   1, 64, None, None, fake, fake, None) == -1
+                                   1, 64, None, None, fake, fake, 0, None) == -1
     assert L.mdl_attn_prefill_lead(fake, 96, fake, fake, fake, 32, 32, 8, 10, 10, 12, 0.125, 1, 4,
-                                   1, 32, None, None, None, fake, None) == -4
+                                   1, 32, None, None, None, fake, 0, None) == -4
     assert L.mdl_attn_prefill_lead(fake, 194, fake, fake, fake, 32, 32, 8, 10, 10, 12, 0.125, 1, 4,
-                                   1, 64, None, None, None, fake, None) == -2
+                                   1, 64, None, None, None, fake, 0, None) == -2
+    assert L.mdl_attn_prefill_lead(fake, 192, fake, fake, fake, 32, 32, 8, 10, 10, 12, 0.125, 1, 4,
+                                   1, 64, None, None, None, fake, 3, None) == -3
     with pytest.raises(RuntimeError, match="head_dim"):
         _lib.check(-4, "probe")

@@ -538,9 +538,15 @@ def test_attn_prefill_packed_equals_padded(causal):
     out_pk = torch.full((pk.n_valid + 5, 2 * H * 64), 3.0, device=DEV, dtype=torch.bfloat16)
     K().attn_prefill_packed(q_pk, kc_nan, vc_nan, B, S, H, mask8, kv_dev, pk.q_offset,
                             pk.n_valid, causal, out_pk)
+    # the same launch writing the MFMA tile layout (the K6 prefill input) holds the same rows
+    out_t = torch.full((K().split_numel(pk.n_valid, H * 64, True),), 3.0, device=DEV,
+                       dtype=torch.bfloat16)
+    K().attn_prefill_packed(q_pk, kc_nan, vc_nan, B, S, H, mask8, kv_dev, pk.q_offset,
+                            pk.n_valid, causal, out_t, out_tiled=True)
     torch.cuda.synchronize()
     assert torch.equal(out_pk[:pk.n_valid], out_pad[gi])
     assert bool((out_pk[pk.n_valid:] == 3).all())
+    assert torch.equal(K().untile_matrix(out_t, pk.n_valid, 2 * H * 64), out_pk[:pk.n_valid])
 
 
 @pytest.mark.parametrize("packed", [False, True])
@@ -616,6 +622,12 @@ def test_attn_prefill_lead_exact(packed):
             err = (got[r].double() - ref[b, i]).abs()
             assert bool((err <= 1e-5 + 1e-5 * ref[b, i].abs()).all()), (b, i, err.max().item())
     assert torch.equal(out[~lead.to(DEV)], before[~lead.to(DEV)])
+    # the tile-layout output (the K6 prefill input) gets the same values in the same rows
+    out_t = K().tile_matrix(before)
+    K().attn_prefill_lead(qkv_r.to(DEV), rstd_r.to(DEV), pos_r.to(DEV), tab, geom, 0.125, B, S,
+                          H, mask8, kv_dev, pk.q_offset if packed else None, rows, out_t,
+                          out_tiled=True)
+    assert torch.equal(K().untile_matrix(out_t, rows, 2 * d), out)
 
 
 # ---------------------------------------------------------------------------- K4b decode
@@ -1003,7 +1015,7 @@ def test_capi_rejects_bad_arguments_before_launch():
     x = torch.zeros(16, 64, device=DEV)
     # head_dim must be 64
     assert L.mdl_attn_prefill(x.data_ptr(), x.data_ptr(), x.data_ptr(), 1, 4, 1, 32, 4, None,
-                              None, 1, x.data_ptr(), None) == -4
+                              None, 1, x.data_ptr(), 0, None) == -4
     # cache overflow: slot0 + seq > slots
     assert L.mdl_qkv_rope_cache(x.data_ptr(), 192, None, x.data_ptr(), x.data_ptr(), 1, 4, 1, 64,
                                 32, 32, 8, 10, 10, 12, 0.125, x.data_ptr(), x.data_ptr(),
