@@ -337,6 +337,28 @@ int mdl_prefill_gemm_split_residual(const uint16_t* a, int64_t lda, int a_layout
                                     const uint16_t* w, float* x, const float* bias, int m, int n,
                                     int k, void* stream);
 /*
+ * K6 with K2 (mdl_qkv_rope_cache) in its epilogue: ln1 + qkv_proj + RoPE + cache write of a
+ * prompt in one launch.  w: qkv_proj tiled [3 d, d] (d = n_heads * 64, at most 2048); x as for
+ * mdl_prefill_gemm_norm.  Writes, from the projection's fp32 accumulators and rstd, exactly what
+ * mdl_qkv_rope_cache(_packed) writes (the same arithmetic): q_out bf16 [m, d] (RoPE, q_scale),
+ * K / V into one layer's cache [batch, n_heads, cache_slots, 64]; rstd_out [m] (may be NULL);
+ * and the fp32 accumulators of the lead rows -- token slots kv_start[b] .. kv_start[b] + lead - 1
+ * of each batch row (kv_start may be NULL: 0) -- into qkv_lead (row stride ldq, may be NULL), the
+ * rows mdl_attn_prefill_lead reads.  Rows: a packed token list (token_row / token_slot, both or
+ * neither; a negative slot writes no K / V), or [batch, seq] (m = batch * seq, token i of row b
+ * in slot i).  Rope arguments as for mdl_qkv_rope_cache.
+ * Replaces: qkv_proj(ln1(x)) and the q / k / v split, RotaryEmbedding3D and the cache write of
+ *           _prefill / Attention.forward (src/inference.py:396-407; src/transformer.py:248-263,
+ *           :132-187).
+ */
+int mdl_prefill_gemm_norm_qkv(const float* x, const float* gamma, float eps, const uint16_t* w,
+                              int m, int n_heads, float* rstd_out, float* qkv_lead, int64_t ldq,
+                              int lead, const int32_t* kv_start, const int64_t* pos,
+                              const float* rope_tab, int max_x, int max_y, int max_z, int px,
+                              int py, int pz, float q_scale, uint16_t* q_out, uint16_t* k_cache,
+                              uint16_t* v_cache, int cache_slots, int batch, int seq,
+                              const int32_t* token_row, const int32_t* token_slot, void* stream);
+/*
  * dst = src ([rows, cols] bf16, row stride ld) in MDL_LAYOUT_TILES, rows padded to a multiple
  * of 16 with zeros (dst holds ceil(rows / 16) * 16 * cols elements).  cols a multiple of 32.
  * Packs the decode weights once per model version (no reference counterpart: a layout step).

@@ -66,6 +66,9 @@ SIGNATURES: dict[str, tuple[object, list]] = {
                                              P]),
     "mdl_prefill_gemm_split_residual": (c_int, [P, c_int64, c_int, P, P, P, c_int, c_int, c_int,
                                                 P]),
+    "mdl_prefill_gemm_norm_qkv": (c_int, [P, P, c_float, P, c_int, c_int, P, P, c_int64, c_int, P,
+                                          P, P, c_int, c_int, c_int, c_int, c_int, c_int, c_float,
+                                          P, P, P, c_int, c_int, c_int, P, P, P]),
     "mdl_tile_matrix": (c_int, [P, c_int64, c_int, c_int, P, P]),
     "mdl_attn_prefill": (c_int, [P, P, P, c_int, c_int, c_int, c_int, c_int, P, P, c_int, P,
                                  c_int, P]),

@@ -15,7 +15,11 @@
 //                             accumulator pairs (weights with 16-row gate / up blocks
 //                             interleaved), h [M, 2F] in the tile layout;
 //                 E_RESIDUAL  x[m, n] += acc (+ bias[n]) in place, x [M, N] in the fp32 tile
-//                             layout.
+//                             layout;
+//                 E_QKV       K2 on the qkv accumulators (A_NORM): rstd, 3D RoPE of q and k, the
+//                             softmax scale on q; q bf16 [M, d], K / V bf16 into their cache
+//                             slots, and fp32 acc only for the lead rows (the first `lead` tokens
+//                             of each row, which the exact lead-attention pass reads).
 //
 // Block: a 256 x 256 output tile (activation rows x weight rows) on 8 waves, each owning 32 MFMA
 // tiles (128 fp32 accumulators per lane): 64 rows x 128 weight rows in a 4 x 2 wave grid for the
@@ -36,6 +40,7 @@
 
 #include "common.h"
 #include "mfma.h"
+#include "rope.h"
 
 namespace mdl {
 
@@ -51,7 +56,7 @@ constexpr int kLoadsPerStage = 6;                    // DMA instructions per thr
 constexpr int kMaxNormK = 2048;                      // A_NORM: gamma lives in LDS
 
 enum AMode { A_ROWS = 0, A_TILES = 1, A_NORM = 2 };
-enum Epi { E_STORE = 0, E_SWIGLU = 1, E_RESIDUAL = 2 };
+enum Epi { E_STORE = 0, E_SWIGLU = 1, E_RESIDUAL = 2, E_QKV = 3 };
 
 struct Args {
   const uint16_t* a;   // A_ROWS / A_TILES
@@ -68,6 +73,19 @@ struct Args {
   uint16_t* h;         // E_SWIGLU: tiled split [M, 2 d_ff]
   int d_ff;
   float* x_res;        // E_RESIDUAL: [M, N] in the fp32 tile layout
+  // E_QKV: row m is token slot tok_slot[m] of batch row tok_row[m] (packed), or slot m % seq of
+  // row m / seq; out (may be NULL) receives the lead rows' fp32 acc
+  const int64_t* pos;
+  const float* rope_tab;
+  RopeArgs ra;
+  float q_scale;
+  uint16_t* q_out;
+  uint16_t* kc;
+  uint16_t* vc;
+  const int32_t* tok_row;
+  const int32_t* tok_slot;
+  const int32_t* kv_start;
+  int slots, seq, batch, lead;
   int M, N, K, tiles_n, tiles, per_xcd;
 };
 
@@ -235,11 +253,77 @@ __global__ __launch_bounds__(kThreads, 1) void prefill_gemm_kernel(const Args p)
         if (g == 0) rstd_s[16 * (FM * wm + j) + c] = rsqrtf(v / static_cast<float>(K) + p.eps);
       }
       asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
-      if constexpr (EPI == E_STORE) {
+      if constexpr (EPI == E_STORE || EPI == E_QKV) {
         if (p.rstd_out && n0 == 0 && tid < kBM && m0 + tid < M) p.rstd_out[m0 + tid] = rstd_s[tid];
       }
     }
-    if constexpr (EPI == E_SWIGLU) {
+    if constexpr (EPI == E_QKV) {
+      static_assert(AMODE == A_NORM && WNW == 1, "E_QKV follows the norm prologue");
+      // the arithmetic of K2 (rope_cache.hip); n0 and d are multiples of 64, so lane (c, g) of
+      // weight fragment i holds dims 16 (i % 4) + 4 g .. + 3 of its head: RoPE pairs
+      // 8 (i % 4) + 2 g and + 1
+      const int d = N / 3;
+      const int64_t head_stride = static_cast<int64_t>(p.slots) * kHeadDim;
+#pragma unroll
+      for (int j = 0; j < FM; ++j) {
+        const int r = 16 * (FM * wm + j) + c;
+        const int m = m0 + r;
+        if (m >= M) continue;
+        int64_t b;
+        int slot;
+        if (p.tok_slot) {
+          b = p.tok_row[m];
+          slot = p.tok_slot[m];
+        } else {
+          b = m / p.seq;
+          slot = static_cast<int>(m - b * p.seq);
+        }
+        const bool in_cache = slot >= 0 && slot < p.slots && b >= 0 && b < p.batch;
+        const int ks = (p.kv_start && b >= 0 && b < p.batch) ? p.kv_start[b] : 0;
+        const bool lead_row = p.out != nullptr && slot >= ks && slot - ks < p.lead;
+        const float rs = rstd_s[r];
+        const int64_t* pos3 = p.pos + static_cast<int64_t>(m) * 3;
+        float cs[8], sn[8];
+#pragma unroll
+        for (int t = 0; t < 8; ++t)
+          rope_cos_sin(8 * (t >> 1) + 2 * g + (t & 1), pos3, p.rope_tab, p.ra, cs[t], sn[t]);
+        const int64_t cache_row = (b * (d / kHeadDim) * static_cast<int64_t>(p.slots) + slot) *
+                                  kHeadDim;
+#pragma unroll
+        for (int i = 0; i < FN; ++i) {
+          const int n = n0 + 16 * i + 4 * g;
+          if (n >= N) continue;
+          const f32x4_t v = acc[i][j];
+          if (lead_row)
+            *reinterpret_cast<float4*>(p.out + static_cast<int64_t>(m) * p.ldo + n) =
+                make_float4(v[0], v[1], v[2], v[3]);
+          const int part = n / d, e = n - part * d;
+          const int head = e / kHeadDim, dim = e - head * kHeadDim;
+          const int q4 = i & 3;
+          const float a0 = v[0] * rs, a1 = v[1] * rs, a2 = v[2] * rs, a3 = v[3] * rs;
+          uint2 o;
+          if (part == 2) {
+            if (!in_cache) continue;
+            o.x = pack_bf2(a0, a1);
+            o.y = pack_bf2(a2, a3);
+            *reinterpret_cast<uint2*>(p.vc + cache_row + head * head_stride + dim) = o;
+            continue;
+          }
+          float y0, y1, y2, y3;
+          rope_rot(a0, a1, cs[2 * q4], sn[2 * q4], y0, y1);
+          rope_rot(a2, a3, cs[2 * q4 + 1], sn[2 * q4 + 1], y2, y3);
+          if (part == 0) {
+            o.x = pack_bf2(y0 * p.q_scale, y1 * p.q_scale);
+            o.y = pack_bf2(y2 * p.q_scale, y3 * p.q_scale);
+            *reinterpret_cast<uint2*>(p.q_out + static_cast<int64_t>(m) * d + e) = o;
+          } else if (in_cache) {
+            o.x = pack_bf2(y0, y1);
+            o.y = pack_bf2(y2, y3);
+            *reinterpret_cast<uint2*>(p.kc + cache_row + head * head_stride + dim) = o;
+          }
+        }
+      }
+    } else if constexpr (EPI == E_SWIGLU) {
       const int F = p.d_ff;
 #pragma unroll
       for (int pb = 0; pb < FN / 2; ++pb) {
@@ -471,4 +555,41 @@ extern "C" int mdl_prefill_gemm_split_residual(const uint16_t* a, int64_t lda, i
   const hipStream_t st = static_cast<hipStream_t>(stream);
   return a_layout == MDL_LAYOUT_TILES ? launch<A_TILES, E_RESIDUAL>(p, st)
                                       : launch<A_ROWS, E_RESIDUAL>(p, st);
+}
+
+extern "C" int mdl_prefill_gemm_norm_qkv(
+    const float* x, const float* gamma, float eps, const uint16_t* w, int m, int n_heads,
+    float* rstd_out, float* qkv_lead, int64_t ldq, int lead, const int32_t* kv_start,
+    const int64_t* pos, const float* rope_tab, int max_x, int max_y, int max_z, int px, int py,
+    int pz, float q_scale, uint16_t* q_out, uint16_t* k_cache, uint16_t* v_cache,
+    int cache_slots, int batch, int seq, const int32_t* token_row, const int32_t* token_slot,
+    void* stream) {
+  if (n_heads <= 0 || n_heads * kHeadDim > kMaxNormK) return MDL_ERR_SHAPE;
+  const int d = n_heads * kHeadDim;
+  int rc = check_common(w, m, 3 * d, d);
+  if (rc != MDL_OK) return rc;
+  if (!x || !gamma || !pos || !rope_tab || !q_out || !k_cache || !v_cache) return MDL_ERR_NULL;
+  if ((token_row == nullptr) != (token_slot == nullptr)) return MDL_ERR_NULL;
+  if (max_x <= 0 || max_y <= 0 || max_z <= 0 || px < 0 || py < 0 || pz < 0 ||
+      px + py + pz != kHeadDim / 2 || batch < 0 || cache_slots <= 0 || lead < 0)
+    return MDL_ERR_SHAPE;
+  if (!token_slot) {   // [batch, seq] rows: token i of row b is slot i
+    if (seq <= 0 || static_cast<int64_t>(batch) * seq != m) return MDL_ERR_SHAPE;
+    if (seq > cache_slots) return MDL_ERR_CACHE;
+  }
+  if (qkv_lead && (ldq < 3 * static_cast<int64_t>(d) || ldq % 4 != 0 || !aligned16(qkv_lead)))
+    return qkv_lead && ldq < 3 * static_cast<int64_t>(d) ? MDL_ERR_SHAPE : MDL_ERR_ALIGN;
+  if (!aligned16(x) || !aligned16(gamma) || !aligned8(q_out) || !aligned8(k_cache) ||
+      !aligned8(v_cache) || !aligned4(rope_tab))
+    return MDL_ERR_ALIGN;
+  if (m == 0) return MDL_OK;
+  Args p{};
+  p.x = x; p.gamma = gamma; p.eps = eps; p.w = w; p.out = qkv_lead; p.ldo = ldq;
+  p.rstd_out = rstd_out; p.pos = pos; p.rope_tab = rope_tab;
+  p.ra = RopeArgs{max_x, max_y, max_z, px, py, pz};
+  p.q_scale = q_scale; p.q_out = q_out; p.kc = k_cache; p.vc = v_cache;
+  p.tok_row = token_row; p.tok_slot = token_slot; p.kv_start = kv_start;
+  p.slots = cache_slots; p.seq = seq; p.batch = batch; p.lead = lead;
+  p.M = m; p.N = 3 * d; p.K = d;
+  return launch<A_NORM, E_QKV>(p, static_cast<hipStream_t>(stream));
 }

@@ -35,4 +35,15 @@ __device__ __forceinline__ void rope_cos_sin(int j, const int64_t* __restrict__ 
   sn = tab[ti + n_pos * pairs];
 }
 
+// A pair (a, b) rotated by (cs, sn): (a cs - b sn, b cs + a sn), each a fused multiply-add onto
+// a rounded product.  Written out so that every kernel rotating a pair (K2, the fused prefill
+// projection) produces the same bits whatever the compiler contracts elsewhere.
+__device__ __forceinline__ void rope_rot(float a, float b, float cs, float sn, float& o0,
+                                         float& o1) {
+#pragma clang fp contract(off)
+  const float bs = b * sn, as = a * sn;
+  o0 = fmaf(a, cs, -bs);
+  o1 = fmaf(b, cs, as);
+}
+
 }  // namespace mdl

@@ -63,11 +63,12 @@ __global__ __launch_bounds__(256) void qkv_rope_cache_kernel(
     const float2 qa = *reinterpret_cast<const float2*>(row + c);
     const float2 ka = *reinterpret_cast<const float2*>(row + d + c);
     const float q0 = qa.x * r, q1 = qa.y * r, k0 = ka.x * r, k1 = ka.y * r;
-    *reinterpret_cast<uint32_t*>(qrow + c) =
-        pack_bf2((q0 * cs - q1 * sn) * q_scale, (q1 * cs + q0 * sn) * q_scale);
+    float y0, y1, z0, z1;
+    rope_rot(q0, q1, cs, sn, y0, y1);
+    rope_rot(k0, k1, cs, sn, z0, z1);
+    *reinterpret_cast<uint32_t*>(qrow + c) = pack_bf2(y0 * q_scale, y1 * q_scale);
     if (in_cache)
-      *reinterpret_cast<uint32_t*>(kc + cache_row + h * head_stride + 2 * j) =
-          pack_bf2(k0 * cs - k1 * sn, k1 * cs + k0 * sn);
+      *reinterpret_cast<uint32_t*>(kc + cache_row + h * head_stride + 2 * j) = pack_bf2(z0, z1);
   }
   if (!in_cache) return;
   for (int idx = lane; idx < d / 4; idx += 64) {
@@ -137,17 +138,20 @@ __global__ __launch_bounds__(256) void qkv_rope_cache_vec_kernel(
   for (int i = 0; i < NCH; ++i) {
     const int e = 4 * (lane + 64 * i) - (i / kPart) * kD;   // channel inside the q/k/v part
     const float a0 = v[i].x * r, a1 = v[i].y * r, a2 = v[i].z * r, a3 = v[i].w * r;
+    float y0, y1, y2, y3;
+    rope_rot(a0, a1, cs0, sn0, y0, y1);
+    rope_rot(a2, a3, cs1, sn1, y2, y3);
     if (i < kPart) {
       uint2 o;
-      o.x = pack_bf2((a0 * cs0 - a1 * sn0) * q_scale, (a1 * cs0 + a0 * sn0) * q_scale);
-      o.y = pack_bf2((a2 * cs1 - a3 * sn1) * q_scale, (a3 * cs1 + a2 * sn1) * q_scale);
+      o.x = pack_bf2(y0 * q_scale, y1 * q_scale);
+      o.y = pack_bf2(y2 * q_scale, y3 * q_scale);
       st_u2<NT>(q_out + m * kD + e, o);
     } else if (in_cache) {
       uint2 o;
       uint16_t* dst;
       if (i < 2 * kPart) {
-        o.x = pack_bf2(a0 * cs0 - a1 * sn0, a1 * cs0 + a0 * sn0);
-        o.y = pack_bf2(a2 * cs1 - a3 * sn1, a3 * cs1 + a2 * sn1);
+        o.x = pack_bf2(y0, y1);
+        o.y = pack_bf2(y2, y3);
         dst = kc;
       } else {
         o.x = pack_bf2(a0, a1);

@@ -289,9 +289,14 @@ class HipEngine:
         qs = softmax_scale(d // H)
         for li in range(cfg.n_layers):
             kc, vc = kv_layers(li)
-            self._qkv(W, li, sc)
-            K.qkv_rope_cache(sc.qkv, sc.rstd, pos, W.rope_tab, W.rope_geom, B, S, H, qs, sc.q,
-                             kc, vc, slot0=0)
+            if fused:   # ln1 + qkv_proj + K2 in one launch (fp32 qkv only for the lead rows)
+                K.prefill_gemm_norm_qkv(sc.x, W.ln1[li], W.eps, W.qkv_t[li], B * S, H, sc.rstd,
+                                        sc.qkv, K.LEAD_QUERIES if causal else 0, kv_start, pos,
+                                        W.rope_tab, W.rope_geom, qs, sc.q, kc, vc, seq=S)
+            else:
+                gemm_f32(sc.xs, W.qkv[li], sc.qkv)
+                K.qkv_rope_cache(sc.qkv, sc.rstd, pos, W.rope_tab, W.rope_geom, B, S, H, qs,
+                                 sc.q, kc, vc, slot0=0)
             K.attn_prefill(sc.q, kc, vc, B, S, H, key_mask, kv_start, causal, sc.attn,
                            out_tiled=fused)
             if causal:
@@ -325,8 +330,14 @@ class HipEngine:
         qs = softmax_scale(d // H)
         for li in range(cfg.n_layers):
             kc, vc = kv_layers(li)
-            self._qkv(W, li, sc)
-            K.qkv_rope_cache_packed(sc.qkv, sc.rstd, pos_p, W.rope_tab, W.rope_geom,
+            if fused:
+                K.prefill_gemm_norm_qkv(sc.x, W.ln1[li], W.eps, W.qkv_t[li], pk.n_tokens, H,
+                                        sc.rstd, sc.qkv, K.LEAD_QUERIES, kv_start, pos_p,
+                                        W.rope_tab, W.rope_geom, qs, sc.q, kc, vc,
+                                        token_row=pk.token_row, token_slot=pk.token_slot)
+            else:
+                gemm_f32(sc.xs, W.qkv[li], sc.qkv)
+                K.qkv_rope_cache_packed(sc.qkv, sc.rstd, pos_p, W.rope_tab, W.rope_geom,
                                     pk.token_row, pk.token_slot, H, qs, sc.q, kc, vc)
             K.attn_prefill_packed(sc.q, kc, vc, B, S, H, key_mask, kv_start, pk.q_offset,
                                   pk.n_valid, True, sc.attn, out_tiled=fused)
@@ -334,14 +345,6 @@ class HipEngine:
                                 key_mask, kv_start, pk.q_offset, pk.n_tokens, sc.attn,
                                 out_tiled=fused)
             self._mlp(W, li, sc)
-
-    def _qkv(self, W: PackedWeights, li: int, sc: Scratch) -> None:
-        """qkv_proj(ln1(x)) of a prompt: fp32 qkv and the rows' rstd (applied by the consumers)."""
-        if sc.fused:
-            K.prefill_gemm_norm(sc.x, W.ln1[li], W.eps, W.qkv_t[li], sc.qkv, sc.rstd,
-                                self.cfg.d_model)
-        else:
-            gemm_f32(sc.xs, W.qkv[li], sc.qkv)
 
     def _mlp(self, W: PackedWeights, li: int, sc: Scratch) -> None:
         """out_proj + residual, ln2, SwiGLU MLP + residual, next norm (shared by both phases)."""

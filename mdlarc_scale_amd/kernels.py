@@ -16,6 +16,7 @@ from . import _lib
 
 BF16, F32, I64, I32, U8 = torch.bfloat16, torch.float32, torch.int64, torch.int32, torch.uint8
 HEAD_DIM = 64
+LEAD_QUERIES = 64   # queries per row that attn_prefill_lead recomputes exactly (K4c)
 
 
 def _p(t: torch.Tensor | None) -> ctypes.c_void_p | None:
@@ -459,6 +460,51 @@ def prefill_gemm_split_residual(a: torch.Tensor, w: torch.Tensor, x: torch.Tenso
     _lib.check(_lib.lib().mdl_prefill_gemm_split_residual(_p(a), lda, lay, _p(w), _p(x),
                                                           _p(bias), m, n, k, _stream()),
                "mdl_prefill_gemm_split_residual")
+
+
+def prefill_gemm_norm_qkv(x: torch.Tensor, gamma: torch.Tensor, eps: float, w: torch.Tensor,
+                          rows: int, n_heads: int, rstd_out: torch.Tensor | None,
+                          qkv_lead: torch.Tensor | None, lead: int,
+                          kv_start: torch.Tensor | None, pos: torch.Tensor,
+                          rope_tab: torch.Tensor,
+                          rope_geom: tuple[int, int, int, int, int, int], q_scale: float,
+                          q_out: torch.Tensor, k_cache: torch.Tensor, v_cache: torch.Tensor,
+                          token_row: torch.Tensor | None = None,
+                          token_slot: torch.Tensor | None = None, seq: int = 0) -> None:
+    """ln1 + qkv_proj + K2 in one K6 launch: q (bf16 [rows, d]) and K / V into their cache slots
+    as qkv_rope_cache(_packed) writes them from the same projection, rstd of each row, and the
+    fp32 projection rows of each batch row's first ``lead`` tokens (from kv_start) into qkv_lead
+    (may be None).  Rows are a packed token list (token_row / token_slot) or [batch, seq]."""
+    d = n_heads * HEAD_DIM
+    _need(x, "x", F32, tile_rows(rows) * d)
+    _need(gamma, "gamma", F32, d)
+    _need(w, "w", BF16, tile_rows(3 * d) * d)
+    _need(rstd_out, "rstd_out", F32, rows, optional=True)
+    _need(qkv_lead, "qkv_lead", F32, rows * 3 * d, optional=True)
+    if qkv_lead is not None and (qkv_lead.dim() != 2 or qkv_lead.shape[1] != 3 * d):
+        raise ValueError(f"qkv_lead must be [rows, {3 * d}]")
+    _need(pos, "pos", I64, rows * 3)
+    _need(rope_tab, "rope_tab", F32)
+    _need(q_out, "q_out", BF16, rows * d)
+    for name, c in (("k_cache", k_cache), ("v_cache", v_cache)):
+        _need(c, name, BF16)
+        if c.dim() != 4 or c.shape[1] != n_heads or c.shape[3] != 64:
+            raise ValueError(f"{name} must be [batch, n_heads, slots, 64]")
+    batch, slots = k_cache.shape[0], k_cache.shape[2]
+    _need(kv_start, "kv_start", I32, batch, optional=True)
+    if (token_row is None) != (token_slot is None):
+        raise ValueError("token_row and token_slot go together")
+    if token_row is not None:
+        _need(token_row, "token_row", I32, rows)
+        _need(token_slot, "token_slot", I32, rows)
+    elif seq * batch != rows:
+        raise ValueError("unpacked rows need rows == batch * seq")
+    mx, my, mz, px, py, pz = rope_geom
+    _lib.check(_lib.lib().mdl_prefill_gemm_norm_qkv(
+        _p(x), _p(gamma), eps, _p(w), rows, n_heads, _p(rstd_out), _p(qkv_lead), 3 * d, lead,
+        _p(kv_start), _p(pos), _p(rope_tab), mx, my, mz, px, py, pz, q_scale, _p(q_out),
+        _p(k_cache), _p(v_cache), slots, batch, seq, _p(token_row), _p(token_slot), _stream()),
+        "mdl_prefill_gemm_norm_qkv")
 
 
 def tile_f32(x: torch.Tensor) -> torch.Tensor:

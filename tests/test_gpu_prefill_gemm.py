@@ -145,3 +145,78 @@ def test_prefill_gemm_persistent_tiles_cover_everything():
     torch.cuda.synchronize()
     assert not bool(out.isnan().any())
     assert rel(out, ref) < 2e-6
+
+
+def _rope(max_xyz=(30, 30, 8)):
+    from mdlarc_scale_amd.transformer import RotaryEmbedding3D
+
+    rope = RotaryEmbedding3D(64, *max_xyz)
+    return rope.device_table(DEV), (rope.max_x, rope.max_y, rope.max_z, rope.px, rope.py, rope.pz)
+
+
+@pytest.mark.parametrize("packed", [True, False])
+@pytest.mark.parametrize("n_heads", [4, 12])
+def test_norm_qkv_equals_norm_gemm_then_k2(packed, n_heads):
+    """ln1 + qkv_proj + K2 in one launch writes exactly what the E_STORE form followed by K2
+    (qkv_rope_cache / _packed) writes -- q, every cache slot, rstd -- and the fp32 projection
+    rows only for each row's first LEAD_QUERIES tokens from kv_start."""
+    g = torch.Generator().manual_seed(n_heads * 2 + packed)
+    B, S, slots = 3, 150, 170
+    H, d = n_heads, 64 * n_heads
+    kv = [0, 37, 149]
+    if packed:   # valid tokens of each row, then one padding token (slot -1, no cache write)
+        tr, ts = [], []
+        for b, k0 in enumerate(kv):
+            tr += [b] * (S - k0)
+            ts += list(range(k0, S))
+        tr.append(1)
+        ts.append(-1)
+        rows = len(tr)
+        token_row = torch.tensor(tr, dtype=torch.int32, device=DEV)
+        token_slot = torch.tensor(ts, dtype=torch.int32, device=DEV)
+    else:
+        rows = B * S
+        token_row = token_slot = None
+    x = torch.randn(rows, d, generator=g).to(DEV)
+    gam = (1 + 0.1 * torch.randn(d, generator=g)).to(DEV)
+    w = K().tile_matrix((0.05 * torch.randn(3 * d, d, generator=g)).to(torch.bfloat16).to(DEV))
+    pos = torch.randint(0, 35, (rows, 3), generator=g).to(DEV)
+    tab, geom = _rope()
+    kv_dev = torch.tensor(kv, dtype=torch.int32, device=DEV)
+    xt = K().tile_f32(x)
+    # reference: E_STORE form, then K2
+    qkv = torch.empty(rows, 3 * d, device=DEV)
+    rs1 = torch.empty(rows, device=DEV)
+    K().prefill_gemm_norm(xt, gam, 1e-5, w, qkv, rs1, d)
+    sentinel = torch.full((B, H, slots, 64), 7.0, dtype=torch.bfloat16)
+    kc1, vc1 = sentinel.clone().to(DEV), sentinel.clone().to(DEV)
+    q1 = torch.empty(rows, d, dtype=torch.bfloat16, device=DEV)
+    if packed:
+        K().qkv_rope_cache_packed(qkv, rs1, pos, tab, geom, token_row, token_slot, H, 0.125, q1,
+                                  kc1, vc1)
+    else:
+        K().qkv_rope_cache(qkv, rs1, pos, tab, geom, B, S, H, 0.125, q1, kc1, vc1, slot0=0)
+    # fused
+    kc2, vc2 = sentinel.clone().to(DEV), sentinel.clone().to(DEV)
+    q2 = torch.empty(rows, d, dtype=torch.bfloat16, device=DEV)
+    rs2 = torch.empty(rows, device=DEV)
+    lead = torch.full((rows, 3 * d), float("nan"), device=DEV)
+    K().prefill_gemm_norm_qkv(xt, gam, 1e-5, w, rows, H, rs2, lead, K().LEAD_QUERIES, kv_dev, pos,
+                              tab, geom, 0.125, q2, kc2, vc2, token_row=token_row,
+                              token_slot=token_slot, seq=0 if packed else S)
+    torch.cuda.synchronize()
+    assert torch.equal(rs1, rs2)
+    assert torch.equal(q1, q2)
+    assert torch.equal(kc1, kc2) and torch.equal(vc1, vc2)
+    # lead rows: slot in [kv_start[b], kv_start[b] + 64)
+    if packed:
+        rb, sl = token_row.long().cpu(), token_slot.long().cpu()
+    else:
+        rb = torch.arange(rows) // S
+        sl = torch.arange(rows) % S
+    ks = torch.tensor(kv)[rb]
+    is_lead = (sl >= ks) & (sl - ks < K().LEAD_QUERIES)
+    assert int(is_lead.sum()) > 0
+    li = is_lead.to(DEV)
+    assert torch.equal(lead[li], qkv[li])
+    assert bool(lead[~li].isnan().all())
