@@ -138,21 +138,20 @@ def recorded_traffic_ratio(kernel: str, workload: str):
 
 
 def decode_attention_bytes(B, H, t, kv_start, S, holes):
-    """Algorithmic bytes of one fused decode-attention launch (mdl_attn_decode_rope) at cache
-    position t: every (row, head) reads its q/k/v slice of the fp32 qkv row (3 x 64 x 4 B),
-    writes the token's K and V into slot t (2 x 128 B), reads the K and V rows of the slots it
-    attends (kv_start[b]..t, 2 x 128 B each) and writes the split output (2 x 128 B); rows whose
-    prompt mask has holes also read their mask bytes."""
+    """Algorithmic bytes of one decode-attention launch of the step (mdl_attn_decode; the qkv
+    projection's epilogue already wrote q and the token's K/V into slot t) at cache position t:
+    every (row, head) reads its bf16 q (64 x 2 B), the K and V rows of the slots it attends
+    (kv_start[b]..t, 2 x 128 B each) and writes the split output (2 x 128 B); rows whose prompt
+    mask has holes also read their mask bytes."""
     import torch
 
     ks = kv_start.to(torch.int64)
     n = (t + 1 - ks).clamp(min=0)
     kv = int(n.sum()) * H * 64 * 2 * 2
-    qkv_in = B * H * 3 * 64 * 4
-    kv_out = B * H * 2 * 64 * 2
+    q_in = B * H * 64 * 2
     out = B * H * 64 * 2 * 2
     mask = int(((S - ks).clamp(min=0) * holes.to(torch.int64)).sum())
-    return kv + qkv_in + kv_out + out + mask
+    return kv + q_in + out + mask
 
 
 def microbench(dev):
@@ -526,23 +525,21 @@ def measure_workload(spec, steps, warmup, dev, eager=False, snapshot=False):
         # rewrite the slots they attend to
         snap = snapshot_decode_state(st, ex_d) if snapshot else None
 
-        # decode attention (the fused mdl_attn_decode_rope the step runs): re-issue the timed
-        # region's launches (every layer at every cache position t of the timed steps) back to
-        # back on the launching stream, between one pair of HIP events; the queue never drains,
-        # so the events time kernel execution only
+        # decode attention (the mdl_attn_decode launch the step runs on the q the qkv
+        # projection wrote): re-issue the timed region's launches (every layer at every cache
+        # position t of the timed steps) back to back on the launching stream, between one pair
+        # of HIP events; the queue never drains, so the events time kernel execution only
         H = cfg.n_heads
         kv_start_h, holes_h = st.kv_start.cpu(), st.holes.cpu()
         ts = [t_first + i for i in range(steps) for _ in range(cfg.n_layers)]
         layers = [li for _ in range(steps) for li in range(cfg.n_layers)]
-        qs = 1.0 / 8.0
         ta = Timer()
         ta.start()
         for t, li in zip(ts, layers):
             kc, vc = st.cache.layer(li)
-            K.attn_decode_rope(st.sc.qkv, st.sc.rstd, st.pos, W.rope_tab, W.rope_geom, qs, kc,
-                               vc, B, H, st.pmask, S, st.kv_start, t, None, st.ws, st.split_len,
-                               st.sc.attn, row_holes=st.holes, row_order=st.order,
-                               tiled=st.sc.tiled)
+            K.attn_decode(st.sc.q, kc, vc, B, H, st.pmask, S, st.kv_start, t, None, st.ws,
+                          st.split_len, st.sc.attn, row_holes=st.holes, row_order=st.order,
+                          tiled=st.sc.tiled)
         ta.stop()
         attn_ms = ta.ms() / len(ts)
         attn_bytes = sum(decode_attention_bytes(B, H, t, kv_start_h, S, holes_h)
@@ -598,9 +595,10 @@ def roofline_of(r):
     launch duration against the 8 TB/s peak."""
     achieved = r["attn_bytes"] / r["attn_ms"] / 1e6
     return {
-        "kernel": f"attn_decode_kernel<true, {r['decode_nb']}> (mdl_attn_decode_rope: K2 + "
-                  f"decode attention on bf16 MFMA, {16 * r['decode_nb']}-slot wave tiles, "
-                  f"{r['n_split']} split(s) per (row, head))",
+        "kernel": f"attn_decode_kernel<false, {r['decode_nb']}> (mdl_attn_decode: decode "
+                  f"attention on bf16 MFMA over the q and slot-t K/V that the qkv projection's "
+                  f"epilogue wrote, {16 * r['decode_nb']}-slot wave tiles, {r['n_split']} "
+                  f"split(s) per (row, head))",
         "bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS,
         "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4),
         "avg_launch_ms": round(r["attn_ms"], 5), "bytes_per_launch": int(r["attn_bytes"]),

@@ -278,6 +278,21 @@ int mdl_gemm_split_swiglu(const uint16_t* a, const uint16_t* w_gu, const float* 
 int mdl_gemm_norm(const float* x, const float* gamma, float eps, const uint16_t* w, float* out,
                   int64_t ldo, float* rstd_out, int m, int n, int k, int tile, void* stream);
 /*
+ * mdl_gemm_norm with K2 in its epilogue, for the decode step: from qkv = split(x * gamma) . w^T
+ * (w: qkv_proj tiled [3 d, d], d = n_heads * 64) and rstd it writes exactly what
+ * mdl_qkv_rope_cache writes for one token per row (the same arithmetic): q_out bf16 [m, d]
+ * (RoPE, q_scale) and K / V into slot t = *slot_dev (or slot0) of cache row m
+ * ([m, n_heads, cache_slots, 64]); rstd_out may be NULL.  The attention then runs unfused
+ * (mdl_attn_decode on q_out).  tile as for mdl_gemm_norm.
+ * Replaces: qkv_proj(ln1(x)), the q / k / v split, RotaryEmbedding3D and the cache write of
+ *           _decode_step (src/inference.py:437-445; src/transformer.py:132-187, :248-263).
+ */
+int mdl_gemm_norm_qkv(const float* x, const float* gamma, float eps, const uint16_t* w, int m,
+                      int n_heads, float* rstd_out, const int64_t* pos, const float* rope_tab,
+                      int max_x, int max_y, int max_z, int px, int py, int pz, float q_scale,
+                      uint16_t* q_out, uint16_t* k_cache, uint16_t* v_cache, int cache_slots,
+                      int slot0, const int32_t* slot_dev, int tile, void* stream);
+/*
  * mdl_gemm_norm feeding the SwiGLU epilogue of mdl_gemm_split_swiglu (rstd from the prologue):
  * h = split(silu(rstd g + bias_gate) * (rstd u + bias_up)) with g / u the gate / up rows of
  * w_gu against split(x * gamma).  Replaces ffn(ln2(x))'s gate (src/transformer.py:441-449,

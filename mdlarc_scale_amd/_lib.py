@@ -56,6 +56,9 @@ SIGNATURES: dict[str, tuple[object, list]] = {
                                c_int, c_int, P]),
     "mdl_gemm_split_swiglu": (c_int, [P, P, P, P, P, P, c_int, c_int, c_int, c_int, P]),
     "mdl_gemm_norm": (c_int, [P, P, c_float, P, P, c_int64, P, c_int, c_int, c_int, c_int, P]),
+    "mdl_gemm_norm_qkv": (c_int, [P, P, c_float, P, c_int, c_int, P, P, P, c_int, c_int, c_int,
+                                  c_int, c_int, c_int, c_float, P, P, P, c_int, c_int, P, c_int,
+                                  P]),
     "mdl_gemm_norm_swiglu": (c_int, [P, P, c_float, P, P, P, P, c_int, c_int, c_int, c_int, P]),
     "mdl_gemm_split_residual": (c_int, [P, P, P, P, c_int, c_int, c_int, c_int, P]),
     "mdl_gemm_split_tiles": (c_int, []),

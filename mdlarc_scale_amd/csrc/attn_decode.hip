@@ -113,7 +113,8 @@ __global__ __launch_bounds__(256) void attn_decode_kernel(
       const float2 a = *reinterpret_cast<const float2*>(row + (is_k ? d : 0) + h * kHeadDim +
                                                         2 * j);
       const float x0 = a.x * r, x1 = a.y * r;
-      const float y0 = x0 * cs - x1 * sn, y1 = x1 * cs + x0 * sn;
+      float y0, y1;
+      rope_rot(x0, x1, cs, sn, y0, y1);
       const bool writes = t >= lo && t < lo + split_len && t < slots;
       const int64_t slot_row = (static_cast<int64_t>(bh) * slots + t) * kHeadDim;
       if (!is_k) {

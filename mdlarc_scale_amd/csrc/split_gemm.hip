@@ -15,7 +15,10 @@
 //   E_SWIGLU    h = split(silu(rstd g + b_g) * (rstd u + b_u)) from the gate / up pair of
 //               fragments (weights with 16-row gate / up blocks interleaved), tiled;
 //   E_RESIDUAL  x[m, n] += acc (+ bias[n]) in place on the fp32 tile-layout residual stream
-//               (each element has one owner block, so the update needs no synchronisation).
+//               (each element has one owner block, so the update needs no synchronisation);
+//   E_QKV       K2 for the decode token of each row on the qkv accumulators (A_NORM): rstd,
+//               3D RoPE of q and k, the softmax scale on q; q bf16 [M, d] and K / V into cache
+//               slot t (*slot_dev) of row m, so the attention launch needs no prologue.
 //
 // Why not the library GEMM at decode: at M <= 256 rows hipBLASLt runs 64x64 or 32x32 tiles over
 // the doubled K of [W | W] (each weight byte read twice) on at most 144 workgroups for the small
@@ -39,6 +42,7 @@
 // change the result.
 #include "common.h"
 #include "mfma.h"
+#include "rope.h"
 
 namespace mdl {
 
@@ -48,7 +52,7 @@ constexpr int kGemmWaves = 8;
 constexpr int kU = 4;   // k-steps whose loads are in flight together (A_NORM, large tiles: 2)
 
 enum AMode { A_ROWS = 0, A_TILES = 1, A_NORM = 2 };
-enum Epi { E_STORE = 0, E_SWIGLU = 1, E_RESIDUAL = 2 };
+enum Epi { E_STORE = 0, E_SWIGLU = 1, E_RESIDUAL = 2, E_QKV = 3 };
 
 struct GemmArgs {
   const uint16_t* a;       // A_ROWS / A_TILES: split activation
@@ -67,6 +71,16 @@ struct GemmArgs {
   uint16_t* h;             // E_SWIGLU: split [M, 2F], tile layout
   float* x_res;            // E_RESIDUAL: fp32 residual stream [M, N], tile layout
   int d_ff;
+  // E_QKV: row m's token at pos[m], its K / V to slot *slot_dev (or slot0) of cache row m
+  const int64_t* pos;
+  const float* rope_tab;
+  RopeArgs ra;
+  float q_scale;
+  uint16_t* q_out;
+  uint16_t* kc;
+  uint16_t* vc;
+  const int32_t* slot_dev;
+  int slot0, slots;
   int M, N, K, n_tiles, m_tiles, per_xcd;
 };
 
@@ -228,7 +242,7 @@ __global__ __launch_bounds__(64 * kGemmWaves) void split_gemm_kernel(const GemmA
     for (int wv = 1; wv < NW; ++wv) tot += ss_red[wv][r];
     return rsqrtf(tot / static_cast<float>(K) + p.eps);
   };
-  if constexpr (AMODE == A_NORM && EPI == E_STORE) {
+  if constexpr (AMODE == A_NORM && (EPI == E_STORE || EPI == E_QKV)) {
     if (p.rstd_out && nt == 0 && threadIdx.x < TM && m0 + static_cast<int>(threadIdx.x) < M)
       p.rstd_out[m0 + threadIdx.x] = row_rstd(threadIdx.x);
   }
@@ -276,7 +290,45 @@ __global__ __launch_bounds__(64 * kGemmWaves) void split_gemm_kernel(const GemmA
       const int m = m0 + 16 * j + (ln & 15);
       const int n = n0 + 16 * i + 4 * (ln >> 4);
       if (m < M && n < N) {
-        if constexpr (EPI == E_RESIDUAL) {
+        if constexpr (EPI == E_QKV) {
+          static_assert(AMODE == A_NORM, "E_QKV follows the norm prologue");
+          // the arithmetic of K2 (rope_cache.hip): channels n .. n + 3 of row m are dims
+          // dim .. dim + 3 of one head of q, k or v (d is a multiple of 64), RoPE pairs dim / 2
+          // and dim / 2 + 1
+          const int d = N / 3;
+          const int part = n / d, e = n - part * d;
+          const int head = e / kHeadDim, dim = e - head * kHeadDim;
+          const float r = row_rstd(16 * j + (ln & 15));
+          const float a0 = v[0] * r, a1 = v[1] * r, a2 = v[2] * r, a3 = v[3] * r;
+          const int t = p.slot_dev ? *p.slot_dev : p.slot0;
+          const bool in_cache = t >= 0 && t < p.slots;
+          const int64_t crow =
+              ((static_cast<int64_t>(m) * (d / kHeadDim) + head) * p.slots + t) * kHeadDim + dim;
+          uint2 o;
+          if (part == 2) {
+            if (in_cache) {
+              o.x = pack_bf2(a0, a1);
+              o.y = pack_bf2(a2, a3);
+              *reinterpret_cast<uint2*>(p.vc + crow) = o;
+            }
+          } else {
+            float cs0, sn0, cs1, sn1, y0, y1, y2, y3;
+            const int64_t* pos3 = p.pos + static_cast<int64_t>(m) * 3;
+            rope_cos_sin(dim / 2, pos3, p.rope_tab, p.ra, cs0, sn0);
+            rope_cos_sin(dim / 2 + 1, pos3, p.rope_tab, p.ra, cs1, sn1);
+            rope_rot(a0, a1, cs0, sn0, y0, y1);
+            rope_rot(a2, a3, cs1, sn1, y2, y3);
+            if (part == 0) {
+              o.x = pack_bf2(y0 * p.q_scale, y1 * p.q_scale);
+              o.y = pack_bf2(y2 * p.q_scale, y3 * p.q_scale);
+              *reinterpret_cast<uint2*>(p.q_out + static_cast<int64_t>(m) * d + e) = o;
+            } else if (in_cache) {
+              o.x = pack_bf2(y0, y1);
+              o.y = pack_bf2(y2, y3);
+              *reinterpret_cast<uint2*>(p.kc + crow) = o;
+            }
+          }
+        } else if constexpr (EPI == E_RESIDUAL) {
           // x + delta, then + bias: the order of the add+RMSNorm kernel it replaces
           float4* xr = reinterpret_cast<float4*>(p.x_res + tile_off32(m, n, N));
           float4 xv = *xr;
@@ -458,6 +510,47 @@ extern "C" int mdl_gemm_norm(const float* x, const float* gamma, float eps, cons
   p.N = n;
   p.K = k;
   return launch<true, A_NORM, E_STORE>(tile, p, static_cast<hipStream_t>(stream));
+}
+
+extern "C" int mdl_gemm_norm_qkv(const float* x, const float* gamma, float eps,
+                                 const uint16_t* w, int m, int n_heads, float* rstd_out,
+                                 const int64_t* pos, const float* rope_tab, int max_x, int max_y,
+                                 int max_z, int px, int py, int pz, float q_scale,
+                                 uint16_t* q_out, uint16_t* k_cache, uint16_t* v_cache,
+                                 int cache_slots, int slot0, const int32_t* slot_dev, int tile,
+                                 void* stream) {
+  if (!x || !gamma || !w || !pos || !rope_tab || !q_out || !k_cache || !v_cache)
+    return MDL_ERR_NULL;
+  if (n_heads <= 0 || n_heads > (1 << 16)) return MDL_ERR_SHAPE;
+  const int d = n_heads * kHeadDim;
+  if (!decode_shape_ok(m, 3 * d, d, tile) || max_x <= 0 || max_y <= 0 || max_z <= 0 ||
+      px < 0 || py < 0 || pz < 0 || px + py + pz != kHeadDim / 2)
+    return MDL_ERR_SHAPE;
+  if (cache_slots <= 0 || (!slot_dev && (slot0 < 0 || slot0 >= cache_slots))) return MDL_ERR_CACHE;
+  if (!aligned16(x) || !aligned16(gamma) || !aligned16(w) || !aligned8(q_out) ||
+      !aligned8(k_cache) || !aligned8(v_cache) || !aligned4(rope_tab))
+    return MDL_ERR_ALIGN;
+  if (m == 0) return MDL_OK;
+  GemmArgs p{};
+  p.x = x;
+  p.gamma = gamma;
+  p.eps = eps;
+  p.w = w;
+  p.rstd_out = rstd_out;
+  p.pos = pos;
+  p.rope_tab = rope_tab;
+  p.ra = RopeArgs{max_x, max_y, max_z, px, py, pz};
+  p.q_scale = q_scale;
+  p.q_out = q_out;
+  p.kc = k_cache;
+  p.vc = v_cache;
+  p.slot_dev = slot_dev;
+  p.slot0 = slot0;
+  p.slots = cache_slots;
+  p.M = m;
+  p.N = 3 * d;
+  p.K = d;
+  return launch<true, A_NORM, E_QKV>(tile, p, static_cast<hipStream_t>(stream));
 }
 
 extern "C" int mdl_gemm_norm_swiglu(const float* x, const float* gamma, float eps,

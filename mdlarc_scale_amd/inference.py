@@ -353,14 +353,21 @@ class Generator:
         slot = st.counters[0:1]
         for li in range(cfg.n_layers):
             kc, vc = st.cache.layer(li)
-            if sc.tiled:     # ln1 in the projection's prologue; rstd for the attention launch
-                K.gemm_norm(sc.x, W.ln1[li], W.eps, W.qkv_t[li], sc.qkv, sc.rstd, cfg.d_model)
+            if sc.tiled:
+                # ln1 in the projection's prologue, K2 (RoPE, q scale, K/V into slot t) in its
+                # epilogue; the attention reads q and the cache
+                K.gemm_norm_qkv(sc.x, W.ln1[li], W.eps, W.qkv_t[li], B, H, None, st.pos,
+                                W.rope_tab, W.rope_geom, qs, sc.q, kc, vc, slot_dev=slot)
+                K.attn_decode(sc.q, kc, vc, B, H, st.pmask, st.S, st.kv_start, 0, slot, st.ws,
+                              st.split_len, sc.attn, row_holes=st.holes, row_order=st.order,
+                              tiled=True)
             else:
                 gemm_f32(sc.xs, W.qkv[li], sc.qkv)
-            # RMSNorm scale + split + 3D RoPE + cache write fused into the attention launch
-            K.attn_decode_rope(sc.qkv, sc.rstd, st.pos, W.rope_tab, W.rope_geom, qs, kc, vc, B,
-                               H, st.pmask, st.S, st.kv_start, 0, slot, st.ws, st.split_len,
-                               sc.attn, row_holes=st.holes, row_order=st.order, tiled=sc.tiled)
+                # RMSNorm scale + split + 3D RoPE + cache write fused into the attention launch
+                K.attn_decode_rope(sc.qkv, sc.rstd, st.pos, W.rope_tab, W.rope_geom, qs, kc, vc,
+                                   B, H, st.pmask, st.S, st.kv_start, 0, slot, st.ws,
+                                   st.split_len, sc.attn, row_holes=st.holes, row_order=st.order,
+                                   tiled=False)
             self.eng._mlp(W, li, sc)
 
     def decode_layers(self, st: DecodeState, W: PackedWeights, want_logits: bool) -> None:

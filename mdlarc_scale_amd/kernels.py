@@ -361,6 +361,35 @@ def gemm_norm(x: torch.Tensor, gamma: torch.Tensor, eps: float, w: torch.Tensor,
                                         m, n, k, tile, _stream()), "mdl_gemm_norm")
 
 
+def gemm_norm_qkv(x: torch.Tensor, gamma: torch.Tensor, eps: float, w: torch.Tensor, m: int,
+                  n_heads: int, rstd_out: torch.Tensor | None, pos: torch.Tensor,
+                  rope_tab: torch.Tensor, rope_geom: tuple[int, int, int, int, int, int],
+                  q_scale: float, q_out: torch.Tensor, k_cache: torch.Tensor,
+                  v_cache: torch.Tensor, slot0: int = 0, slot_dev: torch.Tensor | None = None,
+                  tile: int = 0) -> None:
+    """ln1 + qkv_proj + K2 of the decode token of each row in one K5 launch: q (bf16 [m, d]),
+    K / V into slot slot_dev[0] (or slot0) of each cache row; x the fp32 tile-layout residual
+    stream, w the tiled qkv weight."""
+    d = n_heads * HEAD_DIM
+    _need(x, "x", F32, tile_rows(m) * d)
+    _need(gamma, "gamma", F32, d)
+    _need(w, "w", BF16, tile_rows(3 * d) * d)
+    _need(rstd_out, "rstd_out", F32, m, optional=True)
+    _need(pos, "pos", I64, m * 3)
+    _need(rope_tab, "rope_tab", F32)
+    _need(q_out, "q_out", BF16, m * d)
+    for name, c in (("k_cache", k_cache), ("v_cache", v_cache)):
+        _need(c, name, BF16)
+        if c.dim() != 4 or c.shape[0] != m or c.shape[1] != n_heads or c.shape[3] != 64:
+            raise ValueError(f"{name} must be [m, n_heads, slots, 64]")
+    _need(slot_dev, "slot_dev", I32, 1, optional=True)
+    mx, my, mz, px, py, pz = rope_geom
+    _lib.check(_lib.lib().mdl_gemm_norm_qkv(
+        _p(x), _p(gamma), eps, _p(w), m, n_heads, _p(rstd_out), _p(pos), _p(rope_tab), mx, my,
+        mz, px, py, pz, q_scale, _p(q_out), _p(k_cache), _p(v_cache), k_cache.shape[2], slot0,
+        _p(slot_dev), tile, _stream()), "mdl_gemm_norm_qkv")
+
+
 def gemm_norm_swiglu(x: torch.Tensor, gamma: torch.Tensor, eps: float, w_gu: torch.Tensor,
                      bias_gate: torch.Tensor | None, bias_up: torch.Tensor | None,
                      h_out: torch.Tensor, m: int, d_ff: int, k: int, tile: int = 0) -> None:

@@ -1252,6 +1252,45 @@ def test_gemm_norm_equals_add_rmsnorm_then_gemm(m, n, k):
     assert torch.equal(lr, lt)
 
 
+@pytest.mark.parametrize("m,h", [(256, 12), (37, 4), (64, 20)])
+def test_gemm_norm_qkv_equals_gemm_norm_then_k2(m, h):
+    """The decode qkv projection with K2 in its epilogue writes exactly what the store form
+    followed by qkv_rope_cache (one token per row, slot from the device counter) writes: q, the
+    slot-t K / V, rstd -- for every block shape; no other cache slot changes."""
+    from mdlarc_scale_amd.transformer import RotaryEmbedding3D
+
+    g = torch.Generator().manual_seed(m + h)
+    d, slots, t = 64 * h, 40, 29
+    x = (torch.randn(m, d, generator=g) * 1.5).to(DEV)
+    gamma = (1 + 0.1 * torch.randn(d, generator=g)).to(DEV)
+    wt = K().tile_matrix((torch.randn(3 * d, d, generator=g) * 0.05).to(torch.bfloat16).to(DEV))
+    pos = torch.randint(0, 35, (m, 3), generator=g).to(DEV)
+    rope = RotaryEmbedding3D(64, 30, 30, 8)
+    tab, geom = rope.device_table(DEV), (30, 30, 8, rope.px, rope.py, rope.pz)
+    slot = torch.tensor([t], dtype=torch.int32, device=DEV)
+    xt = K().tile_f32(x)
+    cache0 = bf(torch.randn(m, h, slots, 64, generator=g)).to(DEV)
+    for tl in list(range(1, K().gemm_split_tiles() + 1)) + [0]:
+        qkv = torch.empty(m, 3 * d, device=DEV)
+        rs1 = torch.empty(m, device=DEV)
+        K().gemm_norm(xt, gamma, 1e-5, wt, qkv, rs1, d, tile=tl)
+        q1 = torch.empty(m, d, device=DEV, dtype=torch.bfloat16)
+        kc1, vc1 = cache0.clone(), cache0.clone()
+        K().qkv_rope_cache(qkv, rs1, pos, tab, geom, m, 1, h, 0.125, q1, kc1, vc1, slot_dev=slot)
+        q2 = torch.empty(m, d, device=DEV, dtype=torch.bfloat16)
+        kc2, vc2 = cache0.clone(), cache0.clone()
+        rs2 = torch.empty(m, device=DEV)
+        K().gemm_norm_qkv(xt, gamma, 1e-5, wt, m, h, rs2, pos, tab, geom, 0.125, q2, kc2, vc2,
+                          slot_dev=slot, tile=tl)
+        torch.cuda.synchronize()
+        assert torch.equal(q1, q2), f"tile {tl}"
+        assert torch.equal(kc1, kc2) and torch.equal(vc1, vc2), f"tile {tl}"
+        assert torch.equal(rs1, rs2), f"tile {tl}"
+        others = torch.ones(slots, dtype=torch.bool)
+        others[t] = False
+        assert torch.equal(kc2[:, :, others.to(DEV)], cache0[:, :, others.to(DEV)])
+
+
 @pytest.mark.parametrize("m,f,k", [(256, 2048, 768), (37, 704, 256), (64, 3392, 1280)])
 def test_gemm_norm_swiglu_equals_unfused(m, f, k):
     """The gate / up projection with the RMSNorm prologue and the SwiGLU epilogue against
