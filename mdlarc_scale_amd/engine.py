@@ -186,7 +186,9 @@ class PackedPrompt:
 def pack_prompt(kv_start: np.ndarray, last_row: np.ndarray, batch: int, seq: int,
                 device: torch.device) -> PackedPrompt:
     """PackedPrompt of a batch whose rows start at ``kv_start`` (first valid index) and report
-    logits at flat row ``last_row`` (b*S + index), both host int arrays of length ``batch``."""
+    logits at flat row ``last_row`` (b*S + index), both host int arrays of length ``batch``.
+    The per-row quantities are computed on the host; the per-token lists are built on
+    ``device`` from them (no host copy of the token lists)."""
     if batch * seq >= 2 ** 31:
         raise ValueError("packed prompts index [B, S] with int32; B*S must stay below 2^31")
     kv = np.clip(np.asarray(kv_start, dtype=np.int64), 0, seq)
@@ -196,20 +198,27 @@ def pack_prompt(kv_start: np.ndarray, last_row: np.ndarray, batch: int, seq: int
     n = seq - kv
     off = np.concatenate([[0], np.cumsum(n)[:-1]]).astype(np.int64)
     n_valid = int(n.sum())
-    rows = np.repeat(np.arange(batch, dtype=np.int64), n)
-    slot = np.arange(n_valid, dtype=np.int64) - np.repeat(off, n) + np.repeat(kv, n)
     inside = last >= kv
     extra = np.nonzero(~inside)[0]
     head = np.where(inside, off + last - kv, 0)
     head[extra] = n_valid + np.arange(extra.size)
     total = n_valid + extra.size
-    host = np.concatenate([rows * seq + slot, extra * seq + last[extra], rows, extra, slot,
-                           np.full(extra.size, -1), off, head]).astype(np.int32)
-    dev = torch.from_numpy(host).to(device)
-    t, b = total, batch
-    return PackedPrompt(gather=dev[0:t], token_row=dev[t:2 * t], token_slot=dev[2 * t:3 * t],
-                        q_offset=dev[3 * t:3 * t + b], head_row=dev[3 * t + b:3 * t + 2 * b],
-                        n_valid=n_valid, n_tokens=total)
+    e = extra.size
+    small = torch.from_numpy(np.concatenate(
+        [kv, n, off, head, extra * seq + last[extra], extra]).astype(np.int64)).to(device)
+    kv_d, n_d, off_d = small[:batch], small[batch:2 * batch], small[2 * batch:3 * batch]
+    head_d = small[3 * batch:4 * batch]
+    ex_gather, ex_row = small[4 * batch:4 * batch + e], small[4 * batch + e:4 * batch + 2 * e]
+    rows = torch.repeat_interleave(torch.arange(batch, device=device), n_d,
+                                   output_size=n_valid)
+    slot = torch.arange(n_valid, device=device) - off_d[rows] + kv_d[rows]
+    i32 = torch.int32
+    return PackedPrompt(
+        gather=torch.cat([rows * seq + slot, ex_gather]).to(i32),
+        token_row=torch.cat([rows, ex_row]).to(i32),
+        token_slot=torch.cat([slot, torch.full((e,), -1, dtype=torch.int64,
+                                               device=device)]).to(i32),
+        q_offset=off_d.to(i32), head_row=head_d.to(i32), n_valid=n_valid, n_tokens=total)
 
 
 DECODE_MIN_BLOCKS = 2048   # 8 four-wave blocks per CU on 256 CUs
