@@ -578,16 +578,89 @@ def measure_workload(spec, steps, warmup, dev, eager=False, snapshot=False):
         pa_ms = sorted(rounds)[len(rounds) // 2]
         del qp, op
 
+        # the prompt projections alone (K6): one layer's four launches as the prefill makes
+        # them (pk.n_tokens rows, the layer-0 weights), on synthetic activations and a scratch
+        # cache layer (the kernels' time does not depend on values); steady state as above
+        proj = prefill_projections_timing(K, W, cfg, pk, st, dev) if W.tiles_ok else None
+
     res.update(
         B=B, S=S, total=total, max_new=max_new, t_first=t_first, host_build_s=host_build_s,
         prefill_ms=prefill_ms, timed_ms=timed_ms, wall_s=wall_s,
         value=B * steps / (timed_ms / 1e3), attn_ms=attn_ms, attn_bytes=attn_bytes,
         attn_launches=len(ts), n_split=n_split, decode_nb=decode_nb, n_valid=n_valid,
         pa_ms=pa_ms, pa_flops=pa_flops, prefill_flops=cfg.n_layers * pa_flops, snap=snap,
+        proj=proj,
         model_state=model_state, cfg=cfg)
     if snapshot:
         res.update(model=model, st=st)
     return res
+
+
+def prefill_projections_timing(K, W, cfg, pk, st, dev):
+    """Milliseconds per launch of each K6 form of one prefill layer (median of 5 rounds of 5
+    back-to-back launches after 2 warm ones) and its executed MFMA flops (4·M·N·K: the hi and lo
+    products)."""
+    import torch
+
+    from mdlarc_scale_amd.engine import Scratch
+
+    m, d, F, H = pk.n_tokens, cfg.d_model, cfg.d_ff, cfg.n_heads
+    sc = Scratch.alloc(m, d, F, dev, fused=True)
+    g = torch.Generator(device=dev).manual_seed(5)
+    sc.x.normal_(generator=g)
+    sc.attn.copy_(torch.randn(sc.attn.shape, generator=g, device=dev).to(torch.bfloat16))
+    sc.h.copy_(torch.randn(sc.h.shape, generator=g, device=dev).to(torch.bfloat16))
+    kc0, _ = st.cache.layer(0)
+    kc, vc = torch.empty_like(kc0), torch.empty_like(kc0)
+    pos = torch.zeros(m, 3, dtype=torch.int64, device=dev)
+    qs = 1.0 / 8.0
+    forms = {
+        "qkv_rope": (4 * m * 3 * d * d, lambda: K.prefill_gemm_norm_qkv(
+            sc.x, W.ln1[0], W.eps, W.qkv_t[0], m, H, sc.rstd, sc.qkv, K.LEAD_QUERIES,
+            st.kv_start, pos, W.rope_tab, W.rope_geom, qs, sc.q, kc, vc,
+            token_row=pk.token_row, token_slot=pk.token_slot)),
+        "out_residual": (4 * m * d * d, lambda: K.prefill_gemm_split_residual(
+            sc.attn, W.out_t[0], sc.x, None, m, d, d, a_tiled=True)),
+        "gate_up_swiglu": (4 * m * 2 * F * d, lambda: K.prefill_gemm_norm_swiglu(
+            sc.x, W.ln2[0], W.eps, W.gu_t[0], W.b_gate[0], W.b_up[0], sc.h, m, F, d)),
+        "down_residual": (4 * m * d * F, lambda: K.prefill_gemm_split_residual(
+            sc.h, W.down_t[0], sc.x, W.b_down[0], m, d, F, a_tiled=True)),
+    }
+    out = {}
+    for name, (flops, fn) in forms.items():
+        for _ in range(2):
+            fn()
+        rounds = []
+        for _ in range(5):
+            t = Timer()
+            t.start()
+            for _ in range(5):
+                fn()
+            t.stop()
+            rounds.append(t.ms() / 5)
+        out[name] = (sorted(rounds)[2], flops)
+    del sc, kc, vc
+    return out
+
+
+def prefill_projections_of(r):
+    """The prompt projections' MFMA rate (K6, one layer): executed flops over launch time."""
+    proj = r.get("proj")
+    if not proj:
+        return None
+    ms = sum(v[0] for v in proj.values())
+    fl = sum(v[1] for v in proj.values())
+    return {
+        "kernel": "prefill_gemm_kernel (K6: mdl_prefill_gemm_norm_qkv, "
+                  "mdl_prefill_gemm_split_residual x 2, mdl_prefill_gemm_norm_swiglu)",
+        "bound": "mfma", "ms_per_layer": round(ms, 4), "tflop_per_layer": round(fl / 1e12, 4),
+        "achieved": round(fl / ms / 1e9, 1), "peak": BF16_PEAK_TFLOPS, "unit": "TFLOP/s",
+        "frac": round(fl / ms / 1e9 / BF16_PEAK_TFLOPS, 4),
+        "forms": {k: {"ms": round(v[0], 4), "tflop_s": round(v[1] / v[0] / 1e9, 1)}
+                  for k, v in proj.items()},
+        "flops": "executed bf16 MFMA flops, 4·M·N·K per projection (the hi and lo products of "
+                 "the split activations; the useful flops are half)",
+    }
 
 
 def roofline_of(r):
@@ -641,6 +714,7 @@ def side_config(name, dev, steps=32, warmup=4):
         "timed_cache_fill": [r["t_first"], r["t_first"] + steps],
         "decode_attention": roofline_of(r), "prefill": prefill_of(r),
         "prefill_attention": prefill_attention_of(r),
+        "prefill_projections": prefill_projections_of(r),
     }
     del r
     torch.cuda.empty_cache()
@@ -721,6 +795,7 @@ def main() -> int:
         "cpu_baseline": cpu,
         "prefill": prefill_of(r),
         "prefill_attention": prefill_attention_of(r),
+        "prefill_projections": prefill_projections_of(r),
         "microbench": micro,
         **({"configs": sides} if sides else {}),
         **({"augmentation": augment} if augment is not None else {}),

@@ -220,3 +220,29 @@ def test_norm_qkv_equals_norm_gemm_then_k2(packed, n_heads):
     li = is_lead.to(DEV)
     assert torch.equal(lead[li], qkv[li])
     assert bool(lead[~li].isnan().all())
+
+
+def test_split_gemm_at_config2_size_against_hipblaslt():
+    """At config 2's packed prefill size (268,148 rows, the qkv projection's N = 2304, K = 768)
+    K6 agrees with hipBLASLt on the [W | W] operand (an independent GEMM, fp32 accumulation in
+    another order) to fp32 rounding over every element, and with fp64 on sampled rows."""
+    from mdlarc_scale_amd.engine import gemm_f32, pack_split_weight
+
+    g = torch.Generator(device=DEV).manual_seed(3)
+    m, n, k = 268_148, 2304, 768
+    w = (0.05 * torch.randn(n, k, generator=g, device=DEV)).to(torch.bfloat16)
+    v = torch.randn(m, k, generator=g, device=DEV)
+    hi, lo = split(v)
+    a = torch.cat([hi, lo], 1).contiguous()
+    del v, lo
+    out = torch.empty(m, n, device=DEV)
+    K().prefill_gemm_split(K().tile_matrix(a), K().tile_matrix(w), out, k, a_tiled=True)
+    ref = torch.empty(m, n, device=DEV)
+    gemm_f32(a, pack_split_weight(w, DEV), ref)
+    torch.cuda.synchronize()
+    scale = ref.abs().max()
+    assert float((out - ref).abs().max() / scale) < 2e-6
+    rows = torch.randint(0, m, (512,), generator=g, device=DEV)
+    aa = a[rows].double()
+    sub = (aa[:, :k] + aa[:, k:]) @ w.double().t()
+    assert float((out[rows].double() - sub).abs().max() / sub.abs().max()) < 2e-6
