@@ -1,32 +1,36 @@
 """HIP execution engine of the TinyTransformer inference path.
 
-Dataflow per layer (M token rows, d channels, F ffn width; fp32 residual stream x):
+Dataflow per layer (M token rows, d channels, F ffn width; fp32 residual stream x), written in
+its unfused form:
 
-    xs = split(x * g1), rstd         <- K1 (layer 0) or add_rmsnorm (previous layer) [M, 2d] bf16
-    qkv = xs @ [W_qkv|W_qkv]^T       (hipBLASLt, bf16 x bf16 -> fp32)            [M, 3d] fp32
+    xs = split(x * g1), rstd                                                    [M, 2d] bf16
+    qkv = xs @ [W_qkv|W_qkv]^T       (bf16 x bf16 -> fp32)                       [M, 3d] fp32
     K2: q = rope(rstd*q)/8 -> [M, d] bf16; k, v = rope(rstd*k), rstd*v -> bf16 cache slots
     attn = K4(q, cache)              (prefill: MFMA flash; decode: split-K)      [M, 2d] bf16
            (prefill: the first 64 queries of each row recomputed exactly in fp32, K4c)
-    delta = attn @ [W_out|W_out]^T                                              [M, d] fp32
-    x += delta; xs = split(x * g2), rstd                           <- add_rmsnorm
-    gu = xs @ [W_gu|W_gu]^T          (gate and up concatenated)                  [M, 2F] fp32
-    h = split(silu(rstd*g + b_g) * (rstd*u + b_u))                  <- K3        [M, 2F] bf16
-    delta = h @ [W_down|W_down]^T                                               [M, d] fp32
-    x += delta + b_down; xs = split(x * g1_next), rstd              <- add_rmsnorm
+    x += attn @ [W_out|W_out]^T
+    gu = split(x * g2) @ [W_gu|W_gu]^T  (gate and up concatenated)               [M, 2F] fp32
+    h = split(silu(rstd*g + b_g) * (rstd*u + b_u))                               [M, 2F] bf16
+    x += h @ [W_down|W_down]^T + b_down
   final: logits = lm_head(ln_f(x)) and greedy argmax                <- lm_head kernel
 
-At decode (M = batch rows) the projections run on K5 instead of hipBLASLt, on activations and
-tiled copies of W (read once, not as [W | W]) in the MFMA tile layout, and the small kernels go
-into K5's prologues and epilogues: per layer
+Every projection runs on a hand-written MFMA GEMM that reads the tiled copy of W (read once,
+not as [W | W], in the MFMA tile layout) and takes the small kernels into its prologue and
+epilogue; x (fp32) lives in the fp32 tile layout.  Per layer:
 
-    qkv = split(x * g1) @ Wqkv^T, rstd             <- gemm_norm (ln1 in the prologue)
+    q, K, V = K2(split(x * g1) @ Wqkv^T)           <- norm_qkv (ln1 in the prologue, K2 in the
+                                                      epilogue)
     attn = K4(...)                                 (tiled output)
-    x += attn @ Wo^T                                <- gemm_split_residual
+    x += attn @ Wo^T                                <- split_residual
     h = split(silu(rstd*g + b_g) * (rstd*u + b_u)), g / u = split(x * g2) @ Wg^T / Wu^T
-                                                    <- gemm_norm_swiglu (ln2 in the prologue)
-    x += h @ Wd^T + b_down                          <- gemm_split_residual
+                                                    <- norm_swiglu (ln2 in the prologue)
+    x += h @ Wd^T + b_down                          <- split_residual
 
-with x (fp32) in the fp32 tile layout; the head kernel takes ln_f itself.
+At decode (M = batch rows) these are K5 launches (tall thin GEMMs: the weights are the traffic);
+for a prompt (M = batch * prompt length) they are K6 launches (persistent 256 x 256 tiles).
+The head kernel takes ln_f itself.  Shapes outside K6's limits (d_model > 2048, or a width that
+is not a multiple of 32) run the prompt's projections on hipBLASLt against [W | W] with K1,
+add_rmsnorm, K2 and K3 as separate passes.
 
 "split" stores a GEMM input as a hi|lo pair of bf16 (hi = bf16(v), lo = bf16(v - hi)); against a
 weight packed as [W | W] the bf16 MFMA GEMM then sees the activation to ~2^-17 instead of 2^-9.
