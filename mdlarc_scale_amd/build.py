@@ -9,6 +9,7 @@ The library is written next to this file so it travels with the source tree; obj
 from __future__ import annotations
 
 import os
+import re
 import shutil
 import subprocess
 import sys
@@ -57,15 +58,42 @@ def _hipcc() -> str:
     raise RuntimeError("hipcc not found (ROCm toolchain required to build libmdlarc_hip.so)")
 
 
-def _run(cmd: list[str]) -> None:
+def _run(cmd: list[str]) -> str:
     res = subprocess.run(cmd, capture_output=True, text=True)
     if res.returncode != 0:
         raise RuntimeError(f"command failed ({res.returncode}): {' '.join(cmd)}\n"
                            f"{res.stdout}\n{res.stderr}")
     noisy = [ln for ln in res.stderr.splitlines()
-             if ln.strip() and "packed-fp32-ops" not in ln]
+             if ln.strip() and "packed-fp32-ops" not in ln and "remark:" not in ln]
     if noisy:
         print("\n".join(noisy), file=sys.stderr)
+    return res.stderr
+
+
+# Kernels that copy global memory straight into LDS by inline assembly (lds_dma.h) wait for those
+# copies with their own s_waitcnt; they are only ever run without register spills, so their files
+# are compiled with the resource report and any scratch use fails the build.
+DMA_HEADER = "lds_dma.h"
+_SCRATCH = re.compile(r"ScratchSize \[bytes/lane\]: (\d+)")
+_FUNC = re.compile(r"Function Name: (\S+)")
+
+
+def _uses_dma(src: Path) -> bool:
+    return f'#include "{DMA_HEADER}"' in src.read_text()
+
+
+def check_no_scratch(report: str, src: str) -> None:
+    """Raise if the compiler's resource report for ``src`` gives any kernel scratch memory."""
+    func = "?"
+    for ln in report.splitlines():
+        m = _FUNC.search(ln)
+        if m:
+            func = m.group(1)
+            continue
+        m = _SCRATCH.search(ln)
+        if m and int(m.group(1)) != 0:
+            raise RuntimeError(f"{src}: kernel {func} uses {m.group(1)} bytes of scratch per lane; "
+                               f"kernels including {DMA_HEADER} must not spill")
 
 
 def build(verbose: bool = False) -> Path:
@@ -75,10 +103,16 @@ def build(verbose: bool = False) -> Path:
     objs = [BUILD / (Path(s).stem + ".o") for s in SOURCES]
 
     def compile_one(i: int) -> None:
-        cmd = [hipcc, *FLAGS, "-c", str(CSRC / SOURCES[i]), "-o", str(objs[i])]
+        src = CSRC / SOURCES[i]
+        dma = _uses_dma(src)
+        cmd = [hipcc, *FLAGS,
+               *(["-Rpass-analysis=kernel-resource-usage", "-fno-caret-diagnostics"] if dma else []),
+               "-c", str(src), "-o", str(objs[i])]
         if verbose:
             print(" ".join(cmd))
-        _run(cmd)
+        report = _run(cmd)
+        if dma:
+            check_no_scratch(report, SOURCES[i])
 
     with ThreadPoolExecutor(max_workers=min(len(SOURCES), os.cpu_count() or 4)) as ex:
         list(ex.map(compile_one, range(len(SOURCES))))

@@ -1,10 +1,9 @@
 // K4a -- prefill / full-sequence attention on bf16 MFMA (gfx950 v_mfma_f32_16x16x32_bf16).
 //
 // Block = 4 wavefronts = 128 queries of one (b, h); wave w owns queries q0+32w .. q0+32w+31 as
-// two groups of 16 (j = 0, 1).  Key tiles of 64 are staged in LDS row-major, K and V alike.
-// Working with S^T = K Q^T instead of S makes the MFMA accumulator of the scores (lane = one
-// query, 4 keys per 16-key block) exactly the B-operand layout P^T needs in O^T = V^T P^T, so the
-// probabilities never leave registers:
+// two groups of 16 (j = 0, 1).  Working with S^T = K Q^T instead of S makes the MFMA accumulator
+// of the scores (lane = one query, 4 keys per 16-key block) exactly the B-operand layout P^T
+// needs in O^T = V^T P^T, so the probabilities never leave registers:
 //   score block nb (keys 16nb..16nb+15), lane (c = lane%16, g = lane/16) holds keys 16nb+4g+i,
 //   i = 0..3, of query c.  The P^T operand of k-step kk takes blocks 2kk and 2kk+1: element e of
 //   lane group g is key 32kk + (e<4 ? 4g+e : 16+4g+e-4).
@@ -16,20 +15,37 @@
 // B whatever k that is inside the instruction, so any common key order of the operands is exact.
 // Each A operand read from LDS (K rows, V^T rows) feeds both query groups' MFMAs.
 //
-// Masking: wave 0 folds key validity (inside [kv_start, S) and the key mask) of the tile into a
-// 64-bit ballot in LDS.  Tiles that are fully valid and entirely in the past of the wave's queries
-// skip all per-element work; the others AND the ballot with the causal prefix of each query.
+// Staging: key tiles of 64 go through a ring of two LDS stages (K and V, 8 KB each, 128-byte
+// rows) filled by direct global -> LDS copies (global_load_lds_dwordx4: each wave instruction
+// writes one contiguous kilobyte, 8 key rows).  The copy of tile t+1 is issued right after the
+// barrier that publishes tile t, so it runs under tile t's MFMA and softmax work; one barrier per
+// tile.  Rows cannot be padded within a kilobyte, so the 16-byte chunks of a row are XOR-swizzled
+// instead (chunk c of row r at chunk c ^ swz(r)): the column reads of the K operand (16 rows, one
+// chunk) and the transposing V reads then hit distinct banks.  Keys outside [kv_start, S) load
+// the nearest valid key (finite data; their probabilities are 0, so they add exact zeros).
+//
+// Masking: each wave folds key validity (inside [kv_start, S) and the key mask) of a tile into a
+// 64-bit ballot, from a mask byte it loaded one tile ahead.  Tiles that are fully valid and
+// entirely in the past of the wave's queries skip all per-element work; the others AND the ballot
+// with the causal prefix of each query.
 //
 // Online softmax in the log2 domain, fp32 (v_exp_f32 directly: results below 2^-126 flush to 0,
-// which no softmax weight of a visible key can reach relative to the row maximum).  The row sums
-// come from one more MFMA per k-step against a ones operand, so they sum the same bf16-rounded
-// probabilities the PV product uses.  Queries with no visible key produce 0.  The output (the
-// out-projection GEMM input) is written as a hi|lo bf16 pair per row, see common.h.
+// which no softmax weight of a visible key can reach relative to the running maximum).  A query's
+// reference maximum m moves only when a score exceeds it by more than 2^8 (its first visible key
+// always sets it), so p = 2^(s - m) <= 256 and the o / row-sum rescale runs only in the tiles
+// where some lane's maximum jumps: that decision is per lane (alpha = 1 exactly elsewhere), and a
+// wave-wide ballot only skips the rescale code when no lane needs it.  The row sums come from one
+// more MFMA per k-step against a ones operand, so they sum the same bf16-rounded probabilities
+// the PV product uses.  Queries with no visible key produce 0.  The output (the out-projection
+// GEMM input) is written as a hi|lo bf16 pair per row, see common.h.
 //
 // Block order: block i runs on XCD i % 8; each (b, h) is pinned to one XCD, whose L2 then serves
 // all of that head's query tiles, and heads are dealt round-robin over the XCDs so that rows of
 // different lengths spread evenly.  Within a head the latest (most expensive) query tile runs
 // first.
+#include <type_traits>
+
+#include "lds_dma.h"
 #include "mfma.h"
 #include "rope.h"
 
@@ -38,8 +54,13 @@ namespace mdl {
 constexpr int kQW = 32;          // queries per wave
 constexpr int kBM = 4 * kQW;     // queries per block
 constexpr int kBN = 64;          // keys per tile
-constexpr int kLds = 72;         // LDS row stride (bf16 elements): 144 B rows, 16 B aligned
 constexpr int kXcds = 8;
+constexpr int kTileBytes = kBN * kHeadDim * 2;   // one K or V tile: 64 rows of 128 bytes
+constexpr float kRescaleGap = 8.f;               // log2 of the largest p between rescales
+
+// Chunk swizzle of the K / V tiles: any 16 consecutive rows put a given chunk in 16 distinct
+// (row parity, chunk) slots and any 8 in 8 distinct chunks.
+__device__ __forceinline__ int tile_swz(int r) { return (r ^ (r >> 3)) & 7; }
 
 __global__ __launch_bounds__(256, 3) void attn_prefill_kernel(
     const uint16_t* __restrict__ q, const uint16_t* __restrict__ kc,
@@ -63,9 +84,8 @@ __global__ __launch_bounds__(256, 3) void attn_prefill_kernel(
   const int64_t qbase = q_offset ? static_cast<int64_t>(q_offset[b]) - kstart
                                  : static_cast<int64_t>(b) * S;
 
-  __shared__ __attribute__((aligned(16))) uint16_t Ks[kBN * kLds];
-  __shared__ __attribute__((aligned(16))) uint16_t Vs[kBN * kLds];
-  __shared__ uint64_t Mw;
+  __shared__ __attribute__((aligned(16))) uint16_t Ks[2][kBN * kHeadDim];
+  __shared__ __attribute__((aligned(16))) uint16_t Vs[2][kBN * kHeadDim];
 
   const int wq0 = q0 + kQW * wave;
   int qi[2];
@@ -87,9 +107,53 @@ __global__ __launch_bounds__(256, 3) void attn_prefill_kernel(
   const uint16_t* Kg = kc + head_off;
   const uint16_t* Vg = vc + head_off;
   const int kt0 = (kstart / kBN) * kBN;
-  const int kend = causal ? min(S, q0 + kBM) : S;
+  // a row with no valid key attends to nothing: its tiles are skipped (o and the sum stay 0)
+  const int kend = kstart >= S ? kt0 : (causal ? min(S, q0 + kBM) : S);
   const uint8_t* mrow = kmask ? kmask + static_cast<int64_t>(b) * S : nullptr;
   const bf16x8_t ones = bf16_ones8();
+
+  // Tile kt -> stage st: wave w copies key rows 8 (4 r + w) .. + 7 (r = 0, 1), one kilobyte of K
+  // and one of V per r; lane l takes physical chunk l % 8 of row l / 8, i.e. logical chunk
+  // (l % 8) ^ swz(row).  Rows outside [kstart, S) copy the nearest valid key.
+  const uint32_t ks0 = lds_addr(&Ks[0][0]), vs0 = lds_addr(&Vs[0][0]);
+  auto issue = [&](int kt, int st) {
+#pragma unroll
+    for (int r = 0; r < 2; ++r) {
+      const int row = 8 * (4 * r + wave) + (lane >> 3);
+      const int kj = min(max(kt + row, kstart), S - 1);
+      const int64_t off =
+          static_cast<int64_t>(kj) * kHeadDim + 8 * ((lane & 7) ^ tile_swz(row));
+      const uint32_t run = st * kTileBytes + (4 * r + wave) * 1024;
+      dma16(Kg + off, __builtin_amdgcn_readfirstlane(ks0 + run));
+      dma16(Vg + off, __builtin_amdgcn_readfirstlane(vs0 + run));
+    }
+  };
+  // this lane's key of tile kt is valid: inside [kstart, S) and not masked
+  auto mask_byte = [&](int kt) -> int {
+    const int kj = kt + lane;
+    if (kj >= S || kj < kstart) return 0;
+    return mrow ? mrow[kj] : 1;
+  };
+
+  // Lane parts of the swizzled LDS read addresses (bytes).  K operand (score block nb, k-step
+  // kk): row 16 nb + c16, logical chunk 4 kk + g, physical chunk L ^ (2 nb ^ 4 kk) with
+  // L = g ^ c16 ^ (c16 >> 3).  V^T operand (k-step kk, dim block db, rows r0 and r0 + 16,
+  // r0 = 32 kk + 4 g + c16 / 4): physical chunk Mv ^ (2 db ^ 4 kk [^ 2 for r0 + 16]).  Both
+  // constants take the values 0, 2, 4, 6, so four offsets per operand cover every read; the row
+  // and stage parts are immediate offsets.
+  uint32_t kofs[4], vofs[4];
+  {
+    const int L = (g ^ c16 ^ (c16 >> 3)) & 7;
+    const int Mv = ((4 * (g & 1) + (c16 >> 2)) ^ (g >> 1) ^ ((c16 >> 1) & 1)) & 7;
+    const int rl = 4 * g + (c16 >> 2);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      kofs[i] = c16 * 128 + 16 * (L ^ (2 * i));
+      vofs[i] = rl * 128 + 16 * (Mv ^ (2 * i)) + 8 * (c16 & 1);
+    }
+  }
+  const char* Kb = reinterpret_cast<const char*>(&Ks[0][0]);
+  const char* Vb = reinterpret_cast<const char*>(&Vs[0][0]);
 
   float m_run[2] = {-INFINITY, -INFINITY};
   f32x4_t lsum[2], o[2][4];
@@ -100,42 +164,7 @@ __global__ __launch_bounds__(256, 3) void attn_prefill_kernel(
     for (int db = 0; db < 4; ++db) o[j][db] = f32x4_t{0.f, 0.f, 0.f, 0.f};
   }
 
-  for (int kt = kt0; kt < kend; kt += kBN) {
-    // stage the tile: 64 keys x 128 B of K and of V, 16 B per lane per load
-    uint4 pk[2], pv[2];
-#pragma unroll
-    for (int rep = 0; rep < 2; ++rep) {
-      const int ch = tid + rep * 256;
-      const int key = ch >> 3, d0 = (ch & 7) * 8;
-      const int kj = kt + key;
-      pk[rep] = make_uint4(0, 0, 0, 0);
-      pv[rep] = pk[rep];
-      if (kj < S && kj >= kstart) {    // slots before kstart may hold stale values
-        pk[rep] = *reinterpret_cast<const uint4*>(Kg + static_cast<int64_t>(kj) * kHeadDim + d0);
-        pv[rep] = *reinterpret_cast<const uint4*>(Vg + static_cast<int64_t>(kj) * kHeadDim + d0);
-      }
-    }
-    bool key_ok = false;
-    if (wave == 0) {
-      const int kj = kt + lane;
-      key_ok = kj < S && kj >= kstart && (!mrow || mrow[kj] != 0);
-    }
-    __syncthreads();   // the previous tile's LDS readers are done
-#pragma unroll
-    for (int rep = 0; rep < 2; ++rep) {
-      const int ch = tid + rep * 256;
-      const int key = ch >> 3, d0 = (ch & 7) * 8;
-      *reinterpret_cast<uint4*>(&Ks[key * kLds + d0]) = pk[rep];
-      *reinterpret_cast<uint4*>(&Vs[key * kLds + d0]) = pv[rep];
-    }
-    if (wave == 0) {
-      const uint64_t bal = __ballot(key_ok);
-      if (lane == 0) Mw = bal;
-    }
-    __syncthreads();
-    if (causal && kt > wq0 + kQW - 1) continue;   // the whole tile is in this wave's future
-    const uint64_t mw = Mw;
-
+  auto compute = [&](const char* Kt, const char* Vt, int kt, uint64_t mw) {
     // S^T = K Q^T: 4 blocks of 16 keys for both query groups
     f32x4_t sc[2][4];
 #pragma unroll
@@ -144,8 +173,9 @@ __global__ __launch_bounds__(256, 3) void attn_prefill_kernel(
       sc[1][nb] = sc[0][nb];
 #pragma unroll
       for (int kk = 0; kk < 2; ++kk) {
-        const bf16x8_t a = as_bf16x8(
-            *reinterpret_cast<const uint4*>(&Ks[(nb * 16 + c16) * kLds + 32 * kk + 8 * g]));
+        const int kc_ = ((2 * nb) ^ (4 * kk)) & 7;
+        const bf16x8_t a =
+            as_bf16x8(*reinterpret_cast<const uint4*>(Kt + kofs[kc_ >> 1] + 2048 * nb));
         sc[0][nb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, qf[0][kk], sc[0][nb], 0, 0, 0);
         sc[1][nb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, qf[1][kk], sc[1][nb], 0, 0, 0);
       }
@@ -180,14 +210,18 @@ __global__ __launch_bounds__(256, 3) void attn_prefill_kernel(
       for (int nb = 0; nb < 4; ++nb)
 #pragma unroll
         for (int i = 0; i < 4; ++i) tmax = fmaxf(tmax, sc[j][nb][i]);
-      tmax = max_over_groups(tmax);
-      const float mnew = fmaxf(m_run[j], tmax * kLog2eF);
-      const float mb = (mnew == -INFINITY) ? 0.f : mnew;   // no visible key yet: p = 0
-      const float alpha = __builtin_amdgcn_exp2f(m_run[j] - mb);
-      m_run[j] = mnew;
-      lsum[j] *= alpha;
+      tmax = max_over_groups(tmax) * kLog2eF;
+      // move the reference when this lane's maximum passes it by more than the gap (or on its
+      // first visible key: m = -inf, alpha = 0); the other lanes are left untouched
+      const bool move = tmax > m_run[j] + kRescaleGap;
+      if (__ballot(move) != 0 && move) {
+        const float alpha = __builtin_amdgcn_exp2f(m_run[j] - tmax);
+        m_run[j] = tmax;
+        lsum[j] *= alpha;
 #pragma unroll
-      for (int db = 0; db < 4; ++db) o[j][db] *= alpha;
+        for (int db = 0; db < 4; ++db) o[j][db] *= alpha;
+      }
+      const float mb = (m_run[j] == -INFINITY) ? 0.f : m_run[j];   // no visible key yet: p = 0
 #pragma unroll
       for (int nb = 0; nb < 4; ++nb)
 #pragma unroll
@@ -202,13 +236,43 @@ __global__ __launch_bounds__(256, 3) void attn_prefill_kernel(
     for (int kk = 0; kk < 2; ++kk) {
 #pragma unroll
       for (int db = 0; db < 4; ++db) {
-        const bf16x8_t a = vt_operand(Vs, kLds, kk, db, c16, g);
+        const int c0 = ((2 * db) ^ (4 * kk)) & 7, c1 = c0 ^ 2;
+        const s16x4_t lo4 = lds_read_tr16(
+            reinterpret_cast<const uint16_t*>(Vt + vofs[c0 >> 1] + 4096 * kk));
+        const s16x4_t hi4 = lds_read_tr16(
+            reinterpret_cast<const uint16_t*>(Vt + vofs[c1 >> 1] + 4096 * kk + 2048));
+        const bf16x8_t a = __builtin_bit_cast(
+            bf16x8_t, __builtin_shufflevector(lo4, hi4, 0, 1, 2, 3, 4, 5, 6, 7));
         o[0][db] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, pb[0][kk], o[0][db], 0, 0, 0);
         o[1][db] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, pb[1][kk], o[1][db], 0, 0, 0);
       }
       lsum[0] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ones, pb[0][kk], lsum[0], 0, 0, 0);
       lsum[1] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ones, pb[1][kk], lsum[1], 0, 0, 0);
     }
+  };
+
+  int mb_next = 0;                 // this lane's key validity for the next tile's ballot
+  if (kt0 < kend) {
+    mb_next = mask_byte(kt0);
+    issue(kt0, 0);
+  }
+  // One tile in stage ST (a compile-time constant, so the stage offset folds into the LDS reads).
+  // Every wave of the block runs the same tiles, so the barriers match.
+  auto tile = [&](int kt, auto stc) {
+    constexpr int ST = decltype(stc)::value;
+    // tile kt has landed in stage ST for every wave, and every wave is done with stage ST ^ 1
+    asm volatile("s_waitcnt vmcnt(0)\n\ts_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
+    const uint64_t mw = __ballot(mb_next != 0);
+    if (kt + kBN < kend) {
+      mb_next = mask_byte(kt + kBN);
+      issue(kt + kBN, ST ^ 1);
+    }
+    if (causal && kt > wq0 + kQW - 1) return;   // the whole tile is in this wave's future
+    compute(Kb + ST * kTileBytes, Vb + ST * kTileBytes, kt, mw);
+  };
+  for (int kt = kt0; kt < kend; kt += 2 * kBN) {
+    tile(kt, std::integral_constant<int, 0>{});
+    if (kt + kBN < kend) tile(kt + kBN, std::integral_constant<int, 1>{});
   }
 
   // output row (b, qi) holds 2*H*64 bf16: hi of every head, then lo of every head (row-major,

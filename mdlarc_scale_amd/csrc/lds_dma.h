@@ -1,0 +1,27 @@
+// Direct global -> LDS copies (gfx950 global_load_lds_dwordx4), shared by the kernels that stage
+// their operands in LDS rings (K6, K4a).
+#pragma once
+
+#include "common.h"
+
+namespace mdl {
+
+// LDS byte address of a pointer into __shared__ memory
+__device__ __forceinline__ uint32_t lds_addr(const void* p) {
+  return static_cast<uint32_t>(
+      reinterpret_cast<uintptr_t>((const __attribute__((address_space(3))) void*)(p)));
+}
+
+// 16 bytes per lane from global memory straight into LDS: lane l's bytes land at lds + 16 l
+// (lds wave-uniform, through M0).  Issued as inline assembly, so the compiler neither sees nor
+// waits for these loads: a kernel waits for them itself (s_waitcnt vmcnt) before the barrier
+// that publishes the stage.  The compiler's own waits stay correct beside them: vector memory
+// operations complete in issue order, so loads it does not know of only make its vmcnt(n) waits
+// stricter.  Kernels that use this must not spill: the library build rejects scratch use in the
+// files that include this header.
+__device__ __forceinline__ void dma16(const void* src, uint32_t lds) {
+  asm volatile("s_mov_b32 m0, %1\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, off"
+               :: "v"(src), "s"(lds) : "memory");
+}
+
+}  // namespace mdl

@@ -39,6 +39,7 @@
 #include <algorithm>
 
 #include "common.h"
+#include "lds_dma.h"
 #include "mfma.h"
 #include "rope.h"
 
@@ -89,24 +90,11 @@ struct Args {
   int M, N, K, tiles_n, tiles, per_xcd;
 };
 
-// LDS byte address of a pointer into __shared__ memory
-__device__ __forceinline__ uint32_t lds_addr(const void* p) {
-  return static_cast<uint32_t>(
-      reinterpret_cast<uintptr_t>((const __attribute__((address_space(3))) void*)(p)));
-}
-
-// 16 bytes per lane from global memory straight into LDS: lane l's bytes land at
-// lds + 16 l (lds wave-uniform, through M0).  Issued as inline assembly so that the compiler
-// adds no waits of its own for it: the main loop counts these loads itself (vmcnt), and the
-// kernel issues no other global loads while any is in flight.
-__device__ __forceinline__ void dma16(const void* src, uint32_t lds) {
-  asm volatile("s_mov_b32 m0, %1\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, off"
-               :: "v"(src), "s"(lds) : "memory");
-}
-
-// Wait until at most N of this wave's global loads are in flight, then a block barrier that
-// also waits for this wave's LDS traffic; the memory clobbers keep the compiler from moving
-// LDS accesses across either.
+// Wait until at most N of this wave's global memory operations are in flight, then a block
+// barrier that also waits for this wave's LDS traffic; the memory clobbers keep the compiler from
+// moving LDS accesses across either.  N counts the copies issued for later stages; any other
+// load or store the wave issued after this stage's copies (epilogue traffic of the previous
+// tile) only makes the wait stricter.
 template <int N>
 __device__ __forceinline__ void stage_barrier() {
   asm volatile("s_waitcnt vmcnt(%0)\n\ts_waitcnt lgkmcnt(0)\n\ts_barrier" :: "n"(N) : "memory");
