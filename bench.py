@@ -562,7 +562,7 @@ def measure_workload(spec, steps, warmup, dev, eager=False, snapshot=False):
 
         def prefill_attention():
             K.attn_prefill_packed(qp, kc0, vc0, B, S, H, st.pmask, st.kv_start, pk.q_offset,
-                                  pk.n_valid, True, op)
+                                  pk.n_valid, True, op, row_holes=st.holes)
 
         # steady state: 3 warm launches, then the median of 5 rounds of 10 back-to-back launches
         for _ in range(3):

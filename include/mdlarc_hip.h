@@ -393,11 +393,13 @@ int mdl_tile_matrix(const uint16_t* src, int64_t ld, int rows, int cols, uint16_
  * Query i of row b sees key j iff j < seq, key_mask[b*seq + j] != 0 (key_mask may be NULL),
  * j >= kv_start[b] (kv_start may be NULL; it must not exclude a visible key) and, if causal,
  * j <= i.  A query with no visible key outputs 0 (torch CPU SDPA semantics).
+ * row_holes (uint8 [batch], may be NULL): 0 promises that row b's key mask is set exactly on
+ *   [kv_start[b], seq), so the kernel skips reading it (mdl_grid_init computes it).
  */
 int mdl_attn_prefill(const uint16_t* q, const uint16_t* k_cache, const uint16_t* v_cache,
                      int batch, int seq, int n_heads, int head_dim, int cache_slots,
-                     const uint8_t* key_mask, const int32_t* kv_start, int causal,
-                     uint16_t* out, int out_layout, void* stream);
+                     const uint8_t* key_mask, const uint8_t* row_holes, const int32_t* kv_start,
+                     int causal, uint16_t* out, int out_layout, void* stream);
 
 /*
  * K4a over packed query rows: as mdl_attn_prefill, for the queries i >= kv_start[b] of each row
@@ -411,9 +413,9 @@ int mdl_attn_prefill(const uint16_t* q, const uint16_t* k_cache, const uint16_t*
  */
 int mdl_attn_prefill_packed(const uint16_t* q, const uint16_t* k_cache, const uint16_t* v_cache,
                             int batch, int seq, int n_heads, int head_dim, int cache_slots,
-                            const uint8_t* key_mask, const int32_t* kv_start,
-                            const int32_t* q_offset, int causal, uint16_t* out, int out_layout,
-                            void* stream);
+                            const uint8_t* key_mask, const uint8_t* row_holes,
+                            const int32_t* kv_start, const int32_t* q_offset, int causal,
+                            uint16_t* out, int out_layout, void* stream);
 
 /*
  * K4c -- exact (fp32) causal attention for the lead queries of each row, after K4a.

@@ -73,9 +73,9 @@ SIGNATURES: dict[str, tuple[object, list]] = {
                                           P, P, c_int, c_int, c_int, c_int, c_int, c_int, c_float,
                                           P, P, P, c_int, c_int, c_int, P, P, P]),
     "mdl_tile_matrix": (c_int, [P, c_int64, c_int, c_int, P, P]),
-    "mdl_attn_prefill": (c_int, [P, P, P, c_int, c_int, c_int, c_int, c_int, P, P, c_int, P,
+    "mdl_attn_prefill": (c_int, [P, P, P, c_int, c_int, c_int, c_int, c_int, P, P, P, c_int, P,
                                  c_int, P]),
-    "mdl_attn_prefill_packed": (c_int, [P, P, P, c_int, c_int, c_int, c_int, c_int, P, P, P,
+    "mdl_attn_prefill_packed": (c_int, [P, P, P, c_int, c_int, c_int, c_int, c_int, P, P, P, P,
                                         c_int, P, c_int, P]),
     "mdl_attn_prefill_lead": (c_int, [P, c_int64, P, P, P, c_int, c_int, c_int, c_int, c_int,
                                       c_int, c_float, c_int, c_int, c_int, c_int, P, P, P, P,

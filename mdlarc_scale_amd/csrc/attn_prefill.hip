@@ -25,18 +25,20 @@
 // the nearest valid key (finite data; their probabilities are 0, so they add exact zeros).
 //
 // Masking: each wave folds key validity (inside [kv_start, S) and the key mask) of a tile into a
-// 64-bit ballot, from a mask byte it loaded one tile ahead.  Tiles that are fully valid and
-// entirely in the past of the wave's queries skip all per-element work; the others AND the ballot
-// with the causal prefix of each query.
+// 64-bit ballot: from a mask byte it loaded one tile ahead, or, for a row without a key mask (or
+// whose mask row_holes marks as the run [kv_start, S)), from the range alone, all ones for tiles
+// inside it.  Tiles that are fully valid and entirely in the past of the wave's queries skip all
+// per-element work; the others AND the ballot with the causal prefix of each query.
 //
 // Online softmax in the log2 domain, fp32 (v_exp_f32 directly: results below 2^-126 flush to 0,
 // which no softmax weight of a visible key can reach relative to the running maximum).  A query's
-// reference maximum m moves only when a score exceeds it by more than 2^8 (its first visible key
-// always sets it), so p = 2^(s - m) <= 256 and the o / row-sum rescale runs only in the tiles
-// where some lane's maximum jumps: that decision is per lane (alpha = 1 exactly elsewhere), and a
-// wave-wide ballot only skips the rescale code when no lane needs it.  The row sums come from one
-// more MFMA per k-step against a ones operand, so they sum the same bf16-rounded probabilities
-// the PV product uses.  Queries with no visible key produce 0.  The output (the out-projection
+// reference maximum m moves only when a score exceeds it by more than a factor 2^8 (its first
+// visible key always sets it), so p = 2^(s - m) <= 256 and the o / row-sum rescale runs only in
+// the tiles where some query's maximum jumps.  That decision is per query (the other queries are
+// left untouched), so results do not depend on which queries share a wave; wave-wide ballots
+// only skip the code (the cross-lane maximum, the rescale) when no lane needs it.  The row sums
+// come from one more MFMA per k-step against a ones operand, so they sum the same bf16-rounded
+// probabilities the PV product uses.  Queries with no visible key produce 0.  The output (the out-projection
 // GEMM input) is written as a hi|lo bf16 pair per row, see common.h.
 //
 // Block order: block i runs on XCD i % 8; each (b, h) is pinned to one XCD, whose L2 then serves
@@ -58,15 +60,20 @@ constexpr int kXcds = 8;
 constexpr int kTileBytes = kBN * kHeadDim * 2;   // one K or V tile: 64 rows of 128 bytes
 constexpr float kRescaleGap = 8.f;               // log2 of the largest p between rescales
 
-// Chunk swizzle of the K / V tiles: any 16 consecutive rows put a given chunk in 16 distinct
-// (row parity, chunk) slots and any 8 in 8 distinct chunks.
-__device__ __forceinline__ int tile_swz(int r) { return (r ^ (r >> 3)) & 7; }
+// Chunk swizzle of the K / V tiles, a function of the row's low 4 bits (bit 0 = r0^r3,
+// bit 1 = r0^r2, bit 2 = r1).  Chosen by exhaustive search over the linear swizzles so that both
+// operand reads are free of bank conflicts whether the LDS serves 16-byte reads 8 lanes and
+// 8-byte reads 16 lanes a cycle (32 banks) or 16 and 32 lanes (64 banks).
+__device__ __forceinline__ int tile_swz(int r) {
+  return ((r ^ (r >> 3)) & 1) | (((r ^ (r >> 2)) & 1) << 1) | (((r >> 1) & 1) << 2);
+}
 
 __global__ __launch_bounds__(256, 3) void attn_prefill_kernel(
     const uint16_t* __restrict__ q, const uint16_t* __restrict__ kc,
     const uint16_t* __restrict__ vc, int S, int H, int slots, const uint8_t* __restrict__ kmask,
-    const int32_t* __restrict__ kv_start, const int32_t* __restrict__ q_offset, int causal,
-    uint16_t* __restrict__ out, int out_tiled, int nqt, int n_bh) {
+    const uint8_t* __restrict__ row_holes, const int32_t* __restrict__ kv_start,
+    const int32_t* __restrict__ q_offset, int causal, uint16_t* __restrict__ out, int out_tiled,
+    int nqt, int n_bh) {
   const int slot = blockIdx.x / kXcds;
   const int kq = slot / nqt;
   const int bh = blockIdx.x % kXcds + kXcds * kq;
@@ -109,14 +116,35 @@ __global__ __launch_bounds__(256, 3) void attn_prefill_kernel(
   const int kt0 = (kstart / kBN) * kBN;
   // a row with no valid key attends to nothing: its tiles are skipped (o and the sum stay 0)
   const int kend = kstart >= S ? kt0 : (causal ? min(S, q0 + kBM) : S);
-  const uint8_t* mrow = kmask ? kmask + static_cast<int64_t>(b) * S : nullptr;
+  // row_holes[b] == 0: the key mask of row b is exactly [kstart, S), which kstart already says
+  const bool dense = row_holes && row_holes[b] == 0;
+  const uint8_t* mrow = kmask && !dense ? kmask + static_cast<int64_t>(b) * S : nullptr;
   const bf16x8_t ones = bf16_ones8();
 
   // Tile kt -> stage st: wave w copies key rows 8 (4 r + w) .. + 7 (r = 0, 1), one kilobyte of K
   // and one of V per r; lane l takes physical chunk l % 8 of row l / 8, i.e. logical chunk
-  // (l % 8) ^ swz(row).  Rows outside [kstart, S) copy the nearest valid key.
+  // (l % 8) ^ swz(row).  A tile inside [kstart, S) is copied from the scalar tile address plus a
+  // fixed lane offset; in the first and last tiles of a row, rows outside [kstart, S) copy the
+  // nearest valid key instead.
   const uint32_t ks0 = lds_addr(&Ks[0][0]), vs0 = lds_addr(&Vs[0][0]);
+  uint32_t loff[2];
+#pragma unroll
+  for (int r = 0; r < 2; ++r) {
+    const int row = 8 * (4 * r + wave) + (lane >> 3);
+    loff[r] = row * 128 + 16 * ((lane & 7) ^ tile_swz(row));
+  }
   auto issue = [&](int kt, int st) {
+    if (kt >= kstart && kt + kBN <= S) {
+      const uint16_t* kb = Kg + static_cast<int64_t>(kt) * kHeadDim;
+      const uint16_t* vb = Vg + static_cast<int64_t>(kt) * kHeadDim;
+#pragma unroll
+      for (int r = 0; r < 2; ++r) {
+        const uint32_t run = st * kTileBytes + (4 * r + wave) * 1024;
+        dma16_sbase(kb, loff[r], __builtin_amdgcn_readfirstlane(ks0 + run));
+        dma16_sbase(vb, loff[r], __builtin_amdgcn_readfirstlane(vs0 + run));
+      }
+      return;
+    }
 #pragma unroll
     for (int r = 0; r < 2; ++r) {
       const int row = 8 * (4 * r + wave) + (lane >> 3);
@@ -135,22 +163,21 @@ __global__ __launch_bounds__(256, 3) void attn_prefill_kernel(
     return mrow ? mrow[kj] : 1;
   };
 
-  // Lane parts of the swizzled LDS read addresses (bytes).  K operand (score block nb, k-step
-  // kk): row 16 nb + c16, logical chunk 4 kk + g, physical chunk L ^ (2 nb ^ 4 kk) with
-  // L = g ^ c16 ^ (c16 >> 3).  V^T operand (k-step kk, dim block db, rows r0 and r0 + 16,
-  // r0 = 32 kk + 4 g + c16 / 4): physical chunk Mv ^ (2 db ^ 4 kk [^ 2 for r0 + 16]).  Both
-  // constants take the values 0, 2, 4, 6, so four offsets per operand cover every read; the row
-  // and stage parts are immediate offsets.
-  uint32_t kofs[4], vofs[4];
+  // Lane parts of the swizzled LDS read addresses (bytes).  The swizzle of a row depends on its
+  // low 4 bits only, so it is the same for rows 16 apart.  K operand (score block nb, k-step
+  // kk): row 16 nb + c16, logical chunk 4 kk + g, physical chunk (g ^ swz(c16)) ^ 4 kk.  V^T
+  // operand (k-step kk, dim block db, rows r0 and r0 + 16, r0 = 32 kk + rl, rl = 4 g + c16 / 4,
+  // dims 16 db + 4 (c16 % 4) ..): physical chunk (c16 / 2 % 2 ^ swz(rl)) ^ 2 db.  The row and
+  // stage parts are immediate offsets.
+  uint32_t kofs[2], vofs[4];
   {
-    const int L = (g ^ c16 ^ (c16 >> 3)) & 7;
-    const int Mv = ((4 * (g & 1) + (c16 >> 2)) ^ (g >> 1) ^ ((c16 >> 1) & 1)) & 7;
+    const int L = g ^ tile_swz(c16);
     const int rl = 4 * g + (c16 >> 2);
+    const int Mv = ((c16 >> 1) & 1) ^ tile_swz(rl);
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      kofs[i] = c16 * 128 + 16 * (L ^ (2 * i));
-      vofs[i] = rl * 128 + 16 * (Mv ^ (2 * i)) + 8 * (c16 & 1);
-    }
+    for (int kk = 0; kk < 2; ++kk) kofs[kk] = c16 * 128 + 16 * (L ^ (4 * kk));
+#pragma unroll
+    for (int db = 0; db < 4; ++db) vofs[db] = rl * 128 + 16 * (Mv ^ (2 * db)) + 8 * (c16 & 1);
   }
   const char* Kb = reinterpret_cast<const char*>(&Ks[0][0]);
   const char* Vb = reinterpret_cast<const char*>(&Vs[0][0]);
@@ -173,9 +200,8 @@ __global__ __launch_bounds__(256, 3) void attn_prefill_kernel(
       sc[1][nb] = sc[0][nb];
 #pragma unroll
       for (int kk = 0; kk < 2; ++kk) {
-        const int kc_ = ((2 * nb) ^ (4 * kk)) & 7;
         const bf16x8_t a =
-            as_bf16x8(*reinterpret_cast<const uint4*>(Kt + kofs[kc_ >> 1] + 2048 * nb));
+            as_bf16x8(*reinterpret_cast<const uint4*>(Kt + kofs[kk] + 2048 * nb));
         sc[0][nb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, qf[0][kk], sc[0][nb], 0, 0, 0);
         sc[1][nb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, qf[1][kk], sc[1][nb], 0, 0, 0);
       }
@@ -205,21 +231,24 @@ __global__ __launch_bounds__(256, 3) void attn_prefill_kernel(
     bf16x8_t pb[2][2];
 #pragma unroll
     for (int j = 0; j < 2; ++j) {
-      float tmax = -INFINITY;
+      float lmax = -INFINITY;
 #pragma unroll
       for (int nb = 0; nb < 4; ++nb)
 #pragma unroll
-        for (int i = 0; i < 4; ++i) tmax = fmaxf(tmax, sc[j][nb][i]);
-      tmax = max_over_groups(tmax) * kLog2eF;
-      // move the reference when this lane's maximum passes it by more than the gap (or on its
-      // first visible key: m = -inf, alpha = 0); the other lanes are left untouched
-      const bool move = tmax > m_run[j] + kRescaleGap;
-      if (__ballot(move) != 0 && move) {
-        const float alpha = __builtin_amdgcn_exp2f(m_run[j] - tmax);
-        m_run[j] = tmax;
-        lsum[j] *= alpha;
+        for (int i = 0; i < 4; ++i) lmax = fmaxf(lmax, sc[j][nb][i]);
+      // Move a query's reference when its maximum over the tile passes it by more than the gap
+      // (or on its first visible key: m = -inf, alpha = 0); other queries are left untouched.
+      // That maximum can pass only if one of its four lanes' maxima does (same test, monotone),
+      // so the cross-lane maximum is formed only in the tiles where some lane's does.
+      if (__ballot(lmax * kLog2eF > m_run[j] + kRescaleGap) != 0) {
+        const float tmax = max_over_groups(lmax) * kLog2eF;
+        if (tmax > m_run[j] + kRescaleGap) {
+          const float alpha = __builtin_amdgcn_exp2f(m_run[j] - tmax);
+          m_run[j] = tmax;
+          lsum[j] *= alpha;
 #pragma unroll
-        for (int db = 0; db < 4; ++db) o[j][db] *= alpha;
+          for (int db = 0; db < 4; ++db) o[j][db] *= alpha;
+        }
       }
       const float mb = (m_run[j] == -INFINITY) ? 0.f : m_run[j];   // no visible key yet: p = 0
 #pragma unroll
@@ -236,11 +265,10 @@ __global__ __launch_bounds__(256, 3) void attn_prefill_kernel(
     for (int kk = 0; kk < 2; ++kk) {
 #pragma unroll
       for (int db = 0; db < 4; ++db) {
-        const int c0 = ((2 * db) ^ (4 * kk)) & 7, c1 = c0 ^ 2;
         const s16x4_t lo4 = lds_read_tr16(
-            reinterpret_cast<const uint16_t*>(Vt + vofs[c0 >> 1] + 4096 * kk));
+            reinterpret_cast<const uint16_t*>(Vt + vofs[db] + 4096 * kk));
         const s16x4_t hi4 = lds_read_tr16(
-            reinterpret_cast<const uint16_t*>(Vt + vofs[c1 >> 1] + 4096 * kk + 2048));
+            reinterpret_cast<const uint16_t*>(Vt + vofs[db] + 4096 * kk + 2048));
         const bf16x8_t a = __builtin_bit_cast(
             bf16x8_t, __builtin_shufflevector(lo4, hi4, 0, 1, 2, 3, 4, 5, 6, 7));
         o[0][db] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, pb[0][kk], o[0][db], 0, 0, 0);
@@ -251,9 +279,10 @@ __global__ __launch_bounds__(256, 3) void attn_prefill_kernel(
     }
   };
 
-  int mb_next = 0;                 // this lane's key validity for the next tile's ballot
+  // with a key mask, this lane's key validity for the next tile's ballot (loaded a tile ahead)
+  int mb_next = 0;
   if (kt0 < kend) {
-    mb_next = mask_byte(kt0);
+    if (mrow) mb_next = mask_byte(kt0);
     issue(kt0, 0);
   }
   // One tile in stage ST (a compile-time constant, so the stage offset folds into the LDS reads).
@@ -262,9 +291,15 @@ __global__ __launch_bounds__(256, 3) void attn_prefill_kernel(
     constexpr int ST = decltype(stc)::value;
     // tile kt has landed in stage ST for every wave, and every wave is done with stage ST ^ 1
     asm volatile("s_waitcnt vmcnt(0)\n\ts_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
-    const uint64_t mw = __ballot(mb_next != 0);
+    uint64_t mw;
+    if (mrow)
+      mw = __ballot(mb_next != 0);
+    else if (kt >= kstart && kt + kBN <= S)
+      mw = ~0ull;
+    else
+      mw = __ballot(kt + lane >= kstart && kt + lane < S);
     if (kt + kBN < kend) {
-      mb_next = mask_byte(kt + kBN);
+      if (mrow) mb_next = mask_byte(kt + kBN);
       issue(kt + kBN, ST ^ 1);
     }
     if (causal && kt > wq0 + kQW - 1) return;   // the whole tile is in this wave's future
@@ -447,8 +482,9 @@ namespace mdl {
 
 int launch_prefill(const uint16_t* q, const uint16_t* k_cache, const uint16_t* v_cache,
                    int batch, int seq, int n_heads, int head_dim, int cache_slots,
-                   const uint8_t* key_mask, const int32_t* kv_start, const int32_t* q_offset,
-                   int causal, uint16_t* out, int out_layout, hipStream_t st) {
+                   const uint8_t* key_mask, const uint8_t* row_holes, const int32_t* kv_start,
+                   const int32_t* q_offset, int causal, uint16_t* out, int out_layout,
+                   hipStream_t st) {
   if (!q || !k_cache || !v_cache || !out) return MDL_ERR_NULL;
   if (out_layout != MDL_LAYOUT_ROWS && out_layout != MDL_LAYOUT_TILES) return MDL_ERR_SHAPE;
   if (head_dim != kHeadDim) return MDL_ERR_HEAD_DIM;
@@ -463,7 +499,7 @@ int launch_prefill(const uint16_t* q, const uint16_t* k_cache, const uint16_t* v
   const int64_t blocks = (heads + kXcds - 1) / kXcds * kXcds * nqt;
   if (blocks > 0x7fffffff) return MDL_ERR_SHAPE;
   attn_prefill_kernel<<<static_cast<unsigned>(blocks), 256, 0, st>>>(
-      q, k_cache, v_cache, seq, n_heads, cache_slots, key_mask, kv_start, q_offset,
+      q, k_cache, v_cache, seq, n_heads, cache_slots, key_mask, row_holes, kv_start, q_offset,
       causal ? 1 : 0, out, out_layout == MDL_LAYOUT_TILES ? 1 : 0, static_cast<int>(nqt),
       static_cast<int>(heads));
   return launch_status();
@@ -474,22 +510,22 @@ int launch_prefill(const uint16_t* q, const uint16_t* k_cache, const uint16_t* v
 extern "C" int mdl_attn_prefill(const uint16_t* q, const uint16_t* k_cache,
                                 const uint16_t* v_cache, int batch, int seq, int n_heads,
                                 int head_dim, int cache_slots, const uint8_t* key_mask,
-                                const int32_t* kv_start, int causal, uint16_t* out,
-                                int out_layout, void* stream) {
+                                const uint8_t* row_holes, const int32_t* kv_start, int causal,
+                                uint16_t* out, int out_layout, void* stream) {
   return launch_prefill(q, k_cache, v_cache, batch, seq, n_heads, head_dim, cache_slots,
-                        key_mask, kv_start, nullptr, causal, out, out_layout,
+                        key_mask, row_holes, kv_start, nullptr, causal, out, out_layout,
                         static_cast<hipStream_t>(stream));
 }
 
 extern "C" int mdl_attn_prefill_packed(const uint16_t* q, const uint16_t* k_cache,
                                        const uint16_t* v_cache, int batch, int seq, int n_heads,
                                        int head_dim, int cache_slots, const uint8_t* key_mask,
-                                       const int32_t* kv_start, const int32_t* q_offset,
-                                       int causal, uint16_t* out, int out_layout,
-                                       void* stream) {
+                                       const uint8_t* row_holes, const int32_t* kv_start,
+                                       const int32_t* q_offset, int causal, uint16_t* out,
+                                       int out_layout, void* stream) {
   if (!kv_start || !q_offset) return MDL_ERR_NULL;
   return launch_prefill(q, k_cache, v_cache, batch, seq, n_heads, head_dim, cache_slots,
-                        key_mask, kv_start, q_offset, causal, out, out_layout,
+                        key_mask, row_holes, kv_start, q_offset, causal, out, out_layout,
                         static_cast<hipStream_t>(stream));
 }
 

@@ -24,4 +24,11 @@ __device__ __forceinline__ void dma16(const void* src, uint32_t lds) {
                :: "v"(src), "s"(lds) : "memory");
 }
 
+// dma16 from base + off: a wave-uniform (scalar) base address and a per-lane byte offset, so a
+// kernel that walks a buffer moves one scalar pointer instead of recomputing lane addresses.
+__device__ __forceinline__ void dma16_sbase(const void* base, uint32_t off, uint32_t lds) {
+  asm volatile("s_mov_b32 m0, %2\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, %1"
+               :: "v"(off), "s"(base), "s"(lds) : "memory");
+}
+
 }  // namespace mdl

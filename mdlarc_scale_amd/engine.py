@@ -287,9 +287,11 @@ class HipEngine:
     def run_prompt(self, W: PackedWeights, ids: torch.Tensor, pos: torch.Tensor,
                    ex_ids: torch.Tensor | None, key_mask: torch.Tensor | None,
                    kv_start: torch.Tensor | None, causal: bool, kv_layers,
-                   sc: Scratch) -> None:
+                   sc: Scratch, row_holes: torch.Tensor | None = None) -> None:
         """Run every layer over [B, S] tokens; leaves the final residual in ``sc.x``.
-        ``kv_layers(li)`` returns the (k, v) [B, H, slots, 64] views to write slots [0, S)."""
+        ``kv_layers(li)`` returns the (k, v) [B, H, slots, 64] views to write slots [0, S).
+        ``row_holes`` (uint8 [B], from grid_init) lets the attention skip reading the key mask of
+        the rows where it is the run [kv_start, S)."""
         cfg = self.cfg
         B, S = ids.shape
         H, d = cfg.n_heads, cfg.d_model
@@ -311,7 +313,7 @@ class HipEngine:
                 K.qkv_rope_cache(sc.qkv, sc.rstd, pos, W.rope_tab, W.rope_geom, B, S, H, qs,
                                  sc.q, kc, vc, slot0=0)
             K.attn_prefill(sc.q, kc, vc, B, S, H, key_mask, kv_start, causal, sc.attn,
-                           out_tiled=fused)
+                           out_tiled=fused, row_holes=row_holes)
             if causal:
                 K.attn_prefill_lead(sc.qkv, sc.rstd, pos, W.rope_tab, W.rope_geom, qs, B, S, H,
                                     key_mask, kv_start, None, B * S, sc.attn, out_tiled=fused)
@@ -319,11 +321,12 @@ class HipEngine:
 
     def run_packed(self, W: PackedWeights, ids: torch.Tensor, pos: torch.Tensor,
                    ex_ids: torch.Tensor | None, key_mask: torch.Tensor | None,
-                   kv_start: torch.Tensor, pk: PackedPrompt, kv_layers, sc: Scratch) -> None:
+                   kv_start: torch.Tensor, pk: PackedPrompt, kv_layers, sc: Scratch,
+                   row_holes: torch.Tensor | None = None) -> None:
         """``run_prompt`` (causal) over the packed tokens ``pk`` of the [B, S] batch ``ids`` /
         ``pos``: every GEMM and elementwise kernel sees pk.n_tokens rows instead of B*S.  K/V of
         the valid tokens go to their slots; leaves the final residual in ``sc.x`` (packed rows).
-        ``sc`` must hold pk.n_tokens rows."""
+        ``sc`` must hold pk.n_tokens rows; ``row_holes`` as in ``run_prompt``."""
         cfg = self.cfg
         B, S = ids.shape
         H, d = cfg.n_heads, cfg.d_model
@@ -353,7 +356,8 @@ class HipEngine:
                 K.qkv_rope_cache_packed(sc.qkv, sc.rstd, pos_p, W.rope_tab, W.rope_geom,
                                     pk.token_row, pk.token_slot, H, qs, sc.q, kc, vc)
             K.attn_prefill_packed(sc.q, kc, vc, B, S, H, key_mask, kv_start, pk.q_offset,
-                                  pk.n_valid, True, sc.attn, out_tiled=fused)
+                                  pk.n_valid, True, sc.attn, out_tiled=fused,
+                                  row_holes=row_holes)
             K.attn_prefill_lead(sc.qkv, sc.rstd, pos_p, W.rope_tab, W.rope_geom, qs, B, S, H,
                                 key_mask, kv_start, pk.q_offset, pk.n_tokens, sc.attn,
                                 out_tiled=fused)

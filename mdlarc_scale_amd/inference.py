@@ -325,13 +325,13 @@ class Generator:
             sc = Scratch.alloc(pk.n_tokens, cfg.d_model, cfg.d_ff, dev,
                                fused=prompt_gemms_fused(cfg.d_model, cfg.d_ff))
             self.eng.run_packed(W, input_ids, positions_3d, st.ex, st.pmask, st.kv_start, pk,
-                                st.cache.layer, sc)
+                                st.cache.layer, sc, row_holes=st.holes)
             head_row = pk.head_row
         else:
             sc = Scratch.alloc(st.B * st.S, cfg.d_model, cfg.d_ff, dev,
                                fused=prompt_gemms_fused(cfg.d_model, cfg.d_ff))
             self.eng.run_prompt(W, input_ids, positions_3d, st.ex, st.pmask, st.kv_start, True,
-                                st.cache.layer, sc)
+                                st.cache.layer, sc, row_holes=st.holes)
             head_row = st.last_row
         K.lm_head(sc.x, head_row, st.B, W.ln_f, W.eps, W.head, st.logits, st.tok, cons,
                   x_tiled=sc.fused)

@@ -586,8 +586,10 @@ def tile_matrix(src: torch.Tensor, cols: int | None = None) -> torch.Tensor:
 def attn_prefill(q: torch.Tensor, k_cache: torch.Tensor, v_cache: torch.Tensor, batch: int,
                  seq: int, n_heads: int, key_mask: torch.Tensor | None,
                  kv_start: torch.Tensor | None, causal: bool, out: torch.Tensor,
-                 out_tiled: bool = False) -> None:
-    """out: split [batch*seq, 2*n_heads*64] bf16 (row-major, or the MFMA tile layout)."""
+                 out_tiled: bool = False, row_holes: torch.Tensor | None = None) -> None:
+    """out: split [batch*seq, 2*n_heads*64] bf16 (row-major, or the MFMA tile layout).
+    row_holes (uint8 [batch], from grid_init): 0 marks a row whose key mask is exactly
+    [kv_start, seq), which the kernel then does not read."""
     n = batch * seq * n_heads * HEAD_DIM
     _need(q, "q", BF16, n)
     _need(out, "out", BF16, split_numel(batch * seq, n_heads * HEAD_DIM, out_tiled))
@@ -596,20 +598,23 @@ def attn_prefill(q: torch.Tensor, k_cache: torch.Tensor, v_cache: torch.Tensor, 
         if c.dim() != 4 or c.shape[0] != batch or c.shape[1] != n_heads or c.shape[3] != 64:
             raise ValueError(f"{name} must be [batch, n_heads, slots, 64]")
     _need(key_mask, "key_mask", U8, batch * seq, optional=True)
+    _need(row_holes, "row_holes", U8, batch, optional=True)
     _need(kv_start, "kv_start", I32, batch, optional=True)
     _lib.check(_lib.lib().mdl_attn_prefill(
         _p(q), _p(k_cache), _p(v_cache), batch, seq, n_heads, HEAD_DIM, k_cache.shape[2],
-        _p(key_mask), _p(kv_start), 1 if causal else 0, _p(out), _layout(out_tiled), _stream()),
-        "mdl_attn_prefill")
+        _p(key_mask), _p(row_holes), _p(kv_start), 1 if causal else 0, _p(out),
+        _layout(out_tiled), _stream()), "mdl_attn_prefill")
 
 
 def attn_prefill_packed(q: torch.Tensor, k_cache: torch.Tensor, v_cache: torch.Tensor,
                         batch: int, seq: int, n_heads: int, key_mask: torch.Tensor | None,
                         kv_start: torch.Tensor, q_offset: torch.Tensor, n_rows: int,
-                        causal: bool, out: torch.Tensor, out_tiled: bool = False) -> None:
+                        causal: bool, out: torch.Tensor, out_tiled: bool = False,
+                        row_holes: torch.Tensor | None = None) -> None:
     """Packed query rows: query i >= kv_start[b] of row b is row q_offset[b] + i - kv_start[b]
     of q ([n_rows, n_heads*64]) and out (split [n_rows, 2*n_heads*64], row-major or tiled).
-    The caller guarantees q_offset[b] + seq - kv_start[b] <= n_rows for every row."""
+    The caller guarantees q_offset[b] + seq - kv_start[b] <= n_rows for every row.  row_holes
+    as in attn_prefill."""
     n = n_rows * n_heads * HEAD_DIM
     _need(q, "q", BF16, n)
     _need(out, "out", BF16, split_numel(n_rows, n_heads * HEAD_DIM, out_tiled))
@@ -618,11 +623,12 @@ def attn_prefill_packed(q: torch.Tensor, k_cache: torch.Tensor, v_cache: torch.T
         if c.dim() != 4 or c.shape[0] != batch or c.shape[1] != n_heads or c.shape[3] != 64:
             raise ValueError(f"{name} must be [batch, n_heads, slots, 64]")
     _need(key_mask, "key_mask", U8, batch * seq, optional=True)
+    _need(row_holes, "row_holes", U8, batch, optional=True)
     _need(kv_start, "kv_start", I32, batch)
     _need(q_offset, "q_offset", I32, batch)
     _lib.check(_lib.lib().mdl_attn_prefill_packed(
         _p(q), _p(k_cache), _p(v_cache), batch, seq, n_heads, HEAD_DIM, k_cache.shape[2],
-        _p(key_mask), _p(kv_start), _p(q_offset), 1 if causal else 0, _p(out),
+        _p(key_mask), _p(row_holes), _p(kv_start), _p(q_offset), 1 if causal else 0, _p(out),
         _layout(out_tiled), _stream()), "mdl_attn_prefill_packed")
 
 

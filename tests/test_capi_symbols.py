@@ -43,10 +43,10 @@ def test_argument_errors_are_reported_before_any_launch():
     _require_lib()
     L = _lib.lib()
     fake = 1 << 20                                  # never dereferenced: rejected first
-    assert L.mdl_attn_prefill(fake, fake, fake, 1, 4, 1, 32, 4, None, None, 1, fake, 0,
+    assert L.mdl_attn_prefill(fake, fake, fake, 1, 4, 1, 32, 4, None, None, None, 1, fake, 0,
                               None) == -4
     # output layout codes are 0 / 1
-    assert L.mdl_attn_prefill(fake, fake, fake, 1, 4, 1, 64, 4, None, None, 1, fake, 2,
+    assert L.mdl_attn_prefill(fake, fake, fake, 1, 4, 1, 64, 4, None, None, None, 1, fake, 2,
                               None) == -3
     assert L.mdl_swiglu(None, 16, None, None, None, 1, 8, fake, 0, None) == -1
     assert L.mdl_swiglu(fake, 16, None, None, None, 1, 12, fake, 0, None) == -3
@@ -100,10 +100,10 @@ def test_argument_errors_are_reported_before_any_launch():
     assert L.mdl_gemm_split_tiles() >= 1
     assert 1 <= L.mdl_gemm_split_pick(256, 2304, 768) <= L.mdl_gemm_split_tiles()
     # packed prefill: the per-row starts / offsets and the per-token rows / slots are required
-    assert L.mdl_attn_prefill_packed(fake, fake, fake, 1, 4, 1, 64, 4, None, None, fake, 1, fake,
-                                     0, None) == -1
-    assert L.mdl_attn_prefill_packed(fake, fake, fake, 1, 4, 1, 32, 4, None, fake, fake, 1, fake,
-                                     1, None) == -4
+    assert L.mdl_attn_prefill_packed(fake, fake, fake, 1, 4, 1, 64, 4, None, None, None, fake, 1,
+                                     fake, 0, None) == -1
+    assert L.mdl_attn_prefill_packed(fake, fake, fake, 1, 4, 1, 32, 4, None, None, fake, fake, 1,
+                                     fake, 1, None) == -4
     assert L.mdl_qkv_rope_cache_packed(fake, 192, None, fake, fake, 4, None, fake, 1, 1, 64, 32,
                                        32, 8, 10, 10, 12, 0.125, fake, fake, fake, 4, None) == -1
     assert L.mdl_qkv_rope_cache_packed(fake, 192, None, fake, fake, 4, fake, fake, 1, 1, 32, 32,

@@ -550,6 +550,52 @@ def test_attn_prefill_packed_equals_padded(causal):
 
 
 @pytest.mark.parametrize("packed", [False, True])
+def test_attn_prefill_row_holes(packed):
+    """row_holes[b] == 0 (the key mask of row b is the run [kv_start, S)) lets the kernel skip
+    the mask: same outputs bit for bit as reading it.  The flag is a promise: set on the row
+    that has holes, that row's holes are ignored and only its outputs change."""
+    g = torch.Generator().manual_seed(77 + packed)
+    B, H, S, slots = 6, 3, 300, 320
+    q = bf(torch.randn(B, S, H, 64, generator=g) * 0.125).to(DEV)
+    kc = bf(torch.randn(B, H, slots, 64, generator=g)).to(DEV)
+    vc = bf(torch.randn(B, H, slots, 64, generator=g)).to(DEV)
+    kv = [0, 299, 170, 300, 64, 1]
+    mask = torch.ones(B, S, dtype=torch.bool)
+    for b, k0 in enumerate(kv):
+        mask[b, :k0] = False
+    mask[4, 200:230] = False                       # the only row with holes
+    mask8 = mask.to(torch.uint8).to(DEV)
+    kv_dev = torch.tensor(kv, dtype=torch.int32, device=DEV)
+    holes = torch.tensor([0, 0, 0, 0, 1, 0], dtype=torch.uint8, device=DEV)
+    if packed:
+        pk = _pack(kv, B, S)
+        gi = pk.gather[:pk.n_valid].long()
+        qq, rows = q.reshape(B * S, H * 64)[gi].contiguous(), pk.n_valid
+        row_b = torch.repeat_interleave(torch.arange(B), torch.tensor([S - k for k in kv]))
+    else:
+        qq, rows = q, B * S
+        row_b = torch.arange(B).repeat_interleave(S)
+
+    def run(row_holes):
+        out = torch.full((rows, 2 * H * 64), 3.0, device=DEV, dtype=torch.bfloat16)
+        if packed:
+            K().attn_prefill_packed(qq, kc, vc, B, S, H, mask8, kv_dev, pk.q_offset, rows, True,
+                                    out, row_holes=row_holes)
+        else:
+            K().attn_prefill(qq, kc, vc, B, S, H, mask8, kv_dev, True, out, row_holes=row_holes)
+        torch.cuda.synchronize()
+        return out
+
+    ref = run(None)
+    assert torch.equal(run(holes), ref)
+    wrong = run(torch.zeros_like(holes)).cpu()
+    refc = ref.cpu()
+    same = (wrong == refc).all(1)
+    assert bool(same[row_b != 4].all())
+    assert not bool(same[row_b == 4].all())
+
+
+@pytest.mark.parametrize("packed", [False, True])
 def test_attn_prefill_lead_exact(packed):
     """K4c: the first 64 queries at or after kv_start of each row come out as exact causal
     attention (fp64 reference from the same fp32 projection output: RMSNorm scale, 3D RoPE,
@@ -1015,7 +1061,7 @@ def test_capi_rejects_bad_arguments_before_launch():
     x = torch.zeros(16, 64, device=DEV)
     # head_dim must be 64
     assert L.mdl_attn_prefill(x.data_ptr(), x.data_ptr(), x.data_ptr(), 1, 4, 1, 32, 4, None,
-                              None, 1, x.data_ptr(), 0, None) == -4
+                              None, None, 1, x.data_ptr(), 0, None) == -4
     # cache overflow: slot0 + seq > slots
     assert L.mdl_qkv_rope_cache(x.data_ptr(), 192, None, x.data_ptr(), x.data_ptr(), 1, 4, 1, 64,
                                 32, 32, 8, 10, 10, 12, 0.125, x.data_ptr(), x.data_ptr(),
