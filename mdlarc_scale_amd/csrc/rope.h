@@ -15,24 +15,35 @@ struct RopeArgs {
   int max_x, max_y, max_z, px, py, pz;
 };
 
-// cos / sin of pair j for the token at pos3 (x, y, z).
-__device__ __forceinline__ void rope_cos_sin(int j, const int64_t* __restrict__ pos3,
-                                             const float* __restrict__ tab, const RopeArgs& ra,
-                                             float& cs, float& sn) {
-  int axis, n_pos, pairs, jj, off;
+// cos / sin of pair j for the token at position (p0, p1, p2) = (x, y, z).
+__device__ __forceinline__ void rope_cos_sin3(int j, int64_t p0, int64_t p1, int64_t p2,
+                                              const float* __restrict__ tab, const RopeArgs& ra,
+                                              float& cs, float& sn) {
+  int n_pos, pairs, jj, off;
+  int64_t p;
   if (j < ra.px) {
-    axis = 0; n_pos = ra.max_x; pairs = ra.px; jj = j; off = 0;
+    n_pos = ra.max_x; pairs = ra.px; jj = j; off = 0; p = p0;
   } else if (j < ra.px + ra.py) {
-    axis = 1; n_pos = ra.max_y; pairs = ra.py; jj = j - ra.px; off = 2 * ra.max_x * ra.px;
+    n_pos = ra.max_y; pairs = ra.py; jj = j - ra.px; off = 2 * ra.max_x * ra.px; p = p1;
   } else {
-    axis = 2; n_pos = ra.max_z; pairs = ra.pz; jj = j - ra.px - ra.py;
-    off = 2 * ra.max_x * ra.px + 2 * ra.max_y * ra.py;
+    n_pos = ra.max_z; pairs = ra.pz; jj = j - ra.px - ra.py;
+    off = 2 * ra.max_x * ra.px + 2 * ra.max_y * ra.py; p = p2;
   }
-  int64_t p = pos3[axis];
   p = p < 0 ? 0 : (p >= n_pos ? n_pos - 1 : p);
   const int ti = off + static_cast<int>(p) * pairs + jj;
   cs = tab[ti];
   sn = tab[ti + n_pos * pairs];
+}
+
+// cos / sin of pair j for the token at pos3 (x, y, z).
+__device__ __forceinline__ void rope_cos_sin(int j, const int64_t* __restrict__ pos3,
+                                             const float* __restrict__ tab, const RopeArgs& ra,
+                                             float& cs, float& sn) {
+  int64_t p0 = 0, p1 = 0, p2 = 0;
+  if (j < ra.px) p0 = pos3[0];
+  else if (j < ra.px + ra.py) p1 = pos3[1];
+  else p2 = pos3[2];
+  rope_cos_sin3(j, p0, p1, p2, tab, ra, cs, sn);
 }
 
 // A pair (a, b) rotated by (cs, sn): (a cs - b sn, b cs + a sn), each a fused multiply-add onto

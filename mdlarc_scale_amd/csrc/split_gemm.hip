@@ -150,6 +150,25 @@ __global__ __launch_bounds__(64 * kGemmWaves) void split_gemm_kernel(const GemmA
 #pragma unroll
   for (int j = 0; j < FM; ++j) ss[j] = 0.f;
 
+  // E_QKV: the epilogue's RoPE inputs are fetched ahead -- the positions of its rows here, the
+  // table entries right after the k-loop (their latency under the cross-wave reduction) -- so
+  // no chain of dependent loads follows the GEMM.  Thread's element group gi is q = tid + gi *
+  // 64 NW of the epilogue loop below.
+  constexpr int G = (FN * FM + NW - 1) / NW;   // epilogue element groups per thread
+  int64_t rpos[EPI == E_QKV ? G : 1][3];
+  if constexpr (EPI == E_QKV) {
+#pragma unroll
+    for (int gi = 0; gi < G; ++gi) {
+      const int q = threadIdx.x + gi * 64 * NW;
+      const int t = q >> 6, ln = q & 63;
+      const int m = min(m0 + 16 * (t % FM) + (ln & 15), M - 1);
+      const int64_t* pos3 = p.pos + static_cast<int64_t>(m) * 3;
+      rpos[gi][0] = pos3[0];
+      rpos[gi][1] = pos3[1];
+      rpos[gi][2] = pos3[2];
+    }
+  }
+
   // k-steps of 32: wave w takes [nk w / NW, nk (w + 1) / NW), contiguous
   const int nk = K >> 5;
   const int s0 = (nk * wave) / NW, s1 = (nk * (wave + 1)) / NW;
@@ -213,6 +232,24 @@ __global__ __launch_bounds__(64 * kGemmWaves) void split_gemm_kernel(const GemmA
                                                                 0, 0, 0);
           }
       }
+    }
+  }
+
+  // E_QKV: cos / sin of RoPE pairs dim / 2 and dim / 2 + 1 of each element group (q, k parts)
+  float rcs[EPI == E_QKV ? G : 1][4];
+  if constexpr (EPI == E_QKV) {
+#pragma unroll
+    for (int gi = 0; gi < G; ++gi) {
+      const int q = threadIdx.x + gi * 64 * NW;
+      const int t = q >> 6, ln = q & 63;
+      const int n = min(n0 + 16 * (t / FM) + 4 * (ln >> 4), N - 1);
+      const int d = N / 3;
+      const int e = n - (n / d) * d;
+      const int dim = e - (e / kHeadDim) * kHeadDim;
+      rope_cos_sin3(dim / 2, rpos[gi][0], rpos[gi][1], rpos[gi][2], p.rope_tab, p.ra,
+                    rcs[gi][0], rcs[gi][1]);
+      rope_cos_sin3(dim / 2 + 1, rpos[gi][0], rpos[gi][1], rpos[gi][2], p.rope_tab, p.ra,
+                    rcs[gi][2], rcs[gi][3]);
     }
   }
 
@@ -281,7 +318,10 @@ __global__ __launch_bounds__(64 * kGemmWaves) void split_gemm_kernel(const GemmA
       }
     }
   } else {
-    for (int q = threadIdx.x; q < FN * FM * 64; q += 64 * NW) {
+#pragma unroll
+    for (int gi = 0; gi < G; ++gi) {
+      const int q = threadIdx.x + gi * 64 * NW;
+      if (q >= FN * FM * 64) break;
       const int t = q >> 6, ln = q & 63;
       f32x4_t v = red[0][t][ln];
 #pragma unroll
@@ -312,12 +352,9 @@ __global__ __launch_bounds__(64 * kGemmWaves) void split_gemm_kernel(const GemmA
               *reinterpret_cast<uint2*>(p.vc + crow) = o;
             }
           } else {
-            float cs0, sn0, cs1, sn1, y0, y1, y2, y3;
-            const int64_t* pos3 = p.pos + static_cast<int64_t>(m) * 3;
-            rope_cos_sin(dim / 2, pos3, p.rope_tab, p.ra, cs0, sn0);
-            rope_cos_sin(dim / 2 + 1, pos3, p.rope_tab, p.ra, cs1, sn1);
-            rope_rot(a0, a1, cs0, sn0, y0, y1);
-            rope_rot(a2, a3, cs1, sn1, y2, y3);
+            float y0, y1, y2, y3;
+            rope_rot(a0, a1, rcs[gi][0], rcs[gi][1], y0, y1);
+            rope_rot(a2, a3, rcs[gi][2], rcs[gi][3], y2, y3);
             if (part == 0) {
               o.x = pack_bf2(y0 * p.q_scale, y1 * p.q_scale);
               o.y = pack_bf2(y2 * p.q_scale, y3 * p.q_scale);
