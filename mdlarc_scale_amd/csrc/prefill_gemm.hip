@@ -214,15 +214,38 @@ __global__ __launch_bounds__(kThreads, 1) void prefill_gemm_kernel(const Args p)
                                                    16 * lane);
       }
     }
+    // The hi products before the lo products, so that consecutive MFMAs write different
+    // accumulators (each accumulator still adds hi before lo).  The split forms (8 weight
+    // fragments) hold all their weight fragments and run two passes; the norm forms (16, whose
+    // registers that would exhaust) take one fragment at a time, hi for both row blocks, then lo.
+    if constexpr (AMODE == A_NORM) {
 #pragma unroll
-    for (int i = 0; i < FN; ++i) {
-      const bf16x8_t wf = *reinterpret_cast<const bf16x8_t*>(
-          base + (kAFrags + FN * wn + i) * 1024 + 16 * lane);
+      for (int i = 0; i < FN; ++i) {
+        const bf16x8_t wf = *reinterpret_cast<const bf16x8_t*>(
+            base + (kAFrags + FN * wn + i) * 1024 + 16 * lane);
 #pragma unroll
-      for (int j = 0; j < FM; ++j) {
-        acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(wf, ah[j], acc[i][j], 0, 0, 0);
-        acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(wf, al[j], acc[i][j], 0, 0, 0);
+        for (int j = 0; j < FM; ++j)
+          acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(wf, ah[j], acc[i][j], 0, 0, 0);
+#pragma unroll
+        for (int j = 0; j < FM; ++j)
+          acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(wf, al[j], acc[i][j], 0, 0, 0);
       }
+    } else {
+      bf16x8_t wf[FN];
+#pragma unroll
+      for (int i = 0; i < FN; ++i)
+        wf[i] = *reinterpret_cast<const bf16x8_t*>(base + (kAFrags + FN * wn + i) * 1024 +
+                                                   16 * lane);
+#pragma unroll
+      for (int i = 0; i < FN; ++i)
+#pragma unroll
+        for (int j = 0; j < FM; ++j)
+          acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(wf[i], ah[j], acc[i][j], 0, 0, 0);
+#pragma unroll
+      for (int i = 0; i < FN; ++i)
+#pragma unroll
+        for (int j = 0; j < FM; ++j)
+          acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(wf[i], al[j], acc[i][j], 0, 0, 0);
     }
   };
 
