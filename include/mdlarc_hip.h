@@ -149,7 +149,8 @@ int mdl_add_rmsnorm(float* x, const float* delta, const float* bias, int rows, i
  * rope_tab: fp32 [cos_x(max_x*px) | sin_x | cos_y(max_y*py) | sin_y | cos_z(max_z*pz) | sin_z],
  *      the tables of RotaryEmbedding3D._build_cache (src/transformer.py:95-126).
  * Outputs: q_out bf16 [batch*seq, d] = rope(q * rstd) * q_scale; k/v written to cache slot
- *      (slot_dev ? *slot_dev : slot0) + s for token s of each batch row.
+ *      (slot_dev ? *slot_dev : slot0) + s for token s of each batch row.  For the attention
+ *      kernels (K4a, K4b) q_scale is the softmax scale times log2(e): their softmax is base 2.
  */
 int mdl_qkv_rope_cache(const float* qkv, int64_t qkv_ld, const float* rstd,
                        const int64_t* pos, const float* rope_tab, int batch, int seq,
@@ -386,7 +387,8 @@ int mdl_tile_matrix(const uint16_t* src, int64_t ld, int rows, int cols, uint16_
  * Replaces: F.scaled_dot_product_attention in _prefill (src/inference.py:409, mask from
  *           _build_sdpa_mask :372-380, is_causal=True) and in MultiHeadSelfAttention.forward
  *           (src/transformer.py:333-349, is_causal either way).
- * q: bf16 [batch, seq, n_heads, 64], already multiplied by the softmax scale.
+ * q: bf16 [batch, seq, n_heads, 64], already multiplied by the softmax scale and by log2(e)
+ *    (the kernel's softmax is base 2: p = 2^(q.k - max)).
  * out: split bf16 [batch*seq, 2*n_heads*64] (the out-projection GEMM input) in out_layout
  *      (MDL_LAYOUT_ROWS, or MDL_LAYOUT_TILES with rows padded to a multiple of 16).
  * keys:    k_cache / v_cache slots [0, seq) of [batch, n_heads, cache_slots, 64].
@@ -424,7 +426,8 @@ int mdl_attn_prefill_packed(const uint16_t* q, const uint16_t* k_cache, const ui
  *           see at most 64 keys, so K4a's bf16 roundings of q, K, V and the probabilities are
  *           not averaged away there.
  * qkv / rstd / pos: the projection GEMM's fp32 output and the inputs K2 consumed
- *   (mdl_qkv_rope_cache, same layout and rope arguments; q_scale as there).  Token position i
+ *   (mdl_qkv_rope_cache, same layout and rope arguments).  q_scale is the softmax scale itself
+ *   (this pass computes its softmax in fp32 with natural exponentials).  Token position i
  *   of row b is row b*seq + i of them and of out, or, with q_offset (packed rows; kv_start then
  *   required), row q_offset[b] + i - kv_start[b].
  * Recomputes q, k, v of those tokens in fp32 (RMSNorm scale, 3D RoPE, softmax scale), applies
@@ -445,7 +448,8 @@ int mdl_attn_prefill_lead(const float* qkv, int64_t qkv_ld, const float* rstd,
  * the PV product rounded to bf16).
  * Replaces: F.scaled_dot_product_attention in _decode_step (src/inference.py:452) with the
  *           mask rebuilt from full_attention_mask (src/inference.py:446-450, :557-558, :626).
- * q: bf16 [batch, n_heads, 64] (pre-scaled); out: split bf16 [batch, 2*n_heads*64] in
+ * q: bf16 [batch, n_heads, 64], pre-scaled as for mdl_attn_prefill (softmax scale times
+ *    log2(e)); out: split bf16 [batch, 2*n_heads*64] in
  * out_layout (MDL_LAYOUT_ROWS or MDL_LAYOUT_TILES).
  * The query of row b sees slot j iff
  *   kv_start[b] <= j <= t, t = (seq_dev ? *seq_dev : seq_pos), and

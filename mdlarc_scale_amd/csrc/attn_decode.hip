@@ -14,7 +14,8 @@
 //     back transposed (ds_read_b64_tr_b16); P^T comes from the score accumulators, in the key
 //     order the transposing reads produce; the row sum is one more MFMA against ones, so it sums
 //     the same bf16-rounded probabilities the PV product uses.
-// The single query costs 15/16 of every MFMA, which is free: the kernel streams 256 bytes of K/V
+// q comes multiplied by the softmax scale and log2(e), so the scores are the exponents of a base-2
+// softmax (v_exp_f32).  The single query costs 15/16 of every MFMA, which is free: the kernel streams 256 bytes of K/V
 // per slot from HBM and does 2 x 128 useful flops per slot, so MFMA and VALU stay far below their
 // rates.  K and V use non-temporal loads (read once per launch; keeps the projection weights
 // cached between layers).  The 4 waves, then the splits (second kernel) merge with the usual
@@ -221,7 +222,7 @@ __global__ __launch_bounds__(256) void attn_decode_kernel(
 #pragma unroll
         for (int i = 0; i < 4; ++i) tmax = fmaxf(tmax, sc[nb][i]);
       tmax = max_over_groups(tmax);
-      const float mnew = fmaxf(m, tmax * kLog2eF);
+      const float mnew = fmaxf(m, tmax);   // q carries log2(e): scores are log2-domain
       const float mb = (mnew == -INFINITY) ? 0.f : mnew;
       const float alpha = __builtin_amdgcn_exp2f(m - mb);
       m = mnew;
@@ -232,7 +233,7 @@ __global__ __launch_bounds__(256) void attn_decode_kernel(
       for (int nb = 0; nb < NB; ++nb)
 #pragma unroll
         for (int i = 0; i < 4; ++i)
-          sc[nb][i] = __builtin_amdgcn_exp2f(fmaf(sc[nb][i], kLog2eF, -mb));
+          sc[nb][i] = __builtin_amdgcn_exp2f(sc[nb][i] - mb);
       bf16x8_t pb[NB / 2];
 #pragma unroll
       for (int kk = 0; kk < NB / 2; ++kk) pb[kk] = pt_operand(sc[2 * kk], sc[2 * kk + 1]);

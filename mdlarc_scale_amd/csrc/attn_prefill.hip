@@ -31,10 +31,12 @@
 // per-element work; the others AND the ballot with the causal prefix of each query.
 //
 // Online softmax in the log2 domain, fp32 (v_exp_f32 directly: results below 2^-126 flush to 0,
-// which no softmax weight of a visible key can reach relative to the running maximum).  A query's
-// reference maximum m moves only when a score exceeds it by more than a factor 2^8 (its first
-// visible key always sets it), so p = 2^(s - m) <= 256 and the o / row-sum rescale runs only in
-// the tiles where some query's maximum jumps.  That decision is per query (the other queries are
+// which no softmax weight of a visible key can reach relative to the running maximum).  q comes
+// multiplied by log2(e) with the softmax scale, and each QK^T accumulator starts at -m, so the
+// MFMA yields the exponent s - m itself.  A query's reference maximum m moves only when a score
+// exceeds it by more than a factor 2^8 (its first visible key always sets it), so
+// p = 2^(s - m) <= 256 and the o / row-sum rescale runs only in the tiles where some query's
+// maximum jumps.  That decision is per query (the other queries are
 // left untouched), so results do not depend on which queries share a wave; wave-wide ballots
 // only skip the code (the cross-lane maximum, the rescale) when no lane needs it.  The row sums
 // come from one more MFMA per k-step against a ones operand, so they sum the same bf16-rounded
@@ -192,18 +194,27 @@ __global__ __launch_bounds__(256, 3) void attn_prefill_kernel(
   }
 
   auto compute = [&](const char* Kt, const char* Vt, int kt, uint64_t mw) {
-    // S^T = K Q^T: 4 blocks of 16 keys for both query groups
+    // S^T = K Q^T: 4 blocks of 16 keys for both query groups.  Every accumulator starts at -m,
+    // its query's reference maximum (0 before the query's first visible key); q carries log2(e),
+    // so the MFMA yields the exponents s - m of the log2-domain softmax directly.
     f32x4_t sc[2][4];
+    f32x4_t minit[2];
+#pragma unroll
+    for (int j = 0; j < 2; ++j) {
+      const float r = m_run[j] == -INFINITY ? 0.f : -m_run[j];
+      minit[j] = f32x4_t{r, r, r, r};
+    }
 #pragma unroll
     for (int nb = 0; nb < 4; ++nb) {
-      sc[0][nb] = f32x4_t{0.f, 0.f, 0.f, 0.f};
-      sc[1][nb] = sc[0][nb];
 #pragma unroll
       for (int kk = 0; kk < 2; ++kk) {
         const bf16x8_t a =
             as_bf16x8(*reinterpret_cast<const uint4*>(Kt + kofs[kk] + 2048 * nb));
-        sc[0][nb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, qf[0][kk], sc[0][nb], 0, 0, 0);
-        sc[1][nb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, qf[1][kk], sc[1][nb], 0, 0, 0);
+#pragma unroll
+        for (int j = 0; j < 2; ++j)
+          sc[j][nb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, qf[j][kk],
+                                                              kk == 0 ? minit[j] : sc[j][nb],
+                                                              0, 0, 0);
       }
     }
 
@@ -237,25 +248,27 @@ __global__ __launch_bounds__(256, 3) void attn_prefill_kernel(
 #pragma unroll
         for (int i = 0; i < 4; ++i) lmax = fmaxf(lmax, sc[j][nb][i]);
       // Move a query's reference when its maximum over the tile passes it by more than the gap
-      // (or on its first visible key: m = -inf, alpha = 0); other queries are left untouched.
-      // That maximum can pass only if one of its four lanes' maxima does (same test, monotone),
-      // so the cross-lane maximum is formed only in the tiles where some lane's does.
-      if (__ballot(lmax * kLog2eF > m_run[j] + kRescaleGap) != 0) {
-        const float tmax = max_over_groups(lmax) * kLog2eF;
-        if (tmax > m_run[j] + kRescaleGap) {
-          const float alpha = __builtin_amdgcn_exp2f(m_run[j] - tmax);
-          m_run[j] = tmax;
+      // (or on its first visible key, while m = -inf and the scores are absolute; alpha = 0);
+      // other queries are left untouched.  That maximum can pass only if one of its four lanes'
+      // maxima does (same test), so the cross-lane maximum is formed only in those tiles.
+      const bool fresh = m_run[j] == -INFINITY;
+      if (__ballot(fresh ? lmax > -INFINITY : lmax > kRescaleGap) != 0) {
+        const float tmax = max_over_groups(lmax);
+        if (fresh ? tmax > -INFINITY : tmax > kRescaleGap) {
+          const float alpha = fresh ? 0.f : __builtin_amdgcn_exp2f(-tmax);
+          m_run[j] = fresh ? tmax : m_run[j] + tmax;
+#pragma unroll
+          for (int nb = 0; nb < 4; ++nb) sc[j][nb] -= tmax;
           lsum[j] *= alpha;
 #pragma unroll
           for (int db = 0; db < 4; ++db) o[j][db] *= alpha;
         }
       }
-      const float mb = (m_run[j] == -INFINITY) ? 0.f : m_run[j];   // no visible key yet: p = 0
+      // p = 2^(s - m): 0 for masked keys (and for a query with no visible key yet)
 #pragma unroll
       for (int nb = 0; nb < 4; ++nb)
 #pragma unroll
-        for (int i = 0; i < 4; ++i)
-          sc[j][nb][i] = __builtin_amdgcn_exp2f(fmaf(sc[j][nb][i], kLog2eF, -mb));
+        for (int i = 0; i < 4; ++i) sc[j][nb][i] = __builtin_amdgcn_exp2f(sc[j][nb][i]);
 #pragma unroll
       for (int kk = 0; kk < 2; ++kk) pb[j][kk] = pt_operand(sc[j][2 * kk], sc[j][2 * kk + 1]);
     }

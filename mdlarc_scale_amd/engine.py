@@ -52,7 +52,7 @@ import numpy as np
 import torch
 
 from . import kernels as K
-from .transformer import TinyTransformer, softmax_scale
+from .transformer import TinyTransformer, attention_q_scale, softmax_scale
 
 START, NEWLINE, IO_SEP, END = 10, 11, 12, 13
 GRID_MAX_X, GRID_MAX_Y = 30, 29     # GridStateUpdater defaults (src/inference.py:107)
@@ -301,16 +301,17 @@ class HipEngine:
         K.embed_rmsnorm(ids.reshape(-1), use_ex, tok, ex if use_ex is not None else None, S,
                         W.ln1[0], W.eps, sc.x, None if fused else sc.xs,
                         None if fused else sc.rstd, tiled=fused)
-        qs = softmax_scale(d // H)
+        qs = softmax_scale(d // H)          # the exact lead pass (K4c)
+        qa = attention_q_scale(d // H)      # q for the attention kernels (log2-domain softmax)
         for li in range(cfg.n_layers):
             kc, vc = kv_layers(li)
             if fused:   # ln1 + qkv_proj + K2 in one launch (fp32 qkv only for the lead rows)
                 K.prefill_gemm_norm_qkv(sc.x, W.ln1[li], W.eps, W.qkv_t[li], B * S, H, sc.rstd,
                                         sc.qkv, K.LEAD_QUERIES if causal else 0, kv_start, pos,
-                                        W.rope_tab, W.rope_geom, qs, sc.q, kc, vc, seq=S)
+                                        W.rope_tab, W.rope_geom, qa, sc.q, kc, vc, seq=S)
             else:
                 gemm_f32(sc.xs, W.qkv[li], sc.qkv)
-                K.qkv_rope_cache(sc.qkv, sc.rstd, pos, W.rope_tab, W.rope_geom, B, S, H, qs,
+                K.qkv_rope_cache(sc.qkv, sc.rstd, pos, W.rope_tab, W.rope_geom, B, S, H, qa,
                                  sc.q, kc, vc, slot0=0)
             K.attn_prefill(sc.q, kc, vc, B, S, H, key_mask, kv_start, causal, sc.attn,
                            out_tiled=fused, row_holes=row_holes)
@@ -343,18 +344,19 @@ class HipEngine:
                 zero_tiled_rows(sc.attn, pk.n_valid, pk.n_tokens, 2 * d)
             else:
                 sc.attn[pk.n_valid:pk.n_tokens].zero_()
-        qs = softmax_scale(d // H)
+        qs = softmax_scale(d // H)          # the exact lead pass (K4c)
+        qa = attention_q_scale(d // H)      # q for the attention kernels (log2-domain softmax)
         for li in range(cfg.n_layers):
             kc, vc = kv_layers(li)
             if fused:
                 K.prefill_gemm_norm_qkv(sc.x, W.ln1[li], W.eps, W.qkv_t[li], pk.n_tokens, H,
                                         sc.rstd, sc.qkv, K.LEAD_QUERIES, kv_start, pos_p,
-                                        W.rope_tab, W.rope_geom, qs, sc.q, kc, vc,
+                                        W.rope_tab, W.rope_geom, qa, sc.q, kc, vc,
                                         token_row=pk.token_row, token_slot=pk.token_slot)
             else:
                 gemm_f32(sc.xs, W.qkv[li], sc.qkv)
                 K.qkv_rope_cache_packed(sc.qkv, sc.rstd, pos_p, W.rope_tab, W.rope_geom,
-                                    pk.token_row, pk.token_slot, H, qs, sc.q, kc, vc)
+                                    pk.token_row, pk.token_slot, H, qa, sc.q, kc, vc)
             K.attn_prefill_packed(sc.q, kc, vc, B, S, H, key_mask, kv_start, pk.q_offset,
                                   pk.n_valid, True, sc.attn, out_tiled=fused,
                                   row_holes=row_holes)

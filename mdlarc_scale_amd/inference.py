@@ -39,7 +39,7 @@ from .data import (
 from .engine import GRID_MAX_X, GRID_MAX_Y, HipEngine, PackedWeights, Scratch, choose_split_len
 from .engine import pack_prompt
 from .engine import engine_for, gemm_f32, prompt_gemms_fused, tiles_supported
-from .transformer import TinyTransformer, softmax_scale
+from .transformer import TinyTransformer, attention_q_scale
 
 SYNC_EVERY = 8
 # Greedy constrained decoding applies the constraints inside the head kernel (and replays the
@@ -349,7 +349,7 @@ class Generator:
         cfg = self.model.config
         sc, B = st.sc, st.B
         H = cfg.n_heads
-        qs = softmax_scale(cfg.d_model // H)
+        qs = attention_q_scale(cfg.d_model // H)   # q for the attention kernels
         slot = st.counters[0:1]
         for li in range(cfg.n_layers):
             kc, vc = st.cache.layer(li)

@@ -310,3 +310,12 @@ def create_large_model(**kwargs) -> TinyTransformer:
 def softmax_scale(head_dim: int) -> float:
     """SDPA's default 1/sqrt(head_dim); 1/8 for head_dim 64, exact in bf16."""
     return 1.0 / math.sqrt(head_dim)
+
+
+LOG2E = 1.4426950408889634
+
+
+def attention_q_scale(head_dim: int) -> float:
+    """The factor the q producers apply for the attention kernels: the softmax scale times
+    log2(e), so the kernels' QK^T products are the exponents of their base-2 softmax."""
+    return softmax_scale(head_dim) * LOG2E

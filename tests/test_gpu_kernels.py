@@ -12,6 +12,7 @@ import numpy as np
 import pytest
 import torch
 
+from mdlarc_scale_amd.transformer import LOG2E
 from oracle import reference_path as rp
 
 pytestmark = pytest.mark.gpu
@@ -403,7 +404,9 @@ def _masks(B, S, kind, g):
 def test_attn_prefill(S, kind, causal):
     g = torch.Generator().manual_seed(S * 7 + len(kind) + causal)
     B, H, slots = 3, 2, S + 9
-    q = bf(torch.randn(B, S, H, 64, generator=g) * 0.125)            # pre-scaled by 1/8
+    # q as the producers write it for the attention kernels: times the softmax scale 1/8 and
+    # log2(e) (base-2 softmax); the reference undoes both
+    q = bf(torch.randn(B, S, H, 64, generator=g) * 0.125)
     kc = bf(torch.randn(B, H, slots, 64, generator=g))
     vc = bf(torch.randn(B, H, slots, 64, generator=g))
     mask = _masks(B, S, kind, g) if kind != "none" else None
@@ -415,7 +418,8 @@ def test_attn_prefill(S, kind, causal):
     K().attn_prefill(q.to(DEV), kc.to(DEV), vc.to(DEV), B, S, H,
                      None if mask is None else mask.to(torch.uint8).to(DEV), kv_start, causal, out)
     torch.cuda.synchronize()
-    ref = rp.attention((q.float() * 8).transpose(1, 2), kc[:, :, :S].float(), vc[:, :, :S].float(),
+    ref = rp.attention((q.float() * 8 / LOG2E).transpose(1, 2), kc[:, :, :S].float(),
+                       vc[:, :, :S].float(),
                        mask, causal)
     # P is rounded to bf16 for the PV MFMA: bf16-level agreement
     close_bf16(unsplit(out).view(B, S, H, 64).transpose(1, 2), ref, atol=8e-3, rtol=2e-2)
@@ -439,7 +443,8 @@ def test_attn_prefill_many_heads(causal):
     K().attn_prefill(q.to(DEV), kc.to(DEV), vc.to(DEV), B, S, H, mask.to(torch.uint8).to(DEV),
                      first.to(torch.int32).to(DEV), causal, out)
     torch.cuda.synchronize()
-    ref = rp.attention((q.float() * 8).transpose(1, 2), kc[:, :, :S].float(), vc[:, :, :S].float(),
+    ref = rp.attention((q.float() * 8 / LOG2E).transpose(1, 2), kc[:, :, :S].float(),
+                       vc[:, :, :S].float(),
                        mask, causal)
     close_bf16(unsplit(out).view(B, S, H, 64).transpose(1, 2), ref, atol=8e-3, rtol=2e-2)
 
@@ -458,7 +463,8 @@ def test_attn_prefill_kv_start_clamped():
     mask = torch.ones(B, S, dtype=torch.bool)
     mask[1] = False
     mask[2, :5] = False
-    ref = rp.attention((q.float() * 8).transpose(1, 2), kc[:, :, :S].float(), vc[:, :, :S].float(),
+    ref = rp.attention((q.float() * 8 / LOG2E).transpose(1, 2), kc[:, :, :S].float(),
+                       vc[:, :, :S].float(),
                        mask, True)
     close_bf16(unsplit(out).view(B, S, H, 64).transpose(1, 2), ref, atol=8e-3, rtol=2e-2)
 
@@ -721,7 +727,7 @@ def test_attn_decode(split_len, slots, t, with_mask):
         keymask = torch.ones(B, t + 1, dtype=torch.bool)
         if pm is not None:
             keymask[:, :S] = pm
-        ref = rp.attention((q.double() * 8)[:, :, None], kc[:, :, :t + 1].double(),
+        ref = rp.attention((q.double() * 8 / LOG2E)[:, :, None], kc[:, :, :t + 1].double(),
                            vc[:, :, :t + 1].double(), keymask, causal=False)[:, :, 0]
         # fp32 softmax and accumulation; the probabilities enter the PV product (and the row sum)
         # rounded to bf16, as in the prefill kernel: bf16-level agreement
