@@ -62,23 +62,40 @@ __global__ __launch_bounds__(256) void swiglu_kernel(const float* __restrict__ g
 }
 
 // Config-1 format of K3: gate|up [rows, 2 d_ff] bf16 in, h [rows, d_ff] bf16 out (one rounding).
-// Block (y, x) covers channels 2048 y .. 2048 y + 2047 of row x, a thread 8 of them: one 16-byte
-// load from each half and one 16-byte store, no index division.
+// Block (y, x) covers channels 2048 y .. 2048 y + 2047 of rows kBf16Rows x .. kBf16Rows x + 3, a
+// thread 8 channels of each: the rows' 16-byte loads from both halves are all issued before the
+// first store (8 loads in flight per thread), no index division.  Prompt-sized batches take the
+// non-temporal hint on loads and stores.  Measured at config 1 (65,536 rows, d_ff 2,048):
+// one row per block 151 us; four rows, plain loads 131 us; four rows, both hints 126 us (6.38
+// TB/s), against 123 us for a copy kernel that moves the same bytes with both hints.
+constexpr int kBf16Rows = 4;
+
 template <bool NT>
 __global__ __launch_bounds__(256) void swiglu_bf16_kernel(const uint16_t* __restrict__ gu,
                                                           int64_t ld,
                                                           const float* __restrict__ rstd,
                                                           const float* __restrict__ bg,
-                                                          const float* __restrict__ bu,
+                                                          const float* __restrict__ bu, int rows,
                                                           int d_ff, uint16_t* __restrict__ h) {
-  const int64_t m = blockIdx.x;
+  const int64_t m0 = static_cast<int64_t>(blockIdx.x) * kBf16Rows;
   const int c = 8 * (static_cast<int>(blockIdx.y) * 256 + static_cast<int>(threadIdx.x));
   if (c >= d_ff) return;
-  const uint16_t* row = gu + m * ld;
-  float g[8], u[8], b1[8], b2[8];
-  // plain loads: as in K3, only the store takes the non-temporal hint
-  unpack8(*reinterpret_cast<const uint4*>(row + c), g);
-  unpack8(*reinterpret_cast<const uint4*>(row + d_ff + c), u);
+  uint4 G[kBf16Rows], U[kBf16Rows];
+  float rs[kBf16Rows];
+#pragma unroll
+  for (int r = 0; r < kBf16Rows; ++r) {
+    const int64_t m = min(m0 + r, static_cast<int64_t>(rows) - 1);   // tail rows: loads only
+    const uint16_t* row = gu + m * ld;
+    if constexpr (NT) {
+      G[r] = load_nt16(row + c);
+      U[r] = load_nt16(row + d_ff + c);
+    } else {
+      G[r] = *reinterpret_cast<const uint4*>(row + c);
+      U[r] = *reinterpret_cast<const uint4*>(row + d_ff + c);
+    }
+    rs[r] = rstd ? rstd[m] : 1.f;
+  }
+  float b1[8], b2[8];
   if (bg) {
     load8f(bg + c, b1);
   } else {
@@ -91,11 +108,16 @@ __global__ __launch_bounds__(256) void swiglu_bf16_kernel(const uint16_t* __rest
 #pragma unroll
     for (int i = 0; i < 8; ++i) b2[i] = 0.f;
   }
-  const float r = rstd ? rstd[m] : 1.f;
-  float o[8];
 #pragma unroll
-  for (int i = 0; i < 8; ++i) o[i] = silu_mul(fmaf(r, g[i], b1[i]), fmaf(r, u[i], b2[i]));
-  st_u4<NT>(h + m * d_ff + c, pack8(o));
+  for (int r = 0; r < kBf16Rows; ++r) {
+    if (m0 + r >= rows) break;
+    float g[8], u[8], o[8];
+    unpack8(G[r], g);
+    unpack8(U[r], u);
+#pragma unroll
+    for (int i = 0; i < 8; ++i) o[i] = silu_mul(fmaf(rs[r], g[i], b1[i]), fmaf(rs[r], u[i], b2[i]));
+    st_u4<NT>(h + (m0 + r) * d_ff + c, pack8(o));
+  }
 }
 
 }  // namespace mdl
@@ -114,14 +136,15 @@ extern "C" int mdl_swiglu_bf16(const uint16_t* gate_up, int64_t ld, const float*
       (bias_gate && !aligned16(bias_gate)) || (bias_up && !aligned16(bias_up)))
     return MDL_ERR_ALIGN;
   if (rows == 0) return MDL_OK;
-  const dim3 grid(static_cast<unsigned>(rows), static_cast<unsigned>((d_ff + 2047) / 2048));
+  const dim3 grid(static_cast<unsigned>((rows + kBf16Rows - 1) / kBf16Rows),
+                  static_cast<unsigned>((d_ff + 2047) / 2048));
   const hipStream_t st = static_cast<hipStream_t>(stream);
   if (static_cast<int64_t>(rows) * d_ff * 6 >= kStreamBytes)
-    swiglu_bf16_kernel<true><<<grid, 256, 0, st>>>(gate_up, ld, rstd, bias_gate, bias_up, d_ff,
-                                                   h_out);
+    swiglu_bf16_kernel<true><<<grid, 256, 0, st>>>(gate_up, ld, rstd, bias_gate, bias_up, rows,
+                                                   d_ff, h_out);
   else
-    swiglu_bf16_kernel<false><<<grid, 256, 0, st>>>(gate_up, ld, rstd, bias_gate, bias_up, d_ff,
-                                                    h_out);
+    swiglu_bf16_kernel<false><<<grid, 256, 0, st>>>(gate_up, ld, rstd, bias_gate, bias_up, rows,
+                                                    d_ff, h_out);
   return launch_status();
 }
 
