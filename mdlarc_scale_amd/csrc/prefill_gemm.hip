@@ -217,26 +217,29 @@ __global__ __launch_bounds__(kThreads, 1) void prefill_gemm_kernel(const Args p)
     // The hi products before the lo products, so that consecutive MFMAs write different
     // accumulators (each accumulator still adds hi before lo).  The split forms (8 weight
     // fragments) hold all their weight fragments and run two passes; the norm forms (16, whose
-    // registers that would exhaust) take two fragments at a time: hi for both fragments and
-    // both row blocks, then lo, so an accumulator's lo product issues four MFMAs after its hi
-    // product (one fragment at a time, two after: 3% slower on the qkv launch at config 2).
+    // registers that would exhaust) take four fragments at a time: hi for the four fragments
+    // and both row blocks, then lo, so an accumulator's lo product issues eight MFMAs after its
+    // hi product (measured at config 2 against one fragment at a time: qkv 7%, gate/up 6%
+    // faster; two at a time sits between; eight is within 1% of four and takes the E_QKV form
+    // to the 256-register limit).
     if constexpr (AMODE == A_NORM) {
-      static_assert(FN % 2 == 0, "the norm forms pair their weight fragments");
+      constexpr int kGroup = 4;
+      static_assert(FN % kGroup == 0, "the norm forms group their weight fragments");
 #pragma unroll
-      for (int i = 0; i < FN; i += 2) {
-        bf16x8_t wf[2];
+      for (int i = 0; i < FN; i += kGroup) {
+        bf16x8_t wf[kGroup];
 #pragma unroll
-        for (int u = 0; u < 2; ++u)
+        for (int u = 0; u < kGroup; ++u)
           wf[u] = *reinterpret_cast<const bf16x8_t*>(base + (kAFrags + FN * wn + i + u) * 1024 +
                                                      16 * lane);
 #pragma unroll
-        for (int u = 0; u < 2; ++u)
+        for (int u = 0; u < kGroup; ++u)
 #pragma unroll
           for (int j = 0; j < FM; ++j)
             acc[i + u][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(wf[u], ah[j], acc[i + u][j],
                                                                     0, 0, 0);
 #pragma unroll
-        for (int u = 0; u < 2; ++u)
+        for (int u = 0; u < kGroup; ++u)
 #pragma unroll
           for (int j = 0; j < FM; ++j)
             acc[i + u][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(wf[u], al[j], acc[i + u][j],

@@ -220,17 +220,22 @@ __global__ __launch_bounds__(64 * kGemmWaves) void split_gemm_kernel(const GemmA
             split8(t, ah[u][j], al[u][j]);
           }
         }
+        // every hi product before the lo products: consecutive MFMAs write different
+        // accumulators, and each accumulator still adds hi before lo
 #pragma unroll
         for (int i = 0; i < FN; ++i)
 #pragma unroll
-          for (int j = 0; j < FM; ++j) {
+          for (int j = 0; j < FM; ++j)
             acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf16x8(wf[u][i]),
                                                                 as_bf16x8(ah[u][j]), acc[i][j],
                                                                 0, 0, 0);
+#pragma unroll
+        for (int i = 0; i < FN; ++i)
+#pragma unroll
+          for (int j = 0; j < FM; ++j)
             acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf16x8(wf[u][i]),
                                                                 as_bf16x8(al[u][j]), acc[i][j],
                                                                 0, 0, 0);
-          }
       }
     }
   }
