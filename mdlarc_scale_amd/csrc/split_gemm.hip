@@ -169,6 +169,26 @@ __global__ __launch_bounds__(64 * kGemmWaves) void split_gemm_kernel(const GemmA
     }
   }
 
+  // E_RESIDUAL: the epilogue's x elements (and bias) are loaded here, before the k-loop: this
+  // block is their only writer, so the values are those the epilogue would read, and the load
+  // latency is spent under the GEMM instead of after the reduction
+  float4 xpre[EPI == E_RESIDUAL ? G : 1], bpre[EPI == E_RESIDUAL ? G : 1];
+  if constexpr (EPI == E_RESIDUAL) {
+#pragma unroll
+    for (int gi = 0; gi < G; ++gi) {
+      const int q = threadIdx.x + gi * 64 * NW;
+      const int t = q >> 6, ln = q & 63;
+      const int i = t / FM, j = t - i * FM;
+      const int m = m0 + 16 * j + (ln & 15);
+      const int n = n0 + 16 * i + 4 * (ln >> 4);
+      xpre[gi] = bpre[gi] = make_float4(0.f, 0.f, 0.f, 0.f);
+      if (q < FN * FM * 64 && m < M && n < N) {
+        xpre[gi] = *reinterpret_cast<const float4*>(p.x_res + tile_off32(m, n, N));
+        if (p.bias_a) bpre[gi] = *reinterpret_cast<const float4*>(p.bias_a + n);
+      }
+    }
+  }
+
   // k-steps of 32: wave w takes [nk w / NW, nk (w + 1) / NW), contiguous
   const int nk = K >> 5;
   const int s0 = (nk * wave) / NW, s1 = (nk * (wave + 1)) / NW;
@@ -372,14 +392,13 @@ __global__ __launch_bounds__(64 * kGemmWaves) void split_gemm_kernel(const GemmA
           }
         } else if constexpr (EPI == E_RESIDUAL) {
           // x + delta, then + bias: the order of the add+RMSNorm kernel it replaces
-          float4* xr = reinterpret_cast<float4*>(p.x_res + tile_off32(m, n, N));
-          float4 xv = *xr;
+          float4 xv = xpre[gi];
           xv.x += v[0]; xv.y += v[1]; xv.z += v[2]; xv.w += v[3];
           if (p.bias_a) {
-            const float4 b = *reinterpret_cast<const float4*>(p.bias_a + n);
+            const float4 b = bpre[gi];
             xv.x += b.x; xv.y += b.y; xv.z += b.z; xv.w += b.w;
           }
-          *xr = xv;
+          *reinterpret_cast<float4*>(p.x_res + tile_off32(m, n, N)) = xv;
         } else {
           *reinterpret_cast<float4*>(p.out + static_cast<int64_t>(m) * p.ldo + n) =
               make_float4(v[0], v[1], v[2], v[3]);
