@@ -36,12 +36,12 @@
 // MFMA yields the exponent s - m itself.  A query's reference maximum m moves only when a score
 // exceeds it by more than a factor 2^8 (its first visible key always sets it), so
 // p = 2^(s - m) <= 256 and the o / row-sum rescale runs only in the tiles where some query's
-// maximum jumps.  That decision is per query (the other queries are
-// left untouched), so results do not depend on which queries share a wave; wave-wide ballots
-// only skip the code (the cross-lane maximum, the rescale) when no lane needs it.  The row sums
-// come from one more MFMA per k-step against a ones operand, so they sum the same bf16-rounded
-// probabilities the PV product uses.  Queries with no visible key produce 0.  The output (the out-projection
-// GEMM input) is written as a hi|lo bf16 pair per row, see common.h.
+// maximum jumps.  That decision is per query (the other queries are left untouched), so results
+// do not depend on which queries share a wave; wave-wide ballots only skip the code (the
+// cross-lane maximum, the rescale) when no lane needs it.  The row sums come from one more MFMA
+// per k-step against a ones operand, so they sum the same bf16-rounded probabilities the PV
+// product uses.  Queries with no visible key produce 0.  The output (the out-projection GEMM
+// input) is written as a hi|lo bf16 pair per row, see common.h.
 //
 // Block order: block i runs on XCD i % 8; each (b, h) is pinned to one XCD, whose L2 then serves
 // all of that head's query tiles, and heads are dealt round-robin over the XCDs so that rows of
