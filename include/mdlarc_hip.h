@@ -127,7 +127,8 @@ int mdl_decode_embed(const int64_t* token, const int64_t* example_ids, const voi
  * Replaces: the residual adds of TransformerBlock.forward (src/transformer.py:494-496),
  *           _prefill / _decode_step (src/inference.py:412-413, :455-456), the fc_down bias
  *           (src/transformer.py:443), and the reduction of the following ln2 / ln1 / ln_f.
- *   x[m]    += delta[m] (+ bias)           delta fp32 [rows, d] (may be NULL), bias fp32 [d] or NULL
+ *   x[m]    += delta[m] (+ bias)           delta fp32 [rows, d] (may be NULL),
+ *                                           bias fp32 [d] or NULL
  *   rstd[m]  = 1 / sqrt(mean(x[m]^2) + eps)
  *   xs[m]    = split(x[m] * gamma)         bf16 [rows, 2d] (skipped when xs_out is NULL), in
  *                                          xs_layout: MDL_LAYOUT_ROWS, or the bf16 tile layout

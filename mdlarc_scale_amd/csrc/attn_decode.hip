@@ -15,9 +15,9 @@
 //     order the transposing reads produce; the row sum is one more MFMA against ones, so it sums
 //     the same bf16-rounded probabilities the PV product uses.
 // q comes multiplied by the softmax scale and log2(e), so the scores are the exponents of a base-2
-// softmax (v_exp_f32).  The single query costs 15/16 of every MFMA, which is free: the kernel streams 256 bytes of K/V
-// per slot from HBM and does 2 x 128 useful flops per slot, so MFMA and VALU stay far below their
-// rates.  K and V use non-temporal loads (read once per launch; keeps the projection weights
+// softmax (v_exp_f32).  The single query costs 15/16 of every MFMA, which is free: the kernel
+// streams 256 bytes of K/V per slot from HBM and does 2 x 128 useful flops per slot, so MFMA and
+// VALU stay far below their rates.  K and V use non-temporal loads (read once per launch; keeps the projection weights
 // cached between layers).  The 4 waves, then the splits (second kernel) merge with the usual
 // max-rescaled sums.
 //

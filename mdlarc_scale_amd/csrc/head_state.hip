@@ -302,7 +302,8 @@ extern "C" const char* mdl_error_string(int code) {
     case MDL_ERR_CACHE: return "slot range outside the KV cache";
     case MDL_ERR_WORKSPACE: return "workspace too small";
     case MDL_ERR_DTYPE: return "unsupported dtype code";
-    case MDL_ERR_SCRATCH: return "work exceeds the static scratch buffer (MDL_DECODE_SCRATCH_BYTES)";
+    case MDL_ERR_SCRATCH:
+      return "work exceeds the static scratch buffer (MDL_DECODE_SCRATCH_BYTES)";
     default: return code > 0 ? hipGetErrorString(static_cast<hipError_t>(code)) : "unknown";
   }
 }
