@@ -17,9 +17,9 @@
 // q comes multiplied by the softmax scale and log2(e), so the scores are the exponents of a base-2
 // softmax (v_exp_f32).  The single query costs 15/16 of every MFMA, which is free: the kernel
 // streams 256 bytes of K/V per slot from HBM and does 2 x 128 useful flops per slot, so MFMA and
-// VALU stay far below their rates.  K and V use non-temporal loads (read once per launch; keeps the projection weights
-// cached between layers).  The 4 waves, then the splits (second kernel) merge with the usual
-// max-rescaled sums.
+// VALU stay far below their rates.  K and V use non-temporal loads (read once per launch; keeps
+// the projection weights cached between layers).  The 4 waves, then the splits (second kernel)
+// merge with the usual max-rescaled sums.
 //
 // Slot j of row b is visible iff kv_start[b] <= j <= t and (j >= prompt_len or
 // prompt_mask[b, j]), the decode mask of the reference (prompt mask, then every generated slot).

@@ -24,8 +24,8 @@
 // Block: a 256 x 256 output tile (activation rows x weight rows) on 8 waves, each owning 32 MFMA
 // tiles (128 fp32 accumulators per lane): 64 rows x 128 weight rows in a 4 x 2 wave grid for the
 // split forms, 32 rows x 256 weight rows (8 x 1) for A_NORM.  K advances 32 at a time through a
-// ring of three LDS stages of 48 KB.  A stage holds 16 weight fragments and 32 activation fragments of 1 KB in MFMA lane
-// order (bf16 {hi, lo} of 16 row blocks; for A_NORM the fp32 x of 16 row blocks in the fp32 tile
+// ring of three LDS stages of 48 KB.  A stage holds 16 weight fragments and 32 activation
+// fragments of 1 KB in MFMA lane order (bf16 {hi, lo} of 16 row blocks; for A_NORM the fp32 x of 16 row blocks in the fp32 tile
 // layout, split after the read), so every fragment read is one conflict-free 16-byte LDS read
 // per lane.  Global data goes straight to LDS (global_load_lds_dwordx4, 16 bytes per lane, one
 // kilobyte per wave instruction), issued two k-steps ahead; nothing is staged in registers, and
