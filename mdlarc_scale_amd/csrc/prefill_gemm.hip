@@ -25,9 +25,9 @@
 // tiles (128 fp32 accumulators per lane): 64 rows x 128 weight rows in a 4 x 2 wave grid for the
 // split forms, 32 rows x 256 weight rows (8 x 1) for A_NORM.  K advances 32 at a time through a
 // ring of three LDS stages of 48 KB.  A stage holds 16 weight fragments and 32 activation
-// fragments of 1 KB in MFMA lane order (bf16 {hi, lo} of 16 row blocks; for A_NORM the fp32 x of 16 row blocks in the fp32 tile
-// layout, split after the read), so every fragment read is one conflict-free 16-byte LDS read
-// per lane.  Global data goes straight to LDS (global_load_lds_dwordx4, 16 bytes per lane, one
+// fragments of 1 KB in MFMA lane order (bf16 {hi, lo} of 16 row blocks; for A_NORM the fp32 x of
+// 16 row blocks in the fp32 tile layout, split after the read), so every fragment read is one
+// conflict-free 16-byte LDS read per lane.  Global data goes straight to LDS (global_load_lds_dwordx4, 16 bytes per lane, one
 // kilobyte per wave instruction), issued two k-steps ahead; nothing is staged in registers, and
 // a step ends with one barrier after an exact vmcnt wait for the next stage's loads.  Blocks are
 // persistent (one per CU, each walking its tiles), and the load ring runs on across tile
