@@ -27,12 +27,12 @@
 // ring of three LDS stages of 48 KB.  A stage holds 16 weight fragments and 32 activation
 // fragments of 1 KB in MFMA lane order (bf16 {hi, lo} of 16 row blocks; for A_NORM the fp32 x of
 // 16 row blocks in the fp32 tile layout, split after the read), so every fragment read is one
-// conflict-free 16-byte LDS read per lane.  Global data goes straight to LDS (global_load_lds_dwordx4, 16 bytes per lane, one
-// kilobyte per wave instruction), issued two k-steps ahead; nothing is staged in registers, and
-// a step ends with one barrier after an exact vmcnt wait for the next stage's loads.  Blocks are
-// persistent (one per CU, each walking its tiles), and the load ring runs on across tile
-// boundaries, so a tile's epilogue overlaps the next tile's first loads.
-// Every weight fragment feeds two MFMAs (hi and lo rows), as in K5.
+// conflict-free 16-byte LDS read per lane.  Global data goes straight to LDS
+// (global_load_lds_dwordx4, 16 bytes per lane, one kilobyte per wave instruction), issued two
+// k-steps ahead; nothing is staged in registers, and a step ends with one barrier after an exact
+// vmcnt wait for the next stage's loads.  Blocks are persistent (one per CU, each walking its
+// tiles), and the load ring runs on across tile boundaries, so a tile's epilogue overlaps the
+// next tile's first loads. Every weight fragment feeds two MFMAs (hi and lo rows), as in K5.
 // Blocks are numbered so that an XCD (block i runs on XCD i mod 8) takes a contiguous run of
 // tiles, row tile major: the N tiles of one row tile share its activation rows in one L2.
 // Summation order is fixed (k-steps in order, hi before lo), so results are reproducible.
