@@ -367,6 +367,8 @@ __global__ __launch_bounds__(64 * kGemmWaves) void split_gemm_kernel(const GemmA
           const float a0 = v[0] * r, a1 = v[1] * r, a2 = v[2] * r, a3 = v[3] * r;
           const int t = p.slot_dev ? *p.slot_dev : p.slot0;
           const bool in_cache = t >= 0 && t < p.slots;
+          // K / V go out with the non-temporal hint: 8 bytes per (row, head, slot t) of cache
+          // rows megabytes apart, read next by the attention's non-temporal loads
           const int64_t crow =
               ((static_cast<int64_t>(m) * (d / kHeadDim) + head) * p.slots + t) * kHeadDim + dim;
           uint2 o;
@@ -374,7 +376,7 @@ __global__ __launch_bounds__(64 * kGemmWaves) void split_gemm_kernel(const GemmA
             if (in_cache) {
               o.x = pack_bf2(a0, a1);
               o.y = pack_bf2(a2, a3);
-              *reinterpret_cast<uint2*>(p.vc + crow) = o;
+              st_u2<true>(p.vc + crow, o);
             }
           } else {
             float y0, y1, y2, y3;
@@ -387,7 +389,7 @@ __global__ __launch_bounds__(64 * kGemmWaves) void split_gemm_kernel(const GemmA
             } else if (in_cache) {
               o.x = pack_bf2(y0, y1);
               o.y = pack_bf2(y2, y3);
-              *reinterpret_cast<uint2*>(p.kc + crow) = o;
+              st_u2<true>(p.kc + crow, o);
             }
           }
         } else if constexpr (EPI == E_RESIDUAL) {
