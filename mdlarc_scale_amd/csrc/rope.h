@@ -39,11 +39,9 @@ __device__ __forceinline__ void rope_cos_sin3(int j, int64_t p0, int64_t p1, int
 __device__ __forceinline__ void rope_cos_sin(int j, const int64_t* __restrict__ pos3,
                                              const float* __restrict__ tab, const RopeArgs& ra,
                                              float& cs, float& sn) {
-  int64_t p0 = 0, p1 = 0, p2 = 0;
-  if (j < ra.px) p0 = pos3[0];
-  else if (j < ra.px + ra.py) p1 = pos3[1];
-  else p2 = pos3[2];
-  rope_cos_sin3(j, p0, p1, p2, tab, ra, cs, sn);
+  // all three positions, unconditionally (one 24-byte line): a load per axis behind a lane-
+  // dependent branch serialises the table reads that follow it
+  rope_cos_sin3(j, pos3[0], pos3[1], pos3[2], tab, ra, cs, sn);
 }
 
 // A pair (a, b) rotated by (cs, sn): (a cs - b sn, b cs + a sn), each a fused multiply-add onto
