@@ -464,7 +464,7 @@ def measure_workload(spec, steps, warmup, dev, eager=False, snapshot=False):
     from mdlarc_scale_amd import inference as I
     from mdlarc_scale_amd.data import END_TOKEN_ID
     from mdlarc_scale_amd.engine import engine_for, pack_prompt
-    from mdlarc_scale_amd.transformer import MODEL_SIZES, create_model
+    from mdlarc_scale_amd.transformer import MODEL_SIZES, attention_q_scale, create_model
     from mdlarc_scale_amd.workload import build_prompts, left_pad
 
     t_build = time.perf_counter()
@@ -550,13 +550,15 @@ def measure_workload(spec, steps, warmup, dev, eager=False, snapshot=False):
         decode_nb = 4 if min(st.split_len, total) > 2048 else 2
 
         # prefill attention alone: one layer's launch as the prefill makes it (packed query
-        # rows) over the batch's own masks and cache, with synthetic q (the kernel's time does
-        # not depend on values)
+        # rows) over the batch's own masks and cache, with synthetic q of unit-variance rows
+        # pre-scaled as the projection scales q (the softmax scale times log2(e)); the kernel's
+        # time depends on values only through how often a query's running maximum moves
         n_valid = mask.sum(1)
         pa_flops = 4 * 64 * H * int((n_valid * (n_valid + 1) // 2).sum())
         starts = torch.stack([st.kv_start, st.last_row]).cpu().numpy()
         pk = pack_prompt(starts[0], starts[1], B, S, dev)
-        qp = (torch.randn(pk.n_valid, H * 64, device=dev) * 0.125).to(torch.bfloat16)
+        qp = (torch.randn(pk.n_valid, H * 64, device=dev)
+              * attention_q_scale(64)).to(torch.bfloat16)
         op = torch.empty(pk.n_valid, 2 * H * 64, device=dev, dtype=torch.bfloat16)
         kc0, vc0 = st.cache.layer(0)
 
