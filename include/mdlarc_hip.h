@@ -31,6 +31,13 @@
  *     kilobytes per wave load).
  *   - KV cache layout is the reference StaticKVCache layout (src/inference.py:73-77):
  *     one layer's K (or V) is [batch, n_heads, cache_slots, 64] bf16, slot-major rows of 128 B.
+ *     The fp32 form keeps the same layout in fp32 (rows of 256 B).
+ *   - Two forms of the path.  A bf16 model (the reference's configurations 2-4) runs the bf16
+ *     form: bf16 weights, bf16 q / K / V and cache.  A model with fp32 parameters runs the fp32
+ *     form, as the reference keeps its cache and attention in the parameter dtype
+ *     (src/inference.py:522, :544): each weight W passes as two bf16 matrices w = bf16(W) and
+ *     w_lo = bf16(W - w) (the *_lo arguments of the K5 entries), q / K / V and the cache are
+ *     fp32 (mdl_qkv_rope_cache with MDL_DTYPE_F32) and the attention is K4f (fp32 MFMA).
  */
 #ifndef MDLARC_HIP_H
 #define MDLARC_HIP_H
@@ -149,16 +156,18 @@ int mdl_add_rmsnorm(float* x, const float* delta, const float* bias, int rows, i
  * pos: int64 [batch*seq, 3] (x, y, z); clamped to [0,max-1] per axis.
  * rope_tab: fp32 [cos_x(max_x*px) | sin_x | cos_y(max_y*py) | sin_y | cos_z(max_z*pz) | sin_z],
  *      the tables of RotaryEmbedding3D._build_cache (src/transformer.py:95-126).
- * Outputs: q_out bf16 [batch*seq, d] = rope(q * rstd) * q_scale; k/v written to cache slot
+ * Outputs: q_out [batch*seq, d] = rope(q * rstd) * q_scale; k/v written to cache slot
  *      (slot_dev ? *slot_dev : slot0) + s for token s of each batch row.  For the attention
- *      kernels (K4a, K4b) q_scale is the softmax scale times log2(e): their softmax is base 2.
+ *      kernels (K4a, K4b, K4f) q_scale is the softmax scale times log2(e): their softmax is
+ *      base 2.  out_dtype (MDL_DTYPE_BF16 or MDL_DTYPE_F32) is the type of q_out and of the
+ *      cache: bf16 for the bf16 form, fp32 for the fp32 form (then nothing is rounded).
  */
 int mdl_qkv_rope_cache(const float* qkv, int64_t qkv_ld, const float* rstd,
                        const int64_t* pos, const float* rope_tab, int batch, int seq,
                        int n_heads, int head_dim, int max_x, int max_y, int max_z, int px,
-                       int py, int pz, float q_scale, uint16_t* q_out, uint16_t* k_cache,
-                       uint16_t* v_cache, int cache_slots, int slot0, const int32_t* slot_dev,
-                       void* stream);
+                       int py, int pz, float q_scale, void* q_out, void* k_cache,
+                       void* v_cache, int out_dtype, int cache_slots, int slot0,
+                       const int32_t* slot_dev, void* stream);
 
 /*
  * K2 over a packed token list (the prompt tokens of every row without their left padding).
@@ -167,14 +176,15 @@ int mdl_qkv_rope_cache(const float* qkv, int64_t qkv_ld, const float* rstd,
  *           the padding's K/V are never visible to a later query).
  * qkv / rstd / pos / q_out hold n_tokens rows.  Token m belongs to batch row token_row[m] and
  * writes its k / v into cache slot token_slot[m] of that row (nothing when token_slot[m] < 0,
- * or outside [0, cache_slots) or a token_row outside [0, batch)).
+ * or outside [0, cache_slots) or a token_row outside [0, batch)).  out_dtype as for
+ * mdl_qkv_rope_cache.
  */
 int mdl_qkv_rope_cache_packed(const float* qkv, int64_t qkv_ld, const float* rstd,
                               const int64_t* pos, const float* rope_tab, int64_t n_tokens,
                               const int32_t* token_row, const int32_t* token_slot, int batch,
                               int n_heads, int head_dim, int max_x, int max_y, int max_z, int px,
-                              int py, int pz, float q_scale, uint16_t* q_out, uint16_t* k_cache,
-                              uint16_t* v_cache, int cache_slots, void* stream);
+                              int py, int pz, float q_scale, void* q_out, void* k_cache,
+                              void* v_cache, int out_dtype, int cache_slots, void* stream);
 
 /*
  * K3 -- SwiGLU gate: silu(gate) * up, with the RMSNorm multiply of ln2 and the fc biases.
@@ -201,7 +211,7 @@ int mdl_swiglu(const float* gate_up, int64_t ld, const float* rstd, const float*
  * (src/transformer.py:584-589, RMSNorm :37-48) for a bf16 model.
  * tok_table / ex_table bf16 [vocab, d] / [n_examples, d]; example_ids as mdl_embed_rmsnorm
  * (may be NULL).  x_out = bf16(tok + ex) and xn_out = bf16(x * rstd * gamma), rstd from the
- * rounded x; both bf16 [rows, d] row-major.  d a multiple of 4, at most 2048.
+ * rounded x; both bf16 [rows, d] row-major.  d a multiple of 8, at most 2048.
  */
 int mdl_embed_rmsnorm_bf16(const int64_t* ids, const int64_t* example_ids,
                            const uint16_t* tok_table, const uint16_t* ex_table, int vocab,
@@ -274,11 +284,15 @@ int mdl_gemm_split_swiglu(const uint16_t* a, const uint16_t* w_gu, const float* 
  * split(x * gamma) and rstd are what mdl_add_rmsnorm would write (rstd to fp32 rounding: the
  * sum of squares is taken in another order), so this replaces that launch and the split
  * activation buffer.  k a positive multiple of 32, n of 16.
+ * w_lo (may be NULL): the low bf16 part of an fp32 weight (w_lo = bf16(W - w), tiled like w);
+ * each k-step then also adds split_hi . w_lo, so the product sees W to ~2^-17 (the fp32 form).
+ * Any m: the fp32 form also runs a prompt's projections here.
  * Replaces: qkv_proj(ln1(x)) (src/inference.py:438-439; RMSNorm.forward
  *           src/transformer.py:45-48).
  */
-int mdl_gemm_norm(const float* x, const float* gamma, float eps, const uint16_t* w, float* out,
-                  int64_t ldo, float* rstd_out, int m, int n, int k, int tile, void* stream);
+int mdl_gemm_norm(const float* x, const float* gamma, float eps, const uint16_t* w,
+                  const uint16_t* w_lo, float* out, int64_t ldo, float* rstd_out, int m, int n,
+                  int k, int tile, void* stream);
 /*
  * mdl_gemm_norm with K2 in its epilogue, for the decode step: from qkv = split(x * gamma) . w^T
  * (w: qkv_proj tiled [3 d, d], d = n_heads * 64) and rstd it writes exactly what
@@ -297,21 +311,22 @@ int mdl_gemm_norm_qkv(const float* x, const float* gamma, float eps, const uint1
 /*
  * mdl_gemm_norm feeding the SwiGLU epilogue of mdl_gemm_split_swiglu (rstd from the prologue):
  * h = split(silu(rstd g + bias_gate) * (rstd u + bias_up)) with g / u the gate / up rows of
- * w_gu against split(x * gamma).  Replaces ffn(ln2(x))'s gate (src/transformer.py:441-449,
- * :494-496).
+ * w_gu against split(x * gamma).  w_gu_lo (may be NULL): the low part of an fp32 w_gu, as
+ * w_lo of mdl_gemm_norm.  Replaces ffn(ln2(x))'s gate (src/transformer.py:441-449, :494-496).
  */
 int mdl_gemm_norm_swiglu(const float* x, const float* gamma, float eps, const uint16_t* w_gu,
-                         const float* bias_gate, const float* bias_up, uint16_t* h_out, int m,
-                         int d_ff, int k, int tile, void* stream);
+                         const uint16_t* w_gu_lo, const float* bias_gate, const float* bias_up,
+                         uint16_t* h_out, int m, int d_ff, int k, int tile, void* stream);
 /*
  * K5 with the residual add in its epilogue (decode step): x[i, j] += sum_k (a_hi + a_lo)[i, k]
  * w[j, k] (+ bias[j]), in place on the fp32 residual stream x [m, n] in MDL_LAYOUT_TILES; a the
  * tiled split activation [m, 2k], w tiled [n, k], bias [n] or NULL.  n a multiple of 32.
+ * w_lo (may be NULL): the low part of an fp32 w, as for mdl_gemm_norm.
  * Replaces: the residual adds x + out_proj(...) and x + fc_down(...) (+ its bias) of
  *           _decode_step (src/inference.py:453-456; src/transformer.py:443, :494-496).
  */
-int mdl_gemm_split_residual(const uint16_t* a, const uint16_t* w, float* x, const float* bias,
-                            int m, int n, int k, int tile, void* stream);
+int mdl_gemm_split_residual(const uint16_t* a, const uint16_t* w, const uint16_t* w_lo, float* x,
+                            const float* bias, int m, int n, int k, int tile, void* stream);
 /* Number of compiled block shapes, and the automatic choice for (m, n, k) of the split forms
  * (host only; the norm forms weight the activation rows twice, see csrc/split_gemm.hip). */
 int mdl_gemm_split_tiles(void);
@@ -511,6 +526,42 @@ int mdl_attn_decode_rope_noalloc(const float* qkv, int64_t qkv_ld, const float* 
                                  const int32_t* kv_start, const int32_t* row_order, int seq_pos,
                                  const int32_t* seq_dev, int split_len, uint16_t* out,
                                  int out_layout, void* stream);
+
+/*
+ * K4f -- attention of the fp32 form over an fp32 cache, on fp32 MFMA: the operands enter the
+ * products unrounded and the softmax stays fp32; only the output is stored, as the split
+ * (hi|lo bf16) input of the out projection.
+ * Replaces: F.scaled_dot_product_attention of _prefill (src/inference.py:409) and of
+ *           TinyTransformer.forward (src/transformer.py:333-349) for a model whose parameters
+ *           (and so its cache, src/inference.py:522, :544) are fp32.
+ * q: fp32 [rows, n_heads, 64], pre-scaled by the softmax scale times log2(e) (mdl_qkv_rope_cache
+ *    with MDL_DTYPE_F32); k_cache / v_cache: fp32 [batch, n_heads, cache_slots, 64], keys in
+ *    slots [0, seq).
+ * Query i of row b sees key j iff j < seq, kv_start[b] <= j (kv_start may be NULL), key_mask[b *
+ * seq + j] != 0 (key_mask may be NULL) and, if causal, j <= i; a query with no visible key
+ * outputs 0.  Query rows: b * seq + i, or with q_offset (packed rows; kv_start then required)
+ * row q_offset[b] + i - kv_start[b] for the queries i >= kv_start[b] only.
+ * out: split bf16 [rows, 2 * n_heads * 64] in out_layout; rows not named are not written.
+ */
+int mdl_attn_prefill_f32(const float* q, const float* k_cache, const float* v_cache, int batch,
+                         int seq, int n_heads, int head_dim, int cache_slots,
+                         const uint8_t* key_mask, const int32_t* kv_start,
+                         const int32_t* q_offset, int causal, uint16_t* out, int out_layout,
+                         void* stream);
+
+/*
+ * K4f at decode: the query of row b (q row b) sees slot j iff kv_start[b] <= j <= t,
+ * t = (seq_dev ? *seq_dev : seq_pos), and (j >= prompt_len || prompt_mask[b * prompt_len + j]
+ * != 0) (prompt_mask may be NULL) -- the visibility rule of mdl_attn_decode.  K / V of slot t
+ * must be written first (mdl_qkv_rope_cache, seq = 1, slot_dev).  Arguments otherwise as for
+ * mdl_attn_prefill_f32.
+ * Replaces: F.scaled_dot_product_attention in _decode_step (src/inference.py:452) for an fp32
+ *           model, with the mask of src/inference.py:446-450.
+ */
+int mdl_attn_decode_f32(const float* q, const float* k_cache, const float* v_cache, int batch,
+                        int n_heads, int head_dim, int cache_slots, const uint8_t* prompt_mask,
+                        int prompt_len, const int32_t* kv_start, int seq_pos,
+                        const int32_t* seq_dev, uint16_t* out, int out_layout, void* stream);
 
 /*
  * Final RMSNorm + LM head + greedy argmax.

@@ -40,11 +40,11 @@ SIGNATURES: dict[str, tuple[object, list]] = {
                                  P, P, c_int, c_int, P, P, P, P, P, c_int, P]),
     "mdl_add_rmsnorm": (c_int, [P, P, P, c_int, c_int, P, c_float, P, P, c_int, P]),
     "mdl_qkv_rope_cache": (c_int, [P, c_int64, P, P, P, c_int, c_int, c_int, c_int, c_int, c_int,
-                                   c_int, c_int, c_int, c_int, c_float, P, P, P, c_int, c_int, P,
-                                   P]),
+                                   c_int, c_int, c_int, c_int, c_float, P, P, P, c_int, c_int,
+                                   c_int, P, P]),
     "mdl_qkv_rope_cache_packed": (c_int, [P, c_int64, P, P, P, c_int64, P, P, c_int, c_int, c_int,
                                           c_int, c_int, c_int, c_int, c_int, c_int, c_float, P, P,
-                                          P, c_int, P]),
+                                          P, c_int, c_int, P]),
     "mdl_swiglu": (c_int, [P, c_int64, P, P, P, c_int, c_int, P, c_int, P]),
     "mdl_embed_rmsnorm_bf16": (c_int, [P, P, P, P, c_int, c_int, c_int, c_int, c_int, P, c_float,
                                        P, P, P]),
@@ -55,12 +55,14 @@ SIGNATURES: dict[str, tuple[object, list]] = {
     "mdl_gemm_split": (c_int, [P, c_int64, c_int, P, c_int64, c_int, P, c_int64, c_int, c_int,
                                c_int, c_int, P]),
     "mdl_gemm_split_swiglu": (c_int, [P, P, P, P, P, P, c_int, c_int, c_int, c_int, P]),
-    "mdl_gemm_norm": (c_int, [P, P, c_float, P, P, c_int64, P, c_int, c_int, c_int, c_int, P]),
+    "mdl_gemm_norm": (c_int, [P, P, c_float, P, P, P, c_int64, P, c_int, c_int, c_int, c_int,
+                              P]),
     "mdl_gemm_norm_qkv": (c_int, [P, P, c_float, P, c_int, c_int, P, P, P, c_int, c_int, c_int,
                                   c_int, c_int, c_int, c_float, P, P, P, c_int, c_int, P, c_int,
                                   P]),
-    "mdl_gemm_norm_swiglu": (c_int, [P, P, c_float, P, P, P, P, c_int, c_int, c_int, c_int, P]),
-    "mdl_gemm_split_residual": (c_int, [P, P, P, P, c_int, c_int, c_int, c_int, P]),
+    "mdl_gemm_norm_swiglu": (c_int, [P, P, c_float, P, P, P, P, P, c_int, c_int, c_int, c_int,
+                                     P]),
+    "mdl_gemm_split_residual": (c_int, [P, P, P, P, P, c_int, c_int, c_int, c_int, P]),
     "mdl_gemm_split_tiles": (c_int, []),
     "mdl_gemm_split_pick": (c_int, [c_int, c_int, c_int]),
     "mdl_prefill_gemm_split": (c_int, [P, c_int64, c_int, P, P, c_int64, c_int, c_int, c_int, P]),
@@ -90,6 +92,10 @@ SIGNATURES: dict[str, tuple[object, list]] = {
                                              c_int, c_int, c_float, P, P, c_int, c_int, c_int,
                                              c_int, P, c_int, P, P, P, c_int, P, c_int, P, c_int,
                                              P]),
+    "mdl_attn_prefill_f32": (c_int, [P, P, P, c_int, c_int, c_int, c_int, c_int, P, P, P, c_int,
+                                     P, c_int, P]),
+    "mdl_attn_decode_f32": (c_int, [P, P, P, c_int, c_int, c_int, c_int, P, c_int, P, c_int, P, P,
+                                    c_int, P]),
     "mdl_lm_head": (c_int, [P, P, c_int, c_int, P, c_float, P, c_int, P, P, CONS, c_int, P]),
     "mdl_decode_head": (c_int, [P, c_int, c_int, P, c_float, P, c_int, P, P, P, c_int64, c_int,
                                 P, P, c_int, c_int, CONS, c_int, P]),

@@ -290,7 +290,7 @@ int launch_head(const float* x, const int32_t* row_index, int rows, int d, const
 
 using namespace mdl;
 
-extern "C" int mdl_version(void) { return 102; }
+extern "C" int mdl_version(void) { return 200; }
 
 extern "C" const char* mdl_error_string(int code) {
   switch (code) {

@@ -305,7 +305,9 @@ __global__ __launch_bounds__(kThreads, 1) void prefill_gemm_kernel(const Args p)
           slot = static_cast<int>(m - b * p.seq);
         }
         const bool in_cache = slot >= 0 && slot < p.slots && b >= 0 && b < p.batch;
-        const int ks = (p.kv_start && b >= 0 && b < p.batch) ? p.kv_start[b] : 0;
+        // clamped below at 0 as the lead-attention pass (K4c) clamps it, so the rows written
+        // here are exactly the rows it reads
+        const int ks = (p.kv_start && b >= 0 && b < p.batch) ? max(p.kv_start[b], 0) : 0;
         const bool lead_row = p.out != nullptr && slot >= ks && slot - ks < p.lead;
         const float rs = rstd_s[r];
         const int64_t* pos3 = p.pos + static_cast<int64_t>(m) * 3;

@@ -31,13 +31,26 @@ __device__ __forceinline__ void token_slot(int64_t m, int seq, int slot0,
   }
 }
 
+// Stores of the K2 outputs in the cache dtype: bf16 (the attention kernels' MFMA operands) or
+// fp32 (the fp32 form: a model with fp32 parameters keeps an fp32 cache, src/inference.py:522).
+__device__ __forceinline__ void store2(uint16_t* p, float a, float b) {
+  *reinterpret_cast<uint32_t*>(p) = pack_bf2(a, b);
+}
+__device__ __forceinline__ void store2(float* p, float a, float b) {
+  *reinterpret_cast<float2*>(p) = make_float2(a, b);
+}
+__device__ __forceinline__ void store4(uint16_t* p, float4 v) {
+  *reinterpret_cast<uint2*>(p) = make_uint2(pack_bf2(v.x, v.y), pack_bf2(v.z, v.w));
+}
+__device__ __forceinline__ void store4(float* p, float4 v) { *reinterpret_cast<float4*>(p) = v; }
+
+template <typename TO>
 __global__ __launch_bounds__(256) void qkv_rope_cache_kernel(
     const float* __restrict__ qkv, int64_t ld, const float* __restrict__ rstd,
     const int64_t* __restrict__ pos, const float* __restrict__ tab, RopeArgs ra, int64_t rows,
-    int seq, int n_heads, float q_scale, uint16_t* __restrict__ q_out,
-    uint16_t* __restrict__ kc, uint16_t* __restrict__ vc, int slots, int slot0,
-    const int32_t* __restrict__ slot_dev, const int32_t* __restrict__ tok_row,
-    const int32_t* __restrict__ tok_slot, int64_t batch) {
+    int seq, int n_heads, float q_scale, TO* __restrict__ q_out, TO* __restrict__ kc,
+    TO* __restrict__ vc, int slots, int slot0, const int32_t* __restrict__ slot_dev,
+    const int32_t* __restrict__ tok_row, const int32_t* __restrict__ tok_slot, int64_t batch) {
   const int lane = threadIdx.x & 63;
   const int64_t m = static_cast<int64_t>(blockIdx.x) * 4 + (threadIdx.x >> 6);
   if (m >= rows) return;
@@ -54,7 +67,7 @@ __global__ __launch_bounds__(256) void qkv_rope_cache_kernel(
   token_slot(m, seq, slot0, slot_dev, tok_row, tok_slot, b, slot);
   // host guarantees the range; never write outside
   const bool in_cache = slot >= 0 && slot < slots && b >= 0 && b < batch;
-  uint16_t* qrow = q_out + m * d;
+  TO* qrow = q_out + m * d;
   const int64_t head_stride = static_cast<int64_t>(slots) * kHeadDim;
   const int64_t cache_row = (b * n_heads * static_cast<int64_t>(slots) + slot) * kHeadDim;
 
@@ -66,18 +79,15 @@ __global__ __launch_bounds__(256) void qkv_rope_cache_kernel(
     float y0, y1, z0, z1;
     rope_rot(q0, q1, cs, sn, y0, y1);
     rope_rot(k0, k1, cs, sn, z0, z1);
-    *reinterpret_cast<uint32_t*>(qrow + c) = pack_bf2(y0 * q_scale, y1 * q_scale);
-    if (in_cache)
-      *reinterpret_cast<uint32_t*>(kc + cache_row + h * head_stride + 2 * j) = pack_bf2(z0, z1);
+    store2(qrow + c, y0 * q_scale, y1 * q_scale);
+    if (in_cache) store2(kc + cache_row + h * head_stride + 2 * j, z0, z1);
   }
   if (!in_cache) return;
   for (int idx = lane; idx < d / 4; idx += 64) {
     const float4 v = *reinterpret_cast<const float4*>(row + 2 * d + 4 * idx);
     const int hv = (4 * idx) / kHeadDim, dm = (4 * idx) % kHeadDim;
-    uint2 o;
-    o.x = pack_bf2(v.x * r, v.y * r);
-    o.y = pack_bf2(v.z * r, v.w * r);
-    *reinterpret_cast<uint2*>(vc + cache_row + hv * head_stride + dm) = o;
+    store4(vc + cache_row + hv * head_stride + dm,
+           make_float4(v.x * r, v.y * r, v.z * r, v.w * r));
   }
 }
 
@@ -171,11 +181,22 @@ namespace mdl {
 
 int launch_k2(const float* qkv, int64_t qkv_ld, const float* rstd, const int64_t* pos,
               const float* rope_tab, int64_t rows, int seq, int n_heads, const RopeArgs& ra,
-              float q_scale, uint16_t* q_out, uint16_t* k_cache, uint16_t* v_cache,
+              float q_scale, void* q_out_v, void* k_cache_v, void* v_cache_v, int out_dtype,
               int cache_slots, int slot0, const int32_t* slot_dev, const int32_t* tok_row,
               const int32_t* tok_slot, int64_t batch, hipStream_t st) {
   if (rows == 0) return MDL_OK;
+  if ((rows + 3) / 4 > 0x7fffffff) return MDL_ERR_SHAPE;
   const dim3 grid(static_cast<unsigned>((rows + 3) / 4));
+  if (out_dtype == MDL_DTYPE_F32) {
+    qkv_rope_cache_kernel<float><<<grid, 256, 0, st>>>(
+        qkv, qkv_ld, rstd, pos, rope_tab, ra, rows, seq, n_heads, q_scale,
+        static_cast<float*>(q_out_v), static_cast<float*>(k_cache_v),
+        static_cast<float*>(v_cache_v), cache_slots, slot0, slot_dev, tok_row, tok_slot, batch);
+    return launch_status();
+  }
+  uint16_t* q_out = static_cast<uint16_t*>(q_out_v);
+  uint16_t* k_cache = static_cast<uint16_t*>(k_cache_v);
+  uint16_t* v_cache = static_cast<uint16_t*>(v_cache_v);
   const bool nt = rows * n_heads * kHeadDim * 18 >= kStreamBytes;
 #define MDL_K2_VEC(NCH)                                                                        \
   if (nt)                                                                                     \
@@ -192,10 +213,9 @@ int launch_k2(const float* qkv, int64_t qkv_ld, const float* rstd, const int64_t
     case 16: MDL_K2_VEC(12); break;
     case 20: MDL_K2_VEC(15); break;
     default:
-      qkv_rope_cache_kernel<<<grid, 256, 0, st>>>(qkv, qkv_ld, rstd, pos, rope_tab, ra, rows,
-                                                  seq, n_heads, q_scale, q_out, k_cache,
-                                                  v_cache, cache_slots, slot0, slot_dev, tok_row,
-                                                  tok_slot, batch);
+      qkv_rope_cache_kernel<uint16_t><<<grid, 256, 0, st>>>(
+          qkv, qkv_ld, rstd, pos, rope_tab, ra, rows, seq, n_heads, q_scale, q_out, k_cache,
+          v_cache, cache_slots, slot0, slot_dev, tok_row, tok_slot, batch);
   }
 #undef MDL_K2_VEC
   return launch_status();
@@ -203,8 +223,9 @@ int launch_k2(const float* qkv, int64_t qkv_ld, const float* rstd, const int64_t
 
 int check_k2(const float* qkv, int64_t qkv_ld, const int64_t* pos, const float* rope_tab,
              int n_heads, int head_dim, int max_x, int max_y, int max_z, int px, int py, int pz,
-             const uint16_t* q_out, const uint16_t* k_cache, const uint16_t* v_cache) {
+             const void* q_out, const void* k_cache, const void* v_cache, int out_dtype) {
   if (!qkv || !pos || !rope_tab || !q_out || !k_cache || !v_cache) return MDL_ERR_NULL;
+  if (out_dtype != MDL_DTYPE_F32 && out_dtype != MDL_DTYPE_BF16) return MDL_ERR_DTYPE;
   if (head_dim != kHeadDim) return MDL_ERR_HEAD_DIM;
   if (n_heads <= 0 || max_x <= 0 || max_y <= 0 || max_z <= 0 || px < 0 || py < 0 || pz < 0 ||
       px + py + pz != kHeadDim / 2 || qkv_ld < 3 * n_heads * 64)
@@ -220,19 +241,19 @@ int check_k2(const float* qkv, int64_t qkv_ld, const int64_t* pos, const float* 
 extern "C" int mdl_qkv_rope_cache(const float* qkv, int64_t qkv_ld, const float* rstd,
                                   const int64_t* pos, const float* rope_tab, int batch, int seq,
                                   int n_heads, int head_dim, int max_x, int max_y, int max_z,
-                                  int px, int py, int pz, float q_scale, uint16_t* q_out,
-                                  uint16_t* k_cache, uint16_t* v_cache, int cache_slots,
+                                  int px, int py, int pz, float q_scale, void* q_out,
+                                  void* k_cache, void* v_cache, int out_dtype, int cache_slots,
                                   int slot0, const int32_t* slot_dev, void* stream) {
   const int c = check_k2(qkv, qkv_ld, pos, rope_tab, n_heads, head_dim, max_x, max_y, max_z, px,
-                         py, pz, q_out, k_cache, v_cache);
+                         py, pz, q_out, k_cache, v_cache, out_dtype);
   if (c != MDL_OK) return c;
   if (batch < 0 || seq <= 0) return MDL_ERR_SHAPE;
   if (cache_slots <= 0 || (!slot_dev && (slot0 < 0 || slot0 + seq > cache_slots)))
     return MDL_ERR_CACHE;
   const RopeArgs ra{max_x, max_y, max_z, px, py, pz};
   return launch_k2(qkv, qkv_ld, rstd, pos, rope_tab, static_cast<int64_t>(batch) * seq, seq,
-                   n_heads, ra, q_scale, q_out, k_cache, v_cache, cache_slots, slot0, slot_dev,
-                   nullptr, nullptr, batch, static_cast<hipStream_t>(stream));
+                   n_heads, ra, q_scale, q_out, k_cache, v_cache, out_dtype, cache_slots, slot0,
+                   slot_dev, nullptr, nullptr, batch, static_cast<hipStream_t>(stream));
 }
 
 extern "C" int mdl_qkv_rope_cache_bf16(const uint16_t* qkv, int64_t qkv_ld, const float* rstd,
@@ -282,16 +303,16 @@ extern "C" int mdl_qkv_rope_cache_packed(const float* qkv, int64_t qkv_ld, const
                                          int64_t n_tokens, const int32_t* token_row,
                                          const int32_t* token_slot, int batch, int n_heads,
                                          int head_dim, int max_x, int max_y, int max_z, int px,
-                                         int py, int pz, float q_scale, uint16_t* q_out,
-                                         uint16_t* k_cache, uint16_t* v_cache, int cache_slots,
-                                         void* stream) {
+                                         int py, int pz, float q_scale, void* q_out,
+                                         void* k_cache, void* v_cache, int out_dtype,
+                                         int cache_slots, void* stream) {
   const int c = check_k2(qkv, qkv_ld, pos, rope_tab, n_heads, head_dim, max_x, max_y, max_z, px,
-                         py, pz, q_out, k_cache, v_cache);
+                         py, pz, q_out, k_cache, v_cache, out_dtype);
   if (c != MDL_OK) return c;
   if (!token_row || !token_slot) return MDL_ERR_NULL;
   if (n_tokens < 0 || batch < 0 || cache_slots <= 0) return MDL_ERR_SHAPE;
   const RopeArgs ra{max_x, max_y, max_z, px, py, pz};
   return launch_k2(qkv, qkv_ld, rstd, pos, rope_tab, n_tokens, 1, n_heads, ra, q_scale, q_out,
-                   k_cache, v_cache, cache_slots, 0, nullptr, token_row, token_slot, batch,
-                   static_cast<hipStream_t>(stream));
+                   k_cache, v_cache, out_dtype, cache_slots, 0, nullptr, token_row, token_slot,
+                   batch, static_cast<hipStream_t>(stream));
 }

@@ -40,6 +40,11 @@
 // Summation order is fixed (each wave's k-steps in order, hi before lo, waves summed 0..7 in the
 // reduction), so a given tile shape is bit-reproducible; the A source and the layouts do not
 // change the result.
+//
+// fp32 weights (WL forms): a model whose parameters are fp32 passes its weight as two bf16
+// matrices in the same tile layout, w = bf16(W) and w_lo = bf16(W - w).  Every k-step then adds
+// a third product, a_hi . w_lo, after the hi and lo products, so the GEMM sees W to ~2^-17 like
+// the activation (the dropped a_lo . w_lo term is ~2^-18 of the product).
 #include "common.h"
 #include "mfma.h"
 #include "rope.h"
@@ -61,6 +66,7 @@ struct GemmArgs {
   const float* gamma;      // A_NORM: RMSNorm gain [K]
   float eps;
   const uint16_t* w;
+  const uint16_t* wl;      // WL forms: low bf16 part of an fp32 weight, tiled like w
   int64_t ldw;             // row-major w row stride (elements)
   float* out;              // E_STORE: [M, N] fp32, row stride ldo
   int64_t ldo;
@@ -104,12 +110,14 @@ __device__ __forceinline__ int64_t frag_step(int s) {
   return TILED ? static_cast<int64_t>(512) * s : static_cast<int64_t>(32) * s;
 }
 
-template <int TN, int TM, bool WT, int AMODE, int EPI>
+template <int TN, int TM, bool WT, int AMODE, int EPI, bool WL>
 __global__ __launch_bounds__(64 * kGemmWaves) void split_gemm_kernel(const GemmArgs p) {
   constexpr int FN = TN / 16, FM = TM / 16, NW = kGemmWaves;
+  static_assert(!WL || WT, "the low weight part is tiled");
   // k-steps in flight: the fp32 x and gamma fragments of A_NORM take twice the registers of a
-  // split operand, and 4 steps of the two largest tiles would spill
-  constexpr int U = (AMODE == A_NORM && FN * FM >= 16) ? 3 : kU;
+  // split operand, and 4 steps of the two largest tiles would spill; the WL forms hold a second
+  // weight fragment per step
+  constexpr int U = WL ? 2 : ((AMODE == A_NORM && FN * FM >= 16) ? 3 : kU);
   static_assert(TN % 16 == 0 && TM % 16 == 0, "tile must be a multiple of 16");
   const int M = p.M, N = p.N, K = p.K;
   // logical tile of this block: tiles per_xcd * x .. per_xcd * (x + 1) - 1 run on XCD x
@@ -124,6 +132,11 @@ __global__ __launch_bounds__(64 * kGemmWaves) void split_gemm_kernel(const GemmA
   const uint16_t* wp[FN];
 #pragma unroll
   for (int i = 0; i < FN; ++i) wp[i] = frag_base<WT>(p.w, p.ldw, n0 / 16 + i, N, K, lane);
+  const uint16_t* wlp[WL ? FN : 1];
+  if constexpr (WL) {
+#pragma unroll
+    for (int i = 0; i < FN; ++i) wlp[i] = frag_base<true>(p.wl, 0, n0 / 16 + i, N, K, lane);
+  }
   const uint16_t* ap[FM];
   const float* xp[FM];
   int64_t lo_off = 0;
@@ -193,7 +206,7 @@ __global__ __launch_bounds__(64 * kGemmWaves) void split_gemm_kernel(const GemmA
   const int nk = K >> 5;
   const int s0 = (nk * wave) / NW, s1 = (nk * (wave + 1)) / NW;
   for (int s = s0; s < s1; s += U) {
-    uint4 wf[U][FN], ah[U][FM], al[U][FM];
+    uint4 wf[U][FN], ah[U][FM], al[U][FM], wlf[U][WL ? FN : 1];
     float4 xv[U][FM][2], gv[U][2];
 #pragma unroll
     for (int u = 0; u < U; ++u) {
@@ -202,6 +215,11 @@ __global__ __launch_bounds__(64 * kGemmWaves) void split_gemm_kernel(const GemmA
 #pragma unroll
       for (int i = 0; i < FN; ++i)
         wf[u][i] = *reinterpret_cast<const uint4*>(wp[i] + frag_step<WT>(su));
+      if constexpr (WL) {
+#pragma unroll
+        for (int i = 0; i < FN; ++i)
+          wlf[u][i] = *reinterpret_cast<const uint4*>(wlp[i] + frag_step<true>(su));
+      }
       if constexpr (AMODE == A_NORM) {
         gv[u][0] = *reinterpret_cast<const float4*>(p.gamma + 32 * su + 8 * g);
         gv[u][1] = *reinterpret_cast<const float4*>(p.gamma + 32 * su + 8 * g + 4);
@@ -256,6 +274,14 @@ __global__ __launch_bounds__(64 * kGemmWaves) void split_gemm_kernel(const GemmA
             acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf16x8(wf[u][i]),
                                                                 as_bf16x8(al[u][j]), acc[i][j],
                                                                 0, 0, 0);
+        if constexpr (WL) {
+#pragma unroll
+          for (int i = 0; i < FN; ++i)
+#pragma unroll
+            for (int j = 0; j < FM; ++j)
+              acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(
+                  as_bf16x8(wlf[u][i]), as_bf16x8(ah[u][j]), acc[i][j], 0, 0, 0);
+        }
       }
     }
   }
@@ -426,13 +452,13 @@ constexpr int kNumTiles = sizeof(kTiles) / sizeof(kTiles[0]);
 // block: 4 for a split operand (hi + lo), 8 for A_NORM, whose fp32 x also goes through the
 // norm and split arithmetic in every block sharing its rows (with 8 it picks the measured
 // fastest shape at the 6 norm-fused decode shapes).
-int pick_tile(int M, int N, int K, double a_bytes = 4.0) {
+int pick_tile(int M, int N, int K, double a_bytes = 4.0, double w_bytes = 2.0) {
   int best = 0;
   double best_key = 1e300, best_total = 1e300;
   for (int t = 0; t < kNumTiles; ++t) {
     const double blocks = static_cast<double>((N + kTiles[t].tn - 1) / kTiles[t].tn) *
                           ((M + kTiles[t].tm - 1) / kTiles[t].tm);
-    const double per_block = (2.0 * kTiles[t].tn + a_bytes * kTiles[t].tm) * K;
+    const double per_block = (w_bytes * kTiles[t].tn + a_bytes * kTiles[t].tm) * K;
     const double rounds = static_cast<double>((static_cast<int64_t>(blocks) + 255) / 256);
     const double key = per_block * rounds, total = per_block * blocks;
     if (key < best_key * 0.999 || (key < best_key * 1.001 && total < best_total)) {
@@ -444,7 +470,7 @@ int pick_tile(int M, int N, int K, double a_bytes = 4.0) {
   return best + 1;
 }
 
-template <int TN, int TM, bool WT, int AMODE, int EPI>
+template <int TN, int TM, bool WT, int AMODE, int EPI, bool WL>
 int launch_tile(GemmArgs p, hipStream_t st) {
   p.n_tiles = (p.N + TN - 1) / TN;
   p.m_tiles = (p.M + TM - 1) / TM;
@@ -452,22 +478,29 @@ int launch_tile(GemmArgs p, hipStream_t st) {
   const int64_t per_xcd = (tiles + 7) / 8;
   if (8 * per_xcd > 0x7fffffff) return MDL_ERR_SHAPE;
   p.per_xcd = static_cast<int>(per_xcd);
-  hipLaunchKernelGGL((split_gemm_kernel<TN, TM, WT, AMODE, EPI>),
+  hipLaunchKernelGGL((split_gemm_kernel<TN, TM, WT, AMODE, EPI, WL>),
                      dim3(static_cast<unsigned>(8 * per_xcd)), dim3(64 * kGemmWaves), 0, st, p);
   return launch_status();
 }
 
-template <bool WT, int AMODE, int EPI>
+template <bool WT, int AMODE, int EPI, bool WL = false>
 int launch(int tile, const GemmArgs& p, hipStream_t st) {
-  switch (tile ? tile : pick_tile(p.M, p.N, p.K, AMODE == A_NORM ? 8.0 : 4.0)) {
-    case 1: return launch_tile<64, 64, WT, AMODE, EPI>(p, st);
-    case 2: return launch_tile<128, 32, WT, AMODE, EPI>(p, st);
-    case 3: return launch_tile<64, 32, WT, AMODE, EPI>(p, st);
-    case 4: return launch_tile<32, 32, WT, AMODE, EPI>(p, st);
-    case 5: return launch_tile<64, 16, WT, AMODE, EPI>(p, st);
-    case 6: return launch_tile<32, 16, WT, AMODE, EPI>(p, st);
+  switch (tile ? tile : pick_tile(p.M, p.N, p.K, AMODE == A_NORM ? 8.0 : 4.0, WL ? 4.0 : 2.0)) {
+    case 1: return launch_tile<64, 64, WT, AMODE, EPI, WL>(p, st);
+    case 2: return launch_tile<128, 32, WT, AMODE, EPI, WL>(p, st);
+    case 3: return launch_tile<64, 32, WT, AMODE, EPI, WL>(p, st);
+    case 4: return launch_tile<32, 32, WT, AMODE, EPI, WL>(p, st);
+    case 5: return launch_tile<64, 16, WT, AMODE, EPI, WL>(p, st);
+    case 6: return launch_tile<32, 16, WT, AMODE, EPI, WL>(p, st);
     default: return MDL_ERR_SHAPE;
   }
+}
+
+// the plain form, or the WL form when the caller passes the low weight part
+template <int AMODE, int EPI>
+int launch_w(int tile, const GemmArgs& p, hipStream_t st) {
+  return p.wl ? launch<true, AMODE, EPI, true>(tile, p, st)
+              : launch<true, AMODE, EPI, false>(tile, p, st);
 }
 
 // dst = src in the bf16 tile layout, rows padded to a multiple of 16 with zeros.  One thread per
@@ -554,11 +587,12 @@ extern "C" int mdl_gemm_split_swiglu(const uint16_t* a, const uint16_t* w_gu, co
 }
 
 extern "C" int mdl_gemm_norm(const float* x, const float* gamma, float eps, const uint16_t* w,
-                             float* out, int64_t ldo, float* rstd_out, int m, int n, int k,
-                             int tile, void* stream) {
+                             const uint16_t* w_lo, float* out, int64_t ldo, float* rstd_out,
+                             int m, int n, int k, int tile, void* stream) {
   if (!x || !gamma || !w || !out) return MDL_ERR_NULL;
   if (!decode_shape_ok(m, n, k, tile) || ldo < n) return MDL_ERR_SHAPE;
-  if (!aligned16(x) || !aligned16(gamma) || !aligned16(w) || !aligned16(out) || ldo % 4 != 0)
+  if (!aligned16(x) || !aligned16(gamma) || !aligned16(w) || !aligned16(out) || ldo % 4 != 0 ||
+      (w_lo && !aligned16(w_lo)))
     return MDL_ERR_ALIGN;
   if (m == 0 || n == 0) return MDL_OK;
   GemmArgs p{};
@@ -566,13 +600,14 @@ extern "C" int mdl_gemm_norm(const float* x, const float* gamma, float eps, cons
   p.gamma = gamma;
   p.eps = eps;
   p.w = w;
+  p.wl = w_lo;
   p.out = out;
   p.ldo = ldo;
   p.rstd_out = rstd_out;
   p.M = m;
   p.N = n;
   p.K = k;
-  return launch<true, A_NORM, E_STORE>(tile, p, static_cast<hipStream_t>(stream));
+  return launch_w<A_NORM, E_STORE>(tile, p, static_cast<hipStream_t>(stream));
 }
 
 extern "C" int mdl_gemm_norm_qkv(const float* x, const float* gamma, float eps,
@@ -617,14 +652,15 @@ extern "C" int mdl_gemm_norm_qkv(const float* x, const float* gamma, float eps,
 }
 
 extern "C" int mdl_gemm_norm_swiglu(const float* x, const float* gamma, float eps,
-                                    const uint16_t* w_gu, const float* bias_gate,
-                                    const float* bias_up, uint16_t* h_out, int m, int d_ff, int k,
-                                    int tile, void* stream) {
+                                    const uint16_t* w_gu, const uint16_t* w_gu_lo,
+                                    const float* bias_gate, const float* bias_up, uint16_t* h_out,
+                                    int m, int d_ff, int k, int tile, void* stream) {
   if (!x || !gamma || !w_gu || !h_out) return MDL_ERR_NULL;
   if (d_ff <= 0 || d_ff % 16 != 0 || d_ff > (1 << 29) || !decode_shape_ok(m, 2 * d_ff, k, tile))
     return MDL_ERR_SHAPE;
   if (!aligned16(x) || !aligned16(gamma) || !aligned16(w_gu) || !aligned8(h_out) ||
-      (bias_gate && !aligned16(bias_gate)) || (bias_up && !aligned16(bias_up)))
+      (bias_gate && !aligned16(bias_gate)) || (bias_up && !aligned16(bias_up)) ||
+      (w_gu_lo && !aligned16(w_gu_lo)))
     return MDL_ERR_ALIGN;
   if (m == 0) return MDL_OK;
   GemmArgs p{};
@@ -632,6 +668,7 @@ extern "C" int mdl_gemm_norm_swiglu(const float* x, const float* gamma, float ep
   p.gamma = gamma;
   p.eps = eps;
   p.w = w_gu;
+  p.wl = w_gu_lo;
   p.bias_a = bias_gate;
   p.bias_b = bias_up;
   p.h = h_out;
@@ -639,26 +676,28 @@ extern "C" int mdl_gemm_norm_swiglu(const float* x, const float* gamma, float ep
   p.M = m;
   p.N = 2 * d_ff;
   p.K = k;
-  return launch<true, A_NORM, E_SWIGLU>(tile, p, static_cast<hipStream_t>(stream));
+  return launch_w<A_NORM, E_SWIGLU>(tile, p, static_cast<hipStream_t>(stream));
 }
 
-extern "C" int mdl_gemm_split_residual(const uint16_t* a, const uint16_t* w, float* x,
-                                       const float* bias, int m, int n, int k, int tile,
-                                       void* stream) {
+extern "C" int mdl_gemm_split_residual(const uint16_t* a, const uint16_t* w,
+                                       const uint16_t* w_lo, float* x, const float* bias, int m,
+                                       int n, int k, int tile, void* stream) {
   if (!a || !w || !x) return MDL_ERR_NULL;
   if (!decode_shape_ok(m, n, k, tile) || n % 32 != 0) return MDL_ERR_SHAPE;
-  if (!aligned16(a) || !aligned16(w) || !aligned16(x) || (bias && !aligned16(bias)))
+  if (!aligned16(a) || !aligned16(w) || !aligned16(x) || (bias && !aligned16(bias)) ||
+      (w_lo && !aligned16(w_lo)))
     return MDL_ERR_ALIGN;
   if (m == 0 || n == 0) return MDL_OK;
   GemmArgs p{};
   p.a = a;
   p.w = w;
+  p.wl = w_lo;
   p.x_res = x;
   p.bias_a = bias;
   p.M = m;
   p.N = n;
   p.K = k;
-  return launch<true, A_TILES, E_RESIDUAL>(tile, p, static_cast<hipStream_t>(stream));
+  return launch_w<A_TILES, E_RESIDUAL>(tile, p, static_cast<hipStream_t>(stream));
 }
 
 extern "C" int mdl_gemm_split_tiles(void) { return kNumTiles; }

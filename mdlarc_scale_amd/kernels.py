@@ -60,6 +60,15 @@ def split_numel(rows: int, k: int, tiled: bool) -> int:
     return (tile_rows(rows) if tiled else rows) * 2 * k
 
 
+def cache_dtype_code(t: torch.Tensor) -> int:
+    """MDL_DTYPE_* of a cache (or q) tensor: bf16 (bf16 form) or fp32 (fp32 form)."""
+    if t.dtype == F32:
+        return 0
+    if t.dtype == BF16:
+        return 1
+    raise ValueError(f"the KV cache must be bfloat16 or float32 (got {t.dtype})")
+
+
 def table_dtype_code(t: torch.Tensor) -> int:
     if t.dtype == F32:
         return 0
@@ -153,7 +162,8 @@ def qkv_rope_cache(qkv: torch.Tensor, rstd: torch.Tensor | None, pos: torch.Tens
                    k_cache: torch.Tensor, v_cache: torch.Tensor, slot0: int = 0,
                    slot_dev: torch.Tensor | None = None) -> None:
     """rope_geom = (max_x, max_y, max_z, px, py, pz); k/v_cache are one layer's
-    [batch, n_heads, slots, 64] bf16 (contiguous views of the static cache)."""
+    [batch, n_heads, slots, 64] (contiguous views of the static cache), bf16 or fp32 (the fp32
+    form); q_out has the cache's dtype."""
     rows, d = batch * seq, n_heads * HEAD_DIM
     _need(qkv, "qkv", F32, rows * 3 * d)
     if qkv.dim() != 2 or qkv.shape[1] != 3 * d:
@@ -161,9 +171,10 @@ def qkv_rope_cache(qkv: torch.Tensor, rstd: torch.Tensor | None, pos: torch.Tens
     _need(rstd, "rstd", F32, rows, optional=True)
     _need(pos, "pos", I64, rows * 3)
     _need(rope_tab, "rope_tab", F32)
-    _need(q_out, "q_out", BF16, rows * d)
+    dt = cache_dtype_code(k_cache)
+    _need(q_out, "q_out", k_cache.dtype, rows * d)
     for name, c in (("k_cache", k_cache), ("v_cache", v_cache)):
-        _need(c, name, BF16)
+        _need(c, name, k_cache.dtype)
         if c.dim() != 4 or c.shape[0] != batch or c.shape[1] != n_heads or c.shape[3] != 64:
             raise ValueError(f"{name} must be [batch, n_heads, slots, 64]")
     _need(slot_dev, "slot_dev", I32, 1, optional=True)
@@ -171,7 +182,7 @@ def qkv_rope_cache(qkv: torch.Tensor, rstd: torch.Tensor | None, pos: torch.Tens
     mx, my, mz, px, py, pz = rope_geom
     _lib.check(_lib.lib().mdl_qkv_rope_cache(
         _p(qkv), qkv.shape[1], _p(rstd), _p(pos), _p(rope_tab), batch, seq, n_heads, HEAD_DIM,
-        mx, my, mz, px, py, pz, q_scale, _p(q_out), _p(k_cache), _p(v_cache), slots, slot0,
+        mx, my, mz, px, py, pz, q_scale, _p(q_out), _p(k_cache), _p(v_cache), dt, slots, slot0,
         _p(slot_dev), _stream()), "mdl_qkv_rope_cache")
 
 
@@ -182,7 +193,7 @@ def qkv_rope_cache_packed(qkv: torch.Tensor, rstd: torch.Tensor | None, pos: tor
                           q_scale: float, q_out: torch.Tensor, k_cache: torch.Tensor,
                           v_cache: torch.Tensor) -> None:
     """``qkv_rope_cache`` over a packed token list: token m goes to batch row token_row[m],
-    cache slot token_slot[m] (no cache write when negative)."""
+    cache slot token_slot[m] (no cache write when negative); bf16 or fp32 cache and q_out."""
     rows, d = token_row.numel(), n_heads * HEAD_DIM
     _need(qkv, "qkv", F32, rows * 3 * d)
     if qkv.dim() != 2 or qkv.shape[1] != 3 * d:
@@ -190,11 +201,12 @@ def qkv_rope_cache_packed(qkv: torch.Tensor, rstd: torch.Tensor | None, pos: tor
     _need(rstd, "rstd", F32, rows, optional=True)
     _need(pos, "pos", I64, rows * 3)
     _need(rope_tab, "rope_tab", F32)
-    _need(q_out, "q_out", BF16, rows * d)
+    dt = cache_dtype_code(k_cache)
+    _need(q_out, "q_out", k_cache.dtype, rows * d)
     _need(token_row, "token_row", I32, rows)
     _need(token_slot, "token_slot", I32, rows)
     for name, c in (("k_cache", k_cache), ("v_cache", v_cache)):
-        _need(c, name, BF16)
+        _need(c, name, k_cache.dtype)
         if c.dim() != 4 or c.shape[1] != n_heads or c.shape[3] != 64:
             raise ValueError(f"{name} must be [batch, n_heads, slots, 64]")
     batch, slots = k_cache.shape[0], k_cache.shape[2]
@@ -202,7 +214,7 @@ def qkv_rope_cache_packed(qkv: torch.Tensor, rstd: torch.Tensor | None, pos: tor
     _lib.check(_lib.lib().mdl_qkv_rope_cache_packed(
         _p(qkv), qkv.shape[1], _p(rstd), _p(pos), _p(rope_tab), rows, _p(token_row),
         _p(token_slot), batch, n_heads, HEAD_DIM, mx, my, mz, px, py, pz, q_scale, _p(q_out),
-        _p(k_cache), _p(v_cache), slots, _stream()), "mdl_qkv_rope_cache_packed")
+        _p(k_cache), _p(v_cache), dt, slots, _stream()), "mdl_qkv_rope_cache_packed")
 
 
 def swiglu(gate_up: torch.Tensor, rstd: torch.Tensor | None, bias_gate: torch.Tensor | None,
@@ -348,17 +360,21 @@ def interleave_gate_up(w_gate: torch.Tensor, w_up: torch.Tensor) -> torch.Tensor
 
 
 def gemm_norm(x: torch.Tensor, gamma: torch.Tensor, eps: float, w: torch.Tensor,
-              out: torch.Tensor, rstd_out: torch.Tensor | None, k: int, tile: int = 0) -> None:
+              out: torch.Tensor, rstd_out: torch.Tensor | None, k: int, tile: int = 0,
+              w_lo: torch.Tensor | None = None) -> None:
     """out[m, n] = split(x * gamma) @ W^T with the RMSNorm in K5's prologue; rstd of each row
-    into rstd_out (may be None).  x: fp32 tile layout [tile_rows(m), k]; w tiled [n, k]."""
+    into rstd_out (may be None).  x: fp32 tile layout [tile_rows(m), k]; w tiled [n, k].
+    w_lo (tiled like w, may be None): the low bf16 part of an fp32 weight (the fp32 form)."""
     _need(out, "out", F32)
     m, n = out.shape
     _need(x, "x", F32, tile_rows(m) * k)
     _need(gamma, "gamma", F32, k)
     _need(w, "w", BF16, tile_rows(n) * k)
+    _need(w_lo, "w_lo", BF16, tile_rows(n) * k, optional=True)
     _need(rstd_out, "rstd_out", F32, m, optional=True)
-    _lib.check(_lib.lib().mdl_gemm_norm(_p(x), _p(gamma), eps, _p(w), _p(out), n, _p(rstd_out),
-                                        m, n, k, tile, _stream()), "mdl_gemm_norm")
+    _lib.check(_lib.lib().mdl_gemm_norm(_p(x), _p(gamma), eps, _p(w), _p(w_lo), _p(out), n,
+                                        _p(rstd_out), m, n, k, tile, _stream()),
+               "mdl_gemm_norm")
 
 
 def gemm_norm_qkv(x: torch.Tensor, gamma: torch.Tensor, eps: float, w: torch.Tensor, m: int,
@@ -392,32 +408,36 @@ def gemm_norm_qkv(x: torch.Tensor, gamma: torch.Tensor, eps: float, w: torch.Ten
 
 def gemm_norm_swiglu(x: torch.Tensor, gamma: torch.Tensor, eps: float, w_gu: torch.Tensor,
                      bias_gate: torch.Tensor | None, bias_up: torch.Tensor | None,
-                     h_out: torch.Tensor, m: int, d_ff: int, k: int, tile: int = 0) -> None:
+                     h_out: torch.Tensor, m: int, d_ff: int, k: int, tile: int = 0,
+                     w_gu_lo: torch.Tensor | None = None) -> None:
     """The gate / up projection of split(x * gamma) (RMSNorm in the prologue) with the SwiGLU
     epilogue: h (tiled split [m, 2 d_ff]).  x: fp32 tile layout; w_gu: tiled
-    interleave_gate_up weight."""
+    interleave_gate_up weight; w_gu_lo its low part for an fp32 weight (may be None)."""
     _need(x, "x", F32, tile_rows(m) * k)
     _need(gamma, "gamma", F32, k)
     _need(w_gu, "w_gu", BF16, 2 * d_ff * k)
+    _need(w_gu_lo, "w_gu_lo", BF16, 2 * d_ff * k, optional=True)
     _need(bias_gate, "bias_gate", F32, d_ff, optional=True)
     _need(bias_up, "bias_up", F32, d_ff, optional=True)
     _need(h_out, "h_out", BF16, split_numel(m, d_ff, True))
     _lib.check(_lib.lib().mdl_gemm_norm_swiglu(
-        _p(x), _p(gamma), eps, _p(w_gu), _p(bias_gate), _p(bias_up), _p(h_out), m, d_ff, k,
-        tile, _stream()), "mdl_gemm_norm_swiglu")
+        _p(x), _p(gamma), eps, _p(w_gu), _p(w_gu_lo), _p(bias_gate), _p(bias_up), _p(h_out), m,
+        d_ff, k, tile, _stream()), "mdl_gemm_norm_swiglu")
 
 
 def gemm_split_residual(a: torch.Tensor, w: torch.Tensor, x: torch.Tensor,
                         bias: torch.Tensor | None, m: int, n: int, k: int,
-                        tile: int = 0) -> None:
+                        tile: int = 0, w_lo: torch.Tensor | None = None) -> None:
     """x += (a_hi + a_lo) @ W^T (+ bias) in place; a tiled split [m, 2k], w tiled [n, k], x the
-    fp32 tile-layout residual stream [tile_rows(m), n]."""
+    fp32 tile-layout residual stream [tile_rows(m), n]; w_lo the low part of an fp32 w."""
     _need(a, "a", BF16, tile_rows(m) * 2 * k)
     _need(w, "w", BF16, tile_rows(n) * k)
+    _need(w_lo, "w_lo", BF16, tile_rows(n) * k, optional=True)
     _need(x, "x", F32, tile_rows(m) * n)
     _need(bias, "bias", F32, n, optional=True)
-    _lib.check(_lib.lib().mdl_gemm_split_residual(_p(a), _p(w), _p(x), _p(bias), m, n, k, tile,
-                                                  _stream()), "mdl_gemm_split_residual")
+    _lib.check(_lib.lib().mdl_gemm_split_residual(_p(a), _p(w), _p(w_lo), _p(x), _p(bias), m, n,
+                                                  k, tile, _stream()),
+               "mdl_gemm_split_residual")
 
 
 PREFILL_NORM_MAX_K = 2048   # K6 norm forms: gamma is staged in LDS (kMaxNormK)
@@ -630,6 +650,53 @@ def attn_prefill_packed(q: torch.Tensor, k_cache: torch.Tensor, v_cache: torch.T
         _p(q), _p(k_cache), _p(v_cache), batch, seq, n_heads, HEAD_DIM, k_cache.shape[2],
         _p(key_mask), _p(row_holes), _p(kv_start), _p(q_offset), 1 if causal else 0, _p(out),
         _layout(out_tiled), _stream()), "mdl_attn_prefill_packed")
+
+
+def _f32_cache(k_cache: torch.Tensor, v_cache: torch.Tensor, batch: int, n_heads: int) -> None:
+    for name, c in (("k_cache", k_cache), ("v_cache", v_cache)):
+        _need(c, name, F32)
+        if c.dim() != 4 or c.shape[0] != batch or c.shape[1] != n_heads or c.shape[3] != 64:
+            raise ValueError(f"{name} must be [batch, n_heads, slots, 64]")
+
+
+def attn_prefill_f32(q: torch.Tensor, k_cache: torch.Tensor, v_cache: torch.Tensor, batch: int,
+                     seq: int, n_heads: int, key_mask: torch.Tensor | None,
+                     kv_start: torch.Tensor | None, q_offset: torch.Tensor | None, n_rows: int,
+                     causal: bool, out: torch.Tensor, out_tiled: bool = False) -> None:
+    """K4f, the fp32 form's attention over keys [0, seq) of an fp32 cache: q fp32
+    [n_rows, n_heads*64] (rows b*seq + i, or packed through q_offset / kv_start as in
+    attn_prefill_packed), out split [n_rows, 2*n_heads*64] bf16 (row-major or tiled)."""
+    _need(q, "q", F32, n_rows * n_heads * HEAD_DIM)
+    _need(out, "out", BF16, split_numel(n_rows, n_heads * HEAD_DIM, out_tiled))
+    _f32_cache(k_cache, v_cache, batch, n_heads)
+    _need(key_mask, "key_mask", U8, batch * seq, optional=True)
+    _need(kv_start, "kv_start", I32, batch, optional=q_offset is None)
+    _need(q_offset, "q_offset", I32, batch, optional=True)
+    if q_offset is None and n_rows < batch * seq:
+        raise ValueError("unpacked queries need n_rows >= batch * seq")
+    _lib.check(_lib.lib().mdl_attn_prefill_f32(
+        _p(q), _p(k_cache), _p(v_cache), batch, seq, n_heads, HEAD_DIM, k_cache.shape[2],
+        _p(key_mask), _p(kv_start), _p(q_offset), 1 if causal else 0, _p(out),
+        _layout(out_tiled), _stream()), "mdl_attn_prefill_f32")
+
+
+def attn_decode_f32(q: torch.Tensor, k_cache: torch.Tensor, v_cache: torch.Tensor, batch: int,
+                    n_heads: int, prompt_mask: torch.Tensor | None, prompt_len: int,
+                    kv_start: torch.Tensor | None, seq_pos: int, seq_dev: torch.Tensor | None,
+                    out: torch.Tensor, tiled: bool = False) -> None:
+    """K4f at decode: the query of row b (fp32 q [batch, n_heads*64]) over slots
+    [kv_start[b], t] of the fp32 cache, t = seq_dev[0] (or seq_pos), the prompt mask applying
+    below prompt_len; out split [batch, 2*n_heads*64] bf16."""
+    _need(q, "q", F32, batch * n_heads * HEAD_DIM)
+    _need(out, "out", BF16, split_numel(batch, n_heads * HEAD_DIM, tiled))
+    _f32_cache(k_cache, v_cache, batch, n_heads)
+    _need(prompt_mask, "prompt_mask", U8, batch * prompt_len, optional=True)
+    _need(kv_start, "kv_start", I32, batch, optional=True)
+    _need(seq_dev, "seq_dev", I32, 1, optional=True)
+    _lib.check(_lib.lib().mdl_attn_decode_f32(
+        _p(q), _p(k_cache), _p(v_cache), batch, n_heads, HEAD_DIM, k_cache.shape[2],
+        _p(prompt_mask), prompt_len, _p(kv_start), seq_pos, _p(seq_dev), _p(out),
+        _layout(tiled), _stream()), "mdl_attn_decode_f32")
 
 
 def attn_prefill_lead(qkv: torch.Tensor, rstd: torch.Tensor, pos: torch.Tensor,

@@ -30,7 +30,9 @@ def test_host_only_entry_points():
     """Entry points that do no device work answer without a GPU."""
     _require_lib()
     L = _lib.lib()
-    assert L.mdl_version() >= 100
+    # 200: the q_scale contract of the attention entries carries log2(e), the prefill
+    # attention entries take row_holes and out_layout, and the fp32 form's entries exist
+    assert L.mdl_version() == 200
     assert L.mdl_error_string(0) == b"ok"
     assert b"head_dim" in L.mdl_error_string(-4)
     # workspace sizing is host arithmetic: one split needs none, several need B*H*splits*66 fp32
@@ -67,7 +69,10 @@ def test_argument_errors_are_reported_before_any_launch():
                                     fake, None) == -3        # d % 8 != 0
     assert L.mdl_add_rmsnorm(fake, None, None, 1, 8, fake, 1e-5, fake, fake, 1, None) == -3
     assert L.mdl_qkv_rope_cache(fake, 192, None, fake, fake, 1, 4, 1, 64, 32, 32, 8, 10, 10, 12,
-                                0.125, fake, fake, fake, 4, 1, None, None) == -5
+                                0.125, fake, fake, fake, 1, 4, 1, None, None) == -5
+    # the cache dtype code is MDL_DTYPE_F32 (0) or MDL_DTYPE_BF16 (1)
+    assert L.mdl_qkv_rope_cache(fake, 192, None, fake, fake, 1, 4, 1, 64, 32, 32, 8, 10, 10, 12,
+                                0.125, fake, fake, fake, 2, 4, 0, None, None) == -7
     assert L.mdl_attn_decode(fake, fake, fake, 1, 1, 64, 1024, None, 0, None, None, None, 5,
                              None, None, 0, 128, fake, 0, None) == -6
     # the no-allocation decode refuses work beyond its 4 MiB static scratch before touching a
@@ -86,17 +91,23 @@ def test_argument_errors_are_reported_before_any_launch():
     assert L.mdl_gemm_split(None, 0, 1, fake, 0, 1, fake, 8, 4, 8, 32, 0, None) == -1
     assert L.mdl_tile_matrix(fake, 40, 4, 40, fake, None) == -3
     # fused K5 forms: n a multiple of 16 (32 for the residual form), d_ff of 16, x required
-    assert L.mdl_gemm_norm(fake, fake, 1e-5, fake, fake, 24, None, 4, 24, 32, 0, None) == -3
-    assert L.mdl_gemm_norm(None, fake, 1e-5, fake, fake, 32, None, 4, 32, 32, 0, None) == -1
-    assert L.mdl_gemm_norm_swiglu(fake, fake, 1e-5, fake, None, None, fake, 4, 24, 32, 0,
+    assert L.mdl_gemm_norm(fake, fake, 1e-5, fake, None, fake, 24, None, 4, 24, 32, 0,
+                           None) == -3
+    assert L.mdl_gemm_norm(None, fake, 1e-5, fake, None, fake, 32, None, 4, 32, 32, 0,
+                           None) == -1
+    # the low part of an fp32 weight is 16-byte aligned like the weight
+    assert L.mdl_gemm_norm(fake, fake, 1e-5, fake, fake + 8, fake, 32, None, 4, 32, 32, 0,
+                           None) == -2
+    assert L.mdl_gemm_norm_swiglu(fake, fake, 1e-5, fake, None, None, None, fake, 4, 24, 32, 0,
                                   None) == -3
     # d_ff above 2^29 is refused before 2 d_ff can overflow
-    assert L.mdl_gemm_norm_swiglu(fake, fake, 1e-5, fake, None, None, fake, 4, 1 << 30, 32, 0,
-                                  None) == -3
+    assert L.mdl_gemm_norm_swiglu(fake, fake, 1e-5, fake, None, None, None, fake, 4, 1 << 30,
+                                  32, 0, None) == -3
     assert L.mdl_gemm_split_swiglu(fake, fake, None, None, None, fake, 4, 1 << 30, 32, 0,
                                    None) == -3
-    assert L.mdl_gemm_split_residual(fake, fake, fake, None, 4, 48, 32, 0, None) == -3
-    assert L.mdl_gemm_split_residual(fake, fake, fake + 4, None, 4, 64, 32, 0, None) == -2
+    assert L.mdl_gemm_split_residual(fake, fake, None, fake, None, 4, 48, 32, 0, None) == -3
+    assert L.mdl_gemm_split_residual(fake, fake, None, fake + 4, None, 4, 64, 32, 0, None) == -2
+    assert L.mdl_gemm_split_residual(fake, fake, fake + 8, fake, None, 4, 64, 32, 0, None) == -2
     assert L.mdl_gemm_split_tiles() >= 1
     assert 1 <= L.mdl_gemm_split_pick(256, 2304, 768) <= L.mdl_gemm_split_tiles()
     # packed prefill: the per-row starts / offsets and the per-token rows / slots are required
@@ -105,9 +116,25 @@ def test_argument_errors_are_reported_before_any_launch():
     assert L.mdl_attn_prefill_packed(fake, fake, fake, 1, 4, 1, 32, 4, None, None, fake, fake, 1,
                                      fake, 1, None) == -4
     assert L.mdl_qkv_rope_cache_packed(fake, 192, None, fake, fake, 4, None, fake, 1, 1, 64, 32,
-                                       32, 8, 10, 10, 12, 0.125, fake, fake, fake, 4, None) == -1
+                                       32, 8, 10, 10, 12, 0.125, fake, fake, fake, 1, 4,
+                                       None) == -1
     assert L.mdl_qkv_rope_cache_packed(fake, 192, None, fake, fake, 4, fake, fake, 1, 1, 32, 32,
-                                       32, 8, 10, 10, 12, 0.125, fake, fake, fake, 4, None) == -4
+                                       32, 8, 10, 10, 12, 0.125, fake, fake, fake, 1, 4,
+                                       None) == -4
+    # K4f (fp32 attention): head_dim 64 only, q_offset needs kv_start, keys inside the cache,
+    # the decode slot inside the cache
+    assert L.mdl_attn_prefill_f32(fake, fake, fake, 1, 4, 1, 32, 4, None, None, None, 1, fake, 0,
+                                  None) == -4
+    assert L.mdl_attn_prefill_f32(fake, fake, fake, 1, 4, 1, 64, 4, None, None, fake, 1, fake, 0,
+                                  None) == -1
+    assert L.mdl_attn_prefill_f32(fake, fake, fake, 1, 8, 1, 64, 4, None, None, None, 1, fake, 0,
+                                  None) == -5
+    assert L.mdl_attn_prefill_f32(fake + 4, fake, fake, 1, 4, 1, 64, 4, None, None, None, 1, fake,
+                                  0, None) == -2
+    assert L.mdl_attn_decode_f32(fake, fake, fake, 1, 1, 64, 4, None, 0, None, 4, None, fake, 0,
+                                 None) == -5
+    assert L.mdl_attn_decode_f32(fake, fake, fake, 1, 1, 64, 4, None, 0, None, 0, None, fake, 2,
+                                 None) == -3
     # exact lead attention: q_offset needs kv_start; head_dim 64 only; qkv rows 16-byte aligned
     assert L.mdl_attn_prefill_lead(fake, 192, fake, fake, fake, 32, 32, 8, 10, 10, 12, 0.125, 1, 4,
                                    1, 64, None, None, fake, fake, 0, None) == -1
