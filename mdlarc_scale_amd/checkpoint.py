@@ -11,8 +11,9 @@ two differences:
   file is read with numpy's array and dtype reconstructors allow-listed for the restricted
   unpickler -- data constructors only, still ``weights_only=True``.  ``.safetensors`` files
   hold the state dict, with the model config as JSON in the ``model_config`` metadata entry.
-* On a GPU the packed bf16 GEMM operands ([W | W], gate and up concatenated) are built once at
-  load, so the first generation does not pay for them.
+* On a GPU the kernels' weight operands (bf16 tiles in the MFMA layout, with the low parts of
+  fp32 weights for an fp32 model) are built once at load, so the first generation does not pay
+  for them.
 """
 
 from __future__ import annotations

@@ -42,6 +42,23 @@ q/K/V operands of attention, and the logits land within about 1e-2.
 Weights are packed once per model version (bf16 [W | W] GEMM operands, fp32 gains / biases /
 head); the embedding tables are read live from the module parameters, because test-time
 adaptation edits ``example_embed.weight.data`` between calls.
+
+Two forms, chosen by the model's parameter dtype as the reference chooses its cache dtype
+(``next(model.parameters()).dtype``, src/inference.py:522):
+
+* bf16 form (a bf16 model: the reference's configurations 2-4): everything above.
+* fp32 form (a model with fp32 parameters: configuration 0).  The reference then keeps fp32
+  weights, an fp32 cache and fp32 attention, so this form does too: each weight W goes to the
+  K5 GEMMs as w = bf16(W) plus w_lo = bf16(W - w) (a third product a_hi . w_lo per k-step, W to
+  ~2^-17), q / K / V and the cache are fp32 (K2 with fp32 outputs) and the attention is K4f
+  (fp32 MFMA).  Per layer of a prompt or a decode step:
+
+    qkv, rstd = split(x * g1) @ (w + w_lo)^T                     <- K5 norm (E_STORE), fp32 out
+    q, K, V = K2(qkv) in fp32, K / V into the fp32 cache        <- qkv_rope_cache (fp32)
+    attn = K4f(q, cache)                                         <- attn_prefill_f32 / decode_f32
+    then the three K5 launches of the bf16 decode form, each with its w_lo.
+
+  The prompt's projections run on K5 too (K6 has no room in LDS for a second weight stage).
 """
 
 from __future__ import annotations
@@ -86,6 +103,25 @@ def prompt_gemms_fused(d_model: int, d_ff: int) -> bool:
     return tiles_supported(d_model, d_ff) and d_model <= K.PREFILL_NORM_MAX_K
 
 
+def model_form(model: TinyTransformer) -> str:
+    """"fp32" for a model whose parameters are fp32, "bf16" for a bf16 model: the dtype the
+    reference keeps its cache and attention in (``next(model.parameters()).dtype``,
+    src/inference.py:522, :544)."""
+    dt = next(model.parameters()).dtype
+    if dt == torch.float32:
+        return "fp32"
+    if dt == torch.bfloat16:
+        return "bf16"
+    raise TypeError(f"mdlarc_scale_amd runs float32 and bfloat16 models (got {dt})")
+
+
+def split_weight_lo(w: torch.Tensor) -> torch.Tensor:
+    """bf16(W - bf16(W)): the low part of an fp32 weight (exact in fp32; W = hi + lo to
+    ~2^-17 relative)."""
+    w = w.detach().float()
+    return (w - w.to(torch.bfloat16).float()).to(torch.bfloat16)
+
+
 def pack_split_weight(w: torch.Tensor, device: torch.device) -> torch.Tensor:
     """bf16 [W | W] ([N, 2K]) for a split-activation GEMM input (see gemm_f32)."""
     wb = w.detach().to(device=device, dtype=torch.bfloat16)
@@ -93,33 +129,58 @@ def pack_split_weight(w: torch.Tensor, device: torch.device) -> torch.Tensor:
 
 
 class PackedWeights:
-    """Device copies of the weights in the layout the kernels and GEMMs consume."""
+    """Device copies of the weights in the layout the kernels and GEMMs consume.  ``f32`` marks
+    the fp32 form: the tiled weights then come with their low parts (``*_lo``) and no [W | W]
+    copies are kept (the fp32 form runs every projection on K5)."""
 
     def __init__(self, model: TinyTransformer, device: torch.device):
         cfg = model.config
+        self.f32 = model_form(model) == "fp32"
         f32 = lambda t: t.detach().to(device=device, dtype=torch.float32).contiguous()  # noqa: E731
         pk = lambda t: pack_split_weight(t, device)  # noqa: E731
+        self.tiles_ok = tiles_supported(cfg.d_model, cfg.d_ff)
+        if self.f32 and not self.tiles_ok:
+            raise ValueError("the fp32 form runs its projections on K5, which needs d_model and "
+                             f"d_ff multiples of 32 (got {cfg.d_model}, {cfg.d_ff}); run the "
+                             "model in bfloat16 instead")
         self.qkv, self.out, self.gu, self.down = [], [], [], []
         self.ln1, self.ln2, self.b_gate, self.b_up, self.b_down = [], [], [], [], []
+        w_qkv, w_out, w_gu, w_down = [], [], [], []
         for blk in model.blocks:
-            self.qkv.append(pk(blk.attn.qkv_proj.weight))
-            self.out.append(pk(blk.attn.out_proj.weight))
-            self.gu.append(pk(torch.cat([blk.ffn.fc_gate.weight, blk.ffn.fc_up.weight], 0)))
-            self.down.append(pk(blk.ffn.fc_down.weight))
+            w_qkv.append(blk.attn.qkv_proj.weight)
+            w_out.append(blk.attn.out_proj.weight)
+            w_gu.append((blk.ffn.fc_gate.weight, blk.ffn.fc_up.weight))
+            w_down.append(blk.ffn.fc_down.weight)
+            if not self.f32:
+                self.qkv.append(pk(blk.attn.qkv_proj.weight))
+                self.out.append(pk(blk.attn.out_proj.weight))
+                self.gu.append(pk(torch.cat([blk.ffn.fc_gate.weight, blk.ffn.fc_up.weight], 0)))
+                self.down.append(pk(blk.ffn.fc_down.weight))
             self.ln1.append(f32(blk.ln1.weight))
             self.ln2.append(f32(blk.ln2.weight))
             self.b_gate.append(f32(blk.ffn.fc_gate.bias))
             self.b_up.append(f32(blk.ffn.fc_up.bias))
             self.b_down.append(f32(blk.ffn.fc_down.bias))
-        # decode (K5): each weight once, in the MFMA tile layout (the left half of [W | W])
-        self.tiles_ok = tiles_supported(cfg.d_model, cfg.d_ff)
-        tile = lambda w2: K.tile_matrix(w2, w2.shape[1] // 2)  # noqa: E731
-        self.qkv_t = [tile(w) for w in self.qkv] if self.tiles_ok else None
-        self.out_t = [tile(w) for w in self.out] if self.tiles_ok else None
-        # gate / up with 16-row blocks interleaved: the SwiGLU runs in that GEMM's epilogue
-        self.gu_t = [K.tile_matrix(K.interleave_gate_up(*w[:, :w.shape[1] // 2].chunk(2, 0)))
-                     for w in self.gu] if self.tiles_ok else None
-        self.down_t = [tile(w) for w in self.down] if self.tiles_ok else None
+        # K5 / K6: each weight once, in the MFMA tile layout; gate / up with their 16-row blocks
+        # interleaved (the SwiGLU runs in that GEMM's epilogue).  The fp32 form adds the tiled
+        # low parts.
+        n_l = len(model.blocks)
+        self.qkv_lo = self.out_lo = self.gu_lo = self.down_lo = [None] * n_l
+        self.qkv_t = self.out_t = self.gu_t = self.down_t = None
+        if self.tiles_ok:
+            hi = lambda w: w.detach().to(device=device, dtype=torch.bfloat16)  # noqa: E731
+            lo = lambda w: split_weight_lo(w.to(device))  # noqa: E731
+            tile = lambda w: K.tile_matrix(w.contiguous())  # noqa: E731
+            gu = lambda f, pair: K.interleave_gate_up(f(pair[0]), f(pair[1]))  # noqa: E731
+            self.qkv_t = [tile(hi(w)) for w in w_qkv]
+            self.out_t = [tile(hi(w)) for w in w_out]
+            self.gu_t = [K.tile_matrix(gu(hi, p)) for p in w_gu]
+            self.down_t = [tile(hi(w)) for w in w_down]
+            if self.f32:
+                self.qkv_lo = [tile(lo(w)) for w in w_qkv]
+                self.out_lo = [tile(lo(w)) for w in w_out]
+                self.gu_lo = [K.tile_matrix(gu(lo, p)) for p in w_gu]
+                self.down_lo = [tile(lo(w)) for w in w_down]
         self.ln_f = f32(model.ln_f.weight)
         self.head = f32(model.lm_head.weight)
         rope = model.blocks[0].attn.rope
@@ -147,23 +208,36 @@ class Scratch:
     rows: int = 0
     tiled: bool = False
     fused: bool = False
+    f32: bool = False
 
     @staticmethod
     def alloc(rows: int, d: int, d_ff: int, device: torch.device,
-              tiled: bool = False, fused: bool = False) -> "Scratch":
+              tiled: bool = False, fused: bool = False, f32: bool = False) -> "Scratch":
         """``tiled``: the decode form -- x in the fp32 tile layout and attn / h in the bf16 one
         (whole 16-row blocks); the RMSNorms run inside the K5 launches (``HipEngine._mlp``).
         ``fused``: the prompt form on K6 -- the same layouts; the RMSNorms run inside the K6
-        launches."""
+        launches.  ``f32``: the fp32 form (prompt or decode) -- the ``tiled`` layouts on K5,
+        q in fp32, qkv the fp32 projection output of every row."""
         e = lambda *s, dt=torch.bfloat16: torch.empty(*s, dtype=dt, device=device)  # noqa: E731
         f = torch.float32
+        tiled = tiled or f32
         split_gemm = not (tiled or fused)               # hipBLASLt path: xs, delta, gu
         sr = rows if split_gemm else K.tile_rows(rows)  # rows of the tiled activations
         return Scratch(x=e(sr, d, dt=f), xs=e(sr if split_gemm else 0, 2 * d),
-                       rstd=e(rows, dt=f), qkv=e(rows, 3 * d, dt=f), q=e(rows, d),
+                       rstd=e(rows, dt=f), qkv=e(rows, 3 * d, dt=f),
+                       q=e(rows, d, dt=f if f32 else torch.bfloat16),
                        attn=e(sr, 2 * d), delta=e(rows if split_gemm else 0, d, dt=f),
                        gu=e(rows if split_gemm else 0, 2 * d_ff, dt=f), h=e(sr, 2 * d_ff),
-                       rows=rows, tiled=tiled, fused=fused)
+                       rows=rows, tiled=tiled, fused=fused and not f32, f32=f32)
+
+    @staticmethod
+    def for_prompt(rows: int, cfg, device: torch.device, f32: bool) -> "Scratch":
+        """Scratch of a prompt pass: the fp32 form, or the bf16 form on K6 when the model's
+        shapes fit it (hipBLASLt otherwise)."""
+        if f32:
+            return Scratch.alloc(rows, cfg.d_model, cfg.d_ff, device, f32=True)
+        return Scratch.alloc(rows, cfg.d_model, cfg.d_ff, device,
+                             fused=prompt_gemms_fused(cfg.d_model, cfg.d_ff))
 
 
 @dataclass
@@ -298,13 +372,25 @@ class HipEngine:
         tok, ex = self._tables()
         use_ex = ex_ids if (ex_ids is not None and cfg.use_example_embedding) else None
         fused = sc.fused   # K6: ln1 runs in the qkv launch, so the embedding writes x only
+        nx = fused or sc.f32   # ln1 inside the projection: the embedding writes x only
         K.embed_rmsnorm(ids.reshape(-1), use_ex, tok, ex if use_ex is not None else None, S,
-                        W.ln1[0], W.eps, sc.x, None if fused else sc.xs,
-                        None if fused else sc.rstd, tiled=fused)
+                        W.ln1[0], W.eps, sc.x, None if nx else sc.xs,
+                        None if nx else sc.rstd, tiled=nx)
         qs = softmax_scale(d // H)          # the exact lead pass (K4c)
         qa = attention_q_scale(d // H)      # q for the attention kernels (log2-domain softmax)
         for li in range(cfg.n_layers):
             kc, vc = kv_layers(li)
+            if sc.f32:
+                # fp32 form: projection on K5 with the low weight part, K2 into the fp32 cache,
+                # K4f (the attention is exact, so no lead pass)
+                K.gemm_norm(sc.x, W.ln1[li], W.eps, W.qkv_t[li], sc.qkv, sc.rstd, d,
+                            w_lo=W.qkv_lo[li])
+                K.qkv_rope_cache(sc.qkv, sc.rstd, pos, W.rope_tab, W.rope_geom, B, S, H, qa,
+                                 sc.q, kc, vc, slot0=0)
+                K.attn_prefill_f32(sc.q, kc, vc, B, S, H, key_mask, kv_start, None, B * S,
+                                   causal, sc.attn, out_tiled=True)
+                self._mlp(W, li, sc)
+                continue
             if fused:   # ln1 + qkv_proj + K2 in one launch (fp32 qkv only for the lead rows)
                 K.prefill_gemm_norm_qkv(sc.x, W.ln1[li], W.eps, W.qkv_t[li], B * S, H, sc.rstd,
                                         sc.qkv, K.LEAD_QUERIES if causal else 0, kv_start, pos,
@@ -337,10 +423,11 @@ class HipEngine:
         pos_p = pos.reshape(-1, 3).index_select(0, pk.gather)
         ex_p = ex_ids.reshape(-1).index_select(0, pk.token_row) if use_ex else None
         fused = sc.fused
+        nx = fused or sc.f32   # ln1 inside the projection: the embedding writes x only
         K.embed_rmsnorm(ids_p, ex_p, tok, ex if use_ex else None, 1, W.ln1[0], W.eps, sc.x,
-                        None if fused else sc.xs, None if fused else sc.rstd, tiled=fused)
+                        None if nx else sc.xs, None if nx else sc.rstd, tiled=nx)
         if pk.n_tokens > pk.n_valid:   # padding queries: no visible key, attention output 0
-            if fused:
+            if nx:
                 zero_tiled_rows(sc.attn, pk.n_valid, pk.n_tokens, 2 * d)
             else:
                 sc.attn[pk.n_valid:pk.n_tokens].zero_()
@@ -348,6 +435,15 @@ class HipEngine:
         qa = attention_q_scale(d // H)      # q for the attention kernels (log2-domain softmax)
         for li in range(cfg.n_layers):
             kc, vc = kv_layers(li)
+            if sc.f32:   # fp32 form (see run_prompt)
+                K.gemm_norm(sc.x, W.ln1[li], W.eps, W.qkv_t[li], sc.qkv, sc.rstd, d,
+                            w_lo=W.qkv_lo[li])
+                K.qkv_rope_cache_packed(sc.qkv, sc.rstd, pos_p, W.rope_tab, W.rope_geom,
+                                        pk.token_row, pk.token_slot, H, qa, sc.q, kc, vc)
+                K.attn_prefill_f32(sc.q, kc, vc, B, S, H, key_mask, kv_start, pk.q_offset,
+                                   pk.n_tokens, True, sc.attn, out_tiled=True)
+                self._mlp(W, li, sc)
+                continue
             if fused:
                 K.prefill_gemm_norm_qkv(sc.x, W.ln1[li], W.eps, W.qkv_t[li], pk.n_tokens, H,
                                         sc.rstd, sc.qkv, K.LEAD_QUERIES, kv_start, pos_p,
@@ -384,10 +480,13 @@ class HipEngine:
             # decode: three K5 launches, the residual adds in the epilogues and ln2 in the
             # gate / up prologue; the next layer's ln1 runs in its qkv launch (gemm_norm) and
             # ln_f in the head kernel
-            K.gemm_split_residual(sc.attn, W.out_t[li], sc.x, None, sc.rows, d, d)
+            # (the fp32 form adds each weight's low part)
+            K.gemm_split_residual(sc.attn, W.out_t[li], sc.x, None, sc.rows, d, d,
+                                  w_lo=W.out_lo[li])
             K.gemm_norm_swiglu(sc.x, W.ln2[li], W.eps, W.gu_t[li], W.b_gate[li], W.b_up[li],
-                               sc.h, sc.rows, F, d)
-            K.gemm_split_residual(sc.h, W.down_t[li], sc.x, W.b_down[li], sc.rows, d, F)
+                               sc.h, sc.rows, F, d, w_gu_lo=W.gu_lo[li])
+            K.gemm_split_residual(sc.h, W.down_t[li], sc.x, W.b_down[li], sc.rows, d, F,
+                                  w_lo=W.down_lo[li])
             return
         gemm_f32(sc.attn, W.out[li], sc.delta)
         K.add_rmsnorm(sc.x, sc.delta, None, W.ln2[li], W.eps, sc.xs, sc.rstd)
@@ -397,6 +496,19 @@ class HipEngine:
         last = li + 1 == cfg.n_layers
         K.add_rmsnorm(sc.x, sc.delta, W.b_down[li], W.ln_f if last else W.ln1[li + 1], W.eps,
                       None if last else sc.xs, sc.rstd)
+
+    @staticmethod
+    def key_mask_and_start(attention_mask: torch.Tensor | None, dev: torch.device, S: int):
+        """The [B, S] key mask as uint8 and each row's first valid position (S when it has
+        none): the attention skips the keys before it and the lead-query pass starts there.
+        (None, None) without a mask."""
+        if attention_mask is None:
+            return None, None
+        mask = attention_mask.to(device=dev, dtype=torch.bool).to(torch.uint8).contiguous()
+        first = mask.to(torch.int32).argmax(1)
+        kv_start = torch.where(mask.bool().any(1), first, torch.full_like(first, S)).to(
+            torch.int32).contiguous()
+        return mask, kv_start
 
     @torch.no_grad()
     def forward(self, ids: torch.Tensor, pos: torch.Tensor, ex_ids: torch.Tensor | None,
@@ -416,23 +528,17 @@ class HipEngine:
             ex_ids = ex_ids.to(device=dev, dtype=torch.int64).contiguous()
         self._validate_ids(ids, ex_ids)
         W = self.packed(dev)
-        mask, kv_start = None, None
-        if attention_mask is not None:
-            mask = attention_mask.to(device=dev, dtype=torch.bool).to(torch.uint8).contiguous()
-            # each row's first valid position: the attention skips the keys before it and the
-            # lead-query pass starts there
-            first = mask.to(torch.int32).argmax(1)
-            kv_start = torch.where(mask.bool().any(1), first, torch.full_like(first, S)).to(
-                torch.int32).contiguous()
+        mask, kv_start = self.key_mask_and_start(attention_mask, dev, S)
         H = cfg.n_heads
-        kbuf = torch.empty(B, H, S, 64, dtype=torch.bfloat16, device=dev)
+        kbuf = torch.empty(B, H, S, 64, dtype=torch.float32 if W.f32 else torch.bfloat16,
+                           device=dev)
         vbuf = torch.empty_like(kbuf)
-        sc = Scratch.alloc(B * S, cfg.d_model, cfg.d_ff, dev,
-                           fused=prompt_gemms_fused(cfg.d_model, cfg.d_ff))
+        sc = Scratch.for_prompt(B * S, cfg, dev, W.f32)
         self.run_prompt(W, ids, pos, ex_ids, mask, kv_start, is_causal, lambda li: (kbuf, vbuf),
                         sc)
         logits = torch.empty(B * S, cfg.vocab_size, dtype=torch.float32, device=dev)
-        K.lm_head(sc.x, None, B * S, W.ln_f, W.eps, W.head, logits, None, x_tiled=sc.fused)
+        K.lm_head(sc.x, None, B * S, W.ln_f, W.eps, W.head, logits, None, x_tiled=sc.tiled or
+                  sc.fused)
         return logits.view(B, S, cfg.vocab_size)
 
 

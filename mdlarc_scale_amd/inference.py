@@ -38,7 +38,7 @@ from .data import (
 )
 from .engine import GRID_MAX_X, GRID_MAX_Y, HipEngine, PackedWeights, Scratch, choose_split_len
 from .engine import pack_prompt
-from .engine import engine_for, gemm_f32, prompt_gemms_fused, tiles_supported
+from .engine import engine_for, gemm_f32, model_form, tiles_supported
 from .transformer import TinyTransformer, attention_q_scale
 
 SYNC_EVERY = 8
@@ -144,8 +144,9 @@ def _pick(logits: torch.Tensor, temperature: float, top_k: int | None) -> torch.
 # =============================================================================================
 
 class StaticKVCache:
-    """Preallocated [n_layers, 2, B, H, max_seq_len, head_dim] cache (src/inference.py:51-96).
-    The HIP path keeps it in bf16 (the attention kernels' operand type)."""
+    """Preallocated [n_layers, 2, B, H, max_seq_len, head_dim] cache (src/inference.py:51-96) in
+    the model's parameter dtype, as the reference allocates it (src/inference.py:522, :544):
+    bf16 for a bf16 model, fp32 for an fp32 model (the fp32 form's attention reads it in fp32)."""
 
     def __init__(self, batch_size: int, max_seq_len: int, n_layers: int, n_heads: int,
                  head_dim: int, device: torch.device, dtype: torch.dtype = torch.bfloat16, *,
@@ -283,7 +284,9 @@ class Generator:
         dev = input_ids.device
         B, S = input_ids.shape
         H, hd = cfg.n_heads, cfg.d_model // cfg.n_heads
-        cache = StaticKVCache(B, total, cfg.n_layers, H, hd, dev, zero=False)
+        f32 = model_form(self.model) == "fp32"
+        cache = StaticKVCache(B, total, cfg.n_layers, H, hd, dev,
+                              dtype=torch.float32 if f32 else torch.bfloat16, zero=False)
         pmask = prompt_mask.to(torch.uint8).contiguous()
         i32 = lambda: torch.empty(B, dtype=torch.int32, device=dev)  # noqa: E731
         gx, gy, kv_start, last_row = i32(), i32(), i32(), i32()
@@ -307,7 +310,7 @@ class Generator:
             out_ids=out_ids, finish=torch.full((B,), -1, dtype=torch.int32, device=dev),
             logits=torch.empty(B, cfg.vocab_size, dtype=torch.float32, device=dev),
             cache=cache, ws=ws,
-            sc=Scratch.alloc(B, cfg.d_model, cfg.d_ff, dev,
+            sc=Scratch.alloc(B, cfg.d_model, cfg.d_ff, dev, f32=f32,
                              tiled=DECODE_TILED and tiles_supported(cfg.d_model, cfg.d_ff)),
             split_len=split)
 
@@ -322,19 +325,17 @@ class Generator:
             # one small device->host read of the row starts; the padding then costs nothing
             starts = torch.stack([st.kv_start, st.last_row]).cpu().numpy()
             pk = pack_prompt(starts[0], starts[1], st.B, st.S, dev)
-            sc = Scratch.alloc(pk.n_tokens, cfg.d_model, cfg.d_ff, dev,
-                               fused=prompt_gemms_fused(cfg.d_model, cfg.d_ff))
+            sc = Scratch.for_prompt(pk.n_tokens, cfg, dev, W.f32)
             self.eng.run_packed(W, input_ids, positions_3d, st.ex, st.pmask, st.kv_start, pk,
                                 st.cache.layer, sc, row_holes=st.holes)
             head_row = pk.head_row
         else:
-            sc = Scratch.alloc(st.B * st.S, cfg.d_model, cfg.d_ff, dev,
-                               fused=prompt_gemms_fused(cfg.d_model, cfg.d_ff))
+            sc = Scratch.for_prompt(st.B * st.S, cfg, dev, W.f32)
             self.eng.run_prompt(W, input_ids, positions_3d, st.ex, st.pmask, st.kv_start, True,
                                 st.cache.layer, sc, row_holes=st.holes)
             head_row = st.last_row
         K.lm_head(sc.x, head_row, st.B, W.ln_f, W.eps, W.head, st.logits, st.tok, cons,
-                  x_tiled=sc.fused)
+                  x_tiled=sc.fused or sc.tiled)
         st.cache.seq_len = st.S
 
     def _embed_inputs(self, st: DecodeState):
@@ -353,7 +354,16 @@ class Generator:
         slot = st.counters[0:1]
         for li in range(cfg.n_layers):
             kc, vc = st.cache.layer(li)
-            if sc.tiled:
+            if sc.f32:
+                # fp32 form: projection with the low weight part, K2 of the token into slot t
+                # of the fp32 cache, K4f over slots [kv_start, t]
+                K.gemm_norm(sc.x, W.ln1[li], W.eps, W.qkv_t[li], sc.qkv, sc.rstd, cfg.d_model,
+                            w_lo=W.qkv_lo[li])
+                K.qkv_rope_cache(sc.qkv, sc.rstd, st.pos, W.rope_tab, W.rope_geom, B, 1, H, qs,
+                                 sc.q, kc, vc, slot_dev=slot)
+                K.attn_decode_f32(sc.q, kc, vc, B, H, st.pmask, st.S, st.kv_start, 0, slot,
+                                  sc.attn, tiled=True)
+            elif sc.tiled:
                 # ln1 in the projection's prologue, K2 (RoPE, q scale, K/V into slot t) in its
                 # epilogue; the attention reads q and the cache
                 K.gemm_norm_qkv(sc.x, W.ln1[li], W.eps, W.qkv_t[li], B, H, None, st.pos,
@@ -674,10 +684,25 @@ def predict_with_augmentations(model: TinyTransformer, task: dict, test_idx: int
     ONE batch with those semantics kept per row (``_predict_fused``); sampling, whose random
     draws depend on the batch, keeps the chunk loop, as does ``fuse_chunks=False``."""
     del use_compile
-    model.eval()
     num_samples = max(1, num_samples)
     base_palette = _collect_palette(task, test_idx) if constrain_decoding else None
     base_shape = _infer_output_shape(task) if constrain_decoding else None
+    return _predict_augmentations(model, task, test_idx, device, example_id, use_train_examples,
+                                  num_color_perms, max_output_tokens, num_samples,
+                                  sample_temperature, sample_top_k, constrain_decoding,
+                                  base_palette, base_shape, palette_penalty, shape_penalty,
+                                  batched, max_batch_size, fuse_chunks)
+
+
+def _predict_augmentations(model, task, test_idx, device, example_id, use_train_examples,
+                           num_color_perms, max_output_tokens, num_samples, sample_temperature,
+                           sample_top_k, constrain_decoding, base_palette, base_shape,
+                           palette_penalty, shape_penalty, batched, max_batch_size,
+                           fuse_chunks=True):
+    """The body of predict_with_augmentations after its palette / shape inference: the
+    reference's batched (chunks of ``max_batch_size``) or sequential loop."""
+    model.eval()
+    num_samples = max(1, num_samples)
     chunk = max_batch_size if batched else 1
     fused = fuse_chunks and sample_temperature <= 0 and 8 * num_color_perms * num_samples > 1
     grids = (_task_grids(task, test_idx, use_train_examples)
@@ -808,3 +833,157 @@ def _chunk_constraints(part: list[_Variant], device, palette_penalty, shape_pena
             shp[i] = torch.tensor(v.shape)
     return DecodingConstraints(palette_mask=pal, target_shape=shp.to(device) if any_shape else None,
                                palette_penalty=palette_penalty, shape_penalty=shape_penalty)
+
+
+# =============================================================================================
+# the reference's module-level helpers, for code that calls or patches them
+# (src/inference.py:285-479, :763-1003); the generation path itself does not go through them
+# =============================================================================================
+
+def _apply_logit_constraints(logits: torch.Tensor, grid_state,
+                             constraints: DecodingConstraints | None) -> torch.Tensor:
+    """src/inference.py:285-364 with the reference's arguments: logits [B, V] or [B, 1, V],
+    changed in place and returned; ``grid_state`` is the state after the current token (any
+    object with the ``x`` / ``y`` tensors of GridStateUpdater)."""
+    if constraints is None:
+        return logits
+    apply_logit_constraints(logits.view(-1, logits.shape[-1]), grid_state.x, grid_state.y,
+                            constraints)
+    return logits
+
+
+def _build_sdpa_mask(attention_mask: torch.Tensor | None, dtype: torch.dtype):
+    """src/inference.py:372-380: a [B, S] bool mask as the additive [B, 1, 1, S] SDPA mask
+    (0 where True, -inf where False) in ``dtype``; None stays None."""
+    if attention_mask is None:
+        return None
+    keep = attention_mask.bool()[:, None, None, :]
+    return torch.zeros(keep.shape, dtype=dtype, device=keep.device).masked_fill(~keep,
+                                                                                float("-inf"))
+
+
+def _prefill(model: TinyTransformer, input_ids: torch.Tensor, positions_3d: torch.Tensor,
+             example_ids: torch.Tensor | None, cache: StaticKVCache,
+             attention_mask: torch.Tensor | None = None) -> torch.Tensor:
+    """src/inference.py:383-424 on the HIP kernels: every layer over the [B, S] prompt, K / V
+    into slots [0, S) of ``cache`` (a StaticKVCache of this module, in the model's dtype, not yet
+    advanced), then cache.advance(S).  Returns the logits [B, 1, V] (model dtype) of row
+    lengths-1 of each row -- the reference's index on left-padded batches -- or of the last
+    column without a mask."""
+    eng = engine_for(model)
+    dev = eng._check_device(input_ids)
+    cfg = model.config
+    B, S = input_ids.shape
+    if cache.seq_len != 0:
+        raise ValueError("_prefill writes cache slots [0, S): pass a cache that is not advanced")
+    ids = input_ids.to(torch.int64).contiguous()
+    pos = positions_3d.to(device=dev, dtype=torch.int64).contiguous()
+    ex = None if example_ids is None else example_ids.to(device=dev,
+                                                          dtype=torch.int64).contiguous()
+    eng._validate_ids(ids, ex)
+    with torch.no_grad():
+        W = eng.packed(dev)
+        want = torch.float32 if W.f32 else torch.bfloat16
+        if cache.cache.dtype != want:
+            raise TypeError(f"the cache must be {want} for this model (got {cache.cache.dtype})")
+        mask, kv_start = eng.key_mask_and_start(attention_mask, dev, S)
+        sc = Scratch.for_prompt(B * S, cfg, dev, W.f32)
+        eng.run_prompt(W, ids, pos, ex, mask, kv_start, True, cache.layer, sc)
+        if attention_mask is None:
+            last = torch.full((B,), S - 1, dtype=torch.int64, device=dev)
+        else:
+            last = (attention_mask.to(dev).long().sum(1) - 1).clamp(min=0)
+        rows = (torch.arange(B, device=dev) * S + last).to(torch.int32)
+        logits = torch.empty(B, cfg.vocab_size, dtype=torch.float32, device=dev)
+        K.lm_head(sc.x, rows, B, W.ln_f, W.eps, W.head, logits, None,
+                  x_tiled=sc.fused or sc.tiled)
+    cache.advance(S)
+    return logits.to(model.lm_head.weight.dtype)[:, None]
+
+
+def _decode_step(model: TinyTransformer, token: torch.Tensor, position: torch.Tensor,
+                 example_ids: torch.Tensor | None, cache: StaticKVCache,
+                 attention_mask: torch.Tensor | None = None) -> torch.Tensor:
+    """src/inference.py:427-459 on the HIP kernels, host-launched: the token [B, 1] at position
+    [B, 1, 3] through every layer, its K / V into slot cache.seq_len, attention over slots
+    [0, seq_len] where ``attention_mask`` ([B, >= seq_len + 1] bool, may be None) allows, then
+    cache.advance(1).  Returns the logits [B, 1, V] (model dtype)."""
+    eng = engine_for(model)
+    dev = eng._check_device(token)
+    cfg = model.config
+    B = token.shape[0]
+    H = cfg.n_heads
+    t = cache.seq_len
+    if not 0 <= t < cache.max_seq_len:
+        raise ValueError("the cache is full")
+    tok = token.reshape(B).to(device=dev, dtype=torch.int64).contiguous()
+    ex = (torch.zeros(B, dtype=torch.int64, device=dev) if example_ids is None
+          else example_ids.to(device=dev, dtype=torch.int64).contiguous())
+    eng._validate_ids(tok, ex)
+    gen = Generator(model)
+    f32 = model_form(model) == "fp32"
+    with torch.no_grad():
+        W = eng.packed(dev)
+        want = torch.float32 if W.f32 else torch.bfloat16
+        if cache.cache.dtype != want:
+            raise TypeError(f"the cache must be {want} for this model (got {cache.cache.dtype})")
+        pmask = None
+        if attention_mask is not None:
+            pmask = attention_mask[:, :t + 1].to(device=dev, dtype=torch.uint8).contiguous()
+        slots = cache.max_seq_len
+        split = choose_split_len(B * H, slots)
+        nbytes = K.attn_decode_workspace_bytes(B, H, slots, split)
+        i32 = lambda: torch.zeros(B, dtype=torch.int32, device=dev)  # noqa: E731
+        st = DecodeState(
+            B=B, S=0 if pmask is None else pmask.shape[1], total=slots, ex=ex, pmask=pmask,
+            kv_start=None, last_row=i32(), holes=None, order=None, gx=i32(), gy=i32(),
+            gio=torch.zeros(B, dtype=torch.uint8, device=dev),
+            pos=position.reshape(B, 3).to(device=dev, dtype=torch.int64).contiguous(), tok=tok,
+            counters=torch.tensor([t, 0], dtype=torch.int32, device=dev),
+            out_ids=torch.empty(B, 0, dtype=torch.int64, device=dev),
+            finish=i32(), logits=torch.empty(B, cfg.vocab_size, dtype=torch.float32, device=dev),
+            cache=cache,
+            ws=(torch.empty(max(nbytes // 4, 1), dtype=torch.float32, device=dev)
+                if nbytes else None),
+            sc=Scratch.alloc(B, cfg.d_model, cfg.d_ff, dev, f32=f32,
+                             tiled=DECODE_TILED and tiles_supported(cfg.d_model, cfg.d_ff)),
+            split_len=split)
+        gen.decode_layers(st, W, want_logits=True)
+    cache.advance(1)
+    return st.logits.to(model.lm_head.weight.dtype)[:, None]
+
+
+def _get_decode_fn(use_compile: bool):
+    """src/inference.py:462-479: the decode-step function.  There is no compiler on this path,
+    so ``use_compile`` selects nothing; generate_output replays a captured HIP graph of its own
+    step instead."""
+    del use_compile
+    return _decode_step
+
+
+def _predict_augmentations_batched(model, task, test_idx, device, example_id,
+                                   use_train_examples, num_color_perms, max_output_tokens,
+                                   num_samples, sample_temperature, sample_top_k,
+                                   constrain_decoding, base_palette, base_shape, palette_penalty,
+                                   shape_penalty, use_compile, max_batch_size: int = 16):
+    """src/inference.py:763-920: the augmentations in left-padded chunks of max_batch_size."""
+    del use_compile
+    return _predict_augmentations(model, task, test_idx, device, example_id, use_train_examples,
+                                  num_color_perms, max_output_tokens, num_samples,
+                                  sample_temperature, sample_top_k, constrain_decoding,
+                                  base_palette, base_shape, palette_penalty, shape_penalty, True,
+                                  max_batch_size)
+
+
+def _predict_augmentations_sequential(model, task, test_idx, device, example_id,
+                                      use_train_examples, num_color_perms, max_output_tokens,
+                                      num_samples, sample_temperature, sample_top_k,
+                                      constrain_decoding, base_palette, base_shape,
+                                      palette_penalty, shape_penalty, use_compile):
+    """src/inference.py:923-1003: one augmentation at a time (no padding, no mask)."""
+    del use_compile
+    return _predict_augmentations(model, task, test_idx, device, example_id, use_train_examples,
+                                  num_color_perms, max_output_tokens, num_samples,
+                                  sample_temperature, sample_top_k, constrain_decoding,
+                                  base_palette, base_shape, palette_penalty, shape_penalty, False,
+                                  1)

@@ -1071,7 +1071,7 @@ def test_capi_rejects_bad_arguments_before_launch():
     # cache overflow: slot0 + seq > slots
     assert L.mdl_qkv_rope_cache(x.data_ptr(), 192, None, x.data_ptr(), x.data_ptr(), 1, 4, 1, 64,
                                 32, 32, 8, 10, 10, 12, 0.125, x.data_ptr(), x.data_ptr(),
-                                x.data_ptr(), 4, 1, None, None) == -5
+                                x.data_ptr(), 1, 4, 1, None, None) == -5
     # misaligned pointer
     assert L.mdl_swiglu(x.data_ptr() + 2, 16, None, None, None, 1, 8, x.data_ptr(), 0,
                         None) == -2

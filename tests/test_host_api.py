@@ -164,3 +164,73 @@ def test_workload_specs_meet_their_ranges():
         assert max(lens) + 1 < spec.cache_slots
         # positions of every prompt follow the token format
         assert np.array_equal(M.compute_positions_3d(p[0]), odf.compute_positions_3d(p[0]))
+
+
+def test_reference_private_names_exist_with_their_signatures():
+    """The module-level helpers of src/inference.py that code may call or patch
+    (:285, :372, :383, :427, :466, :763, :923) exist with the reference's parameters."""
+    want = {
+        "_apply_logit_constraints": ["logits", "grid_state", "constraints"],
+        "_build_sdpa_mask": ["attention_mask", "dtype"],
+        "_prefill": ["model", "input_ids", "positions_3d", "example_ids", "cache",
+                     "attention_mask"],
+        "_decode_step": ["model", "token", "position", "example_ids", "cache",
+                         "attention_mask"],
+        "_get_decode_fn": ["use_compile"],
+        "_predict_augmentations_batched": [
+            "model", "task", "test_idx", "device", "example_id", "use_train_examples",
+            "num_color_perms", "max_output_tokens", "num_samples", "sample_temperature",
+            "sample_top_k", "constrain_decoding", "base_palette", "base_shape",
+            "palette_penalty", "shape_penalty", "use_compile", "max_batch_size"],
+        "_predict_augmentations_sequential": [
+            "model", "task", "test_idx", "device", "example_id", "use_train_examples",
+            "num_color_perms", "max_output_tokens", "num_samples", "sample_temperature",
+            "sample_top_k", "constrain_decoding", "base_palette", "base_shape",
+            "palette_penalty", "shape_penalty", "use_compile"],
+    }
+    for name, params in want.items():
+        assert list(inspect.signature(getattr(inference, name)).parameters) == params, name
+    assert inference._get_decode_fn(True) is inference._decode_step
+    assert inference._get_decode_fn(False) is inference._decode_step
+
+
+def test_build_sdpa_mask_closed_form():
+    """src/inference.py:372-380: [B, S] bool -> [B, 1, 1, S], 0 where True, -inf where False."""
+    m = torch.tensor([[True, False, True], [False, False, True]])
+    got = inference._build_sdpa_mask(m, torch.bfloat16)
+    assert got.shape == (2, 1, 1, 3) and got.dtype == torch.bfloat16
+    want = torch.tensor([[0.0, float("-inf"), 0.0], [float("-inf"), float("-inf"), 0.0]])
+    assert torch.equal(got[:, 0, 0].float(), want)
+    assert inference._build_sdpa_mask(None, torch.float32) is None
+
+
+def test_apply_logit_constraints_alias_matches_the_product_rule():
+    """_apply_logit_constraints(logits, grid_state, constraints) on [B, 1, V] logits equals
+    apply_logit_constraints on the [B, V] rows with the state's x / y, in place."""
+    g = torch.Generator().manual_seed(4)
+    B = 5
+    logits = torch.randn(B, 1, 14, generator=g)
+    gx = torch.randint(0, 6, (B,), generator=g)
+    gy = torch.randint(0, 6, (B,), generator=g)
+    cons = inference.DecodingConstraints(
+        palette_mask=torch.rand(B, 10, generator=g) < 0.5,
+        target_shape=torch.randint(1, 5, (B, 2), generator=g))
+    state = types.SimpleNamespace(x=gx, y=gy)
+    want = inference.apply_logit_constraints(logits[:, 0].clone(), gx, gy, cons)
+    got = inference._apply_logit_constraints(logits, state, cons)
+    assert got is logits and torch.equal(got[:, 0], want)
+    assert inference._apply_logit_constraints(logits, state, None) is logits
+
+
+def test_fp32_form_requires_k5_widths():
+    """A model with fp32 parameters runs the fp32 form, whose projections all run on K5: a
+    width that is not a multiple of 32 is refused with a clear error before any device work."""
+    from mdlarc_scale_amd.engine import PackedWeights, model_form
+
+    m = M.create_model(d_model=128, n_heads=2, n_layers=1, d_ff=200)
+    assert model_form(m) == "fp32" and model_form(m.to(torch.bfloat16)) == "bf16"
+    with pytest.raises(ValueError, match="multiples of 32"):
+        PackedWeights(M.create_model(d_model=128, n_heads=2, n_layers=1, d_ff=200),
+                      torch.device("cpu"))
+    with pytest.raises(TypeError, match="float32 and bfloat16"):
+        model_form(M.create_model(d_model=128, n_heads=2, n_layers=1, d_ff=64).half())
