@@ -600,10 +600,13 @@ def measure_workload(spec, steps, warmup, dev, eager=False, snapshot=False):
 
 def prefill_projections_timing(K, W, cfg, pk, st, dev):
     """Milliseconds per launch of each K6 form of one prefill layer (median of 5 rounds of 5
-    back-to-back launches after 2 warm ones) and its executed MFMA flops (4·M·N·K: the hi and lo
-    products)."""
+    back-to-back launches after 2 warm ones) and its executed MFMA flops (2·parts·M·N·K: the hi
+    and lo products of a split activation, the hi product alone for the MLP's single-part
+    inputs), as the prompt path calls them."""
     import torch
 
+    from mdlarc_scale_amd.engine import PROMPT_DOWN_PARTS as dp
+    from mdlarc_scale_amd.engine import PROMPT_GATE_UP_PARTS as gp
     from mdlarc_scale_amd.engine import Scratch
 
     m, d, F, H = pk.n_tokens, cfg.d_model, cfg.d_ff, cfg.n_heads
@@ -623,10 +626,11 @@ def prefill_projections_timing(K, W, cfg, pk, st, dev):
             token_row=pk.token_row, token_slot=pk.token_slot)),
         "out_residual": (4 * m * d * d, lambda: K.prefill_gemm_split_residual(
             sc.attn, W.out_t[0], sc.x, None, m, d, d, a_tiled=True)),
-        "gate_up_swiglu": (4 * m * 2 * F * d, lambda: K.prefill_gemm_norm_swiglu(
-            sc.x, W.ln2[0], W.eps, W.gu_t[0], W.b_gate[0], W.b_up[0], sc.h, m, F, d)),
-        "down_residual": (4 * m * d * F, lambda: K.prefill_gemm_split_residual(
-            sc.h, W.down_t[0], sc.x, W.b_down[0], m, d, F, a_tiled=True)),
+        "gate_up_swiglu": (2 * gp * m * 2 * F * d, lambda: K.prefill_gemm_norm_swiglu(
+            sc.x, W.ln2[0], W.eps, W.gu_t[0], W.b_gate[0], W.b_up[0], sc.h, m, F, d,
+            a_parts=gp, h_parts=dp)),
+        "down_residual": (2 * dp * m * d * F, lambda: K.prefill_gemm_split_residual(
+            sc.h, W.down_t[0], sc.x, W.b_down[0], m, d, F, a_tiled=True, a_parts=dp)),
     }
     out = {}
     for name, (flops, fn) in forms.items():
@@ -660,8 +664,9 @@ def prefill_projections_of(r):
         "frac": round(fl / ms / 1e9 / BF16_PEAK_TFLOPS, 4),
         "forms": {k: {"ms": round(v[0], 4), "tflop_s": round(v[1] / v[0] / 1e9, 1)}
                   for k, v in proj.items()},
-        "flops": "executed bf16 MFMA flops, 4·M·N·K per projection (the hi and lo products of "
-                 "the split activations; the useful flops are half)",
+        "flops": "executed bf16 MFMA flops, 2·parts·M·N·K per projection: the hi and lo "
+                 "products of a split input (half of them useful), the hi product alone for a "
+                 "single-part MLP input (engine.PROMPT_GATE_UP_PARTS / PROMPT_DOWN_PARTS)",
     }
 
 

@@ -342,30 +342,39 @@ int mdl_gemm_split_pick(int m, int n, int k);
  *           :562-599, _prefill src/inference.py:383-424), with the RMSNorms (:45-48) and the
  *           residual adds (TransformerBlock.forward :486-497) fused in.
  *
+ * a_parts (the split forms and the SwiGLU form): 2 -- the activation is split, hi and lo, as
+ * everywhere else; 1 -- the lo term is dropped: a holds hi alone ([m, k]; row stride lda >= k
+ * when row-major), and the norm form uses bf16(x * gamma).  Half the MFMA work; the products
+ * then carry the activation's bf16 rounding (2^-9 relative) instead of ~2^-17.
+ *
  * mdl_prefill_gemm_split:   out[i, j] = sum_k (a_hi + a_lo)[i, k] w[j, k] (fp32, row stride
- *                           ldo); a split [m, 2k] in a_layout (row stride lda when row-major).
+ *                           ldo); a split [m, a_parts k] in a_layout (row stride lda when
+ *                           row-major).
  * mdl_prefill_gemm_norm:    out = split(x * gamma) . w^T and rstd_out[i] (may be NULL) =
  *                           1 / sqrt(mean_k x[i, k]^2 + eps), x the fp32 residual stream [m, k]
  *                           in MDL_LAYOUT_TILES: the ln1 + qkv_proj pair with rstd deferred to
  *                           the consumer (as mdl_gemm_norm); k at most 2048.
  * mdl_prefill_gemm_norm_swiglu: h = split(silu(rstd g + bias_gate) * (rstd u + bias_up)), g / u
  *                           the gate / up rows of w_gu against split(x * gamma) (x as above);
- *                           h_out tiled split [m, 2 d_ff] (ceil(m / 16) * 16 rows); biases may
- *                           be NULL.
+ *                           h_out tiled [m, h_parts d_ff] (ceil(m / 16) * 16 rows): hi, then lo
+ *                           when h_parts is 2 (h_parts 1 feeds a consumer with a_parts 1);
+ *                           biases may be NULL.
  * mdl_prefill_gemm_split_residual: x[i, j] += sum_k (a_hi + a_lo)[i, k] w[j, k] (+ bias[j]) in
  *                           place, x the fp32 residual stream [m, n] in MDL_LAYOUT_TILES (n a
  *                           multiple of 32); bias may be NULL.
+ * a_parts or h_parts other than 1 or 2: MDL_ERR_SHAPE.
  */
-int mdl_prefill_gemm_split(const uint16_t* a, int64_t lda, int a_layout, const uint16_t* w,
-                           float* out, int64_t ldo, int m, int n, int k, void* stream);
+int mdl_prefill_gemm_split(const uint16_t* a, int64_t lda, int a_layout, int a_parts,
+                           const uint16_t* w, float* out, int64_t ldo, int m, int n, int k,
+                           void* stream);
 int mdl_prefill_gemm_norm(const float* x, const float* gamma, float eps, const uint16_t* w,
                           float* out, int64_t ldo, float* rstd_out, int m, int n, int k,
                           void* stream);
-int mdl_prefill_gemm_norm_swiglu(const float* x, const float* gamma, float eps,
+int mdl_prefill_gemm_norm_swiglu(const float* x, const float* gamma, float eps, int a_parts,
                                  const uint16_t* w_gu, const float* bias_gate,
-                                 const float* bias_up, uint16_t* h_out, int m, int d_ff, int k,
-                                 void* stream);
-int mdl_prefill_gemm_split_residual(const uint16_t* a, int64_t lda, int a_layout,
+                                 const float* bias_up, uint16_t* h_out, int h_parts, int m,
+                                 int d_ff, int k, void* stream);
+int mdl_prefill_gemm_split_residual(const uint16_t* a, int64_t lda, int a_layout, int a_parts,
                                     const uint16_t* w, float* x, const float* bias, int m, int n,
                                     int k, void* stream);
 /*

@@ -65,12 +65,13 @@ SIGNATURES: dict[str, tuple[object, list]] = {
     "mdl_gemm_split_residual": (c_int, [P, P, P, P, P, c_int, c_int, c_int, c_int, P]),
     "mdl_gemm_split_tiles": (c_int, []),
     "mdl_gemm_split_pick": (c_int, [c_int, c_int, c_int]),
-    "mdl_prefill_gemm_split": (c_int, [P, c_int64, c_int, P, P, c_int64, c_int, c_int, c_int, P]),
+    "mdl_prefill_gemm_split": (c_int, [P, c_int64, c_int, c_int, P, P, c_int64, c_int, c_int,
+                                       c_int, P]),
     "mdl_prefill_gemm_norm": (c_int, [P, P, c_float, P, P, c_int64, P, c_int, c_int, c_int, P]),
-    "mdl_prefill_gemm_norm_swiglu": (c_int, [P, P, c_float, P, P, P, P, c_int, c_int, c_int,
-                                             P]),
-    "mdl_prefill_gemm_split_residual": (c_int, [P, c_int64, c_int, P, P, P, c_int, c_int, c_int,
-                                                P]),
+    "mdl_prefill_gemm_norm_swiglu": (c_int, [P, P, c_float, c_int, P, P, P, P, c_int, c_int,
+                                             c_int, c_int, P]),
+    "mdl_prefill_gemm_split_residual": (c_int, [P, c_int64, c_int, c_int, P, P, P, c_int, c_int,
+                                                c_int, P]),
     "mdl_prefill_gemm_norm_qkv": (c_int, [P, P, c_float, P, c_int, c_int, P, P, c_int64, c_int, P,
                                           P, P, c_int, c_int, c_int, c_int, c_int, c_int, c_float,
                                           P, P, P, c_int, c_int, c_int, P, P, P]),

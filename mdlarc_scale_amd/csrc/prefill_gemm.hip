@@ -10,10 +10,13 @@
 //            A_NORM  split(x * gamma) of the fp32 residual stream x [M, K] in the fp32 tile
 //                    layout, formed after the LDS read; the block sees whole rows, so it sums
 //                    x^2 and has rstd.
+// AP (activation parts) 1 drops the lo term: A_ROWS / A_TILES then hold hi alone ([M, K]),
+// A_NORM uses bf16(x * gamma); half the MFMAs and, for the split forms, a third fewer loads.
 // epilogue (EPI): E_STORE     out = acc (fp32 row-major; with A_NORM also rstd[m]);
 //                 E_SWIGLU    h = split(silu(rstd g + b_g) * (rstd u + b_u)) from the gate / up
 //                             accumulator pairs (weights with 16-row gate / up blocks
-//                             interleaved), h [M, 2F] in the tile layout;
+//                             interleaved), h [M, 2F] in the tile layout (h_parts 1: hi alone,
+//                             [M, F], for a consumer with AP 1);
 //                 E_RESIDUAL  x[m, n] += acc (+ bias[n]) in place, x [M, N] in the fp32 tile
 //                             layout;
 //                 E_QKV       K2 on the qkv accumulators (A_NORM): rstd, 3D RoPE of q and k, the
@@ -53,7 +56,10 @@ constexpr int kAFrags = (kBM / 16) * 2;   // {hi, lo} fragments of 16 row blocks
 constexpr int kWFrags = kBN / 16;
 constexpr int kStage = (kAFrags + kWFrags) * 1024;   // bytes of one LDS stage
 constexpr int kRing = 3;                             // LDS stages (loads run 2 k-steps ahead)
-constexpr int kLoadsPerStage = 6;                    // DMA instructions per thread per stage
+// DMA instructions per thread per stage: two weight fragments and four activation fragments
+// (two for the split forms with the hi part alone)
+template <int AMODE, int AP>
+constexpr int loads_per_stage() { return AMODE != 2 && AP == 1 ? 4 : 6; }
 constexpr int kMaxNormK = 2048;                      // A_NORM: gamma lives in LDS
 
 enum AMode { A_ROWS = 0, A_TILES = 1, A_NORM = 2 };
@@ -71,8 +77,8 @@ struct Args {
   float* rstd_out;     // E_STORE with A_NORM (may be NULL)
   const float* bias_a; // E_SWIGLU gate bias / E_RESIDUAL bias (may be NULL)
   const float* bias_b; // E_SWIGLU up bias (may be NULL)
-  uint16_t* h;         // E_SWIGLU: tiled split [M, 2 d_ff]
-  int d_ff;
+  uint16_t* h;         // E_SWIGLU: tiled [M, h_parts d_ff] (hi, then lo when h_parts is 2)
+  int d_ff, h_parts;
   float* x_res;        // E_RESIDUAL: [M, N] in the fp32 tile layout
   // E_QKV: row m is token slot tok_slot[m] of batch row tok_row[m] (packed), or slot m % seq of
   // row m / seq; out (may be NULL) receives the lead rows' fp32 acc
@@ -100,8 +106,10 @@ __device__ __forceinline__ void stage_barrier() {
   asm volatile("s_waitcnt vmcnt(%0)\n\ts_waitcnt lgkmcnt(0)\n\ts_barrier" :: "n"(N) : "memory");
 }
 
-template <int AMODE, int EPI>
+template <int AMODE, int EPI, int AP>
 __global__ __launch_bounds__(kThreads, 1) void prefill_gemm_kernel(const Args p) {
+  static_assert(AP == 1 || AP == 2, "activation parts: hi, or hi and lo");
+  constexpr int kLoads = loads_per_stage<AMODE, AP>();
   constexpr int kGammaBytes = AMODE == A_NORM ? kMaxNormK * 4 : 0;
   __shared__ __align__(16) uint8_t lds[kRing * kStage + kGammaBytes];
   __shared__ float rstd_s[kBM];
@@ -131,9 +139,11 @@ __global__ __launch_bounds__(kThreads, 1) void prefill_gemm_kernel(const Args p)
   // The loads of k-step s of the tile at (m0, n0) into ring stage b.  Wave w copies weight
   // fragments 8 j + w (j = 0, 1: row block n0 / 16 + 8 j + w) and activation fragments f = 8 j +
   // w (j = 0..3): row block f / 2, part f % 2 (hi / lo; for A_NORM the first or second kilobyte of
-  // the fp32 16 x 32 block, lane l's columns 0..3 or 4..7).  Every copy is one contiguous
-  // kilobyte per wave, except row-major A.  Row blocks past M or N load valid memory (clamped to
-  // the last; tile-layout buffers hold its padding rows); their results are never stored.
+  // the fp32 16 x 32 block, lane l's columns 0..3 or 4..7); with the hi part alone (AP 1, split
+  // forms) f = 2 (8 j + w), j = 0, 1.  Fragment f lands in stage slot f either way.  Every copy is
+  // one contiguous kilobyte per wave, except row-major A.  Row blocks past M or N load valid
+  // memory (clamped to the last; tile-layout buffers hold its padding rows); their results are
+  // never stored.
   auto issue = [&](int m0, int n0, int s, int b) {
     const uint32_t base = lds0 + b * kStage;
 #pragma unroll
@@ -142,21 +152,22 @@ __global__ __launch_bounds__(kThreads, 1) void prefill_gemm_kernel(const Args p)
       dma16(p.w + (static_cast<int64_t>(nb) * nk + s) * 512 + 8 * lane,
             __builtin_amdgcn_readfirstlane(base + (kAFrags + 8 * j + wave) * 1024));
     }
+    constexpr bool kHiOnly = AMODE != A_NORM && AP == 1;
 #pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      const int f = 8 * j + wave, rb = f >> 1, part = f & 1;
+    for (int j = 0; j < (kHiOnly ? 2 : 4); ++j) {
+      const int f = kHiOnly ? 2 * (8 * j + wave) : 8 * j + wave, rb = f >> 1, part = f & 1;
       const void* src;
       if constexpr (AMODE == A_NORM) {
         const int64_t blk = static_cast<int64_t>(min(m0 / 16 + rb, last_mb)) * nk + s;
         src = p.x + blk * 512 + 256 * part + 4 * lane;
       } else if constexpr (AMODE == A_TILES) {
-        const int64_t blk = static_cast<int64_t>(min(m0 / 16 + rb, last_mb)) * 2 * nk;
+        const int64_t blk = static_cast<int64_t>(min(m0 / 16 + rb, last_mb)) * AP * nk;
         src = p.a + (blk + part * nk + s) * 512 + 8 * lane;
       } else {
         const int row = min(m0 + 16 * rb + c, M - 1);
         src = p.a + static_cast<int64_t>(row) * p.lda + part * K + 32 * s + 8 * g;
       }
-      dma16(src, __builtin_amdgcn_readfirstlane(base + (8 * j + wave) * 1024));
+      dma16(src, __builtin_amdgcn_readfirstlane(base + f * 1024));
     }
   };
 
@@ -200,18 +211,23 @@ __global__ __launch_bounds__(kThreads, 1) void prefill_gemm_kernel(const Args p)
           t[e] = xe[e] * ge[e];
           ss[j] = fmaf(xe[e], xe[e], ss[j]);
         }
-        uint4 hi, lo;
-        split8(t, hi, lo);
-        ah[j] = as_bf16x8(hi);
-        al[j] = as_bf16x8(lo);
+        if constexpr (AP == 2) {
+          uint4 hi, lo;
+          split8(t, hi, lo);
+          ah[j] = as_bf16x8(hi);
+          al[j] = as_bf16x8(lo);
+        } else {
+          ah[j] = as_bf16x8(pack8(t));
+        }
       }
     } else {
 #pragma unroll
       for (int j = 0; j < FM; ++j) {
         ah[j] =
             *reinterpret_cast<const bf16x8_t*>(base + (2 * (FM * wm + j)) * 1024 + 16 * lane);
-        al[j] = *reinterpret_cast<const bf16x8_t*>(base + (2 * (FM * wm + j) + 1) * 1024 +
-                                                   16 * lane);
+        if constexpr (AP == 2)
+          al[j] = *reinterpret_cast<const bf16x8_t*>(base + (2 * (FM * wm + j) + 1) * 1024 +
+                                                     16 * lane);
       }
     }
     // The hi products before the lo products, so that consecutive MFMAs write different
@@ -238,12 +254,14 @@ __global__ __launch_bounds__(kThreads, 1) void prefill_gemm_kernel(const Args p)
           for (int j = 0; j < FM; ++j)
             acc[i + u][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(wf[u], ah[j], acc[i + u][j],
                                                                     0, 0, 0);
+        if constexpr (AP == 2) {
 #pragma unroll
-        for (int u = 0; u < kGroup; ++u)
+          for (int u = 0; u < kGroup; ++u)
 #pragma unroll
-          for (int j = 0; j < FM; ++j)
-            acc[i + u][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(wf[u], al[j], acc[i + u][j],
-                                                                    0, 0, 0);
+            for (int j = 0; j < FM; ++j)
+              acc[i + u][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(wf[u], al[j],
+                                                                      acc[i + u][j], 0, 0, 0);
+        }
       }
     } else {
       bf16x8_t wf[FN];
@@ -256,11 +274,13 @@ __global__ __launch_bounds__(kThreads, 1) void prefill_gemm_kernel(const Args p)
 #pragma unroll
         for (int j = 0; j < FM; ++j)
           acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(wf[i], ah[j], acc[i][j], 0, 0, 0);
+      if constexpr (AP == 2) {
 #pragma unroll
-      for (int i = 0; i < FN; ++i)
+        for (int i = 0; i < FN; ++i)
 #pragma unroll
-        for (int j = 0; j < FM; ++j)
-          acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(wf[i], al[j], acc[i][j], 0, 0, 0);
+          for (int j = 0; j < FM; ++j)
+            acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(wf[i], al[j], acc[i][j], 0, 0, 0);
+      }
     }
   };
 
@@ -376,8 +396,8 @@ __global__ __launch_bounds__(kThreads, 1) void prefill_gemm_kernel(const Args p)
                               silu_mul(fmaf(rs, gs[3], bg.w), fmaf(rs, us[3], bu.w))};
           uint2 hi, lo;
           split4(o, hi, lo);
-          *reinterpret_cast<uint2*>(p.h + tile_off(m, ch, 2 * F)) = hi;
-          *reinterpret_cast<uint2*>(p.h + tile_off(m, F + ch, 2 * F)) = lo;
+          *reinterpret_cast<uint2*>(p.h + tile_off(m, ch, p.h_parts * F)) = hi;
+          if (p.h_parts == 2) *reinterpret_cast<uint2*>(p.h + tile_off(m, F + ch, 2 * F)) = lo;
         }
       }
     } else {
@@ -436,7 +456,7 @@ __global__ __launch_bounds__(kThreads, 1) void prefill_gemm_kernel(const Args p)
   if (total > 1) {
     issue(im0, in0, is, 1);
     advance_issue();
-    stage_barrier<kLoadsPerStage>();
+    stage_barrier<kLoads>();
   } else {
     stage_barrier<0>();
   }
@@ -451,7 +471,7 @@ __global__ __launch_bounds__(kThreads, 1) void prefill_gemm_kernel(const Args p)
       advance_issue();
     }
     compute(cs, b);
-    if (u + 2 < total) stage_barrier<kLoadsPerStage>();
+    if (u + 2 < total) stage_barrier<kLoads>();
     else stage_barrier<0>();
     b = b == 2 ? 0 : b + 1;
     if (++cs == nk) {
@@ -479,7 +499,7 @@ int device_cus() {
   return cached[dev];
 }
 
-template <int AMODE, int EPI>
+template <int AMODE, int EPI, int AP = 2>
 int launch(Args p, hipStream_t st) {
   const int64_t tm = (static_cast<int64_t>(p.M) + kBM - 1) / kBM;
   const int64_t tn = (static_cast<int64_t>(p.N) + kBN - 1) / kBN;
@@ -491,7 +511,8 @@ int launch(Args p, hipStream_t st) {
   p.tiles_n = static_cast<int>(tn);
   p.tiles = static_cast<int>(tiles);
   p.per_xcd = static_cast<int>(per_xcd);
-  prefill_gemm_kernel<AMODE, EPI><<<dim3(static_cast<unsigned>(8 * bpx)), kThreads, 0, st>>>(p);
+  prefill_gemm_kernel<AMODE, EPI, AP>
+      <<<dim3(static_cast<unsigned>(8 * bpx)), kThreads, 0, st>>>(p);
   return launch_status();
 }
 
@@ -503,12 +524,22 @@ int check_common(const uint16_t* w, int m, int n, int k) {
   return MDL_OK;
 }
 
-int check_a(const uint16_t* a, int64_t lda, int a_layout, int k) {
+int check_a(const uint16_t* a, int64_t lda, int a_layout, int a_parts, int k) {
   if (!a) return MDL_ERR_NULL;
   if (a_layout != MDL_LAYOUT_ROWS && a_layout != MDL_LAYOUT_TILES) return MDL_ERR_SHAPE;
-  if (a_layout == MDL_LAYOUT_ROWS && lda < 2 * static_cast<int64_t>(k)) return MDL_ERR_SHAPE;
+  if (a_parts != 1 && a_parts != 2) return MDL_ERR_SHAPE;
+  if (a_layout == MDL_LAYOUT_ROWS && lda < a_parts * static_cast<int64_t>(k))
+    return MDL_ERR_SHAPE;
   if (!aligned16(a) || (a_layout == MDL_LAYOUT_ROWS && lda % 8 != 0)) return MDL_ERR_ALIGN;
   return MDL_OK;
+}
+
+// the split forms by A layout and parts
+template <int EPI>
+int launch_split(const Args& p, int a_layout, int a_parts, hipStream_t st) {
+  if (a_layout == MDL_LAYOUT_TILES)
+    return a_parts == 1 ? launch<A_TILES, EPI, 1>(p, st) : launch<A_TILES, EPI, 2>(p, st);
+  return a_parts == 1 ? launch<A_ROWS, EPI, 1>(p, st) : launch<A_ROWS, EPI, 2>(p, st);
 }
 
 }  // namespace
@@ -516,11 +547,11 @@ int check_a(const uint16_t* a, int64_t lda, int a_layout, int k) {
 
 using namespace mdl;
 
-extern "C" int mdl_prefill_gemm_split(const uint16_t* a, int64_t lda, int a_layout,
+extern "C" int mdl_prefill_gemm_split(const uint16_t* a, int64_t lda, int a_layout, int a_parts,
                                       const uint16_t* w, float* out, int64_t ldo, int m, int n,
                                       int k, void* stream) {
   int rc = check_common(w, m, n, k);
-  if (rc == MDL_OK) rc = check_a(a, lda, a_layout, k);
+  if (rc == MDL_OK) rc = check_a(a, lda, a_layout, a_parts, k);
   if (rc != MDL_OK) return rc;
   if (!out) return MDL_ERR_NULL;
   if (ldo < n) return MDL_ERR_SHAPE;
@@ -529,8 +560,7 @@ extern "C" int mdl_prefill_gemm_split(const uint16_t* a, int64_t lda, int a_layo
   Args p{};
   p.a = a; p.lda = lda; p.w = w; p.out = out; p.ldo = ldo; p.M = m; p.N = n; p.K = k;
   const hipStream_t st = static_cast<hipStream_t>(stream);
-  return a_layout == MDL_LAYOUT_TILES ? launch<A_TILES, E_STORE>(p, st)
-                                      : launch<A_ROWS, E_STORE>(p, st);
+  return launch_split<E_STORE>(p, a_layout, a_parts, st);
 }
 
 extern "C" int mdl_prefill_gemm_norm(const float* x, const float* gamma, float eps,
@@ -550,10 +580,12 @@ extern "C" int mdl_prefill_gemm_norm(const float* x, const float* gamma, float e
 }
 
 extern "C" int mdl_prefill_gemm_norm_swiglu(const float* x, const float* gamma, float eps,
-                                            const uint16_t* w_gu, const float* bias_gate,
-                                            const float* bias_up, uint16_t* h_out, int m,
-                                            int d_ff, int k, void* stream) {
+                                            int a_parts, const uint16_t* w_gu,
+                                            const float* bias_gate, const float* bias_up,
+                                            uint16_t* h_out, int h_parts, int m, int d_ff, int k,
+                                            void* stream) {
   if (d_ff <= 0 || d_ff % 16 != 0 || d_ff > (1 << 28)) return MDL_ERR_SHAPE;
+  if ((a_parts != 1 && a_parts != 2) || (h_parts != 1 && h_parts != 2)) return MDL_ERR_SHAPE;
   int rc = check_common(w_gu, m, 2 * d_ff, k);
   if (rc != MDL_OK) return rc;
   if (!x || !gamma || !h_out) return MDL_ERR_NULL;
@@ -564,15 +596,17 @@ extern "C" int mdl_prefill_gemm_norm_swiglu(const float* x, const float* gamma, 
   if (m == 0) return MDL_OK;
   Args p{};
   p.x = x; p.gamma = gamma; p.eps = eps; p.w = w_gu; p.bias_a = bias_gate; p.bias_b = bias_up;
-  p.h = h_out; p.d_ff = d_ff; p.M = m; p.N = 2 * d_ff; p.K = k;
-  return launch<A_NORM, E_SWIGLU>(p, static_cast<hipStream_t>(stream));
+  p.h = h_out; p.d_ff = d_ff; p.h_parts = h_parts; p.M = m; p.N = 2 * d_ff; p.K = k;
+  const hipStream_t st = static_cast<hipStream_t>(stream);
+  return a_parts == 1 ? launch<A_NORM, E_SWIGLU, 1>(p, st) : launch<A_NORM, E_SWIGLU, 2>(p, st);
 }
 
 extern "C" int mdl_prefill_gemm_split_residual(const uint16_t* a, int64_t lda, int a_layout,
-                                               const uint16_t* w, float* x, const float* bias,
-                                               int m, int n, int k, void* stream) {
+                                               int a_parts, const uint16_t* w, float* x,
+                                               const float* bias, int m, int n, int k,
+                                               void* stream) {
   int rc = check_common(w, m, n, k);
-  if (rc == MDL_OK) rc = check_a(a, lda, a_layout, k);
+  if (rc == MDL_OK) rc = check_a(a, lda, a_layout, a_parts, k);
   if (rc != MDL_OK) return rc;
   if (!x) return MDL_ERR_NULL;
   if (n % 32 != 0) return MDL_ERR_SHAPE;   // x in the fp32 tile layout: whole 32-column blocks
@@ -581,8 +615,7 @@ extern "C" int mdl_prefill_gemm_split_residual(const uint16_t* a, int64_t lda, i
   Args p{};
   p.a = a; p.lda = lda; p.w = w; p.x_res = x; p.bias_a = bias; p.M = m; p.N = n; p.K = k;
   const hipStream_t st = static_cast<hipStream_t>(stream);
-  return a_layout == MDL_LAYOUT_TILES ? launch<A_TILES, E_RESIDUAL>(p, st)
-                                      : launch<A_ROWS, E_RESIDUAL>(p, st);
+  return launch_split<E_RESIDUAL>(p, a_layout, a_parts, st);
 }
 
 extern "C" int mdl_prefill_gemm_norm_qkv(

@@ -96,6 +96,17 @@ def zero_tiled_rows(buf: torch.Tensor, r0: int, r1: int, cols: int) -> None:
     buf.view(-1, 8)[chunk.reshape(-1)] = 0
 
 
+# Activation parts of the bf16 form's prompt MLP on K6 (2: split hi | lo, as every other
+# projection; 1: the lo term dropped, as the reference's bf16 model rounds a projection's input
+# to bf16).  PROMPT_GATE_UP_PARTS is the gate / up input's (bf16(ln2(x)) at 1),
+# PROMPT_DOWN_PARTS the down input's (h stored as hi alone at 1).  Measured at config 2 (one
+# layer's launches): 1 for both takes gate/up 3.21 -> 2.35 ms and down 1.52 -> 1.01 ms, but the
+# config-2 decode logits move from 4.8e-3 to 2.9e-2 of the fp32 oracle (over the 2e-2 bar);
+# down alone gives 1.2e-2.  Both stay at 2 -- the parity margin is worth more than the 2-5 ms.
+PROMPT_GATE_UP_PARTS = 2
+PROMPT_DOWN_PARTS = 2
+
+
 def prompt_gemms_fused(d_model: int, d_ff: int) -> bool:
     """K6 runs a prompt's projections (RMSNorms and residual adds fused in) when the tiled
     weights exist and the normed inputs fit its LDS copy of gamma; every reference preset does.
@@ -194,7 +205,8 @@ class Scratch:
     """Activation buffers for M rows (reused across layers).  xs / attn / h are split bf16 GEMM
     inputs (2x the channel count; in the MFMA tile layout, whole 16-row blocks, when ``tiled``);
     qkv / delta / gu are fp32 GEMM outputs.  The fused forms (``tiled`` decode on K5, ``fused``
-    prompts on K6) form xs inside the GEMMs and keep no delta / gu: those are empty there."""
+    prompts on K6) form xs inside the GEMMs and keep no delta / gu: those are empty there.  On
+    K6, h holds PROMPT_DOWN_PARTS parts."""
 
     x: torch.Tensor
     xs: torch.Tensor
@@ -223,12 +235,14 @@ class Scratch:
         tiled = tiled or f32
         split_gemm = not (tiled or fused)               # hipBLASLt path: xs, delta, gu
         sr = rows if split_gemm else K.tile_rows(rows)  # rows of the tiled activations
+        fused = fused and not f32
+        h_parts = PROMPT_DOWN_PARTS if fused else 2
         return Scratch(x=e(sr, d, dt=f), xs=e(sr if split_gemm else 0, 2 * d),
                        rstd=e(rows, dt=f), qkv=e(rows, 3 * d, dt=f),
                        q=e(rows, d, dt=f if f32 else torch.bfloat16),
                        attn=e(sr, 2 * d), delta=e(rows if split_gemm else 0, d, dt=f),
-                       gu=e(rows if split_gemm else 0, 2 * d_ff, dt=f), h=e(sr, 2 * d_ff),
-                       rows=rows, tiled=tiled, fused=fused and not f32, f32=f32)
+                       gu=e(rows if split_gemm else 0, 2 * d_ff, dt=f), h=e(sr, h_parts * d_ff),
+                       rows=rows, tiled=tiled, fused=fused, f32=f32)
 
     @staticmethod
     def for_prompt(rows: int, cfg, device: torch.device, f32: bool) -> "Scratch":
@@ -468,13 +482,15 @@ class HipEngine:
         if sc.fused:
             # prompt on K6: residual adds in the out / down epilogues, ln2 in the gate / up
             # prologue with the SwiGLU in its epilogue; the next layer's ln1 runs in its qkv
-            # launch (_qkv) and ln_f in the head kernel
-            m = sc.rows
+            # launch (_qkv) and ln_f in the head kernel.  The MLP's inputs carry
+            # PROMPT_GATE_UP_PARTS / PROMPT_DOWN_PARTS parts.
+            m, parts = sc.rows, PROMPT_DOWN_PARTS
             K.prefill_gemm_split_residual(sc.attn, W.out_t[li], sc.x, None, m, d, d, a_tiled=True)
             K.prefill_gemm_norm_swiglu(sc.x, W.ln2[li], W.eps, W.gu_t[li], W.b_gate[li],
-                                       W.b_up[li], sc.h, m, F, d)
+                                       W.b_up[li], sc.h, m, F, d, a_parts=PROMPT_GATE_UP_PARTS,
+                                       h_parts=parts)
             K.prefill_gemm_split_residual(sc.h, W.down_t[li], sc.x, W.b_down[li], m, d, F,
-                                          a_tiled=True)
+                                          a_tiled=True, a_parts=parts)
             return
         if sc.tiled:
             # decode: three K5 launches, the residual adds in the epilogues and ln2 in the

@@ -443,26 +443,31 @@ def gemm_split_residual(a: torch.Tensor, w: torch.Tensor, x: torch.Tensor,
 PREFILL_NORM_MAX_K = 2048   # K6 norm forms: gamma is staged in LDS (kMaxNormK)
 
 
-def _split_a(a: torch.Tensor, m: int, k: int, tiled: bool) -> tuple[int, int]:
-    """(lda, layout) of a split activation [m, 2k] in either layout."""
+def _split_a(a: torch.Tensor, m: int, k: int, tiled: bool, parts: int = 2) -> tuple[int, int]:
+    """(lda, layout) of an activation [m, parts k] (split hi | lo, or hi alone) in either
+    layout."""
+    if parts not in (1, 2):
+        raise ValueError("a_parts must be 1 (hi) or 2 (hi and lo)")
     if tiled:
-        _need(a, "a", BF16, tile_rows(m) * 2 * k)
-        return 2 * k, LAYOUT_TILES
+        _need(a, "a", BF16, tile_rows(m) * parts * k)
+        return parts * k, LAYOUT_TILES
     _need(a, "a", BF16)
-    if a.dim() != 2 or a.shape[0] < m or a.shape[1] < 2 * k:
-        raise ValueError(f"a must be a row-major split activation [>= {m}, >= {2 * k}]")
+    if a.dim() != 2 or a.shape[0] < m or a.shape[1] < parts * k:
+        raise ValueError(f"a must be a row-major activation [>= {m}, >= {parts * k}]")
     return a.shape[1], LAYOUT_ROWS
 
 
 def prefill_gemm_split(a: torch.Tensor, w: torch.Tensor, out: torch.Tensor, k: int,
-                       a_tiled: bool = False) -> None:
-    """out[m, n] = (a_hi + a_lo) @ W^T on K6 (prompt-sized rows); w tiled [n, k]."""
+                       a_tiled: bool = False, a_parts: int = 2) -> None:
+    """out[m, n] = (a_hi + a_lo) @ W^T on K6 (prompt-sized rows); w tiled [n, k].  a_parts 1:
+    ``a`` holds hi alone ([m, k]) and the product is a_hi @ W^T."""
     _need(out, "out", F32)
     m, n = out.shape
-    lda, lay = _split_a(a, m, k, a_tiled)
+    lda, lay = _split_a(a, m, k, a_tiled, a_parts)
     _need(w, "w", BF16, tile_rows(n) * k)
-    _lib.check(_lib.lib().mdl_prefill_gemm_split(_p(a), lda, lay, _p(w), _p(out), out.stride(0),
-                                                 m, n, k, _stream()), "mdl_prefill_gemm_split")
+    _lib.check(_lib.lib().mdl_prefill_gemm_split(_p(a), lda, lay, a_parts, _p(w), _p(out),
+                                                 out.stride(0), m, n, k, _stream()),
+               "mdl_prefill_gemm_split")
 
 
 def prefill_gemm_norm(x: torch.Tensor, gamma: torch.Tensor, eps: float, w: torch.Tensor,
@@ -483,31 +488,35 @@ def prefill_gemm_norm(x: torch.Tensor, gamma: torch.Tensor, eps: float, w: torch
 def prefill_gemm_norm_swiglu(x: torch.Tensor, gamma: torch.Tensor, eps: float,
                              w_gu: torch.Tensor, bias_gate: torch.Tensor | None,
                              bias_up: torch.Tensor | None, h_out: torch.Tensor, m: int,
-                             d_ff: int, k: int) -> None:
-    """h (tiled split [m, 2 d_ff]) = SwiGLU of the gate / up projection of split(x * gamma);
-    x the fp32 tile-layout residual stream, w_gu the tiled interleave_gate_up weight."""
+                             d_ff: int, k: int, a_parts: int = 2, h_parts: int = 2) -> None:
+    """h (tiled [m, h_parts d_ff]: hi, then lo when h_parts is 2) = SwiGLU of the gate / up
+    projection of split(x * gamma) (a_parts 1: of bf16(x * gamma)); x the fp32 tile-layout
+    residual stream, w_gu the tiled interleave_gate_up weight."""
+    if a_parts not in (1, 2) or h_parts not in (1, 2):
+        raise ValueError("a_parts and h_parts must be 1 (hi) or 2 (hi and lo)")
     _need(x, "x", F32, tile_rows(m) * k)
     _need(gamma, "gamma", F32, k)
     _need(w_gu, "w_gu", BF16, 2 * d_ff * k)
     _need(bias_gate, "bias_gate", F32, d_ff, optional=True)
     _need(bias_up, "bias_up", F32, d_ff, optional=True)
-    _need(h_out, "h_out", BF16, split_numel(m, d_ff, True))
+    _need(h_out, "h_out", BF16, tile_rows(m) * h_parts * d_ff)
     _lib.check(_lib.lib().mdl_prefill_gemm_norm_swiglu(
-        _p(x), _p(gamma), eps, _p(w_gu), _p(bias_gate), _p(bias_up), _p(h_out), m, d_ff, k,
-        _stream()), "mdl_prefill_gemm_norm_swiglu")
+        _p(x), _p(gamma), eps, a_parts, _p(w_gu), _p(bias_gate), _p(bias_up), _p(h_out),
+        h_parts, m, d_ff, k, _stream()), "mdl_prefill_gemm_norm_swiglu")
 
 
 def prefill_gemm_split_residual(a: torch.Tensor, w: torch.Tensor, x: torch.Tensor,
                                 bias: torch.Tensor | None, m: int, n: int, k: int,
-                                a_tiled: bool = False) -> None:
+                                a_tiled: bool = False, a_parts: int = 2) -> None:
     """x += (a_hi + a_lo) @ W^T (+ bias) in place; x the fp32 tile-layout residual stream
-    [tile_rows(m), n], w tiled [n, k], a split [m, 2k] row-major or tiled."""
-    lda, lay = _split_a(a, m, k, a_tiled)
+    [tile_rows(m), n], w tiled [n, k], a split [m, 2k] row-major or tiled (a_parts 1: hi alone,
+    [m, k], and x += a_hi @ W^T)."""
+    lda, lay = _split_a(a, m, k, a_tiled, a_parts)
     _need(x, "x", F32, tile_rows(m) * n)
     _need(w, "w", BF16, tile_rows(n) * k)
     _need(bias, "bias", F32, n, optional=True)
-    _lib.check(_lib.lib().mdl_prefill_gemm_split_residual(_p(a), lda, lay, _p(w), _p(x),
-                                                          _p(bias), m, n, k, _stream()),
+    _lib.check(_lib.lib().mdl_prefill_gemm_split_residual(_p(a), lda, lay, a_parts, _p(w),
+                                                          _p(x), _p(bias), m, n, k, _stream()),
                "mdl_prefill_gemm_split_residual")
 
 

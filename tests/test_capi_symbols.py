@@ -108,6 +108,16 @@ def test_argument_errors_are_reported_before_any_launch():
     assert L.mdl_gemm_split_residual(fake, fake, None, fake, None, 4, 48, 32, 0, None) == -3
     assert L.mdl_gemm_split_residual(fake, fake, None, fake + 4, None, 4, 64, 32, 0, None) == -2
     assert L.mdl_gemm_split_residual(fake, fake, fake + 8, fake, None, 4, 64, 32, 0, None) == -2
+    # K6 activation parts: 1 (hi) or 2 (hi and lo) only; a row-major hi-only a needs lda >= k
+    assert L.mdl_prefill_gemm_split(fake, 64, 0, 3, fake, fake, 32, 4, 32, 32, None) == -3
+    assert L.mdl_prefill_gemm_split(fake, 32, 0, 2, fake, fake, 32, 4, 32, 32, None) == -3
+    assert L.mdl_prefill_gemm_split(fake, 16, 0, 1, fake, fake, 32, 4, 32, 32, None) == -3
+    assert L.mdl_prefill_gemm_split_residual(fake, 64, 1, 0, fake, fake, None, 4, 32, 32,
+                                             None) == -3
+    assert L.mdl_prefill_gemm_norm_swiglu(fake, fake, 1e-5, 0, fake, None, None, fake, 1, 4, 16,
+                                          32, None) == -3
+    assert L.mdl_prefill_gemm_norm_swiglu(fake, fake, 1e-5, 1, fake, None, None, fake, 3, 4, 16,
+                                          32, None) == -3
     assert L.mdl_gemm_split_tiles() >= 1
     assert 1 <= L.mdl_gemm_split_pick(256, 2304, 768) <= L.mdl_gemm_split_tiles()
     # packed prefill: the per-row starts / offsets and the per-token rows / slots are required

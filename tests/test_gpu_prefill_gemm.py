@@ -131,6 +131,76 @@ def test_norm_swiglu_gemm(m, f, k):
     assert rel(hh[:, :f] + hh[:, f:], ref) < 2e-5
 
 
+@pytest.mark.parametrize("m,n,k", [s for s in SHAPES if s[1] % 32 == 0])
+def test_hi_only_split_forms_match_fp64(m, n, k):
+    """a_parts 1: a holds hi alone ([m, k]) and the product is hi . W^T -- against fp64 to fp32
+    accumulation error, in both layouts and both epilogues, and measurably apart from the split
+    product (so a kernel that still added a lo term, or dropped hi, fails)."""
+    g = torch.Generator().manual_seed(5 * m + n + k)
+    w = (0.05 * torch.randn(n, k, generator=g)).to(torch.bfloat16).to(DEV)
+    v = torch.randn(m, k, generator=g).to(DEV)
+    hi, lo = split(v)
+    a = hi.contiguous()
+    ref = hi.double() @ w.double().t()
+    assert rel(v.double() @ w.double().t(), ref) > 1e-4   # the lo term matters at this scale
+    wt = K().tile_matrix(w)
+    out = torch.full((m, n), float("nan"), device=DEV)
+    K().prefill_gemm_split(a, wt, out, k, a_parts=1)
+    out_t = torch.full((m, n), float("nan"), device=DEV)
+    K().prefill_gemm_split(K().tile_matrix(a), wt, out_t, k, a_tiled=True, a_parts=1)
+    x0 = torch.randn(m, n, generator=g).to(DEV)
+    b = torch.randn(n, generator=g).to(DEV)
+    x1 = K().tile_f32(x0)
+    K().prefill_gemm_split_residual(K().tile_matrix(a), wt, x1, b, m, n, k, a_tiled=True,
+                                    a_parts=1)
+    x2 = K().tile_f32(x0)
+    K().prefill_gemm_split_residual(a, wt, x2, b, m, n, k, a_parts=1)
+    torch.cuda.synchronize()
+    assert rel(out, ref) < 2e-6
+    assert torch.equal(out, out_t)
+    assert rel(K().untile_f32(x1, m, n), x0.double() + ref + b.double()) < 2e-6
+    assert torch.equal(x1, x2)
+
+
+@pytest.mark.parametrize("m,f,k", [(1000, 2048, 768), (333, 704, 256), (257, 2752, 1024),
+                                   (5, 2048, 768)])
+def test_norm_swiglu_parts(m, f, k):
+    """a_parts 1 (gate / up of bf16(x * gamma)) against fp64 of the same hi product, h_parts 1
+    (hi of h alone, [m, f]) bit-equal to the hi half of the h_parts 2 output of the same launch
+    form, for both activation forms."""
+    g = torch.Generator().manual_seed(3 * m + f + k)
+    wg = (0.05 * torch.randn(f, k, generator=g)).to(torch.bfloat16).to(DEV)
+    wu = (0.05 * torch.randn(f, k, generator=g)).to(torch.bfloat16).to(DEV)
+    wgu = K().tile_matrix(K().interleave_gate_up(wg, wu))
+    x = torch.randn(m, k, generator=g).to(DEV)
+    gam = (1 + 0.1 * torch.randn(k, generator=g)).to(DEV)
+    bg = torch.randn(f, generator=g).to(DEV)
+    bu = torch.randn(f, generator=g).to(DEV)
+    xt = K().tile_f32(x)
+    hs = {}
+    for ap in (1, 2):
+        for hp in (1, 2):
+            h = torch.empty(K().tile_rows(m) * hp * f, dtype=torch.bfloat16, device=DEV)
+            K().prefill_gemm_norm_swiglu(xt, gam, 1e-5, wgu, bg, bu, h, m, f, k, a_parts=ap,
+                                         h_parts=hp)
+            hs[ap, hp] = K().untile_matrix(h, m, hp * f)
+    torch.cuda.synchronize()
+    for ap in (1, 2):
+        assert torch.equal(hs[ap, 1], hs[ap, 2][:, :f])
+    th, tl = split(x * gam)
+    rs64 = 1 / torch.sqrt((x.double() ** 2).mean(1) + 1e-5)
+
+    def swiglu64(t):
+        gg = rs64[:, None] * (t @ wg.double().t()) + bg.double()
+        uu = rs64[:, None] * (t @ wu.double().t()) + bu.double()
+        return gg / (1 + torch.exp(-gg)) * uu
+
+    ref_hi, ref_split = swiglu64(th.double()), swiglu64(th.double() + tl.double())
+    h12 = hs[1, 2].double()
+    assert rel(h12[:, :f] + h12[:, f:], ref_hi) < 2e-5
+    assert rel(ref_split, ref_hi) > 1e-4   # the lo term is visible at this tolerance
+
+
 def test_prefill_gemm_persistent_tiles_cover_everything():
     """More tiles than CUs (each block walks several, the load ring crossing tile boundaries):
     every output element is written once with the right value."""
