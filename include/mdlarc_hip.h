@@ -562,7 +562,11 @@ int mdl_attn_prefill_f32(const float* q, const float* k_cache, const float* v_ca
  * K4f at decode: the query of row b (q row b) sees slot j iff kv_start[b] <= j <= t,
  * t = (seq_dev ? *seq_dev : seq_pos), and (j >= prompt_len || prompt_mask[b * prompt_len + j]
  * != 0) (prompt_mask may be NULL) -- the visibility rule of mdl_attn_decode.  K / V of slot t
- * must be written first (mdl_qkv_rope_cache, seq = 1, slot_dev).  Arguments otherwise as for
+ * must be written first (mdl_qkv_rope_cache, seq = 1, slot_dev).  The slots of a row are split
+ * into chunks of split_len (a positive multiple of 16), one wave each; with more than one chunk
+ * (cache_slots > split_len) the chunks' states go to `workspace`, which must hold
+ * mdl_attn_decode_workspace_bytes(batch, n_heads, cache_slots, split_len) bytes (16-byte
+ * aligned; else MDL_ERR_WORKSPACE), and a second launch merges them.  Arguments otherwise as for
  * mdl_attn_prefill_f32.
  * Replaces: F.scaled_dot_product_attention in _decode_step (src/inference.py:452) for an fp32
  *           model, with the mask of src/inference.py:446-450.
@@ -570,7 +574,8 @@ int mdl_attn_prefill_f32(const float* q, const float* k_cache, const float* v_ca
 int mdl_attn_decode_f32(const float* q, const float* k_cache, const float* v_cache, int batch,
                         int n_heads, int head_dim, int cache_slots, const uint8_t* prompt_mask,
                         int prompt_len, const int32_t* kv_start, int seq_pos,
-                        const int32_t* seq_dev, uint16_t* out, int out_layout, void* stream);
+                        const int32_t* seq_dev, float* workspace, int64_t workspace_bytes,
+                        int split_len, uint16_t* out, int out_layout, void* stream);
 
 /*
  * Final RMSNorm + LM head + greedy argmax.

@@ -96,7 +96,7 @@ SIGNATURES: dict[str, tuple[object, list]] = {
     "mdl_attn_prefill_f32": (c_int, [P, P, P, c_int, c_int, c_int, c_int, c_int, P, P, P, c_int,
                                      P, c_int, P]),
     "mdl_attn_decode_f32": (c_int, [P, P, P, c_int, c_int, c_int, c_int, P, c_int, P, c_int, P, P,
-                                    c_int, P]),
+                                    c_int64, c_int, P, c_int, P]),
     "mdl_lm_head": (c_int, [P, P, c_int, c_int, P, c_float, P, c_int, P, P, CONS, c_int, P]),
     "mdl_decode_head": (c_int, [P, c_int, c_int, P, c_float, P, c_int, P, P, P, c_int64, c_int,
                                 P, P, c_int, c_int, CONS, c_int, P]),

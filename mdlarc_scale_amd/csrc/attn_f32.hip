@@ -30,6 +30,10 @@
 // per batch row at cache slot t).  Key j is visible to the query at position i iff
 // kv_start[b] <= j < n_keys, (causal) j <= i, and (j >= mask_len or mask[b * mask_len + j] != 0);
 // a query with no visible key outputs 0 (what torch's CPU SDPA returns for an all -inf row).
+// At decode a work item is one split_len-slot chunk of one (row, head): one wave streaming its
+// keys a 16-key tile at a time is latency-bound, so the chunks are what fills the GPU.  With
+// several chunks each writes its running state (m, l, unnormalised o) to the workspace, and
+// attn_f32_combine_kernel merges them.
 #include "common.h"
 #include "mfma.h"
 
@@ -54,11 +58,15 @@ struct F32Args {
   int seq_pos;
   int batch, heads, slots, seq;  // seq: prefill query / key count
   int causal;
-  int q_tiles;                   // work items per (row, head)
+  int q_tiles;                   // work items per (row, head) (M_DECODE: the chunks)
   int64_t items;
   uint16_t* out;                 // split bf16 [rows, 2 d]
   int out_layout;
+  int split_len;                 // M_DECODE: slots per chunk
+  float* ws;                     // M_DECODE with more than one chunk: kPartF floats per chunk
 };
+
+constexpr int kPartF = 2 + kHeadDim;   // m, l, o[64] of one decode chunk
 
 typedef float f32x4 __attribute__((ext_vector_type(4)));
 
@@ -68,7 +76,8 @@ __global__ __launch_bounds__(64 * kWavesF) void attn_f32_kernel(const F32Args p)
   if (item >= p.items) return;   // whole wave; the kernel has no barrier
   const int lane = threadIdx.x & 63, c = lane & 15, g = lane >> 4;
   const int64_t bh = item / p.q_tiles;
-  // the longest query tiles of a row first (causal prefill: the last tiles see the most keys)
+  // the longest query tiles of a row first (causal prefill: the last tiles see the most keys);
+  // at decode, the chunk index
   const int qt = p.q_tiles - 1 - static_cast<int>(item - bh * p.q_tiles);
   const int b = static_cast<int>(bh / p.heads), h = static_cast<int>(bh - b * p.heads);
   const int d = p.heads * kHeadDim;
@@ -82,6 +91,11 @@ __global__ __launch_bounds__(64 * kWavesF) void attn_f32_kernel(const F32Args p)
     n_keys = p.seq;
   }
   if (p.kv_start) klo = min(max(p.kv_start[b], 0), n_keys);
+  int khi = n_keys;   // keys this item visits: [klo, khi)
+  if constexpr (MODE == M_DECODE) {
+    klo = min(klo + qt * p.split_len, n_keys);
+    khi = min(klo + p.split_len, n_keys);
+  }
   int qpos, qfirst;   // this lane's query position; the tile's first position
   int64_t qrow;
   bool qvalid;
@@ -102,7 +116,6 @@ __global__ __launch_bounds__(64 * kWavesF) void attn_f32_kernel(const F32Args p)
   }
   if (qfirst >= p.seq && MODE != M_DECODE) return;   // the whole tile lies past the row
   // keys the tile's last query can see
-  int khi = n_keys;
   if (p.causal && MODE != M_DECODE) khi = min(n_keys, min(qfirst + kQT, p.seq));
 
   // q: dims 16 g .. 16 g + 15 of query c
@@ -187,6 +200,20 @@ __global__ __launch_bounds__(64 * kWavesF) void attn_f32_kernel(const F32Args p)
   }
 
   if (!qvalid) return;
+  if (MODE == M_DECODE && p.ws) {
+    // this chunk's state: m and l (the same in every lane of query column 0), o unnormalised;
+    // lane (0, g) holds dims 16 g + 4 r + db as element r of block db
+    float* part = p.ws + item * kPartF;
+    if (g == 0) {
+      part[0] = m_run;
+      part[1] = l_run;
+    }
+#pragma unroll
+    for (int r = 0; r < 4; ++r)
+#pragma unroll
+      for (int db = 0; db < 4; ++db) part[2 + 16 * g + 4 * r + db] = o[db][r];
+    return;
+  }
   const float inv = l_run > 0.f ? 1.f / l_run : 0.f;
   float res[16];   // dims 16 g + e of query c: element r of block db is dim 16 g + 4 r + db
 #pragma unroll
@@ -208,6 +235,40 @@ __global__ __launch_bounds__(64 * kWavesF) void attn_f32_kernel(const F32Args p)
     *reinterpret_cast<uint4*>(orow + col + 8) = hi1;
     *reinterpret_cast<uint4*>(orow + d + col) = lo0;
     *reinterpret_cast<uint4*>(orow + d + col + 8) = lo1;
+  }
+}
+
+// The decode chunks of one (row, head) merged, lane = channel: the states rescaled to their
+// largest m (base 2), o / l, stored as the split output of mdl_attn_decode_f32.
+__global__ __launch_bounds__(256) void attn_f32_combine_kernel(const float* __restrict__ ws,
+                                                               int n_bh, int n_heads,
+                                                               int n_split,
+                                                               uint16_t* __restrict__ out,
+                                                               int out_layout) {
+  const int bh = blockIdx.x * 4 + (threadIdx.x >> 6);
+  const int lane = threadIdx.x & 63;
+  if (bh >= n_bh) return;
+  const float* part = ws + static_cast<int64_t>(bh) * n_split * kPartF;
+  float M = -INFINITY;
+  for (int s = 0; s < n_split; ++s) M = fmaxf(M, part[s * kPartF]);
+  float L = 0.f, O = 0.f;
+  for (int s = 0; s < n_split; ++s) {
+    const float ms = part[s * kPartF];
+    const float sc = ms == -INFINITY ? 0.f : exp2f(ms - M);
+    L = fmaf(part[s * kPartF + 1], sc, L);
+    O = fmaf(part[s * kPartF + 2 + lane], sc, O);
+  }
+  const float v = L > 0.f ? O / L : 0.f;
+  const int b = bh / n_heads, h = bh - b * n_heads;
+  const int d = n_heads * kHeadDim, col = h * kHeadDim + lane;
+  const uint16_t hi = static_cast<uint16_t>(f2bf(v));
+  const uint16_t lo = static_cast<uint16_t>(f2bf(v - bf2f(hi)));
+  if (out_layout == MDL_LAYOUT_TILES) {
+    out[tile_off(b, col, 2 * d)] = hi;
+    out[tile_off(b, d + col, 2 * d)] = lo;
+  } else {
+    out[static_cast<int64_t>(b) * 2 * d + col] = hi;
+    out[static_cast<int64_t>(b) * 2 * d + d + col] = lo;
   }
 }
 
@@ -267,12 +328,23 @@ extern "C" int mdl_attn_decode_f32(const float* q, const float* k_cache, const f
                                    int batch, int n_heads, int head_dim, int cache_slots,
                                    const uint8_t* prompt_mask, int prompt_len,
                                    const int32_t* kv_start, int seq_pos, const int32_t* seq_dev,
+                                   float* workspace, int64_t workspace_bytes, int split_len,
                                    uint16_t* out, int out_layout, void* stream) {
   const int rc = check_f32(q, k_cache, v_cache, batch, n_heads, head_dim, cache_slots, out,
                            out_layout);
   if (rc != MDL_OK) return rc;
-  if (prompt_len < 0 || (prompt_mask && prompt_len == 0)) return MDL_ERR_SHAPE;
+  if (prompt_len < 0 || (prompt_mask && prompt_len == 0) || split_len < kQT ||
+      split_len % kQT != 0)
+    return MDL_ERR_SHAPE;
   if (!seq_dev && (seq_pos < 0 || seq_pos >= cache_slots)) return MDL_ERR_CACHE;
+  const int n_split = (cache_slots + split_len - 1) / split_len;
+  const int64_t n_bh = static_cast<int64_t>(batch) * n_heads;
+  if (n_split > 1) {
+    if (!workspace) return MDL_ERR_WORKSPACE;
+    if (workspace_bytes < n_bh * n_split * kPartF * static_cast<int64_t>(sizeof(float)))
+      return MDL_ERR_WORKSPACE;
+    if (!aligned16(workspace)) return MDL_ERR_ALIGN;
+  }
   F32Args p{};
   p.q = q; p.kc = k_cache; p.vc = v_cache;
   p.mask = prompt_mask; p.mask_len = prompt_len;
@@ -280,8 +352,17 @@ extern "C" int mdl_attn_decode_f32(const float* q, const float* k_cache, const f
   p.seq_dev = seq_dev; p.seq_pos = seq_pos;
   p.batch = batch; p.heads = n_heads; p.slots = cache_slots; p.seq = cache_slots;
   p.causal = 1;
-  p.q_tiles = 1;
-  p.items = static_cast<int64_t>(batch) * n_heads;
+  p.q_tiles = n_split;
+  p.split_len = split_len;
+  p.ws = n_split > 1 ? workspace : nullptr;
+  p.items = n_bh * n_split;
   p.out = out; p.out_layout = out_layout;
-  return launch_f32<M_DECODE>(p, static_cast<hipStream_t>(stream));
+  const hipStream_t st = static_cast<hipStream_t>(stream);
+  const int rc2 = launch_f32<M_DECODE>(p, st);
+  if (rc2 != MDL_OK || n_split == 1 || n_bh == 0) return rc2;
+  if ((n_bh + 3) / 4 > 0x7fffffff) return MDL_ERR_SHAPE;
+  hipLaunchKernelGGL(attn_f32_combine_kernel, dim3(static_cast<unsigned>((n_bh + 3) / 4)),
+                     dim3(256), 0, st, workspace, static_cast<int>(n_bh), n_heads, n_split, out,
+                     out_layout);
+  return launch_status();
 }

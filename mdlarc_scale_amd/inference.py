@@ -362,7 +362,7 @@ class Generator:
                 K.qkv_rope_cache(sc.qkv, sc.rstd, st.pos, W.rope_tab, W.rope_geom, B, 1, H, qs,
                                  sc.q, kc, vc, slot_dev=slot)
                 K.attn_decode_f32(sc.q, kc, vc, B, H, st.pmask, st.S, st.kv_start, 0, slot,
-                                  sc.attn, tiled=True)
+                                  st.ws, st.split_len, sc.attn, tiled=True)
             elif sc.tiled:
                 # ln1 in the projection's prologue, K2 (RoPE, q scale, K/V into slot t) in its
                 # epilogue; the attention reads q and the cache

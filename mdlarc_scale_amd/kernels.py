@@ -692,20 +692,26 @@ def attn_prefill_f32(q: torch.Tensor, k_cache: torch.Tensor, v_cache: torch.Tens
 def attn_decode_f32(q: torch.Tensor, k_cache: torch.Tensor, v_cache: torch.Tensor, batch: int,
                     n_heads: int, prompt_mask: torch.Tensor | None, prompt_len: int,
                     kv_start: torch.Tensor | None, seq_pos: int, seq_dev: torch.Tensor | None,
-                    out: torch.Tensor, tiled: bool = False) -> None:
+                    workspace: torch.Tensor | None, split_len: int, out: torch.Tensor,
+                    tiled: bool = False) -> None:
     """K4f at decode: the query of row b (fp32 q [batch, n_heads*64]) over slots
     [kv_start[b], t] of the fp32 cache, t = seq_dev[0] (or seq_pos), the prompt mask applying
-    below prompt_len; out split [batch, 2*n_heads*64] bf16."""
+    below prompt_len; out split [batch, 2*n_heads*64] bf16.  The slots go in chunks of
+    ``split_len`` (a multiple of 16), one wave each; with more than one chunk their states are
+    merged through ``workspace`` (attn_decode_workspace_bytes(batch, n_heads, slots,
+    split_len) bytes)."""
     _need(q, "q", F32, batch * n_heads * HEAD_DIM)
     _need(out, "out", BF16, split_numel(batch, n_heads * HEAD_DIM, tiled))
     _f32_cache(k_cache, v_cache, batch, n_heads)
     _need(prompt_mask, "prompt_mask", U8, batch * prompt_len, optional=True)
     _need(kv_start, "kv_start", I32, batch, optional=True)
     _need(seq_dev, "seq_dev", I32, 1, optional=True)
+    _need(workspace, "workspace", F32, optional=True)
+    ws_bytes = workspace.numel() * 4 if workspace is not None else 0
     _lib.check(_lib.lib().mdl_attn_decode_f32(
         _p(q), _p(k_cache), _p(v_cache), batch, n_heads, HEAD_DIM, k_cache.shape[2],
-        _p(prompt_mask), prompt_len, _p(kv_start), seq_pos, _p(seq_dev), _p(out),
-        _layout(tiled), _stream()), "mdl_attn_decode_f32")
+        _p(prompt_mask), prompt_len, _p(kv_start), seq_pos, _p(seq_dev), _p(workspace),
+        ws_bytes, split_len, _p(out), _layout(tiled), _stream()), "mdl_attn_decode_f32")
 
 
 def attn_prefill_lead(qkv: torch.Tensor, rstd: torch.Tensor, pos: torch.Tensor,

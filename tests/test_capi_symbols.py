@@ -141,10 +141,17 @@ def test_argument_errors_are_reported_before_any_launch():
                                   None) == -5
     assert L.mdl_attn_prefill_f32(fake + 4, fake, fake, 1, 4, 1, 64, 4, None, None, None, 1, fake,
                                   0, None) == -2
-    assert L.mdl_attn_decode_f32(fake, fake, fake, 1, 1, 64, 4, None, 0, None, 4, None, fake, 0,
-                                 None) == -5
-    assert L.mdl_attn_decode_f32(fake, fake, fake, 1, 1, 64, 4, None, 0, None, 0, None, fake, 2,
-                                 None) == -3
+    assert L.mdl_attn_decode_f32(fake, fake, fake, 1, 1, 64, 4, None, 0, None, 4, None, None, 0,
+                                 16, fake, 0, None) == -5
+    assert L.mdl_attn_decode_f32(fake, fake, fake, 1, 1, 64, 4, None, 0, None, 0, None, None, 0,
+                                 16, fake, 2, None) == -3
+    # K4f decode chunks: split_len a positive multiple of 16; several chunks need the workspace
+    assert L.mdl_attn_decode_f32(fake, fake, fake, 1, 1, 64, 64, None, 0, None, 0, None, None, 0,
+                                 8, fake, 0, None) == -3
+    assert L.mdl_attn_decode_f32(fake, fake, fake, 1, 1, 64, 64, None, 0, None, 0, None, None, 0,
+                                 16, fake, 0, None) == -6
+    assert L.mdl_attn_decode_f32(fake, fake, fake, 1, 1, 64, 64, None, 0, None, 0, None, fake,
+                                 1000, 16, fake, 0, None) == -6
     # exact lead attention: q_offset needs kv_start; head_dim 64 only; qkv rows 16-byte aligned
     assert L.mdl_attn_prefill_lead(fake, 192, fake, fake, fake, 32, 32, 8, 10, 10, 12, 0.125, 1, 4,
                                    1, 64, None, None, fake, fake, 0, None) == -1

@@ -323,8 +323,15 @@ def test_attn_prefill_f32_packed_equals_padded(causal):
 
 @pytest.mark.parametrize("slots,t", [(64, 0), (300, 211), (1100, 1037)])
 @pytest.mark.parametrize("with_mask", [True, False])
-def test_attn_decode_f32(slots, t, with_mask):
+@pytest.mark.parametrize("split_len", [0, 128, 48])
+def test_attn_decode_f32(slots, t, with_mask, split_len):
+    """K4f decode against fp64, in one chunk (split_len 0: the whole cache) and in chunks of
+    split_len slots merged through the workspace (chunks past t are empty)."""
     g = torch.Generator().manual_seed(slots + t + with_mask)
+    split = split_len or -(-slots // 16) * 16
+    nbytes = K().attn_decode_workspace_bytes(6, 4, slots, split)
+    ws = torch.empty(max(nbytes // 4, 1), device=DEV) if nbytes else None
+    assert (ws is None) == (split >= slots)
     B, H, S = 6, 4, min(150, t + 1)
     q = torch.randn(B, H, 64, generator=g) * 0.3
     kc = torch.randn(B, H, slots, 64, generator=g)
@@ -339,7 +346,8 @@ def test_attn_decode_f32(slots, t, with_mask):
         seq_dev = torch.tensor([t], dtype=torch.int32, device=DEV) if dev_seq else None
         K().attn_decode_f32(q.to(DEV), kc.to(DEV), vc.to(DEV), B, H,
                             None if pm is None else pm.to(torch.uint8).to(DEV),
-                            S if pm is not None else 0, kv_start, t, seq_dev, out, tiled=tiled)
+                            S if pm is not None else 0, kv_start, t, seq_dev, ws, split, out,
+                            tiled=tiled)
         torch.cuda.synchronize()
         got = K().untile_matrix(out, K().tile_rows(B), 2 * H * 64)[:B] if tiled else out
         keymask = torch.ones(B, t + 1, dtype=torch.bool)
