@@ -484,7 +484,8 @@ int mdl_attn_prefill_lead(const float* qkv, int64_t qkv_ld, const float* rstd,
  * row_order (int32 [batch], may be NULL): a permutation of the rows giving the order their work
  *   is dispatched in; longest-first (ascending kv_start) shortens the launch's tail.
  * workspace: fp32, at least mdl_attn_decode_workspace_bytes(...) bytes (may be NULL when
- *   that is 0).  split_len: slots per work item (multiple of 128, >= 128).
+ *   that is 0).  split_len: slots per work item (multiple of 128, >= 128; mdl_attn_decode_f32
+ *   takes multiples of 16 and the same workspace size).
  */
 int64_t mdl_attn_decode_workspace_bytes(int batch, int n_heads, int cache_slots, int split_len);
 int mdl_attn_decode(const uint16_t* q, const uint16_t* k_cache, const uint16_t* v_cache,
