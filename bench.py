@@ -290,11 +290,15 @@ def graph_time_us(fn, reps=50, replays=10):
     with torch.cuda.stream(side):
         for _ in range(3):
             fn()
-    torch.cuda.current_stream().wait_stream(side)
     g = torch.cuda.CUDAGraph()
-    with torch.cuda.graph(g):
-        for _ in range(reps):
-            fn()
+    with torch.cuda.stream(side):   # capture_begin: no allocator-cache release (capture_greedy)
+        g.capture_begin()
+        try:
+            for _ in range(reps):
+                fn()
+        finally:
+            g.capture_end()
+    torch.cuda.current_stream().wait_stream(side)
     g.replay()
     t = Timer()
     t.start()
@@ -724,7 +728,6 @@ def side_config(name, dev, steps=32, warmup=4):
         "prefill_projections": prefill_projections_of(r),
     }
     del r
-    torch.cuda.empty_cache()
     return out
 
 
@@ -763,7 +766,8 @@ def main() -> int:
     r.pop("snap", None)
     r.pop("model", None)
     r.pop("st", None)
-    torch.cuda.empty_cache()
+    # no torch.cuda.empty_cache() between configurations: returning cached memory to the driver
+    # leaves later HBM-bound kernels of the process slower (see Generator.capture_greedy)
     sides = {}
     if headline and not args.no_side:
         for name in ("medium_b128", "large_b64"):

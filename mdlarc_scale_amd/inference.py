@@ -413,10 +413,23 @@ class Generator:
         ``st`` and the cache slot / output column advance through ``st.counters`` on the device,
         so one recording replays as every later step.  Capturing launches nothing; the caller
         must have run the step eagerly once (library handles and GEMM workspaces initialised).
-        The step records no memset nodes."""
+        The step records no memset nodes.
+
+        The capture runs on a side stream through ``capture_begin`` / ``capture_end`` rather than
+        the ``torch.cuda.graph`` context, which first empties torch's allocator cache: returning
+        that memory (the prefill's scratch) to the driver leaves every later HBM-bound kernel of
+        the process about 4% slower on this platform (measured on the decode attention's read
+        pattern; compute-bound kernels are unaffected)."""
         g = torch.cuda.CUDAGraph()
-        with torch.cuda.graph(g):
-            self.greedy_step(st, W, stop_on_end, cons)
+        side = torch.cuda.Stream()
+        side.wait_stream(torch.cuda.current_stream())
+        with torch.cuda.stream(side):
+            g.capture_begin()
+            try:
+                self.greedy_step(st, W, stop_on_end, cons)
+            finally:
+                g.capture_end()
+        torch.cuda.current_stream().wait_stream(side)
         return g
 
 
