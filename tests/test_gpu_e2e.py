@@ -496,6 +496,31 @@ def test_graph_replay_matches_eager_launches(stop_on_end, form):
     assert torch.equal(outs[0], outs[1])
 
 
+def test_graph_capture_keeps_allocator_cache(monkeypatch):
+    """Capturing the greedy step returns no cached memory to the driver: releasing it slows every
+    later HBM-bound kernel of the process, so the capture must not empty torch's cache (the
+    ``torch.cuda.graph`` context does) and the reserved pool may not shrink across a generate."""
+    from mdlarc_scale_amd import generate_output
+    from mdlarc_scale_amd import inference as inf
+
+    m, _ = _preset_model("small", "bf16", seed=3, max_seq_len=1024)
+    rng = np.random.default_rng(7)
+    ids, pos, mask = _left_pad(_random_prompts(rng, 8, 2, 1, 6))
+    calls = []
+    monkeypatch.setattr(torch.cuda, "empty_cache", lambda: calls.append(1))
+    assert inf.USE_GRAPHS
+    with torch.no_grad():
+        generate_output(m, ids.to(DEV), pos.to(DEV), torch.arange(8).to(DEV),
+                        attention_mask=mask.to(DEV), max_new_tokens=20, stop_on_end=False)
+        torch.cuda.synchronize()
+        reserved = torch.cuda.memory_reserved()
+        generate_output(m, ids.to(DEV), pos.to(DEV), torch.arange(8).to(DEV),
+                        attention_mask=mask.to(DEV), max_new_tokens=20, stop_on_end=False)
+        torch.cuda.synchronize()
+    assert not calls
+    assert torch.cuda.memory_reserved() >= reserved
+
+
 def test_predict_with_augmentations_pipeline():
     """The batched augmentation caller runs on the HIP path and returns 8 x perms results with
     the reference's tuple structure (tests/test_inference.py:225-293 of the reference)."""
