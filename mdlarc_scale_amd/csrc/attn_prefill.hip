@@ -302,8 +302,13 @@ __global__ __launch_bounds__(256, 3) void attn_prefill_kernel(
   // Every wave of the block runs the same tiles, so the barriers match.
   auto tile = [&](int kt, auto stc) {
     constexpr int ST = decltype(stc)::value;
-    // tile kt has landed in stage ST for every wave, and every wave is done with stage ST ^ 1
-    asm volatile("s_waitcnt vmcnt(0)\n\ts_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
+    // tile kt has landed in stage ST for every wave, and every wave is done with stage ST ^ 1.
+    // The wait is the builtin, not assembly, so that the compiler sees every load it knows of
+    // (q, the mask bytes) completed here: otherwise it waits for the q fragments again at their
+    // first use inside the loop, and that vmcnt wait also covers the copies of tile kt + 64
+    // issued just before, which then no longer run under this tile's work (5% at config 2).
+    __builtin_amdgcn_s_waitcnt(kWaitAll);
+    asm volatile("s_barrier" ::: "memory");
     uint64_t mw;
     if (mrow)
       mw = __ballot(mb_next != 0);

@@ -12,13 +12,21 @@ __device__ __forceinline__ uint32_t lds_addr(const void* p) {
       reinterpret_cast<uintptr_t>((const __attribute__((address_space(3))) void*)(p)));
 }
 
+// s_waitcnt immediate (gfx9 encoding: vmcnt bits 3:0 and 15:14, expcnt 6:4, lgkmcnt 11:8) for
+// vmcnt(0) lgkmcnt(0).  Issued through __builtin_amdgcn_s_waitcnt, the wait is visible to the
+// compiler's own wait insertion, which then counts every load it issued before as complete.
+constexpr int kWaitAll = 0x0070;
+
 // 16 bytes per lane from global memory straight into LDS: lane l's bytes land at lds + 16 l
 // (lds wave-uniform, through M0).  Issued as inline assembly, so the compiler neither sees nor
 // waits for these loads: a kernel waits for them itself (s_waitcnt vmcnt) before the barrier
 // that publishes the stage.  The compiler's own waits stay correct beside them: vector memory
 // operations complete in issue order, so loads it does not know of only make its vmcnt(n) waits
-// stricter.  Kernels that use this must not spill: the library build rejects scratch use in the
-// files that include this header.
+// stricter.  Stricter is slower, though: a compiler wait for one of its own loads issued before
+// a copy also waits for the copy, so a kernel keeps its own loads and stores out of the way of
+// the copies in flight (batched ahead of them, or retired by a builtin wait the compiler sees).
+// Kernels that use this must not spill: the library build rejects scratch use in the files that
+// include this header.
 //
 // M0 is written here without the compiler knowing (it does not honour M0 in a clobber list, a
 // reserved register).  That is safe only while the compiler itself keeps nothing in M0 in these

@@ -372,62 +372,113 @@ __global__ __launch_bounds__(kThreads, 1) void prefill_gemm_kernel(const Args p)
         }
       }
     } else if constexpr (EPI == E_SWIGLU) {
+      // Gate fragment 2 pb, up fragment 2 pb + 1: channels 16 (n0 / 32 + FN wn / 2 + pb) + 4 g.
+      // The bias loads of kG pairs are issued together, and those of the next kG pairs before
+      // this group's stores: the compiler's wait for a load also waits for every older memory
+      // operation (the stores before it, the next tile's copies), so loads issued one pair at a
+      // time after the previous pair's stores took a full round trip per pair.
       const int F = p.d_ff;
+      constexpr int kG = 2, NP = FN / 2;
+      static_assert(NP % (2 * kG) == 0, "bias groups");
+      auto chan = [&](int pb) { return 16 * (n0 / 32 + NP * wn + pb) + 4 * g; };
+      auto load_bias = [&](int pb0, float4 (&bg)[kG], float4 (&bu)[kG]) {
 #pragma unroll
-      for (int pb = 0; pb < FN / 2; ++pb) {
-        // gate fragment 2 pb, up fragment 2 pb + 1: channels 16 (n0 / 32 + FN wn / 2 + pb) + 4 g
-        const int ch = 16 * (n0 / 32 + FN / 2 * wn + pb) + 4 * g;
-        if (2 * ch >= N) continue;
-        const float4 bg = p.bias_a ? *reinterpret_cast<const float4*>(p.bias_a + ch)
-                                   : make_float4(0.f, 0.f, 0.f, 0.f);
-        const float4 bu = p.bias_b ? *reinterpret_cast<const float4*>(p.bias_b + ch)
-                                   : make_float4(0.f, 0.f, 0.f, 0.f);
-#pragma unroll
-        for (int j = 0; j < FM; ++j) {
-          const int r = 16 * (FM * wm + j) + c;
-          const int m = m0 + r;
-          if (m >= M) continue;
-          const float rs = AMODE == A_NORM ? rstd_s[r] : 1.f;
-          const f32x4_t gs = acc[2 * pb][j], us = acc[2 * pb + 1][j];
-          // the arithmetic of K3 (swiglu.hip)
-          const float o[4] = {silu_mul(fmaf(rs, gs[0], bg.x), fmaf(rs, us[0], bu.x)),
-                              silu_mul(fmaf(rs, gs[1], bg.y), fmaf(rs, us[1], bu.y)),
-                              silu_mul(fmaf(rs, gs[2], bg.z), fmaf(rs, us[2], bu.z)),
-                              silu_mul(fmaf(rs, gs[3], bg.w), fmaf(rs, us[3], bu.w))};
-          uint2 hi, lo;
-          split4(o, hi, lo);
-          *reinterpret_cast<uint2*>(p.h + tile_off(m, ch, p.h_parts * F)) = hi;
-          if (p.h_parts == 2) *reinterpret_cast<uint2*>(p.h + tile_off(m, F + ch, 2 * F)) = lo;
+        for (int q = 0; q < kG; ++q) {
+          const int ch = min(chan(pb0 + q), F - 4);   // in bounds; unused past F
+          bg[q] = p.bias_a ? *reinterpret_cast<const float4*>(p.bias_a + ch)
+                           : make_float4(0.f, 0.f, 0.f, 0.f);
+          bu[q] = p.bias_b ? *reinterpret_cast<const float4*>(p.bias_b + ch)
+                           : make_float4(0.f, 0.f, 0.f, 0.f);
         }
-      }
-    } else {
+      };
+      auto store_h = [&](int pb0, const float4 (&bg)[kG], const float4 (&bu)[kG]) {
 #pragma unroll
-      for (int i = 0; i < FN; ++i) {
-        const int n = n0 + 16 * (FN * wn + i) + 4 * g;
-        if (n >= N) continue;
-        float4 bv = make_float4(0.f, 0.f, 0.f, 0.f);
-        if constexpr (EPI == E_RESIDUAL) {
-          if (p.bias_a) bv = *reinterpret_cast<const float4*>(p.bias_a + n);
-        }
+        for (int q = 0; q < kG; ++q) {
+          const int pb = pb0 + q, ch = chan(pb);
+          if (2 * ch >= N) continue;
 #pragma unroll
-        for (int j = 0; j < FM; ++j) {
-          const int m = m0 + 16 * (FM * wm + j) + c;
-          if (m >= M) continue;
-          const f32x4_t v = acc[i][j];
-          if constexpr (EPI == E_RESIDUAL) {
-            // x + delta, then + bias: the order of the add+RMSNorm kernel it replaces
-            float4* xr = reinterpret_cast<float4*>(p.x_res + tile_off32(m, n, N));
-            float4 xv = *xr;
-            xv.x += v[0]; xv.y += v[1]; xv.z += v[2]; xv.w += v[3];
-            if (p.bias_a) {
-              xv.x += bv.x; xv.y += bv.y; xv.z += bv.z; xv.w += bv.w;
-            }
-            *xr = xv;
-          } else {
-            *reinterpret_cast<float4*>(p.out + static_cast<int64_t>(m) * p.ldo + n) =
-                make_float4(v[0], v[1], v[2], v[3]);
+          for (int j = 0; j < FM; ++j) {
+            const int r = 16 * (FM * wm + j) + c;
+            const int m = m0 + r;
+            if (m >= M) continue;
+            const float rs = AMODE == A_NORM ? rstd_s[r] : 1.f;
+            const f32x4_t gs = acc[2 * pb][j], us = acc[2 * pb + 1][j];
+            // the arithmetic of K3 (swiglu.hip)
+            const float o[4] = {silu_mul(fmaf(rs, gs[0], bg[q].x), fmaf(rs, us[0], bu[q].x)),
+                                silu_mul(fmaf(rs, gs[1], bg[q].y), fmaf(rs, us[1], bu[q].y)),
+                                silu_mul(fmaf(rs, gs[2], bg[q].z), fmaf(rs, us[2], bu[q].z)),
+                                silu_mul(fmaf(rs, gs[3], bg[q].w), fmaf(rs, us[3], bu[q].w))};
+            uint2 hi, lo;
+            split4(o, hi, lo);
+            *reinterpret_cast<uint2*>(p.h + tile_off(m, ch, p.h_parts * F)) = hi;
+            if (p.h_parts == 2) *reinterpret_cast<uint2*>(p.h + tile_off(m, F + ch, 2 * F)) = lo;
           }
         }
+      };
+      float4 ga[kG], ua[kG], gb[kG], ub[kG];
+      load_bias(0, ga, ua);
+#pragma unroll
+      for (int pb0 = 0; pb0 < NP; pb0 += 2 * kG) {
+        load_bias(pb0 + kG, gb, ub);
+        store_h(pb0, ga, ua);
+        if (pb0 + 2 * kG < NP) load_bias(pb0 + 2 * kG, ga, ua);
+        store_h(pb0 + kG, gb, ub);
+      }
+    } else {
+      // The residual's loads of kG weight fragments are issued together, and those of the next
+      // kG before this group's stores (see E_SWIGLU: one load and its wait per fragment, after
+      // the previous fragment's store, took a full round trip each).
+      constexpr int kG = 2;
+      static_assert(FN % (2 * kG) == 0, "residual groups");
+      auto col = [&](int i) { return n0 + 16 * (FN * wn + i) + 4 * g; };
+      auto row = [&](int j) { return m0 + 16 * (FM * wm + j) + c; };
+      auto load_x = [&](int i0, float4 (&xv)[kG][FM], float4 (&bv)[kG]) {
+        if constexpr (EPI == E_RESIDUAL) {
+#pragma unroll
+          for (int u = 0; u < kG; ++u) {
+            const int n = min(col(i0 + u), N - 4);   // in bounds; unused past N or M
+            bv[u] = p.bias_a ? *reinterpret_cast<const float4*>(p.bias_a + n)
+                             : make_float4(0.f, 0.f, 0.f, 0.f);
+#pragma unroll
+            for (int j = 0; j < FM; ++j)
+              xv[u][j] = *reinterpret_cast<const float4*>(
+                  p.x_res + tile_off32(min(row(j), M - 1), n, N));
+          }
+        }
+      };
+      auto store_x = [&](int i0, const float4 (&xv)[kG][FM], const float4 (&bv)[kG]) {
+#pragma unroll
+        for (int u = 0; u < kG; ++u) {
+          const int n = col(i0 + u);
+          if (n >= N) continue;
+#pragma unroll
+          for (int j = 0; j < FM; ++j) {
+            const int m = row(j);
+            if (m >= M) continue;
+            const f32x4_t v = acc[i0 + u][j];
+            if constexpr (EPI == E_RESIDUAL) {
+              // x + delta, then + bias: the order of the add+RMSNorm kernel it replaces
+              float4 x = xv[u][j];
+              x.x += v[0]; x.y += v[1]; x.z += v[2]; x.w += v[3];
+              if (p.bias_a) {
+                x.x += bv[u].x; x.y += bv[u].y; x.z += bv[u].z; x.w += bv[u].w;
+              }
+              *reinterpret_cast<float4*>(p.x_res + tile_off32(m, n, N)) = x;
+            } else {
+              *reinterpret_cast<float4*>(p.out + static_cast<int64_t>(m) * p.ldo + n) =
+                  make_float4(v[0], v[1], v[2], v[3]);
+            }
+          }
+        }
+      };
+      float4 xa[kG][FM], ba[kG], xb[kG][FM], bb[kG];
+      load_x(0, xa, ba);
+#pragma unroll
+      for (int i0 = 0; i0 < FN; i0 += 2 * kG) {
+        load_x(i0 + kG, xb, bb);
+        store_x(i0, xa, ba);
+        if (i0 + 2 * kG < FN) load_x(i0 + 2 * kG, xa, ba);
+        store_x(i0 + kG, xb, bb);
       }
     }
   };
