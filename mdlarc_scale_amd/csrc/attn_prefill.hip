@@ -273,19 +273,27 @@ __global__ __launch_bounds__(256, 3) void attn_prefill_kernel(
       for (int kk = 0; kk < 2; ++kk) pb[j][kk] = pt_operand(sc[j][2 * kk], sc[j][2 * kk + 1]);
     }
 
-    // O^T += V^T P^T and the row sums, two k-steps of 32 keys
+    // O^T += V^T P^T and the row sums, two k-steps of 32 keys.  A k-step's 8 transposing reads
+    // are issued together (the scheduling barrier keeps them ahead of the MFMAs): one LDS round
+    // trip per k-step instead of one per dim block, in the same 122 registers (1-2% faster at
+    // configs 2-4; both k-steps' 16 reads at once need 134, occupancy 3, and ran 3-7% slower)
 #pragma unroll
     for (int kk = 0; kk < 2; ++kk) {
+      bf16x8_t va[4];
 #pragma unroll
       for (int db = 0; db < 4; ++db) {
         const s16x4_t lo4 = lds_read_tr16(
             reinterpret_cast<const uint16_t*>(Vt + vofs[db] + 4096 * kk));
         const s16x4_t hi4 = lds_read_tr16(
             reinterpret_cast<const uint16_t*>(Vt + vofs[db] + 4096 * kk + 2048));
-        const bf16x8_t a = __builtin_bit_cast(
+        va[db] = __builtin_bit_cast(
             bf16x8_t, __builtin_shufflevector(lo4, hi4, 0, 1, 2, 3, 4, 5, 6, 7));
-        o[0][db] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, pb[0][kk], o[0][db], 0, 0, 0);
-        o[1][db] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, pb[1][kk], o[1][db], 0, 0, 0);
+      }
+      __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+      for (int db = 0; db < 4; ++db) {
+        o[0][db] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(va[db], pb[0][kk], o[0][db], 0, 0, 0);
+        o[1][db] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(va[db], pb[1][kk], o[1][db], 0, 0, 0);
       }
       lsum[0] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ones, pb[0][kk], lsum[0], 0, 0, 0);
       lsum[1] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ones, pb[1][kk], lsum[1], 0, 0, 0);
