@@ -94,12 +94,13 @@ def test_residual_gemm_matches_fp64(m, n, k, bias):
     assert torch.equal(untiled(x1)[m:], untiled(x1_before)[m:])
 
 
+@pytest.mark.parametrize("bias", [True, False])
 @pytest.mark.parametrize("m,f,k", [(1000, 2048, 768), (333, 704, 256), (257, 2752, 1024),
                                    (700, 3392, 1280), (5, 2048, 768)])
-def test_norm_swiglu_gemm(m, f, k):
+def test_norm_swiglu_gemm(m, f, k, bias):
     """The ln2 + gate/up + SwiGLU form equals K3 (mdl_swiglu) applied to the same launch's gate /
     up accumulators (the E_STORE form on the interleaved weight, same main loop), bit for bit;
-    and an fp64 reference to fp32 rounding."""
+    and an fp64 reference to fp32 rounding.  Without biases (NULL) the epilogue adds zeros."""
     g = torch.Generator().manual_seed(m + f + k)
     wg = (0.05 * torch.randn(f, k, generator=g)).to(torch.bfloat16).to(DEV)
     wu = (0.05 * torch.randn(f, k, generator=g)).to(torch.bfloat16).to(DEV)
@@ -108,6 +109,8 @@ def test_norm_swiglu_gemm(m, f, k):
     gam = (1 + 0.1 * torch.randn(k, generator=g)).to(DEV)
     bg = torch.randn(f, generator=g).to(DEV)
     bu = torch.randn(f, generator=g).to(DEV)
+    if not bias:
+        bg = bu = None
     xt = K().tile_f32(x)
     h = torch.empty(K().split_numel(m, f, True), dtype=torch.bfloat16, device=DEV)
     K().prefill_gemm_norm_swiglu(xt, gam, 1e-5, wgu, bg, bu, h, m, f, k)
@@ -124,8 +127,10 @@ def test_norm_swiglu_gemm(m, f, k):
     th, tl = split(x * gam)
     t = th.double() + tl.double()
     rs64 = 1 / torch.sqrt((x.double() ** 2).mean(1) + 1e-5)
-    gg = rs64[:, None] * (t @ wg.double().t()) + bg.double()
-    uu = rs64[:, None] * (t @ wu.double().t()) + bu.double()
+    gg = rs64[:, None] * (t @ wg.double().t())
+    uu = rs64[:, None] * (t @ wu.double().t())
+    if bias:
+        gg, uu = gg + bg.double(), uu + bu.double()
     ref = gg / (1 + torch.exp(-gg)) * uu
     hh = K().untile_matrix(h, m, 2 * f).double()
     assert rel(hh[:, :f] + hh[:, f:], ref) < 2e-5
