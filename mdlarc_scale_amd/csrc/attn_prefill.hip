@@ -184,7 +184,10 @@ __global__ __launch_bounds__(256, 3) void attn_prefill_kernel(
   const char* Kb = reinterpret_cast<const char*>(&Ks[0][0]);
   const char* Vb = reinterpret_cast<const char*>(&Vs[0][0]);
 
-  float m_run[2] = {-INFINITY, -INFINITY};
+  // Per query: negm = -m, the negated reference maximum (0 before the first visible key), and
+  // thr, the tile maximum (relative to m) that moves the reference: -inf before the first
+  // visible key, then the gap.  Both change only when the reference moves.
+  float negm[2] = {0.f, 0.f}, thr[2] = {-INFINITY, -INFINITY};
   f32x4_t lsum[2], o[2][4];
 #pragma unroll
   for (int j = 0; j < 2; ++j) {
@@ -201,8 +204,7 @@ __global__ __launch_bounds__(256, 3) void attn_prefill_kernel(
     f32x4_t minit[2];
 #pragma unroll
     for (int j = 0; j < 2; ++j) {
-      const float r = m_run[j] == -INFINITY ? 0.f : -m_run[j];
-      minit[j] = f32x4_t{r, r, r, r};
+      minit[j] = f32x4_t{negm[j], negm[j], negm[j], negm[j]};
     }
 #pragma unroll
     for (int nb = 0; nb < 4; ++nb) {
@@ -251,12 +253,14 @@ __global__ __launch_bounds__(256, 3) void attn_prefill_kernel(
       // (or on its first visible key, while m = -inf and the scores are absolute; alpha = 0);
       // other queries are left untouched.  That maximum can pass only if one of its four lanes'
       // maxima does (same test), so the cross-lane maximum is formed only in those tiles.
-      const bool fresh = m_run[j] == -INFINITY;
-      if (__ballot(fresh ? lmax > -INFINITY : lmax > kRescaleGap) != 0) {
+      if (__ballot(lmax > thr[j]) != 0) {
         const float tmax = max_over_groups(lmax);
-        if (fresh ? tmax > -INFINITY : tmax > kRescaleGap) {
+        if (tmax > thr[j]) {
+          const bool fresh = thr[j] == -INFINITY;
           const float alpha = fresh ? 0.f : __builtin_amdgcn_exp2f(-tmax);
-          m_run[j] = fresh ? tmax : m_run[j] + tmax;
+          // -(m + tmax), as (-m) - tmax: the same value bit for bit
+          negm[j] = fresh ? -tmax : negm[j] - tmax;
+          thr[j] = kRescaleGap;
 #pragma unroll
           for (int nb = 0; nb < 4; ++nb) sc[j][nb] -= tmax;
           lsum[j] *= alpha;
