@@ -63,7 +63,12 @@ __device__ __forceinline__ void split_bf2(float a, float b, uint32_t& hi, uint32
 #pragma clang fp contract(off)
   const bf16x2_t h = {static_cast<__bf16>(a), static_cast<__bf16>(b)};
   hi = __builtin_bit_cast(uint32_t, h);
-  lo = pack_bf2(a - static_cast<float>(h[0]), b - static_cast<float>(h[1]));
+  // the two rounded halves widened from the packed pair itself (a bf16 is the top half of its
+  // fp32): the low one by a byte permute (bytes 1, 0 of hi to bytes 3, 2, zeros below), which
+  // the compiler cannot turn back into a second rounding of a plus a shift, as it does `hi << 16`
+  const float h0 = __builtin_bit_cast(float, __builtin_amdgcn_perm(0u, hi, 0x01000c0cu));
+  const float h1 = __builtin_bit_cast(float, hi & 0xffff0000u);
+  lo = pack_bf2(a - h0, b - h1);
 }
 
 // 4 floats -> hi (uint2) and lo (uint2)
