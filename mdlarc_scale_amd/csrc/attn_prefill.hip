@@ -21,8 +21,10 @@
 // barrier that publishes tile t, so it runs under tile t's MFMA and softmax work; one barrier per
 // tile.  Rows cannot be padded within a kilobyte, so the 16-byte chunks of a row are XOR-swizzled
 // instead (chunk c of row r at chunk c ^ swz(r)): the column reads of the K operand (16 rows, one
-// chunk) and the transposing V reads then hit distinct banks.  Keys outside [kv_start, S) load
-// the nearest valid key (finite data; their probabilities are 0, so they add exact zeros).
+// chunk) and the transposing V reads then hit distinct banks.  Key tiles start at the row's first
+// valid key (kv_start) and packed query tiles at its first query, so no tile straddles the row
+// start; keys past S in a row's last tile load the nearest valid key (finite data; their
+// probabilities are 0, so they add exact zeros).
 //
 // Masking: each wave folds key validity (inside [kv_start, S) and the key mask) of a tile into a
 // 64-bit ballot: from a mask byte it loaded one tile ahead, or, for a row without a key mask (or
@@ -84,12 +86,14 @@ __global__ __launch_bounds__(256, 3) void attn_prefill_kernel(
   const int b = bh / H, h = bh - b * H;
   const int tid = threadIdx.x;
   const int wave = tid >> 6, lane = tid & 63, c16 = lane & 15, g = lane >> 4;
-  const int q0 = qt * kBM;
   const int kstart = kv_start ? min(max(kv_start[b], 0), S) : 0;
   // packed rows: query qi >= kstart of row b is row q_offset[b] + qi - kstart of q and out;
   // queries before kstart are not part of the packed list and are neither read nor written
   const int qlo = q_offset ? kstart : 0;
-  if (q0 + kBM <= qlo) return;                  // the whole query tile is before the row start
+  // query tiles start at the row's first query (packed rows; 0 otherwise), key tiles at its
+  // first valid key: no tile straddles the row start
+  const int q0 = qlo + qt * kBM;
+  if (q0 >= S) return;                          // the whole query tile is past the row end
   const int64_t qbase = q_offset ? static_cast<int64_t>(q_offset[b]) - kstart
                                  : static_cast<int64_t>(b) * S;
 
@@ -115,7 +119,7 @@ __global__ __launch_bounds__(256, 3) void attn_prefill_kernel(
   const int64_t head_off = (static_cast<int64_t>(b) * H + h) * slots * kHeadDim;
   const uint16_t* Kg = kc + head_off;
   const uint16_t* Vg = vc + head_off;
-  const int kt0 = (kstart / kBN) * kBN;
+  const int kt0 = kstart;
   // a row with no valid key attends to nothing: its tiles are skipped (o and the sum stay 0)
   const int kend = kstart >= S ? kt0 : (causal ? min(S, q0 + kBM) : S);
   // row_holes[b] == 0: the key mask of row b is exactly [kstart, S), which kstart already says
