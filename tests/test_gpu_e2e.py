@@ -1032,6 +1032,66 @@ def test_prompt_path_without_k6_vs_oracle(decode_tiled, monkeypatch):
     _compare_with_oracle(m, state, ids, pos, ex, mask, 32, f"no-K6 decode_tiled={decode_tiled}")
 
 
+@pytest.mark.parametrize("spec_name,rows,drops", [
+    ("small_b256", 8, ["qkv", "out", "gate_up", "down", "qkv+out"]),
+    ("medium_b128", 2, ["qkv", "out", "qkv+out"]), ("large_b64", 2, ["qkv", "out", "qkv+out"])])
+def test_prompt_projection_lo_terms(monkeypatch, spec_name, rows, drops):
+    """What each prompt projection's lo term is worth at configs 2-4's real prompt lengths (the
+    parity harness's slices: 8 rows of config 2, 2 of configs 3 and 4; bf16): the prompt path's
+    projections take their
+    split inputs through gemm_f32 when K6 is off, so zeroing the lo half of one projection's
+    input there drops exactly that projection's lo product (qkv, out, gate/up or down; the
+    decode path is untouched, and reads the cache the prefill wrote).  Prints each variant's
+    teacher-forced decode error against the fp32 oracle; asserts only that the split forward
+    keeps the 2e-2 bar and that each variant changes the logits (the drop took effect).
+    Measured: qkv or out alone 7.3e-3 / 8.0e-3 at config 2 and 6.1e-3 / 6.7e-3 at config 3, but
+    1.2e-2 / 1.3e-2 at config 4's 5,000-token prompts (split: 4.8e-3 / 4.4e-3 / 6.0e-3), so the
+    engine keeps both parts on every projection."""
+    from mdlarc_scale_amd import engine
+    from mdlarc_scale_amd.workload import SPECS, build_prompts, left_pad
+
+    spec = SPECS[spec_name]
+    prompts = build_prompts(spec)
+    order = sorted(range(len(prompts)), key=lambda i: len(prompts[i]))
+    sl = [prompts[order[round(k * (len(order) - 1) / (rows - 1))]] for k in range(rows)]
+    ids, pos, mask = left_pad(sl)
+    B, S = ids.shape
+    max_new = 24
+    m, state = _preset_model(spec.preset, "bf16", max_seq_len=spec.cache_slots)
+    om = _oracle_of(m, state)
+    ex = torch.arange(B) * 3
+    tr = rp.generate_output(om, ids, pos, ex, mask, max_new)
+    g = len(tr.step_logits)
+    ref = torch.stack(tr.step_logits, 1)
+
+    monkeypatch.setattr(engine, "prompt_gemms_fused", lambda d_model, d_ff: False)
+    real = engine.gemm_f32
+    names = ["qkv", "out", "gate_up", "down"]   # the prompt path's gemm_f32 calls, per layer
+    errs, outs = {}, {}
+    for drop in [None] + drops:
+        calls = [0]
+
+        def gemm(a, w2, out, drop=drop, calls=calls):
+            if drop is not None and names[calls[0] % 4] in drop.split("+"):
+                a = a.clone()
+                a[:, a.shape[1] // 2:] = 0           # the lo half of the split input
+            calls[0] += 1
+            return real(a, w2, out)
+
+        monkeypatch.setattr(engine, "gemm_f32", gemm)
+        got, _, _ = _teacher_forced_decode(m, ids, pos, ex, mask, tr.tokens, g,
+                                           spec.cache_slots)
+        assert calls[0] == 4 * m.config.n_layers
+        errs[drop] = (got - ref).abs().max().item()
+        outs[drop] = got
+    print(f"{spec_name} slice (prompts {[len(p) for p in sl]}), prompt projection lo term "
+          "dropped -> teacher-forced decode max-abs: "
+          + ", ".join(f"{k or 'none'} {v:.3e}" for k, v in errs.items()))
+    assert errs[None] <= 2e-2
+    for name in drops:
+        assert (outs[name] - outs[None]).abs().max().item() > 0
+
+
 def test_prompt_mlp_single_part_vs_oracle(monkeypatch):
     """The prompt MLP with the lo term dropped (engine.PROMPT_GATE_UP_PARTS and
     PROMPT_DOWN_PARTS at 1: gate / up on bf16(ln2(x)), h stored and read as hi alone) -- an
