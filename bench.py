@@ -30,7 +30,9 @@ Also reported on the same JSON line:
 * ``prefill_attention``: the prefill attention kernel alone over one layer of the batch's cache
   (its real masks and left padding, packed query rows as the prefill launches it), re-launched
   back to back (median of 5 rounds of 10 launches after 3 warm ones); TFLOP/s of the valid
-  causal (query, key) pairs against the 2.5 PFLOP/s dense bf16 MFMA peak.
+  causal (query, key) pairs against the 2.5 PFLOP/s dense bf16 MFMA peak, and (``hbm``) the same
+  launches' algorithmic bytes (q, the K/V of every valid key once, the hi|lo output) against
+  the 8 TB/s HBM peak.
 
 * ``configs``: BASELINE configs 3 (medium, B=128, 4,096-slot cache) and 4 (large, B=64, prompts
   of 5,000-5,726 tokens) measured the same way over 32 graph-replayed steps each: decode
@@ -564,6 +566,10 @@ def measure_workload(spec, steps, warmup, dev, eager=False, snapshot=False):
         # time depends on values only through how often a query's running maximum moves
         n_valid = mask.sum(1)
         pa_flops = 4 * 64 * H * int((n_valid * (n_valid + 1) // 2).sum())
+        # its algorithmic HBM bytes: bf16 q, the K and V rows of every valid key once, the
+        # hi|lo output, and the prompt-mask bytes of rows whose mask has holes
+        pa_bytes = int(n_valid.sum()) * H * 64 * 2 * 5 + int(
+            ((S - kv_start_h.to(torch.int64)).clamp(min=0) * holes_h.to(torch.int64)).sum())
         starts = torch.stack([st.kv_start, st.last_row]).cpu().numpy()
         pk = pack_prompt(starts[0], starts[1], B, S, dev)
         qp = (torch.randn(pk.n_valid, H * 64, device=dev)
@@ -599,7 +605,8 @@ def measure_workload(spec, steps, warmup, dev, eager=False, snapshot=False):
         prefill_ms=prefill_ms, timed_ms=timed_ms, wall_s=wall_s,
         value=B * steps / (timed_ms / 1e3), attn_ms=attn_ms, attn_bytes=attn_bytes,
         attn_launches=len(ts), n_split=n_split, decode_nb=decode_nb, n_valid=n_valid,
-        pa_ms=pa_ms, pa_flops=pa_flops, prefill_flops=cfg.n_layers * pa_flops, snap=snap,
+        pa_ms=pa_ms, pa_flops=pa_flops, pa_bytes=pa_bytes,
+        prefill_flops=cfg.n_layers * pa_flops, snap=snap,
         proj=proj,
         model_state=model_state, cfg=cfg)
     if snapshot:
@@ -697,13 +704,23 @@ def roofline_of(r):
 
 def prefill_attention_of(r):
     pa_ms, pa_flops = r["pa_ms"], r["pa_flops"]
-    return {
+    out = {
         "kernel": "attn_prefill_kernel (mdl_attn_prefill_packed, bf16 MFMA)", "bound": "mfma",
         "ms_per_layer": round(pa_ms, 4), "tflop_per_layer": round(pa_flops / 1e12, 4),
         "achieved": round(pa_flops / pa_ms / 1e9, 1), "peak": BF16_PEAK_TFLOPS,
         "unit": "TFLOP/s", "frac": round(pa_flops / pa_ms / 1e9 / BF16_PEAK_TFLOPS, 4),
         "flops": "valid causal (query, key) pairs x 4 x 64 (QK^T and PV)",
     }
+    if r.get("pa_bytes"):
+        # the same launches against the HBM roofline (the rocprofv3 FETCH_SIZE / WRITE_SIZE
+        # passes measure 1.02-1.04 / 1.00 of these bytes)
+        gbs = r["pa_bytes"] / pa_ms / 1e6
+        out["hbm"] = {"bytes_per_launch": r["pa_bytes"], "achieved": round(gbs, 1),
+                      "peak": HBM_PEAK_GBS, "unit": "GB/s", "frac": round(gbs / HBM_PEAK_GBS, 4),
+                      "bytes": "bf16 q, the K and V rows of every valid key once, the hi|lo "
+                               "output, prompt-mask bytes of rows with holes",
+                      "traffic_source": "profiles/prefill_attention_mfma.md"}
+    return out
 
 
 def prefill_of(r):

@@ -45,6 +45,11 @@ def test_prefill_attention_and_prefill_objects():
     assert pa["bound"] == "mfma" and pa["unit"] == "TFLOP/s"
     assert pa["achieved"] == pytest.approx(625.0)
     assert pa["frac"] == pytest.approx(0.25)
+    assert "hbm" not in pa
+    pa = bench.prefill_attention_of({"pa_ms": 0.8, "pa_flops": 0.5e12, "pa_bytes": 2.0e9})
+    assert pa["hbm"]["unit"] == "GB/s" and pa["hbm"]["peak"] == 8000.0
+    assert pa["hbm"]["achieved"] == pytest.approx(2500.0)     # 2 GB in 0.8 ms
+    assert pa["hbm"]["frac"] == pytest.approx(0.3125)
     r = {"n_valid": torch.tensor([300, 700]), "prefill_ms": 2.0, "B": 2, "S": 700,
          "prefill_flops": 3.0e12}
     pf = bench.prefill_of(r)
