@@ -81,7 +81,7 @@ __global__ __launch_bounds__(256, 3) void attn_prefill_kernel(
   const int slot = blockIdx.x / kXcds;
   const int kq = slot / nqt;
   const int bh = blockIdx.x % kXcds + kXcds * kq;
-  if (bh >= n_bh) return;                       // padding blocks of the last round exit
+  if (bh >= n_bh) return;                       // heads padded to a multiple of 8: extras exit
   const int qt = nqt - 1 - (slot - kq * nqt);
   const int b = bh / H, h = bh - b * H;
   const int tid = threadIdx.x;
